@@ -1,0 +1,267 @@
+/*
+ * mx.h -- C ABI of the MI355X (gfx950) FP32 conv / GEMM / fused-AdamW library.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, returns an
+ * int status (MX_OK == 0) and is asynchronous on the `stream` argument (a
+ * hipStream_t passed as void*; NULL is HIP's null stream, as in the HIP API).
+ * On failure mx_last_error() returns a thread-local message.  All validation
+ * happens on the host before any launch.
+ *
+ * Each declaration names the reference interface it replaces
+ * (mistrjirka/Pytorch-vulkan, paths relative to the repository root).
+ */
+#ifndef MX_H
+#define MX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum mx_status {
+  MX_OK = 0,
+  MX_ERR_INVALID = 1,     /* bad shape / argument: TORCH_CHECK failures in the reference */
+  MX_ERR_UNSUPPORTED = 2, /* forced algorithm not applicable (convolution.cpp:472-473) */
+  MX_ERR_OOM = 3,         /* device allocation failed */
+  MX_ERR_HIP = 4,         /* HIP runtime error */
+  MX_ERR_WORKSPACE = 5    /* workspace budget too small for the requested algorithm */
+};
+
+/* ------------------------------------------------------------------------ */
+/* Errors, version, device                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Thread-local message of the last failing call ("" if none). */
+const char* mx_last_error(void);
+int mx_abi_version(void);
+
+/* Replaces VulkanContext::instance() device creation
+ * (csrc/vulkan_context.cpp:64-83) and validate_vulkan_device. */
+int mx_init(int ordinal);
+int mx_device_count(int* count);
+int mx_get_device(int* ordinal);
+int mx_set_device(int ordinal);
+int mx_device_name(int ordinal, char* buf, size_t len);
+int mx_device_synchronize(void);
+
+/* ------------------------------------------------------------------------ */
+/* Streams and events: replace the single VkQueue + Kompute sequences        */
+/* (csrc/torch_vulkan.cpp:34-103, csrc/vulkan_context.cpp:444-510).           */
+/* ------------------------------------------------------------------------ */
+
+/* The library's default stream of the current device (non-blocking, default
+ * priority); the PrivateUse1 layer's stream 0. */
+int mx_default_stream(void** stream);
+int mx_stream_create(void** stream);
+int mx_stream_destroy(void* stream);
+int mx_stream_synchronize(void* stream);
+/* *done = 1 when all work on the stream has completed. */
+int mx_stream_query(void* stream, int* done);
+int mx_stream_wait_event(void* stream, void* event);
+int mx_event_create(void** event, int enable_timing);
+int mx_event_destroy(void* event);
+int mx_event_record(void* event, void* stream);
+int mx_event_query(void* event, int* done);
+int mx_event_synchronize(void* event);
+int mx_event_elapsed_ms(void* start, void* end, float* ms);
+
+/* ------------------------------------------------------------------------ */
+/* Stream-ordered caching device allocator: replaces VulkanAllocator         */
+/* (csrc/vulkan_allocator.h:22-73, csrc/vulkan_allocator.cpp:19-154).         */
+/* A freed block is reusable at once by later work on its allocation stream; */
+/* use on other streams (mx_record_stream) defers reuse until events recorded */
+/* on those streams at free time have completed.                             */
+/* ------------------------------------------------------------------------ */
+
+typedef struct mx_memory_stats {
+  uint64_t allocated_bytes;  /* bytes in live blocks */
+  uint64_t reserved_bytes;   /* bytes obtained from hipMalloc and not yet released */
+  uint64_t cached_blocks;    /* free blocks held for reuse */
+  uint64_t device_mallocs;   /* hipMalloc calls so far */
+  uint64_t cache_hits;       /* allocations served from the cache */
+} mx_memory_stats;
+
+int mx_malloc(void** ptr, size_t bytes, void* stream);
+int mx_free(void* ptr);
+int mx_record_stream(void* ptr, void* stream);
+int mx_empty_cache(void);
+int mx_memory_stats_get(mx_memory_stats* out);
+
+enum mx_copy_kind { MX_COPY_H2D = 1, MX_COPY_D2H = 2, MX_COPY_D2D = 3 };
+/* Async copy on `stream`.  D2H/H2D with pageable host memory is staged and is
+ * complete on return (as the reference's ensure_host_read,
+ * csrc/vulkan_context.cpp:98-112). */
+int mx_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Elementwise / layout plumbing used by the operator surface                */
+/* (csrc/ops/mm.cpp:480-700, csrc/ops/native_utils.h:106-151).               */
+/* ------------------------------------------------------------------------ */
+
+/* Fill `count` elements of `elem_size` (1,2,4,8) bytes with the low bytes of
+ * `pattern` (fill_.Scalar / zero_, csrc/ops/loss_primitives.cpp:374-375). */
+int mx_fill(void* dst, int64_t count, int elem_size, uint64_t pattern, void* stream);
+
+/* Strided copy of up to 8 dims: dst[idx] = src[idx] with element strides and
+ * element offsets, elements of `elem_size` bytes.  This is the conv2d_pack
+ * view materialisation (csrc/shaders/conv2d_pack.comp:12-22,
+ * csrc/ops/convolution.cpp:62-99) and the strided device copy_
+ * (csrc/ops/mm.cpp:592-608). */
+int mx_copy_strided(void* dst, const void* src, int ndim, const int64_t* sizes,
+                    const int64_t* dst_strides, const int64_t* src_strides,
+                    int64_t dst_offset, int64_t src_offset, int elem_size, void* stream);
+
+/* out[i] = a[i] + alpha * b[i] (FP32, contiguous): aten::add.Tensor used by
+ * autograd gradient accumulation.  With b == NULL: out[i] = a[i] + alpha. */
+int mx_add_f32(float* out, const float* a, const float* b, float alpha, int64_t n, void* stream);
+/* out[i] = a[i] * s (FP32 contiguous): mul.Scalar (csrc/ops/mm.cpp:921-930). */
+int mx_scale_f32(float* out, const float* a, float s, int64_t n, void* stream);
+
+/* Sum over the middle axis of a contiguous [outer, reduce, inner] FP32 view:
+ * out[o, i] = sum_r src[o, r, i].  Replaces sum.dim_IntList
+ * (csrc/ops/reduce.cpp:24-35), e.g. the Linear bias gradient dY.sum(0). */
+int mx_sum_f32(float* out, const float* src, int64_t outer, int64_t reduce, int64_t inner,
+               void* stream);
+
+/* In-place `ptrs[i][0..numels[i]) += value` over a list of FP32 tensors in one
+ * launch (_foreach_add_.Scalar on the optimizer step counters). */
+int mx_foreach_add_scalar_f32(float* const* ptrs, const int64_t* numels, int64_t count,
+                              float value, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Conv2D (FP32 NCHW)                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* ConvParams (csrc/ops/convolution.cpp:45-52). oh/ow are outputs of
+ * mx_conv2d_check. */
+typedef struct mx_conv2d_desc {
+  int64_t n, cin, h, w;      /* input  [n, cin, h, w] */
+  int64_t cout, kh, kw;      /* weight [cout, cin/groups, kh, kw] */
+  int64_t sh, sw, ph, pw, dh, dw, groups;
+  int64_t oh, ow;            /* output [n, cout, oh, ow] (filled by mx_conv2d_check) */
+} mx_conv2d_desc;
+
+enum mx_conv_phase { MX_CONV_FORWARD = 0, MX_CONV_DINPUT = 1, MX_CONV_DWEIGHT = 2, MX_CONV_DBIAS = 3 };
+
+/* Algorithms (candidate menu of csrc/ops/convolution.cpp:161-187):
+ * AUTO lets the planner choose; DIRECT is one-output-per-thread; IMPLICIT_GEMM
+ * is the MFMA tile path; WINOGRAD is F(2x2,3x3) forward; REDUCE is the
+ * no-scratch dWeight / dBias reduction. */
+enum mx_conv_algo {
+  MX_CONV_ALGO_AUTO = 0,
+  MX_CONV_ALGO_DIRECT = 1,
+  MX_CONV_ALGO_IMPLICIT_GEMM = 2,
+  MX_CONV_ALGO_WINOGRAD = 3,
+  MX_CONV_ALGO_REDUCE = 4
+};
+
+/* Validation and output shape: convolution_params
+ * (csrc/ops/convolution.cpp:101-156).  Fills desc->oh / desc->ow. */
+int mx_conv2d_check(mx_conv2d_desc* desc);
+
+/* Algorithm the planner would run for `phase` given `requested`
+ * (heuristic / applicable, csrc/ops/convolution.cpp:357-482).  Returns
+ * MX_ERR_UNSUPPORTED when a forced algorithm does not apply. */
+int mx_conv2d_select(const mx_conv2d_desc* desc, int phase, int requested, int* algo);
+
+/* y = conv(x, w) + bias.  bias may be NULL (zero bias, csrc/ops/convolution.cpp:660).
+ * Replaces convolution_overrideable's dispatch(Forward)
+ * (csrc/ops/convolution.cpp:641-665, conv2d_tiled_body.glsl,
+ * conv2d_winograd_*.comp). */
+int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w,
+                      const float* bias, float* y, int algo, void* stream);
+
+/* dx = conv_transpose(dy, w): dispatch(Input) (csrc/ops/convolution.cpp:684-687,
+ * conv2d_backward_input_tiled_body.glsl). */
+int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const float* w,
+                             float* dx, int algo, void* stream);
+
+/* dw = sum over positions dy x im2col(x); db = sum over positions of dy.
+ * Either dw or db may be NULL.  dispatch(Weight) + dispatch(Bias)
+ * (csrc/ops/convolution.cpp:688-695, conv2d_backward_weight_tiled_body.glsl,
+ * conv2d_backward_weight_finalize.comp, conv2d_backward_bias_reduce.comp),
+ * fused into one launch with a deterministic split-K reduction. */
+int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const float* dy,
+                              float* dw, float* db, int algo, void* stream);
+
+/* db only (conv2d_backward_bias_reduce.comp:10-24). */
+int mx_conv2d_backward_bias(const mx_conv2d_desc* desc, const float* dy, float* db, void* stream);
+
+/* Split-K plan of the dWeight reduction (weight_split_plan,
+ * csrc/ops/convolution.cpp:204-238): number of K splits and workspace bytes
+ * the implicit-GEMM dWeight path uses for this descriptor. */
+int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t* span,
+                           int64_t* workspace_bytes);
+
+/* ------------------------------------------------------------------------ */
+/* GEMM: mm / mm.out / addmm / bmm / bmm.out                                  */
+/* ------------------------------------------------------------------------ */
+
+enum mx_bias_kind { MX_BIAS_NONE = 0, MX_BIAS_COL = 1, MX_BIAS_MATRIX = 2 };
+
+/* C[b] = alpha * A[b] x B[b] + beta * bias, with arbitrary element strides and
+ * offsets for A and B (matmul_strided{,_reg}{,_bias}.comp, bmm_strided.comp;
+ * mm_impl csrc/ops/mm.cpp:244-343, addmm_bias_vulkan :835-879, bmm_impl
+ * csrc/ops/bmm.cpp:16-68).  C is written with row stride ldc and batch stride
+ * batch_stride_c.  bias: MX_BIAS_COL = bias[n] (1-D addmm bias), MX_BIAS_MATRIX
+ * = bias[m*bias_stride_m + n*bias_stride_n].  beta == 0 ignores the bias
+ * entirely, NaN/Inf included (matmul_strided_reg_bias.comp:96).  k == 0 writes
+ * beta*bias (or zeros). */
+typedef struct mx_gemm_desc {
+  int64_t batch, m, n, k;
+  int64_t a_offset, a_stride_b, a_stride_m, a_stride_k;
+  int64_t b_offset, b_stride_b, b_stride_k, b_stride_n;
+  int64_t c_offset, c_stride_b, ldc;
+  int64_t bias_offset, bias_stride_m, bias_stride_n;
+  float alpha, beta;
+  int bias_kind;
+} mx_gemm_desc;
+
+int mx_gemm_f32(const mx_gemm_desc* desc, const float* a, const float* b, const float* bias,
+                float* c, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Multi-tensor fused AdamW                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* One parameter tensor.  Either `step` (host, >= 1; bias corrections in double
+ * on the host as csrc/ops/adamw.cpp:171-178) or `step_dev` (device FP32 scalar,
+ * already incremented, as aten::_fused_adamw_'s state_steps) is used. */
+typedef struct mx_adamw_tensor {
+  float* param;
+  const float* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  float* max_exp_avg_sq; /* AMSGrad only, else NULL */
+  int64_t numel;
+  int64_t step;
+  const float* step_dev;
+} mx_adamw_tensor;
+
+typedef struct mx_adamw_hparams {
+  double lr, beta1, beta2, eps, weight_decay;
+  int amsgrad;
+  int maximize;
+  const float* lr_dev;      /* optional device scalar lr (_fused_adamw_.tensor_lr) */
+  const float* grad_scale;  /* optional device scalar: grads are divided by it */
+  const float* found_inf;   /* optional device scalar: when != 0 the step is skipped */
+} mx_adamw_hparams;
+
+/* Whole list in as few launches as the alias rule allows: entries that share a
+ * written buffer with an earlier entry start a new launch, so repeated
+ * parameters update sequentially (multitensor::partition conflict predicate,
+ * csrc/ops/multitensor_plan.h:22-48, csrc/ops/adamw.cpp:207-215).
+ * Replaces fused_adamw_step_ / fused_adamw_step_batch_impl
+ * (csrc/ops/adamw.cpp:28-284) and adamw_fused{,_amsgrad}.comp /
+ * adamw_multitensor{4,8}[_amsgrad].comp.  *launches (optional) receives the
+ * number of kernel launches issued. */
+int mx_adamw_step(const mx_adamw_tensor* tensors, int64_t count, const mx_adamw_hparams* hp,
+                  int64_t* launches, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MX_H */

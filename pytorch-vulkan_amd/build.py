@@ -1,0 +1,149 @@
+"""Builds the gfx950 libraries in-tree.
+
+    python pytorch-vulkan_amd/build.py [--only mx|ext] [--incremental] [-j N]
+
+Outputs (next to the Python package so they travel with the source tree):
+  torch_vulkan/libmx.so  C-ABI library (include/mx.h): HIP runtime layer and
+                         every gfx950 kernel, built with hipcc.
+  torch_vulkan/_C.so     PrivateUse1 "vulkan" operator surface (C++ against
+                         the installed torch headers), linked to libmx.so.
+
+Both link the HIP runtime that ships inside the installed torch wheel
+(torch/lib/libamdhip64.so) so that a process which imports torch never loads
+a second HIP runtime.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+OUT = PKG / "torch_vulkan"
+INCLUDE = REPO / "include"
+
+ARCH = os.environ.get("MX_OFFLOAD_ARCH", "gfx950")
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
+    # Packed FP32 instructions stay off (the compiler would otherwise form
+    # v_pk_{add,mul,fma}_f32 from scalar code).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}", f"-I{CSRC}",
+]
+MX_SOURCES = ["mx_runtime.hip", "mx_gemm.hip", "mx_conv.hip", "mx_winograd.hip", "mx_adamw.hip", "mx_util.hip"]
+EXT_SOURCES = ["backend.cpp", "ops_conv.cpp", "ops_gemm.cpp", "ops_adamw.cpp", "ops_plumbing.cpp"]
+
+
+def torch_paths():
+    import torch.utils.cpp_extension as ce  # noqa: WPS433 (build-time only)
+    import torch
+    return ce.include_paths(), str(Path(torch.__file__).parent / "lib")
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the gfx950 build needs ROCm's hipcc")
+
+
+def run(cmd: list[str]) -> None:
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in res.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out)
+
+
+def stale(target: Path, deps: list[Path]) -> bool:
+    if not target.exists():
+        return True
+    t = target.stat().st_mtime
+    return any(d.stat().st_mtime > t for d in deps)
+
+
+def build_mx(jobs: int, incremental: bool) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    OUT.mkdir(exist_ok=True)
+    headers = list(CSRC.glob("*.hpp")) + [INCLUDE / "mx.h"]
+    _, torch_lib = torch_paths()
+    cc = hipcc()
+    objs, todo = [], []
+    for src in MX_SOURCES:
+        obj = BUILD / (Path(src).stem + ".o")
+        objs.append(obj)
+        if not incremental or stale(obj, [CSRC / src] + headers):
+            todo.append([cc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for f in [ex.submit(run, c) for c in todo]:
+            f.result()
+    lib = OUT / "libmx.so"
+    if not incremental or stale(lib, objs):
+        tmp = OUT / "libmx.so.tmp"
+        # Plain host link (non-relocatable device code needs no device link
+        # step); hipcc would add -lamdhip64 from /opt/rocm (a second runtime).
+        cxx = os.environ.get("CXX", "g++")
+        run([cxx, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+             f"-L{torch_lib}", f"-Wl,-rpath,{torch_lib}", "-lamdhip64", "-Wl,--no-undefined"])
+        tmp.replace(lib)
+    return lib
+
+
+def build_ext(jobs: int, incremental: bool) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    incs, torch_lib = torch_paths()
+    py_inc = sysconfig.get_paths()["include"]
+    cxx = os.environ.get("CXX", "g++")
+    flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-parameter", "-D_GLIBCXX_USE_CXX11_ABI=1",
+             "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+             f"-I{INCLUDE}", f"-I{PKG / 'csrc' / 'torch'}", f"-I{py_inc}", *[f"-I{i}" for i in incs]]
+    try:
+        import torch
+        abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+        flags = [f for f in flags if not f.startswith("-D_GLIBCXX_USE_CXX11_ABI")] + [f"-D_GLIBCXX_USE_CXX11_ABI={abi}"]
+    except Exception:  # pragma: no cover - torch import failure surfaces below
+        pass
+    headers = list((PKG / "csrc" / "torch").glob("*.h")) + [INCLUDE / "mx.h"]
+    objs, todo = [], []
+    for src in EXT_SOURCES:
+        path = PKG / "csrc" / "torch" / src
+        obj = BUILD / ("ext_" + Path(src).stem + ".o")
+        objs.append(obj)
+        if not incremental or stale(obj, [path] + headers):
+            todo.append([cxx, *flags, "-c", str(path), "-o", str(obj)])
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for f in [ex.submit(run, c) for c in todo]:
+            f.result()
+    so = OUT / "_C.so"
+    if not incremental or stale(so, objs + [OUT / "libmx.so"]):
+        tmp = OUT / "_C.so.tmp"
+        run([cxx, "-shared", "-o", str(tmp), *map(str, objs), f"-L{OUT}", "-lmx", "-Wl,-rpath,$ORIGIN",
+             f"-L{torch_lib}", f"-Wl,-rpath,{torch_lib}", "-lc10", "-ltorch_cpu", "-ltorch", "-ltorch_python"])
+        tmp.replace(so)
+    return so
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--only", choices=["mx", "ext"], default=None)
+    ap.add_argument("--incremental", action="store_true")
+    ap.add_argument("-j", type=int, default=min(8, os.cpu_count() or 4))
+    args = ap.parse_args(argv)
+    if args.only in (None, "mx"):
+        print("built", build_mx(args.j, args.incremental))
+    if args.only in (None, "ext"):
+        print("built", build_ext(args.j, args.incremental))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,368 @@
+// FP32 MFMA tile machinery for gfx950 (CDNA4), shared by the GEMM and the
+// implicit-GEMM convolution kernels.
+//
+// A 256-thread workgroup (4 wave64) computes a BM x BN tile of C = A x B.
+// Operands are staged through LDS in double-buffered BK slabs laid out
+// row-major with k contiguous ([row][BK + pad]) for both A (rows = m) and
+// B (rows = n).  Each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile built
+// from 32x32 blocks of v_mfma_f32_32x32x2f32.  Inside a slab the k index is
+// permuted so that lane half h (lane / 32) handles k in [h*BK/2, (h+1)*BK/2):
+// a lane then fetches its BK/2 operand values with ds_read_b128 and issues
+// BK/2 MFMAs per 32x32 block, and the A/B fragments stay consistent because
+// both use the same permutation.  Summation order within a 32x32 block is the
+// MFMA's own (FP32 accumulate).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mx {
+namespace mfma {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+
+template <int BM_, int BN_, int BK_, int WAVES_M_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_;
+  static constexpr int WAVES_M = WAVES_M_, WAVES_N = 4 / WAVES_M_;
+  static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int PAD = 4;
+  static constexpr int LDK = BK + PAD;
+  static constexpr int KH = BK / 2;
+  static constexpr int A_STAGE = BM * LDK, B_STAGE = BN * LDK;
+  static constexpr int SMEM_FLOATS = 2 * (A_STAGE + B_STAGE);
+  static constexpr int ACC_REGS = FM * FN * 16;
+  static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
+  static_assert(BK % 8 == 0, "BK must be a multiple of 8");
+};
+
+template <class C>
+struct Acc {
+  f32x16 v[C::FM][C::FN];
+};
+
+template <class C>
+__device__ __forceinline__ void acc_zero(Acc<C>& acc) {
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc.v[i][j][r] = 0.f;
+}
+
+// One BK slab: fragments from LDS, BK/2 MFMA steps per 32x32 block.
+template <class C>
+__device__ __forceinline__ void mma_slab(Acc<C>& acc, const float* As, const float* Bs, int wm,
+                                         int wn, int lane) {
+  const int r = lane & 31, h = lane >> 5;
+  float a[C::FM][C::KH];
+  float b[C::FN][C::KH];
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+    const float* src = As + (wm * C::WTM + i * 32 + r) * C::LDK + h * C::KH;
+#pragma unroll
+    for (int q = 0; q < C::KH; q += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(src + q);
+      a[i][q + 0] = t[0];
+      a[i][q + 1] = t[1];
+      a[i][q + 2] = t[2];
+      a[i][q + 3] = t[3];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    const float* src = Bs + (wn * C::WTN + j * 32 + r) * C::LDK + h * C::KH;
+#pragma unroll
+    for (int q = 0; q < C::KH; q += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(src + q);
+      b[j][q + 0] = t[0];
+      b[j][q + 1] = t[1];
+      b[j][q + 2] = t[2];
+      b[j][q + 3] = t[3];
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < C::KH; ++s)
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j)
+        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc.v[i][j], 0, 0, 0);
+}
+
+// Double-buffered main loop over nk slabs.  Loaders expose load() (global ->
+// registers for the next slab, advancing their k cursor) and store(lds).
+template <class C, class LA, class LB>
+__device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la, LB& lb, int nk, float* smem) {
+  float* As = smem;
+  float* Bs = smem + 2 * C::A_STAGE;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  acc_zero<C>(acc);
+  if (nk <= 0) return;
+  la.load();
+  lb.load();
+  la.store(As);
+  lb.store(Bs);
+  __syncthreads();
+  for (int t = 0; t < nk; ++t) {
+    const int cur = t & 1;
+    const bool more = t + 1 < nk;
+    if (more) {
+      la.load();
+      lb.load();
+    }
+    mma_slab<C>(acc, As + cur * C::A_STAGE, Bs + cur * C::B_STAGE, wm, wn, lane);
+    if (more) {
+      la.store(As + (cur ^ 1) * C::A_STAGE);
+      lb.store(Bs + (cur ^ 1) * C::B_STAGE);
+    }
+    __syncthreads();
+  }
+}
+
+// Visits every accumulator with its (row, col) inside the BM x BN tile.
+// 32x32x2 f32 output layout: lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4,
+// column l%32.
+template <class C, class F>
+__device__ __forceinline__ void for_each_acc(const Acc<C>& acc, F&& f) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = wm * C::WTM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int col = wn * C::WTN + j * 32 + r;
+        f(row, col, acc.v[i][j][v]);
+      }
+}
+
+// Register-order index of accumulator (i, j, v) of this thread: partial tiles
+// are spilled and reloaded in this order, fully coalesced.
+template <class C>
+__device__ __forceinline__ int acc_slot(int i, int j, int v) {
+  return ((i * C::FN + j) * 16 + v) * kThreads + threadIdx.x;
+}
+
+// ---------------------------------------------------------------- loaders
+// Operand element (row, k) = base[row * s_row + k * s_k] for rows
+// [row0, row0 + ROWS) clipped to R and k < kmax (zero outside).
+enum class Mode : int {
+  KVEC = 0,     // k contiguous, 16-byte aligned: float4 along k
+  RVEC = 1,     // rows contiguous, 16-byte aligned: float4 along rows
+  KSCALAR = 2,  // consecutive lanes -> consecutive k
+  RSCALAR = 3   // consecutive lanes -> consecutive rows
+};
+
+template <int ROWS, int BK, Mode MODE>
+struct StridedLoader;
+
+template <int ROWS, int BK>
+struct StridedLoader<ROWS, BK, Mode::KVEC> {
+  static constexpr int TPR = BK / 4;                 // threads per row
+  static constexpr int RPP = kThreads / TPR;         // rows per pass
+  static constexpr int PASSES = ROWS / RPP;
+  static_assert(PASSES >= 1 && ROWS % RPP == 0, "KVEC tiling");
+  f32x4 v[PASSES];
+  const float* ptr[PASSES];
+  bool ok[PASSES];
+  int k, kmax, kq;
+  __device__ void init(const float* base, int64_t s_row, int64_t /*s_k*/, int row0, int R, int k0,
+                       int kmax_) {
+    const int tid = threadIdx.x;
+    kq = tid % TPR;
+    k = k0;
+    kmax = kmax_;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = row0 + tid / TPR + p * RPP;
+      ok[p] = row < R;
+      ptr[p] = base + (ok[p] ? int64_t(row) * s_row : 0) + 4 * kq;
+    }
+  }
+  __device__ __forceinline__ void load() {
+    const int kk = k + 4 * kq;
+    const bool kin = kk < kmax;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      if (ok[p] && kin)
+        v[p] = *reinterpret_cast<const f32x4*>(ptr[p] + k);
+      else
+        v[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    k += BK;
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    const int tid = threadIdx.x;
+    constexpr int LDK = BK + 4;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+      *reinterpret_cast<f32x4*>(lds + (tid / TPR + p * RPP) * LDK + 4 * kq) = v[p];
+  }
+};
+
+template <int ROWS, int BK>
+struct StridedLoader<ROWS, BK, Mode::RVEC> {
+  static constexpr int TPK = ROWS / 4;               // threads per k
+  static constexpr int KPP = kThreads / TPK;         // k per pass
+  static constexpr int PASSES = BK / KPP;
+  static_assert(PASSES >= 1 && BK % KPP == 0, "RVEC tiling");
+  f32x4 v[PASSES];
+  const float* ptr;
+  int64_t s_k;
+  bool ok;
+  int k, kmax, kk;
+  __device__ void init(const float* base, int64_t /*s_row*/, int64_t s_k_, int row0, int R, int k0,
+                       int kmax_) {
+    const int tid = threadIdx.x;
+    const int rq = tid % TPK;
+    kk = tid / TPK;
+    const int row = row0 + 4 * rq;
+    ok = row < R;
+    ptr = base + (ok ? row : 0);
+    s_k = s_k_;
+    k = k0;
+    kmax = kmax_;
+  }
+  __device__ __forceinline__ void load() {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int kx = k + kk + p * KPP;
+      if (ok && kx < kmax)
+        v[p] = *reinterpret_cast<const f32x4*>(ptr + int64_t(kx) * s_k);
+      else
+        v[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    k += BK;
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    const int tid = threadIdx.x;
+    const int rq = tid % TPK;
+    constexpr int LDK = BK + 4;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lds[(4 * rq + e) * LDK + kk + p * KPP] = v[p][e];
+  }
+};
+
+template <int ROWS, int BK>
+struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
+  static constexpr int RPP = kThreads / BK;
+  static constexpr int PASSES = ROWS / RPP;
+  static_assert(PASSES >= 1 && ROWS % RPP == 0, "KSCALAR tiling");
+  float v[PASSES];
+  const float* ptr[PASSES];
+  bool ok[PASSES];
+  int64_t s_k;
+  int k, kmax, kk;
+  __device__ void init(const float* base, int64_t s_row, int64_t s_k_, int row0, int R, int k0, int kmax_) {
+    const int tid = threadIdx.x;
+    kk = tid % BK;
+    s_k = s_k_;
+    k = k0;
+    kmax = kmax_;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = row0 + tid / BK + p * RPP;
+      ok[p] = row < R;
+      ptr[p] = base + (ok[p] ? int64_t(row) * s_row : 0);
+    }
+  }
+  __device__ __forceinline__ void load() {
+    const int kx = k + kk;
+    const bool kin = kx < kmax;
+    const int64_t off = int64_t(kx) * s_k;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) v[p] = (ok[p] && kin) ? ptr[p][off] : 0.f;
+    k += BK;
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    const int tid = threadIdx.x;
+    constexpr int LDK = BK + 4;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) lds[(tid / BK + p * RPP) * LDK + kk] = v[p];
+  }
+};
+
+template <int ROWS, int BK>
+struct StridedLoader<ROWS, BK, Mode::RSCALAR> {
+  static_assert(kThreads % ROWS == 0 || ROWS % kThreads == 0, "RSCALAR tiling");
+  static constexpr int EPT = ROWS * BK / kThreads;   // consecutive k per thread
+  static_assert(ROWS <= kThreads, "RSCALAR expects ROWS <= 256");
+  float v[EPT];
+  const float* ptr;
+  int64_t s_k;
+  bool ok;
+  int k, kmax, ks;
+  __device__ void init(const float* base, int64_t s_row, int64_t s_k_, int row0, int R, int k0, int kmax_) {
+    const int tid = threadIdx.x;
+    const int r = tid % ROWS;
+    ks = (tid / ROWS) * EPT;
+    const int row = row0 + r;
+    ok = row < R;
+    ptr = base + (ok ? int64_t(row) * s_row : 0);
+    s_k = s_k_;
+    k = k0;
+    kmax = kmax_;
+  }
+  __device__ __forceinline__ void load() {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int kx = k + ks + e;
+      v[e] = (ok && kx < kmax) ? ptr[int64_t(kx) * s_k] : 0.f;
+    }
+    k += BK;
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    const int tid = threadIdx.x;
+    constexpr int LDK = BK + 4;
+    float* dst = lds + (tid % ROWS) * LDK + ks;
+    if constexpr (EPT % 4 == 0) {
+#pragma unroll
+      for (int e = 0; e < EPT; e += 4)
+        *reinterpret_cast<f32x4*>(dst + e) = f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) dst[e] = v[e];
+    }
+  }
+};
+
+// Bijective block remap so that consecutive logical tiles land on the same
+// XCD (hardware dispatches workgroup b to XCD b % 8): tiles that share an
+// operand panel then share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+  constexpr int X = 8;
+  if (n < 2 * X) return b;
+  const int per = n / X, rem = n % X;
+  const int xcd = b % X, idx = b / X;
+  return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+// Logical tile id -> (tile_m, tile_n) in GROUP_M-row bands (raster order
+// within a band) so a wave of resident tiles reuses A and B panels.
+__device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int GROUP_M = 8;
+  const int band = GROUP_M * tiles_n;
+  const int g = t / band;
+  const int first_m = g * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  const int in = t % band;
+  tm = first_m + in % gm;
+  tn = in / gm;
+}
+
+}  // namespace mfma
+}  // namespace mx

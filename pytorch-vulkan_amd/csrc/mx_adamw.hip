@@ -1,0 +1,289 @@
+// Multi-tensor fused AdamW (decoupled weight decay), optional AMSGrad.
+//
+// Replaces the reference's per-group Vulkan dispatches
+// (fused_adamw_step_batch_impl csrc/ops/adamw.cpp:78-284,
+// adamw_multitensor{4,8}[_amsgrad].comp, multitensor::partition
+// csrc/ops/multitensor_plan.h:22-48): one persistent launch walks a device
+// table of every tensor, each workgroup taking a contiguous run of 1024-element
+// chunks, with 128-bit loads/stores where the four (five) streams are 16-byte
+// aligned.  There is no 8-tensor or 65,535-workgroup cap; a new launch starts
+// only where an entry writes memory an earlier entry of the same launch uses
+// (the reference's alias-conflict predicate, csrc/ops/adamw.cpp:207-215).
+//
+// Per-element arithmetic follows torch.optim.AdamW's single-tensor update
+// (the CPU oracle the reference tests against, tests/test_fused_adamw.py):
+//   p = p * (1 - lr*wd)
+//   m = lerp(m, g, 1 - beta1)
+//   v = v * beta2 + ((1 - beta2) * g) * g
+//   p = p + (-lr/bc1 * m) / (sqrt(v) / sqrt(bc2) + eps)
+// with bc1 = 1 - beta1^step and bc2 = 1 - beta2^step in double, and no
+// multiply-add contraction, in that order.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "mx_internal.hpp"
+
+namespace mx {
+namespace {
+
+constexpr int kChunk = 1024;  // elements per chunk: 256 threads x 4
+
+struct AdamEntry {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  float* vmax;
+  const float* step_dev;
+  int64_t numel;
+  int64_t chunk_begin;
+  float neg_step_size;  // -lr / bc1 (host steps)
+  float bc2_sqrt;       // sqrt(bc2)  (host steps)
+  int vec;              // all streams 16-byte aligned
+  int pad;
+};
+
+struct AdamHP {
+  double lr, beta1, beta2, eps, wd;
+  const float* lr_dev;
+  const float* grad_scale;
+  const float* found_inf;
+  int maximize;
+  int ntens;
+  int64_t total_chunks;
+};
+
+struct Coef {
+  float wdf, b1c, omb1c, b2, b2c, eps, nss, bc2s;
+};
+
+__device__ __forceinline__ Coef coefficients(const AdamEntry& e, const AdamHP& hp) {
+  Coef c;
+  const double lr = hp.lr_dev ? double(*hp.lr_dev) : hp.lr;
+  c.wdf = float(1.0 - lr * hp.wd);
+  c.b1c = float(1.0 - hp.beta1);
+  c.omb1c = 1.f - c.b1c;
+  c.b2 = float(hp.beta2);
+  c.b2c = float(1.0 - hp.beta2);
+  c.eps = float(hp.eps);
+  if (e.step_dev) {
+    const double step = double(*e.step_dev);
+    const double bc1 = 1.0 - pow(hp.beta1, step);
+    const double bc2 = 1.0 - pow(hp.beta2, step);
+    c.nss = float(-(lr / bc1));
+    c.bc2s = float(sqrt(bc2));
+  } else if (hp.lr_dev) {
+    // neg_step_size carries -1/bc1 when the learning rate lives on the device.
+    c.nss = float(lr * double(e.neg_step_size));
+    c.bc2s = e.bc2_sqrt;
+  } else {
+    c.nss = e.neg_step_size;
+    c.bc2s = e.bc2_sqrt;
+  }
+  return c;
+}
+
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
+}
+
+template <bool AMS>
+__device__ __forceinline__ void update(float& p, float g, float& m, float& v, float* vmax_slot, const Coef& c,
+                                       const AdamHP& hp, float scale) {
+#pragma clang fp contract(off)
+  if (hp.maximize) g = -g;
+  if (hp.grad_scale) g = g / scale;
+  p = p * c.wdf;
+  // torch lerp: small weights add weight*(end-self), large ones subtract from end.
+  m = (c.b1c < 0.5f) ? m + c.b1c * (g - m) : g - (g - m) * c.omb1c;
+  v = v * c.b2;
+  v = v + (c.b2c * g) * g;
+  float vd = v;
+  if constexpr (AMS) {
+    vd = nan_max(*vmax_slot, v);
+    *vmax_slot = vd;
+  }
+  const float denom = sqrtf(vd) / c.bc2s + c.eps;
+  p = p + (c.nss * m) / denom;
+}
+
+template <bool AMS>
+__global__ __launch_bounds__(256) void adamw_kernel(const AdamEntry* __restrict__ tab, AdamHP hp) {
+  if (hp.found_inf && *hp.found_inf != 0.f) return;
+  const float scale = hp.grad_scale ? *hp.grad_scale : 1.f;
+  const int64_t per = (hp.total_chunks + gridDim.x - 1) / gridDim.x;
+  const int64_t c0 = int64_t(blockIdx.x) * per;
+  const int64_t c1 = min(hp.total_chunks, c0 + per);
+  if (c0 >= c1) return;
+  int lo = 0, hi = hp.ntens - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].chunk_begin <= c0) lo = mid;
+    else hi = mid - 1;
+  }
+  int t = lo;
+  AdamEntry e = tab[t];
+  int64_t e_end = e.chunk_begin + (e.numel + kChunk - 1) / kChunk;
+  Coef c = coefficients(e, hp);
+  for (int64_t ch = c0; ch < c1; ++ch) {
+    while (ch >= e_end) {
+      e = tab[++t];
+      e_end = e.chunk_begin + (e.numel + kChunk - 1) / kChunk;
+      c = coefficients(e, hp);
+    }
+    const int64_t i0 = (ch - e.chunk_begin) * kChunk + int64_t(threadIdx.x) * 4;
+    if (e.vec && i0 + 3 < e.numel) {
+      float4 p4 = *reinterpret_cast<const float4*>(e.p + i0);
+      const float4 g4 = *reinterpret_cast<const float4*>(e.g + i0);
+      float4 m4 = *reinterpret_cast<const float4*>(e.m + i0);
+      float4 v4 = *reinterpret_cast<const float4*>(e.v + i0);
+      float4 x4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (AMS) x4 = *reinterpret_cast<const float4*>(e.vmax + i0);
+      update<AMS>(p4.x, g4.x, m4.x, v4.x, &x4.x, c, hp, scale);
+      update<AMS>(p4.y, g4.y, m4.y, v4.y, &x4.y, c, hp, scale);
+      update<AMS>(p4.z, g4.z, m4.z, v4.z, &x4.z, c, hp, scale);
+      update<AMS>(p4.w, g4.w, m4.w, v4.w, &x4.w, c, hp, scale);
+      *reinterpret_cast<float4*>(e.p + i0) = p4;
+      *reinterpret_cast<float4*>(e.m + i0) = m4;
+      *reinterpret_cast<float4*>(e.v + i0) = v4;
+      if constexpr (AMS) *reinterpret_cast<float4*>(e.vmax + i0) = x4;
+    } else {
+      for (int64_t i = i0; i < min(i0 + 4, e.numel); ++i) {
+        float p = e.p[i], m = e.m[i], v = e.v[i];
+        float x = AMS ? e.vmax[i] : 0.f;
+        update<AMS>(p, e.g[i], m, v, &x, c, hp, scale);
+        e.p[i] = p;
+        e.m[i] = m;
+        e.v[i] = v;
+        if constexpr (AMS) e.vmax[i] = x;
+      }
+    }
+  }
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+struct Interval {
+  uintptr_t lo, hi;
+  int64_t entry;
+  bool written;
+};
+
+// For each entry j, the latest earlier entry i whose memory conflicts with j
+// (one of them writes bytes the other reads or writes), or -1.
+std::vector<int64_t> latest_conflict(const mx_adamw_tensor* t, int64_t n, bool ams) {
+  std::vector<Interval> iv;
+  iv.reserve(size_t(n) * 5);
+  for (int64_t i = 0; i < n; ++i) {
+    if (t[i].numel <= 0) continue;
+    const uintptr_t bytes = uintptr_t(t[i].numel) * 4;
+    auto add = [&](const void* ptr, bool w) {
+      if (ptr) iv.push_back({reinterpret_cast<uintptr_t>(ptr), reinterpret_cast<uintptr_t>(ptr) + bytes, i, w});
+    };
+    add(t[i].param, true);
+    add(t[i].grad, false);
+    add(t[i].exp_avg, true);
+    add(t[i].exp_avg_sq, true);
+    if (ams) add(t[i].max_exp_avg_sq, true);
+  }
+  std::sort(iv.begin(), iv.end(), [](const Interval& a, const Interval& b) { return a.lo < b.lo; });
+  std::vector<int64_t> conf(size_t(n), -1);
+  // Sweep: compare each interval with the following ones that start before it ends.
+  for (size_t a = 0; a < iv.size(); ++a)
+    for (size_t b = a + 1; b < iv.size() && iv[b].lo < iv[a].hi; ++b) {
+      if (iv[a].entry == iv[b].entry || !(iv[a].written || iv[b].written)) continue;
+      const int64_t lo = std::min(iv[a].entry, iv[b].entry), hi = std::max(iv[a].entry, iv[b].entry);
+      conf[size_t(hi)] = std::max(conf[size_t(hi)], lo);
+    }
+  return conf;
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_adamw_step(const mx_adamw_tensor* tensors, int64_t count, const mx_adamw_hparams* hp_in,
+                             int64_t* launches, void* stream) {
+  MX_ABI_BEGIN
+  if (launches) *launches = 0;
+  MX_REQUIRE(hp_in, MX_ERR_INVALID, "fused AdamW: null hyperparameters");
+  MX_REQUIRE(count >= 0, MX_ERR_INVALID, "fused AdamW: negative tensor count");
+  const mx_adamw_hparams& h = *hp_in;
+  MX_REQUIRE(h.lr >= 0 && h.beta1 >= 0 && h.beta1 < 1 && h.beta2 >= 0 && h.beta2 < 1 && h.eps >= 0 &&
+                 h.weight_decay >= 0,
+             MX_ERR_INVALID, "fused AdamW batch: invalid hyperparameters");
+  if (count == 0) return MX_OK;
+  MX_REQUIRE(tensors, MX_ERR_INVALID, "fused AdamW: null tensor list");
+  const bool ams = h.amsgrad != 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const mx_adamw_tensor& t = tensors[i];
+    MX_REQUIRE(t.numel >= 0, MX_ERR_INVALID, "fused AdamW batch: negative numel at ", i);
+    if (t.numel == 0) continue;
+    MX_REQUIRE(t.param && t.grad && t.exp_avg && t.exp_avg_sq && (!ams || t.max_exp_avg_sq), MX_ERR_INVALID,
+               "fused AdamW batch: null buffer at ", i);
+    MX_REQUIRE(t.step_dev || t.step >= 1, MX_ERR_INVALID, "fused AdamW batch: step must be positive");
+  }
+  hipStream_t s = resolve_stream(stream);
+  const std::vector<int64_t> conf = latest_conflict(tensors, count, ams);
+  AdamHP hp{};
+  hp.lr = h.lr;
+  hp.beta1 = h.beta1;
+  hp.beta2 = h.beta2;
+  hp.eps = h.eps;
+  hp.wd = h.weight_decay;
+  hp.lr_dev = h.lr_dev;
+  hp.grad_scale = h.grad_scale;
+  hp.found_inf = h.found_inf;
+  hp.maximize = h.maximize;
+  std::vector<AdamEntry> tab;
+  int64_t first = 0;
+  while (first < count) {
+    // Extend the launch while no entry conflicts with one already in it.
+    int64_t last = first + 1;
+    while (last < count && conf[size_t(last)] < first) ++last;
+    tab.clear();
+    int64_t chunks = 0;
+    for (int64_t i = first; i < last; ++i) {
+      const mx_adamw_tensor& t = tensors[i];
+      if (t.numel == 0) continue;
+      AdamEntry e{};
+      e.p = t.param;
+      e.g = t.grad;
+      e.m = t.exp_avg;
+      e.v = t.exp_avg_sq;
+      e.vmax = ams ? t.max_exp_avg_sq : nullptr;
+      e.step_dev = t.step_dev;
+      e.numel = t.numel;
+      e.chunk_begin = chunks;
+      if (!t.step_dev) {
+        const double bc1 = 1.0 - std::pow(h.beta1, double(t.step));
+        const double bc2 = 1.0 - std::pow(h.beta2, double(t.step));
+        e.neg_step_size = h.lr_dev ? float(-1.0 / bc1) : float(-(h.lr / bc1));
+        e.bc2_sqrt = float(std::sqrt(bc2));
+      }
+      e.vec = aligned16(e.p) && aligned16(e.g) && aligned16(e.m) && aligned16(e.v) && (!ams || aligned16(e.vmax));
+      chunks += (t.numel + kChunk - 1) / kChunk;
+      tab.push_back(e);
+    }
+    if (!tab.empty()) {
+      hp.ntens = int(tab.size());
+      hp.total_chunks = chunks;
+      Scratch dtab;
+      MX_TRY(upload(tab.data(), tab.size() * sizeof(AdamEntry), s, dtab));
+      const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(chunks, int64_t(cu_count()) * 8));
+      if (ams)
+        hipLaunchKernelGGL(adamw_kernel<true>, dim3(unsigned(grid)), dim3(256), 0, s, dtab.as<AdamEntry>(), hp);
+      else
+        hipLaunchKernelGGL(adamw_kernel<false>, dim3(unsigned(grid)), dim3(256), 0, s, dtab.as<AdamEntry>(), hp);
+      MX_HIP(hipGetLastError());
+      if (launches) ++*launches;
+    }
+    first = last;
+  }
+  return MX_OK;
+  MX_ABI_END
+}

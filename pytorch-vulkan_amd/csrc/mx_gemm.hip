@@ -1,0 +1,191 @@
+// FP32 strided / batched GEMM with fused alpha, beta*bias epilogue on gfx950
+// MFMA (v_mfma_f32_32x32x2f32).
+//
+// Covers the reference's matmul_strided{,_reg}{,_bias}.comp and
+// bmm_strided.comp (mm_impl csrc/ops/mm.cpp:244-343, addmm_bias_vulkan
+// csrc/ops/mm.cpp:835-879, bmm_impl csrc/ops/bmm.cpp:16-68): A and B are read
+// straight from arbitrary strided views (a transposed weight costs no copy),
+// and the bias add of nn.Linear happens in the store.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "mfma_core.hpp"
+#include "mx_internal.hpp"
+
+namespace mx {
+namespace {
+
+using namespace mfma;
+
+struct GemmArgs {
+  const float* a;
+  const float* b;
+  const float* bias;
+  float* c;
+  int64_t a_sb, a_sm, a_sk;
+  int64_t b_sb, b_sk, b_sn;
+  int64_t c_sb, ldc;
+  int64_t bias_sm, bias_sn;
+  int M, N, K, batch;
+  int tiles_m, tiles_n;
+  float alpha, beta;
+  int bias_kind;
+};
+
+template <class C, Mode MA, Mode MB>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
+  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
+  const int ntiles = p.tiles_m * p.tiles_n;
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, tm, tn);
+  const int row0 = tm * C::BM, col0 = tn * C::BN;
+  const int nk = (p.K + C::BK - 1) / C::BK;
+  for (int bz = blockIdx.z; bz < p.batch; bz += gridDim.z) {
+    StridedLoader<C::BM, C::BK, MA> la;
+    StridedLoader<C::BN, C::BK, MB> lb;
+    la.init(p.a + int64_t(bz) * p.a_sb, p.a_sm, p.a_sk, row0, p.M, 0, p.K);
+    lb.init(p.b + int64_t(bz) * p.b_sb, p.b_sn, p.b_sk, col0, p.N, 0, p.K);
+    Acc<C> acc;
+    mainloop<C>(acc, la, lb, nk, smem);
+    float* cb = p.c + int64_t(bz) * p.c_sb;
+    const bool use_bias = p.bias_kind != MX_BIAS_NONE && p.beta != 0.f;
+    for_each_acc<C>(acc, [&](int r, int c, float v) {
+      const int row = row0 + r, col = col0 + c;
+      if (row < p.M && col < p.N) {
+        float out = p.alpha * v;
+        if (use_bias) {
+          const float bv = p.bias_kind == MX_BIAS_COL ? p.bias[int64_t(col) * p.bias_sn]
+                                                      : p.bias[int64_t(row) * p.bias_sm + int64_t(col) * p.bias_sn];
+          out += p.beta * bv;
+        }
+        cb[int64_t(row) * p.ldc + col] = out;
+      }
+    });
+  }
+}
+
+// k == 0: C = beta * bias (or zeros when beta == 0 / no bias).
+__global__ void gemm_k0_kernel(GemmArgs p) {
+  const int64_t total = int64_t(p.batch) * p.M * p.N;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int col = int(i % p.N);
+    const int64_t rest = i / p.N;
+    const int row = int(rest % p.M);
+    const int bz = int(rest / p.M);
+    float out = 0.f;
+    if (p.bias_kind != MX_BIAS_NONE && p.beta != 0.f) {
+      const float bv = p.bias_kind == MX_BIAS_COL ? p.bias[int64_t(col) * p.bias_sn]
+                                                  : p.bias[int64_t(row) * p.bias_sm + int64_t(col) * p.bias_sn];
+      out = p.beta * bv;
+    }
+    p.c[int64_t(bz) * p.c_sb + int64_t(row) * p.ldc + col] = out;
+  }
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// Operand layout -> loader mode.  rows = m for A, n for B.
+Mode pick_mode(const float* base, int64_t s_row, int64_t s_k, int64_t s_batch, int64_t batch, int64_t R,
+               int64_t K) {
+  const bool batch_ok = batch <= 1 || s_batch % 4 == 0;
+  if (s_k == 1 && aligned16(base) && s_row % 4 == 0 && batch_ok && K % 4 == 0) return Mode::KVEC;
+  if (s_row == 1 && aligned16(base) && s_k % 4 == 0 && batch_ok && R % 4 == 0) return Mode::RVEC;
+  if (s_k == 1) return Mode::KSCALAR;
+  if (s_row == 1) return Mode::RSCALAR;
+  return std::llabs(s_k) <= std::llabs(s_row) ? Mode::KSCALAR : Mode::RSCALAR;
+}
+
+template <class C, Mode MA, Mode MB>
+int launch3(const GemmArgs& p, hipStream_t s) {
+  const int ntiles = p.tiles_m * p.tiles_n;
+  dim3 grid(ntiles, 1, std::min(p.batch, 65535));
+  hipLaunchKernelGGL((gemm_kernel<C, MA, MB>), grid, dim3(256), 0, s, p);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+template <class C, Mode MA>
+int launch2(const GemmArgs& p, Mode mb, hipStream_t s) {
+  switch (mb) {
+    case Mode::KVEC: return launch3<C, MA, Mode::KVEC>(p, s);
+    case Mode::RVEC: return launch3<C, MA, Mode::RVEC>(p, s);
+    case Mode::KSCALAR: return launch3<C, MA, Mode::KSCALAR>(p, s);
+    default: return launch3<C, MA, Mode::RSCALAR>(p, s);
+  }
+}
+
+template <class C>
+int launch1(GemmArgs p, Mode ma, Mode mb, hipStream_t s) {
+  p.tiles_m = (p.M + C::BM - 1) / C::BM;
+  p.tiles_n = (p.N + C::BN - 1) / C::BN;
+  switch (ma) {
+    case Mode::KVEC: return launch2<C, Mode::KVEC>(p, mb, s);
+    case Mode::RVEC: return launch2<C, Mode::RVEC>(p, mb, s);
+    case Mode::KSCALAR: return launch2<C, Mode::KSCALAR>(p, mb, s);
+    default: return launch2<C, Mode::RSCALAR>(p, mb, s);
+  }
+}
+
+using BigTile = Cfg<128, 128, 16, 2>;
+using SmallTile = Cfg<64, 64, 16, 2>;
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_gemm_f32(const mx_gemm_desc* d, const float* a, const float* b, const float* bias,
+                           float* c, void* stream) {
+  MX_ABI_BEGIN
+  MX_REQUIRE(d, MX_ERR_INVALID, "mx_gemm_f32: null descriptor");
+  MX_REQUIRE(d->batch >= 0 && d->m >= 0 && d->n >= 0 && d->k >= 0, MX_ERR_INVALID,
+             "mx_gemm_f32: negative dimension");
+  MX_REQUIRE(d->m <= INT32_MAX && d->n <= INT32_MAX && d->k <= INT32_MAX && d->batch <= INT32_MAX,
+             MX_ERR_INVALID, "mx_gemm_f32: dimension exceeds int32");
+  MX_REQUIRE(d->bias_kind >= MX_BIAS_NONE && d->bias_kind <= MX_BIAS_MATRIX, MX_ERR_INVALID,
+             "mx_gemm_f32: bad bias kind");
+  if (d->batch == 0 || d->m == 0 || d->n == 0) return MX_OK;
+  MX_REQUIRE(c, MX_ERR_INVALID, "mx_gemm_f32: null output");
+  MX_REQUIRE(d->bias_kind == MX_BIAS_NONE || bias, MX_ERR_INVALID, "mx_gemm_f32: null bias");
+  hipStream_t s = resolve_stream(stream);
+  GemmArgs p{};
+  p.a = a ? a + d->a_offset : nullptr;
+  p.b = b ? b + d->b_offset : nullptr;
+  p.bias = bias ? bias + d->bias_offset : nullptr;
+  p.c = c + d->c_offset;
+  p.a_sb = d->a_stride_b;
+  p.a_sm = d->a_stride_m;
+  p.a_sk = d->a_stride_k;
+  p.b_sb = d->b_stride_b;
+  p.b_sk = d->b_stride_k;
+  p.b_sn = d->b_stride_n;
+  p.c_sb = d->c_stride_b;
+  p.ldc = d->ldc;
+  p.bias_sm = d->bias_stride_m;
+  p.bias_sn = d->bias_stride_n;
+  p.M = int(d->m);
+  p.N = int(d->n);
+  p.K = int(d->k);
+  p.batch = int(d->batch);
+  p.alpha = d->alpha;
+  p.beta = d->beta;
+  p.bias_kind = d->bias_kind;
+  if (d->k == 0) {
+    const int64_t total = d->batch * d->m * d->n;
+    const int blocks = int(std::min<int64_t>((total + 255) / 256, 65535));
+    hipLaunchKernelGGL(gemm_k0_kernel, dim3(blocks), dim3(256), 0, s, p);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
+  MX_REQUIRE(a && b, MX_ERR_INVALID, "mx_gemm_f32: null operand");
+  const Mode ma = pick_mode(p.a, p.a_sm, p.a_sk, p.a_sb, p.batch, p.M, p.K);
+  const Mode mb = pick_mode(p.b, p.b_sn, p.b_sk, p.b_sb, p.batch, p.N, p.K);
+  const int64_t big_tiles = ((d->m + 127) / 128) * ((d->n + 127) / 128) * d->batch;
+  MX_REQUIRE(((d->m + 63) / 64) * ((d->n + 63) / 64) <= INT32_MAX, MX_ERR_INVALID, "mx_gemm_f32: too many tiles");
+  if (big_tiles >= cu_count()) return launch1<BigTile>(p, ma, mb, s);
+  return launch1<SmallTile>(p, ma, mb, s);
+  MX_ABI_END
+}

@@ -1,0 +1,447 @@
+// PrivateUse1 backend registration over the HIP C ABI.
+//
+// Counterpart of the reference's csrc/torch_vulkan.cpp:40-283 (device guard,
+// hooks, allocator, pybind module): the device name stays "vulkan" so user
+// code and tests written for the reference run unchanged, but streams are
+// real HIP streams (the reference serialises every logical stream on one
+// VkQueue, csrc/torch_vulkan.cpp:34-37), events are HIP events, and storage
+// comes from the library's stream-ordered caching allocator.
+#include <ATen/detail/PrivateUse1HooksInterface.h>
+#include <ATen/native/CPUFallback.h>
+#include <c10/core/GeneratorImpl.h>
+#include <c10/core/impl/DeviceGuardImplInterface.h>
+#include <c10/core/impl/VirtualGuardImpl.h>
+#include <torch/csrc/Stream.h>
+#include <torch/extension.h>
+
+#include <array>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "common.h"
+
+namespace tvk {
+
+// ------------------------------------------------------------------ counters
+Counters& counters() {
+  static Counters c;
+  return c;
+}
+
+static std::mutex g_sel_mu;
+static std::map<std::string, uint64_t> g_sel;
+
+void count_selection(const std::string& key, uint64_t n) {
+  std::lock_guard<std::mutex> lock(g_sel_mu);
+  g_sel[key] += n;
+}
+std::map<std::string, uint64_t> selection_stats() {
+  std::lock_guard<std::mutex> lock(g_sel_mu);
+  return g_sel;
+}
+void clear_selection_stats() {
+  std::lock_guard<std::mutex> lock(g_sel_mu);
+  g_sel.clear();
+}
+
+void note_cpu_fallback(const char* what) {
+  counters().cpu_fallback_calls.fetch_add(1);
+  if (std::getenv("TORCH_VULKAN_TRACE_FALLBACK")) std::fprintf(stderr, "PV_FALLBACK %s\n", what);
+  const char* forbid = std::getenv("TORCH_VULKAN_FORBID_CPU_FALLBACK");
+  TORCH_CHECK(!(forbid && *forbid && std::strcmp(forbid, "0") != 0), "CPU fallback forbidden: ", what);
+}
+
+// ------------------------------------------------------------------ streams
+namespace {
+
+constexpr int kMaxDev = 64;
+thread_local std::array<c10::StreamId, kMaxDev> tl_stream{};  // 0 = default stream
+
+std::mutex g_stream_mu;
+std::array<void*, kMaxDev> g_default{};
+std::array<std::vector<void*>, kMaxDev> g_pool;  // id k >= 1 -> g_pool[dev][k-1]
+
+}  // namespace
+
+int cur_dev() {
+  int d = 0;
+  if (mx_get_device(&d) != MX_OK) return 0;
+  return d;
+}
+
+void* stream_for_id(c10::DeviceIndex device, c10::StreamId id) {
+  const int dev = device < 0 ? cur_dev() : device;
+  TORCH_CHECK(dev >= 0 && dev < kMaxDev, "vulkan: device index out of range");
+  std::lock_guard<std::mutex> lock(g_stream_mu);
+  if (id == 0) {
+    if (!g_default[dev]) {
+      const int prev = cur_dev();
+      if (prev != dev) TVK_MX(mx_set_device(dev));
+      void* s = nullptr;
+      const int rc = mx_default_stream(&s);
+      if (prev != dev) mx_set_device(prev);
+      TORCH_CHECK(rc == MX_OK, mx_last_error());
+      g_default[dev] = s;
+    }
+    return g_default[dev];
+  }
+  TORCH_CHECK(id >= 1 && size_t(id) <= g_pool[dev].size(), "vulkan: unknown stream id ", id);
+  return g_pool[dev][size_t(id - 1)];
+}
+
+void* current_stream() {
+  const int dev = cur_dev();
+  return stream_for_id(dev, tl_stream[dev]);
+}
+
+static c10::StreamId new_stream_id(int dev) {
+  const int prev = cur_dev();
+  if (prev != dev) TVK_MX(mx_set_device(dev));
+  void* s = nullptr;
+  const int rc = mx_stream_create(&s);
+  if (prev != dev) mx_set_device(prev);
+  TORCH_CHECK(rc == MX_OK, mx_last_error());
+  std::lock_guard<std::mutex> lock(g_stream_mu);
+  g_pool[dev].push_back(s);
+  return c10::StreamId(g_pool[dev].size());
+}
+
+// ---------------------------------------------------------------- allocator
+namespace {
+
+void raw_delete(void* p) {
+  if (p) mx_free(p);
+}
+
+struct VkAllocator final : public c10::Allocator {
+  c10::DataPtr allocate(size_t n) override {
+    const int dev = cur_dev();
+    void* p = nullptr;
+    if (n) {
+      const int rc = mx_malloc(&p, n, current_stream());
+      TORCH_CHECK_WITH(OutOfMemoryError, rc == MX_OK, "vulkan: out of device memory allocating ", n,
+                       " bytes: ", mx_last_error());
+    }
+    return {p, p, &raw_delete, c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(dev))};
+  }
+  c10::DeleterFnPtr raw_deleter() const override { return &raw_delete; }
+  void copy_data(void* dest, const void* src, std::size_t count) const override {
+    TVK_MX(mx_memcpy(dest, src, count, MX_COPY_D2D, current_stream()));
+  }
+};
+
+VkAllocator g_allocator;
+
+}  // namespace
+
+c10::Allocator* allocator() { return &g_allocator; }
+
+// ------------------------------------------------------------- device guard
+namespace {
+
+struct VkGuardImpl final : public c10::impl::DeviceGuardImplInterface {
+  c10::DeviceType type() const override { return c10::DeviceType::PrivateUse1; }
+  c10::Device exchangeDevice(c10::Device d) const override {
+    const c10::Device old = getDevice();
+    if (old.index() != d.index()) setDevice(d);
+    return old;
+  }
+  c10::Device getDevice() const override {
+    return c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(cur_dev()));
+  }
+  void setDevice(c10::Device d) const override {
+    TORCH_CHECK(d.type() == c10::DeviceType::PrivateUse1, "vulkan guard: expected a vulkan device, got ", d);
+    if (d.index() >= 0) TVK_MX(mx_set_device(d.index()));
+  }
+  void uncheckedSetDevice(c10::Device d) const noexcept override {
+    if (d.index() >= 0) mx_set_device(d.index());
+  }
+  c10::Stream getStream(c10::Device d) const override {
+    const int dev = d.index() < 0 ? cur_dev() : d.index();
+    return c10::Stream(c10::Stream::UNSAFE, c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(dev)),
+                       tl_stream[dev]);
+  }
+  c10::Stream getDefaultStream(c10::Device d) const override {
+    const int dev = d.index() < 0 ? cur_dev() : d.index();
+    return c10::Stream(c10::Stream::DEFAULT, c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(dev)));
+  }
+  c10::Stream getNewStream(c10::Device d, int priority = 0) const override {
+    // Every stream keeps the default priority.
+    TORCH_CHECK(priority == 0, "vulkan streams support the default priority only");
+    const int dev = d.index() < 0 ? cur_dev() : d.index();
+    return c10::Stream(c10::Stream::UNSAFE, c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(dev)),
+                       new_stream_id(dev));
+  }
+  c10::Stream getStreamFromGlobalPool(c10::Device d, bool isHighPriority = false) const override {
+    TORCH_CHECK(!isHighPriority, "vulkan streams support the default priority only");
+    return getNewStream(d, 0);
+  }
+  c10::Stream exchangeStream(c10::Stream s) const override {
+    const int dev = s.device_index() < 0 ? cur_dev() : s.device_index();
+    const c10::Stream old = getStream(c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(dev)));
+    tl_stream[dev] = s.id();
+    return old;
+  }
+  c10::DeviceIndex deviceCount() const noexcept override {
+    int n = 0;
+    if (mx_device_count(&n) != MX_OK) return 0;
+    return c10::DeviceIndex(n);
+  }
+  void destroyEvent(void* event, const c10::DeviceIndex) const noexcept override {
+    if (event) mx_event_destroy(event);
+  }
+  void record(void** event, const c10::Stream& stream, const c10::DeviceIndex, const c10::EventFlag flag) const override {
+    TORCH_CHECK(flag != c10::EventFlag::INVALID, "Invalid event flag");
+    if (!*event) TVK_MX(mx_event_create(event, flag == c10::EventFlag::BACKEND_DEFAULT ? 1 : 0));
+    TVK_MX(mx_event_record(*event, stream_for_id(stream.device_index(), stream.id())));
+  }
+  void block(void* event, const c10::Stream& stream) const override {
+    if (!event) return;
+    TVK_MX(mx_stream_wait_event(stream_for_id(stream.device_index(), stream.id()), event));
+  }
+  bool queryEvent(void* event) const override {
+    if (!event) return true;
+    int done = 0;
+    TVK_MX(mx_event_query(event, &done));
+    return done != 0;
+  }
+  bool queryStream(const c10::Stream& stream) const override {
+    int done = 0;
+    TVK_MX(mx_stream_query(stream_for_id(stream.device_index(), stream.id()), &done));
+    return done != 0;
+  }
+  void synchronizeStream(const c10::Stream& stream) const override {
+    TVK_MX(mx_stream_synchronize(stream_for_id(stream.device_index(), stream.id())));
+  }
+  void synchronizeEvent(void* event) const override {
+    if (event) TVK_MX(mx_event_synchronize(event));
+  }
+  void synchronizeDevice(const c10::DeviceIndex) const override { TVK_MX(mx_device_synchronize()); }
+  void recordDataPtrOnStream(const c10::DataPtr& ptr, const c10::Stream& stream) const override {
+    if (ptr.get()) TVK_MX(mx_record_stream(ptr.get(), stream_for_id(stream.device_index(), stream.id())));
+  }
+  double elapsedTime(void* e1, void* e2, const c10::DeviceIndex) const override {
+    TORCH_CHECK(e1 && e2, "Both events must be recorded before calculating elapsed time.");
+    float ms = 0.f;
+    TVK_MX(mx_event_elapsed_ms(e1, e2, &ms));
+    return double(ms);
+  }
+};
+
+C10_REGISTER_GUARD_IMPL(PrivateUse1, VkGuardImpl);
+
+// ----------------------------------------------------------------- generator
+// Seed/offset holder so torch.manual_seed and RNG-state APIs work for the
+// device; random ops themselves run through the CPU fallback.
+struct VkGenerator final : public c10::GeneratorImpl {
+  explicit VkGenerator(c10::DeviceIndex idx)
+      : c10::GeneratorImpl(c10::Device(c10::DeviceType::PrivateUse1, idx),
+                           c10::DispatchKeySet(c10::DispatchKey::PrivateUse1)) {}
+  void set_current_seed(uint64_t s) override {
+    seed_ = s;
+    offset_ = 0;
+  }
+  void set_offset(uint64_t o) override { offset_ = o; }
+  uint64_t get_offset() const override { return offset_; }
+  uint64_t current_seed() const override { return seed_; }
+  uint64_t seed() override {
+    seed_ = c10::detail::getNonDeterministicRandom();
+    offset_ = 0;
+    return seed_;
+  }
+  void set_state(const c10::TensorImpl& st) override {
+    TORCH_CHECK(st.numel() == 16 && st.dtype() == at::kByte, "vulkan RNG state must be 16 bytes");
+    const auto* p = static_cast<const uint8_t*>(st.data());
+    std::memcpy(&seed_, p, 8);
+    std::memcpy(&offset_, p + 8, 8);
+  }
+  c10::intrusive_ptr<c10::TensorImpl> get_state() const override {
+    auto t = at::empty({16}, at::TensorOptions().dtype(at::kByte));
+    std::memcpy(t.data_ptr(), &seed_, 8);
+    std::memcpy(static_cast<uint8_t*>(t.data_ptr()) + 8, &offset_, 8);
+    return t.getIntrusivePtr();
+  }
+  static c10::DeviceType device_type() { return c10::DeviceType::PrivateUse1; }
+
+ private:
+  VkGenerator* clone_impl() const override {
+    auto* g = new VkGenerator(device().index());
+    g->seed_ = seed_;
+    g->offset_ = offset_;
+    return g;
+  }
+  uint64_t seed_ = 67280421310721ULL;
+  uint64_t offset_ = 0;
+};
+
+at::Generator& default_generator(c10::DeviceIndex idx) {
+  static std::mutex mu;
+  static std::array<at::Generator, kMaxDev> gens;
+  const int dev = idx < 0 ? cur_dev() : idx;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!gens[dev].defined()) gens[dev] = at::make_generator<VkGenerator>(c10::DeviceIndex(dev));
+  return gens[dev];
+}
+
+// --------------------------------------------------------------------- hooks
+void resize_storage_bytes(c10::StorageImpl* impl, size_t bytes) {
+  const size_t old = impl->nbytes();
+  if (bytes <= old && impl->data() != nullptr) {
+    impl->set_nbytes(bytes);
+    return;
+  }
+  c10::DataPtr next = g_allocator.allocate(bytes);
+  if (old && impl->data() && bytes)
+    TVK_MX(mx_memcpy(next.get(), impl->data(), std::min(old, bytes), MX_COPY_D2D, current_stream()));
+  impl->set_data_ptr_noswap(std::move(next));
+  impl->set_nbytes(bytes);
+}
+
+struct VkHooks final : public at::PrivateUse1HooksInterface {
+  bool isBuilt() const override { return true; }
+  bool isAvailable() const override {
+    int n = 0;
+    return mx_device_count(&n) == MX_OK && n > 0;
+  }
+  const at::Generator& getDefaultGenerator(c10::DeviceIndex idx) const override { return default_generator(idx); }
+  at::Generator getNewGenerator(c10::DeviceIndex idx = -1) const override {
+    return at::make_generator<VkGenerator>(idx < 0 ? c10::DeviceIndex(cur_dev()) : idx);
+  }
+  at::Device getDeviceFromPtr(void*) const override {
+    return c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(cur_dev()));
+  }
+  bool hasPrimaryContext(c10::DeviceIndex) const override { return true; }
+  c10::DeviceIndex deviceCount() const override {
+    int n = 0;
+    if (mx_device_count(&n) != MX_OK) return 0;
+    return c10::DeviceIndex(n);
+  }
+  c10::DeviceIndex getCurrentDevice() const override { return c10::DeviceIndex(cur_dev()); }
+  void setCurrentDevice(c10::DeviceIndex idx) const override { TVK_MX(mx_set_device(idx)); }
+  void init() const override {}
+  void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {
+    resize_storage_bytes(storage.unsafeGetStorageImpl(), newsize);
+  }
+};
+
+VkHooks g_hooks;
+
+// ------------------------------------------------------------- CPU fallback
+// Boxed fallback for every operator this backend does not implement (the
+// reference's cpu_fallback, csrc/ops/mm.cpp:1071-1087): counted, traceable and
+// forbiddable.  The conv/GEMM/AdamW path never reaches it.
+void cpu_fallback_boxed(const c10::OperatorHandle& op, torch::jit::Stack* stack) {
+  note_cpu_fallback(op.schema().name().c_str());
+  at::native::cpu_fallback(op, stack);
+}
+
+}  // namespace
+
+void resize_vk_storage(c10::StorageImpl* impl, size_t bytes) { resize_storage_bytes(impl, bytes); }
+
+}  // namespace tvk
+
+TORCH_LIBRARY_IMPL(_, PrivateUse1, m) {
+  m.fallback(torch::CppFunction::makeFromBoxedFunction<&tvk::cpu_fallback_boxed>());
+}
+
+// ------------------------------------------------------------------- pybind
+namespace {
+
+py::dict execution_stats() {
+  auto& c = tvk::counters();
+  py::dict d;
+  d["cpu_fallback_calls"] = c.cpu_fallback_calls.load();
+  d["host_reads"] = c.host_reads.load();
+  d["kernel_launches"] = c.kernel_launches.load();
+  d["adamw_launches"] = c.adamw_launches.load();
+  return d;
+}
+
+void reset_execution_stats() {
+  auto& c = tvk::counters();
+  c.cpu_fallback_calls = 0;
+  c.host_reads = 0;
+  c.kernel_launches = 0;
+  c.adamw_launches = 0;
+}
+
+py::dict memory_stats() {
+  mx_memory_stats s{};
+  TVK_MX(mx_memory_stats_get(&s));
+  py::dict d;
+  d["allocated_bytes"] = s.allocated_bytes;
+  d["reserved_bytes"] = s.reserved_bytes;
+  d["cached_blocks"] = s.cached_blocks;
+  d["device_mallocs"] = s.device_mallocs;
+  d["cache_hits"] = s.cache_hits;
+  return d;
+}
+
+std::string device_name(int idx) {
+  char buf[256] = {0};
+  TVK_MX(mx_device_name(idx, buf, sizeof(buf)));
+  return buf;
+}
+
+int device_count() {
+  int n = 0;
+  if (mx_device_count(&n) != MX_OK) return 0;
+  return n;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_C, m) {
+  c10::register_privateuse1_backend("vulkan");
+  at::RegisterPrivateUse1HooksInterface(&tvk::g_hooks);
+  c10::SetAllocator(c10::DeviceType::PrivateUse1, tvk::allocator());
+
+  m.def("_device_count", &device_count);
+  m.def("_is_available", []() { return device_count() > 0; });
+  m.def("_device_name", &device_name, py::arg("index") = 0);
+  m.def("_init", [](int idx) { TVK_MX(mx_init(idx)); });
+  m.def("_synchronize", []() { TVK_MX(mx_device_synchronize()); });
+  m.def("_current_device", []() {
+    int d = 0;
+    TVK_MX(mx_get_device(&d));
+    return d;
+  });
+  m.def("_set_device", [](int d) { TVK_MX(mx_set_device(d)); });
+  m.def("_execution_stats", &execution_stats);
+  m.def("_reset_execution_stats", &reset_execution_stats);
+  m.def("_memory_stats", &memory_stats);
+  m.def("_empty_cache", []() { TVK_MX(mx_empty_cache()); });
+  m.def("_conv_dispatch_stats", []() { return tvk::selection_stats(); });
+  m.def("_clear_conv_dispatch_cache", []() { tvk::clear_selection_stats(); });
+  m.def("_current_stream_ptr", []() { return reinterpret_cast<uintptr_t>(tvk::current_stream()); });
+  m.def("_current_stream", [](int device) {
+    const c10::DeviceIndex d = c10::DeviceIndex(device < 0 ? tvk::cur_dev() : device);
+    c10::Stream s = c10::impl::VirtualGuardImpl(c10::DeviceType::PrivateUse1)
+                        .getStream(c10::Device(c10::DeviceType::PrivateUse1, d));
+    return py::reinterpret_steal<py::object>(THPStream_Wrap(s));
+  }, py::arg("device") = -1);
+  m.def("_default_stream", [](int device) {
+    const c10::DeviceIndex d = c10::DeviceIndex(device < 0 ? tvk::cur_dev() : device);
+    return py::reinterpret_steal<py::object>(
+        THPStream_Wrap(c10::Stream(c10::Stream::DEFAULT, c10::Device(c10::DeviceType::PrivateUse1, d))));
+  }, py::arg("device") = -1);
+  m.def("_set_stream", [](int64_t stream_id, int device) {
+    const c10::DeviceIndex d = c10::DeviceIndex(device < 0 ? tvk::cur_dev() : device);
+    tvk::stream_for_id(d, stream_id);  // validates the id
+    c10::impl::VirtualGuardImpl(c10::DeviceType::PrivateUse1)
+        .exchangeStream(c10::Stream(c10::Stream::UNSAFE, c10::Device(c10::DeviceType::PrivateUse1, d), stream_id));
+  });
+  m.def("_stream_ptr", [](int64_t id, int device) { return reinterpret_cast<uintptr_t>(tvk::stream_for_id(device, id)); });
+  m.def("_manual_seed", [](uint64_t seed) {
+    for (int d = 0; d < std::max(1, device_count()); ++d) {
+      auto& g = tvk::default_generator(c10::DeviceIndex(d));
+      std::lock_guard<std::mutex> lock(g.mutex());
+      g.set_current_seed(seed);
+    }
+  });
+  m.def("_initial_seed", []() { return tvk::default_generator(-1).current_seed(); });
+  m.def("_abi_version", []() { return mx_abi_version(); });
+}

@@ -1,0 +1,262 @@
+"""ctypes binding of the C ABI in include/mx.h (libmx.so).
+
+This is the binding a Python caller of the reference's path would add: plain
+pointers and sizes in, an int status out (MXError raised with mx_last_error()
+on failure).  Device buffers can come from anywhere in the process that uses
+the same HIP runtime (torch's ROCm tensors included); ``stream`` is a
+hipStream_t as an int, 0/None for the library's default stream.
+
+Load order matters: torch must be imported before libmx.so so that both bind
+the same HIP runtime (torch/lib/libamdhip64.so).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch  # noqa: F401  (HIP runtime first, see module docstring)
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmx.so")
+
+MX_OK, MX_ERR_INVALID, MX_ERR_UNSUPPORTED, MX_ERR_OOM, MX_ERR_HIP, MX_ERR_WORKSPACE = range(6)
+MX_COPY_H2D, MX_COPY_D2H, MX_COPY_D2D = 1, 2, 3
+MX_CONV_FORWARD, MX_CONV_DINPUT, MX_CONV_DWEIGHT, MX_CONV_DBIAS = range(4)
+ALGO_AUTO, ALGO_DIRECT, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_REDUCE = range(5)
+BIAS_NONE, BIAS_COL, BIAS_MATRIX = range(3)
+
+# Every entry point declared in include/mx.h (checked by the CPU test suite).
+EXPORTS = [
+    "mx_last_error", "mx_abi_version", "mx_init", "mx_device_count", "mx_get_device", "mx_set_device",
+    "mx_device_name", "mx_device_synchronize", "mx_default_stream", "mx_stream_create", "mx_stream_destroy",
+    "mx_stream_synchronize", "mx_stream_query", "mx_stream_wait_event", "mx_event_create", "mx_event_destroy",
+    "mx_event_record", "mx_event_query", "mx_event_synchronize", "mx_event_elapsed_ms", "mx_malloc", "mx_free",
+    "mx_record_stream", "mx_empty_cache", "mx_memory_stats_get", "mx_memcpy", "mx_fill", "mx_copy_strided",
+    "mx_add_f32", "mx_scale_f32", "mx_sum_f32", "mx_foreach_add_scalar_f32", "mx_conv2d_check",
+    "mx_conv2d_select", "mx_conv2d_forward", "mx_conv2d_backward_input", "mx_conv2d_backward_weight",
+    "mx_conv2d_backward_bias", "mx_conv2d_dweight_plan", "mx_gemm_f32", "mx_adamw_step",
+]
+
+
+class MXError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"mx status {status}: {message}")
+        self.status = status
+
+
+class ConvDesc(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in
+                ("n", "cin", "h", "w", "cout", "kh", "kw", "sh", "sw", "ph", "pw", "dh", "dw", "groups", "oh", "ow")]
+
+
+class GemmDesc(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in
+                ("batch", "m", "n", "k", "a_offset", "a_stride_b", "a_stride_m", "a_stride_k",
+                 "b_offset", "b_stride_b", "b_stride_k", "b_stride_n", "c_offset", "c_stride_b", "ldc",
+                 "bias_offset", "bias_stride_m", "bias_stride_n")] + [
+                ("alpha", C.c_float), ("beta", C.c_float), ("bias_kind", C.c_int)]
+
+
+class AdamWTensor(C.Structure):
+    _fields_ = [("param", C.c_void_p), ("grad", C.c_void_p), ("exp_avg", C.c_void_p), ("exp_avg_sq", C.c_void_p),
+                ("max_exp_avg_sq", C.c_void_p), ("numel", C.c_int64), ("step", C.c_int64),
+                ("step_dev", C.c_void_p)]
+
+
+class AdamWHParams(C.Structure):
+    _fields_ = [("lr", C.c_double), ("beta1", C.c_double), ("beta2", C.c_double), ("eps", C.c_double),
+                ("weight_decay", C.c_double), ("amsgrad", C.c_int), ("maximize", C.c_int),
+                ("lr_dev", C.c_void_p), ("grad_scale", C.c_void_p), ("found_inf", C.c_void_p)]
+
+
+class MemoryStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in
+                ("allocated_bytes", "reserved_bytes", "cached_blocks", "device_mallocs", "cache_hits")]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded libmx.so with argument types declared."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise ImportError(f"{_LIB_PATH} is not built; run `python pytorch-vulkan_amd/build.py`")
+        L = C.CDLL(_LIB_PATH)
+        vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int
+        sig = {
+            "mx_last_error": ([], C.c_char_p),
+            "mx_abi_version": ([], i32),
+            "mx_init": ([i32], i32),
+            "mx_device_count": ([C.POINTER(i32)], i32),
+            "mx_get_device": ([C.POINTER(i32)], i32),
+            "mx_set_device": ([i32], i32),
+            "mx_device_name": ([i32, C.c_char_p, C.c_size_t], i32),
+            "mx_device_synchronize": ([], i32),
+            "mx_default_stream": ([C.POINTER(vp)], i32),
+            "mx_stream_create": ([C.POINTER(vp)], i32),
+            "mx_stream_destroy": ([vp], i32),
+            "mx_stream_synchronize": ([vp], i32),
+            "mx_stream_query": ([vp, C.POINTER(i32)], i32),
+            "mx_stream_wait_event": ([vp, vp], i32),
+            "mx_event_create": ([C.POINTER(vp), i32], i32),
+            "mx_event_destroy": ([vp], i32),
+            "mx_event_record": ([vp, vp], i32),
+            "mx_event_query": ([vp, C.POINTER(i32)], i32),
+            "mx_event_synchronize": ([vp], i32),
+            "mx_event_elapsed_ms": ([vp, vp, C.POINTER(C.c_float)], i32),
+            "mx_malloc": ([C.POINTER(vp), C.c_size_t, vp], i32),
+            "mx_free": ([vp], i32),
+            "mx_record_stream": ([vp, vp], i32),
+            "mx_empty_cache": ([], i32),
+            "mx_memory_stats_get": ([C.POINTER(MemoryStats)], i32),
+            "mx_memcpy": ([vp, vp, C.c_size_t, i32, vp], i32),
+            "mx_fill": ([vp, i64, i32, C.c_uint64, vp], i32),
+            "mx_copy_strided": ([vp, vp, i32, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64), i64, i64, i32, vp], i32),
+            "mx_add_f32": ([vp, vp, vp, C.c_float, i64, vp], i32),
+            "mx_scale_f32": ([vp, vp, C.c_float, i64, vp], i32),
+            "mx_sum_f32": ([vp, vp, i64, i64, i64, vp], i32),
+            "mx_foreach_add_scalar_f32": ([C.POINTER(vp), C.POINTER(i64), i64, C.c_float, vp], i32),
+            "mx_conv2d_check": ([C.POINTER(ConvDesc)], i32),
+            "mx_conv2d_select": ([C.POINTER(ConvDesc), i32, i32, C.POINTER(i32)], i32),
+            "mx_conv2d_forward": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
+            "mx_conv2d_backward_input": ([C.POINTER(ConvDesc), vp, vp, vp, i32, vp], i32),
+            "mx_conv2d_backward_weight": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
+            "mx_conv2d_backward_bias": ([C.POINTER(ConvDesc), vp, vp, vp], i32),
+            "mx_conv2d_dweight_plan": ([C.POINTER(ConvDesc), C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)], i32),
+            "mx_gemm_f32": ([C.POINTER(GemmDesc), vp, vp, vp, vp, vp], i32),
+            "mx_adamw_step": ([C.POINTER(AdamWTensor), i64, C.POINTER(AdamWHParams), C.POINTER(i64), vp], i32),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != MX_OK:
+        raise MXError(status, lib().mx_last_error().decode())
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (or None)."""
+    return None if t is None else t.data_ptr()
+
+
+def conv_desc(x_shape, w_shape, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1) -> ConvDesc:
+    d = ConvDesc(n=x_shape[0], cin=x_shape[1], h=x_shape[2], w=x_shape[3], cout=w_shape[0], kh=w_shape[2],
+                 kw=w_shape[3], sh=stride[0], sw=stride[1], ph=padding[0], pw=padding[1], dh=dilation[0],
+                 dw=dilation[1], groups=groups)
+    check(lib().mx_conv2d_check(C.byref(d)))
+    return d
+
+
+def conv2d_forward(d: ConvDesc, x, w, b, y, algo=ALGO_AUTO, stream=None) -> None:
+    check(lib().mx_conv2d_forward(C.byref(d), ptr(x), ptr(w), ptr(b), ptr(y), algo, stream))
+
+
+def conv2d_backward_input(d: ConvDesc, dy, w, dx, algo=ALGO_AUTO, stream=None) -> None:
+    check(lib().mx_conv2d_backward_input(C.byref(d), ptr(dy), ptr(w), ptr(dx), algo, stream))
+
+
+def conv2d_backward_weight(d: ConvDesc, x, dy, dw, db, algo=ALGO_AUTO, stream=None) -> None:
+    check(lib().mx_conv2d_backward_weight(C.byref(d), ptr(x), ptr(dy), ptr(dw), ptr(db), algo, stream))
+
+
+def conv2d_backward_bias(d: ConvDesc, dy, db, stream=None) -> None:
+    check(lib().mx_conv2d_backward_bias(C.byref(d), ptr(dy), ptr(db), stream))
+
+
+def conv2d_select(d: ConvDesc, phase: int, requested: int = ALGO_AUTO) -> int:
+    out = C.c_int(-1)
+    check(lib().mx_conv2d_select(C.byref(d), phase, requested, C.byref(out)))
+    return out.value
+
+
+def gemm(a, b, c, *, bias=None, alpha=1.0, beta=0.0, bias_kind=None, stream=None) -> None:
+    """c[b] = alpha * a[b] @ b[b] + beta * bias for 2-D or 3-D strided torch tensors (any device layout)."""
+    batched = a.dim() == 3
+    m, k = a.shape[-2], a.shape[-1]
+    n = b.shape[-1]
+    d = GemmDesc(batch=a.shape[0] if batched else 1, m=m, n=n, k=k,
+                 a_offset=a.storage_offset(), a_stride_b=a.stride(0) if batched else 0,
+                 a_stride_m=a.stride(-2), a_stride_k=a.stride(-1),
+                 b_offset=b.storage_offset(), b_stride_b=b.stride(0) if batched else 0,
+                 b_stride_k=b.stride(-2), b_stride_n=b.stride(-1),
+                 c_offset=c.storage_offset(), c_stride_b=c.stride(0) if batched else 0, ldc=c.stride(-2),
+                 alpha=alpha, beta=beta, bias_kind=BIAS_NONE)
+    bias_base = None
+    if bias is not None:
+        if bias_kind is None:
+            bias_kind = BIAS_COL if bias.dim() == 1 else BIAS_MATRIX
+        d.bias_kind = bias_kind
+        d.bias_offset = bias.storage_offset()
+        if bias_kind == BIAS_COL:
+            d.bias_stride_n = bias.stride(0)
+        else:
+            e = bias.expand(m, n)
+            d.bias_stride_m, d.bias_stride_n = e.stride(0), e.stride(1)
+        bias_base = bias.untyped_storage().data_ptr()
+    assert c.stride(-1) == 1, "output rows must be contiguous"
+    check(lib().mx_gemm_f32(C.byref(d), a.untyped_storage().data_ptr(), b.untyped_storage().data_ptr(), bias_base,
+                            c.untyped_storage().data_ptr(), stream))
+
+
+def adamw_step(params, grads, exp_avgs, exp_avg_sqs, *, lr, beta1, beta2, eps, weight_decay, steps=None,
+               step_tensors=None, max_exp_avg_sqs=None, maximize=False, stream=None) -> int:
+    """One fused AdamW step over tensor lists; returns the number of launches."""
+    n = len(params)
+    arr = (AdamWTensor * max(n, 1))()
+    for i in range(n):
+        e = arr[i]
+        e.param, e.grad = params[i].data_ptr(), grads[i].data_ptr()
+        e.exp_avg, e.exp_avg_sq = exp_avgs[i].data_ptr(), exp_avg_sqs[i].data_ptr()
+        e.max_exp_avg_sq = max_exp_avg_sqs[i].data_ptr() if max_exp_avg_sqs is not None else None
+        e.numel = params[i].numel()
+        if step_tensors is not None:
+            e.step_dev = step_tensors[i].data_ptr()
+        else:
+            e.step = int(steps[i])
+    hp = AdamWHParams(lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay,
+                      amsgrad=1 if max_exp_avg_sqs is not None else 0, maximize=1 if maximize else 0)
+    launches = C.c_int64(0)
+    check(lib().mx_adamw_step(arr, n, C.byref(hp), C.byref(launches), stream))
+    return launches.value
+
+
+def sum_mid(out, src, outer, reduce, inner, stream=None) -> None:
+    check(lib().mx_sum_f32(ptr(out), ptr(src), outer, reduce, inner, stream))
+
+
+def dweight_plan(d: ConvDesc):
+    s, sp, ws = C.c_int64(), C.c_int64(), C.c_int64()
+    check(lib().mx_conv2d_dweight_plan(C.byref(d), C.byref(s), C.byref(sp), C.byref(ws)))
+    return s.value, sp.value, ws.value
+
+
+class Event:
+    """HIP event through the C ABI (timing enabled)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        check(lib().mx_event_create(C.byref(h), 1))
+        self.h = h
+
+    def record(self, stream=None):
+        check(lib().mx_event_record(self.h, stream))
+
+    def synchronize(self):
+        check(lib().mx_event_synchronize(self.h))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        check(lib().mx_event_elapsed_ms(self.h, end.h, C.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            lib().mx_event_destroy(self.h)
+        except Exception:
+            pass
