@@ -195,6 +195,12 @@ int mx_conv2d_backward_bias(const mx_conv2d_desc* desc, const float* dy, float* 
 int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t* span,
                            int64_t* workspace_bytes);
 
+/* Name of the (first) kernel a conv call with these arguments launches, e.g.
+ * "conv_dw_kernel<64x64x16>": matches the kernel-trace names of a profiler and
+ * keys per-kernel timing (the reference's gpu_timing_stats() per shader,
+ * csrc/vulkan_context.cpp:368-404). */
+int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char* buf, size_t len);
+
 /* ------------------------------------------------------------------------ */
 /* GEMM: mm / mm.out / addmm / bmm / bmm.out                                  */
 /* ------------------------------------------------------------------------ */

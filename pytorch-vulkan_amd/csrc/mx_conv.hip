@@ -27,6 +27,8 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstring>
+#include <string>
 
 #include "mfma_core.hpp"
 #include "mx_internal.hpp"
@@ -1040,6 +1042,42 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
     case 1: return launch_dw<TileM>(p, pl, s);
     default: return launch_dw<TileS>(p, pl, s);
   }
+  MX_ABI_END
+}
+
+int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char* buf, size_t len) {
+  MX_ABI_BEGIN
+  mx_conv2d_desc d = *desc;
+  MX_TRY(checked_desc(&d));
+  int chosen = 0;
+  MX_TRY(select_algo(d, phase, algo, &chosen));
+  ConvArgs p = make_args(d);
+  static const char* tiles[] = {"128x128x16", "64x128x16", "64x64x16"};
+  std::string name;
+  if (phase == MX_CONV_DBIAS) {
+    name = chosen == MX_CONV_ALGO_DIRECT ? "conv_db_direct_kernel" : "conv_db_reduce_kernel";
+  } else if (chosen == MX_CONV_ALGO_WINOGRAD) {
+    name = "wino_filter_kernel";
+  } else if (chosen == MX_CONV_ALGO_DIRECT) {
+    name = phase == MX_CONV_FORWARD ? "conv_fwd_direct_kernel"
+           : phase == MX_CONV_DINPUT ? "conv_dx_direct_kernel" : "conv_dw_direct_kernel";
+  } else if (chosen == MX_CONV_ALGO_REDUCE) {
+    name = "conv_dw_reduce_kernel";
+  } else if (phase == MX_CONV_FORWARD) {
+    name = cat("conv_fwd_kernel<", tiles[pick_tile(p.Cout_g, p.N * p.OHOW, p.G)], ">");
+  } else if (phase == MX_CONV_DINPUT) {
+    name = cat("conv_dx_kernel<", tiles[pick_tile(p.Cin_g, p.N * p.HW, p.G)], ">");
+  } else {
+    p.M = p.Cout_g;
+    p.Ncols = p.Cin_g * p.KK;
+    p.K = p.N * p.OHOW;
+    name = cat("conv_dw_kernel<", tiles[plan_dw(p).tile], ">");
+  }
+  if (len) {
+    std::strncpy(buf, name.c_str(), len - 1);
+    buf[len - 1] = 0;
+  }
+  return MX_OK;
   MX_ABI_END
 }
 

@@ -33,7 +33,7 @@ EXPORTS = [
     "mx_record_stream", "mx_empty_cache", "mx_memory_stats_get", "mx_memcpy", "mx_fill", "mx_copy_strided",
     "mx_add_f32", "mx_scale_f32", "mx_sum_f32", "mx_foreach_add_scalar_f32", "mx_conv2d_check",
     "mx_conv2d_select", "mx_conv2d_forward", "mx_conv2d_backward_input", "mx_conv2d_backward_weight",
-    "mx_conv2d_backward_bias", "mx_conv2d_dweight_plan", "mx_gemm_f32", "mx_adamw_step",
+    "mx_conv2d_backward_bias", "mx_conv2d_dweight_plan", "mx_conv2d_kernel_name", "mx_gemm_f32", "mx_adamw_step",
 ]
 
 
@@ -124,6 +124,7 @@ def lib() -> C.CDLL:
             "mx_conv2d_backward_weight": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
             "mx_conv2d_backward_bias": ([C.POINTER(ConvDesc), vp, vp, vp], i32),
             "mx_conv2d_dweight_plan": ([C.POINTER(ConvDesc), C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)], i32),
+            "mx_conv2d_kernel_name": ([C.POINTER(ConvDesc), i32, i32, C.c_char_p, C.c_size_t], i32),
             "mx_gemm_f32": ([C.POINTER(GemmDesc), vp, vp, vp, vp, vp], i32),
             "mx_adamw_step": ([C.POINTER(AdamWTensor), i64, C.POINTER(AdamWHParams), C.POINTER(i64), vp], i32),
         }
@@ -228,6 +229,12 @@ def adamw_step(params, grads, exp_avgs, exp_avg_sqs, *, lr, beta1, beta2, eps, w
 
 def sum_mid(out, src, outer, reduce, inner, stream=None) -> None:
     check(lib().mx_sum_f32(ptr(out), ptr(src), outer, reduce, inner, stream))
+
+
+def conv2d_kernel_name(d: ConvDesc, phase: int, algo: int = ALGO_AUTO) -> str:
+    buf = C.create_string_buffer(128)
+    check(lib().mx_conv2d_kernel_name(C.byref(d), phase, algo, buf, 128))
+    return buf.value.decode()
 
 
 def dweight_plan(d: ConvDesc):
