@@ -118,6 +118,9 @@ int mx_copy_strided(void* dst, const void* src, int ndim, const int64_t* sizes,
 int mx_add_f32(float* out, const float* a, const float* b, float alpha, int64_t n, void* stream);
 /* out[i] = a[i] * s (FP32 contiguous): mul.Scalar (csrc/ops/mm.cpp:921-930). */
 int mx_scale_f32(float* out, const float* a, float s, int64_t n, void* stream);
+/* out[i] = a[i] * b[i] (FP32 contiguous): mul.Tensor on equal shapes (the
+ * addmm backward's beta / alpha scaling arrives as a broadcast operand). */
+int mx_mul_f32(float* out, const float* a, const float* b, int64_t n, void* stream);
 
 /* Sum over the middle axis of a contiguous [outer, reduce, inner] FP32 view:
  * out[o, i] = sum_r src[o, r, i].  Replaces sum.dim_IntList

@@ -13,11 +13,11 @@
 // Per-element arithmetic follows torch.optim.AdamW's single-tensor update
 // (the CPU oracle the reference tests against, tests/test_fused_adamw.py):
 //   p = p * (1 - lr*wd)
-//   m = lerp(m, g, 1 - beta1)
+//   m = lerp(m, g, 1 - beta1)            (one fused multiply-add, as torch's CPU lerp)
 //   v = v * beta2 + ((1 - beta2) * g) * g
 //   p = p + (-lr/bc1 * m) / (sqrt(v) / sqrt(bc2) + eps)
-// with bc1 = 1 - beta1^step and bc2 = 1 - beta2^step in double, and no
-// multiply-add contraction, in that order.
+// with bc1 = 1 - beta1^step and bc2 = 1 - beta2^step in double, in that
+// order, and no multiply-add contraction other than the lerp's.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -97,8 +97,9 @@ __device__ __forceinline__ void update(float& p, float g, float& m, float& v, fl
   if (hp.maximize) g = -g;
   if (hp.grad_scale) g = g / scale;
   p = p * c.wdf;
-  // torch lerp: small weights add weight*(end-self), large ones subtract from end.
-  m = (c.b1c < 0.5f) ? m + c.b1c * (g - m) : g - (g - m) * c.omb1c;
+  // torch's vectorised lerp: one fused multiply-add, fma(w, end-self, self)
+  // for small weights, fma(w-1, end-self, end) otherwise.
+  m = (c.b1c < 0.5f) ? fmaf(c.b1c, g - m, m) : fmaf(c.b1c - 1.f, g - m, g);
   v = v * c.b2;
   v = v + (c.b2c * g) * g;
   float vd = v;

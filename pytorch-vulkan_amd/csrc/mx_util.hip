@@ -59,6 +59,11 @@ __global__ void scale_kernel(float* out, const float* a, float s, int64_t n) {
     out[i] = a[i] * s;
 }
 
+__global__ void mul_kernel(float* out, const float* a, const float* b, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+    out[i] = a[i] * b[i];
+}
+
 // out/partial[split][o][i] = sum over r in the split's range of src[o][r][i].
 __global__ void sum_mid_kernel(float* out, const float* src, int64_t outer, int64_t reduce, int64_t inner,
                                int64_t span) {
@@ -190,6 +195,17 @@ int mx_scale_f32(float* out, const float* a, float sc, int64_t n, void* stream) 
   if (n == 0) return MX_OK;
   hipStream_t s = resolve_stream(stream);
   hipLaunchKernelGGL(scale_kernel, dim3(grid_for(n)), dim3(256), 0, s, out, a, sc, n);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+  MX_ABI_END
+}
+
+int mx_mul_f32(float* out, const float* a, const float* b, int64_t n, void* stream) {
+  MX_ABI_BEGIN
+  MX_REQUIRE(n >= 0, MX_ERR_INVALID, "mx_mul_f32: negative size");
+  if (n == 0) return MX_OK;
+  hipStream_t s = resolve_stream(stream);
+  hipLaunchKernelGGL(mul_kernel, dim3(grid_for(n)), dim3(256), 0, s, out, a, b, n);
   MX_HIP(hipGetLastError());
   return MX_OK;
   MX_ABI_END

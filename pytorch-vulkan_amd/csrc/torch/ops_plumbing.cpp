@@ -247,6 +247,36 @@ at::Tensor add_tensor(const at::Tensor& self, const at::Tensor& other, const at:
   return r.to(self.device());
 }
 
+at::Tensor mul_tensor(const at::Tensor& self, const at::Tensor& other) {
+  const bool f32 = self.scalar_type() == at::kFloat && other.scalar_type() == at::kFloat;
+  const at::Tensor& dev_t = is_vk(self) ? self : other;
+  const at::Tensor& oth = is_vk(self) ? other : self;
+  if (f32 && is_vk(dev_t) && !dev_t.is_neg() && (is_host_scalar(oth) || (is_vk(oth) && !oth.is_neg()))) {
+    c10::DeviceGuard guard(dev_t.device());
+    if (is_host_scalar(oth)) {
+      at::Tensor a = dev_t.contiguous();
+      at::Tensor out = at::empty(dev_t.sizes(), dev_t.options().memory_format(at::MemoryFormat::Contiguous));
+      TVK_MX(mx_scale_f32(out.data_ptr<float>(), a.data_ptr<float>(), oth.item<float>(), a.numel(), current_stream()));
+      counters().kernel_launches++;
+      return out;
+    }
+    const auto shape = at::infer_size(self.sizes(), other.sizes());
+    at::Tensor a = self.expand(shape).contiguous();
+    at::Tensor b = other.expand(shape).contiguous();
+    at::Tensor out = at::empty(shape, self.options().memory_format(at::MemoryFormat::Contiguous));
+    TVK_MX(mx_mul_f32(out.data_ptr<float>(), a.data_ptr<float>(), b.data_ptr<float>(), out.numel(), current_stream()));
+    counters().kernel_launches++;
+    return out;
+  }
+  note_cpu_fallback("mul.Tensor");
+  at::Tensor r = at::mul(self.device().is_cpu() ? self : self.cpu(), other.device().is_cpu() ? other : other.cpu());
+  return r.to(dev_t.device());
+}
+
+at::Tensor mul_scalar(const at::Tensor& self, const at::Scalar& other) {
+  return mul_tensor(self, at::scalar_tensor(other, at::TensorOptions().dtype(self.scalar_type())));
+}
+
 at::Tensor& add_inplace(at::Tensor& self, const at::Tensor& other, const at::Scalar& alpha) {
   at::Tensor r = add_tensor(self, other, alpha);
   TORCH_CHECK(r.sizes().equals(self.sizes()), "output with shape ", self.sizes(),
@@ -357,6 +387,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("zero_", TORCH_FN(tvk::zero_));
   m.impl("add.Tensor", TORCH_FN(tvk::add_tensor));
   m.impl("add_.Tensor", TORCH_FN(tvk::add_inplace));
+  m.impl("mul.Tensor", TORCH_FN(tvk::mul_tensor));
+  m.impl("mul.Scalar", TORCH_FN(tvk::mul_scalar));
   m.impl("sum.dim_IntList", TORCH_FN(tvk::sum_dims));
   m.impl("sum", TORCH_FN(tvk::sum_all));
   m.impl("_foreach_add_.Scalar", TORCH_FN(tvk::foreach_add_scalar));

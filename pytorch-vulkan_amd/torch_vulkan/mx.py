@@ -31,7 +31,7 @@ EXPORTS = [
     "mx_stream_synchronize", "mx_stream_query", "mx_stream_wait_event", "mx_event_create", "mx_event_destroy",
     "mx_event_record", "mx_event_query", "mx_event_synchronize", "mx_event_elapsed_ms", "mx_malloc", "mx_free",
     "mx_record_stream", "mx_empty_cache", "mx_memory_stats_get", "mx_memcpy", "mx_fill", "mx_copy_strided",
-    "mx_add_f32", "mx_scale_f32", "mx_sum_f32", "mx_foreach_add_scalar_f32", "mx_conv2d_check",
+    "mx_add_f32", "mx_scale_f32", "mx_mul_f32", "mx_sum_f32", "mx_foreach_add_scalar_f32", "mx_conv2d_check",
     "mx_conv2d_select", "mx_conv2d_forward", "mx_conv2d_backward_input", "mx_conv2d_backward_weight",
     "mx_conv2d_backward_bias", "mx_conv2d_dweight_plan", "mx_conv2d_kernel_name", "mx_gemm_f32", "mx_adamw_step",
 ]
@@ -115,6 +115,7 @@ def lib() -> C.CDLL:
             "mx_copy_strided": ([vp, vp, i32, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64), i64, i64, i32, vp], i32),
             "mx_add_f32": ([vp, vp, vp, C.c_float, i64, vp], i32),
             "mx_scale_f32": ([vp, vp, C.c_float, i64, vp], i32),
+            "mx_mul_f32": ([vp, vp, vp, i64, vp], i32),
             "mx_sum_f32": ([vp, vp, i64, i64, i64, vp], i32),
             "mx_foreach_add_scalar_f32": ([C.POINTER(vp), C.POINTER(i64), i64, C.c_float, vp], i32),
             "mx_conv2d_check": ([C.POINTER(ConvDesc)], i32),

@@ -1,0 +1,127 @@
+"""The C-ABI library on the CPU (no GPU calls): it loads, exports every entry
+point include/mx.h declares, and its host-side validation and planning behave
+like the reference's (csrc/ops/convolution.cpp:101-156 checks before any
+launch; forced-but-inapplicable algorithms raise, :472-473)."""
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def mx():
+    from torch_vulkan import mx as m
+    m.lib()
+    return m
+
+
+def header_symbols():
+    text = open(os.path.join(REPO, "include", "mx.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(mx):
+    syms = header_symbols()
+    assert len(syms) >= 40
+    missing = [s for s in syms if not hasattr(mx.lib(), s)]
+    assert not missing, missing
+    assert sorted(mx.EXPORTS) == syms, "ctypes binding and header disagree"
+
+
+def test_library_links_torch_hip_runtime_only():
+    import subprocess
+    so = os.path.join(REPO, "pytorch-vulkan_amd", "torch_vulkan", "libmx.so")
+    out = subprocess.run(["readelf", "-d", so], capture_output=True, text=True).stdout
+    assert "libamdhip64" in out and "torch/lib" in out
+
+
+def test_conv_check_fills_output_shape(mx):
+    d = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (1, 1))
+    assert (d.oh, d.ow) == (56, 56)
+    d = mx.conv_desc((64, 3, 224, 224), (64, 3, 7, 7), (2, 2), (3, 3))
+    assert (d.oh, d.ow) == (112, 112)
+
+
+@pytest.mark.parametrize("xs,ws,kw,msg", [
+    ((1, 2, 2, 2), (3, 2, 3, 3), dict(stride=(2, 2)), "effective kernel exceeds padded input"),
+    ((1, 4, 5, 5), (3, 2, 1, 1), dict(groups=3), "invalid shapes"),
+    ((1, 1, 1, 1), (1, 1, 1, 1), dict(stride=(2147483647, 2147483647), padding=(2147483647, 2147483647)),
+     "int32 coordinates"),
+])
+def test_conv_validation_errors(mx, xs, ws, kw, msg):
+    with pytest.raises(mx.MXError, match=msg):
+        mx.conv_desc(xs, ws, kw.get("stride", (1, 1)), kw.get("padding", (0, 0)), (1, 1), kw.get("groups", 1))
+
+
+def test_planner_mirrors_reference_heuristic(mx):
+    dense = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (1, 1))
+    assert mx.conv2d_select(dense, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
+    assert mx.conv2d_select(dense, mx.MX_CONV_DINPUT) == mx.ALGO_IMPLICIT_GEMM
+    assert mx.conv2d_select(dense, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    assert mx.conv2d_select(dense, mx.MX_CONV_DBIAS) == mx.ALGO_REDUCE
+    grouped = mx.conv_desc((2, 128, 64, 64), (128, 16, 3, 3), (1, 1), (1, 1), (1, 1), 8)
+    assert mx.conv2d_select(grouped, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
+    tiny = mx.conv_desc((1, 1, 4, 4), (2, 1, 1, 1))
+    assert mx.conv2d_select(tiny, mx.MX_CONV_FORWARD) == mx.ALGO_DIRECT
+
+
+def test_forced_inapplicable_algorithm_raises(mx):
+    strided = mx.conv_desc((1, 8, 9, 9), (8, 8, 3, 3), (2, 2), (1, 1))
+    with pytest.raises(mx.MXError, match="winograd"):
+        mx.conv2d_select(strided, mx.MX_CONV_FORWARD, mx.ALGO_WINOGRAD)
+    with pytest.raises(mx.MXError):
+        mx.conv2d_select(strided, mx.MX_CONV_DINPUT, mx.ALGO_WINOGRAD)
+    with pytest.raises(mx.MXError):
+        mx.conv2d_select(strided, mx.MX_CONV_FORWARD, mx.ALGO_REDUCE)
+
+
+def test_dweight_split_plan(mx):
+    c1 = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (1, 1))
+    splits, span, ws = mx.dweight_plan(c1)
+    assert splits >= 2 and span % 16 == 0 and splits * span >= 8 * 56 * 56 > (splits - 1) * span
+    assert ws > 0
+    small = mx.conv_desc((1, 9, 1, 64), (17, 9, 1, 1))
+    assert mx.dweight_plan(small)[0] == 1
+
+
+def test_kernel_names(mx):
+    c1 = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (1, 1))
+    assert mx.conv2d_kernel_name(c1, mx.MX_CONV_FORWARD).startswith("conv_fwd_kernel<")
+    assert mx.conv2d_kernel_name(c1, mx.MX_CONV_DWEIGHT).startswith("conv_dw_kernel<")
+    assert mx.conv2d_kernel_name(c1, mx.MX_CONV_FORWARD, mx.ALGO_WINOGRAD).startswith("wino")
+
+
+def test_gemm_rejects_bad_descriptor(mx):
+    import ctypes as C
+    d = mx.GemmDesc(batch=1, m=-1, n=2, k=2)
+    with pytest.raises(mx.MXError, match="negative"):
+        mx.check(mx.lib().mx_gemm_f32(C.byref(d), None, None, None, None, None))
+    d = mx.GemmDesc(batch=1, m=2, n=2, k=2, bias_kind=7)
+    with pytest.raises(mx.MXError, match="bias kind"):
+        mx.check(mx.lib().mx_gemm_f32(C.byref(d), None, None, None, None, None))
+
+
+def test_adamw_rejects_invalid_hyperparameters(mx):
+    import ctypes as C
+    hp = mx.AdamWHParams(lr=1e-3, beta1=1.0, beta2=0.999, eps=1e-8, weight_decay=0.0)
+    with pytest.raises(mx.MXError, match="invalid hyperparameters"):
+        mx.check(mx.lib().mx_adamw_step(None, 0, C.byref(hp), None, None))
+    hp.beta1 = 0.9
+    t = (mx.AdamWTensor * 1)()
+    t[0].numel, t[0].step = 4, 0
+    t[0].param = t[0].grad = t[0].exp_avg = t[0].exp_avg_sq = 16
+    with pytest.raises(mx.MXError, match="step must be positive"):
+        mx.check(mx.lib().mx_adamw_step(t, 1, C.byref(hp), None, None))
+
+
+def test_last_error_is_thread_local_and_cleared(mx):
+    d = mx.ConvDesc(n=1, cin=1, h=1, w=1, cout=1, kh=3, kw=3, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1, groups=1)
+    import ctypes as C
+    assert mx.lib().mx_conv2d_check(C.byref(d)) != mx.MX_OK
+    assert mx.lib().mx_last_error()
+    ok = mx.ConvDesc(n=1, cin=1, h=3, w=3, cout=1, kh=3, kw=3, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1, groups=1)
+    assert mx.lib().mx_conv2d_check(C.byref(ok)) == mx.MX_OK
+    assert mx.lib().mx_last_error() == b""
