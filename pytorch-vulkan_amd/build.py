@@ -38,7 +38,8 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
-MX_SOURCES = ["mx_runtime.hip", "mx_gemm.hip", "mx_conv.hip", "mx_winograd.hip", "mx_adamw.hip", "mx_util.hip"]
+MX_SOURCES = ["mx_runtime.hip", "mx_gemm.hip", "mx_conv.hip", "mx_conv_fwd.hip", "mx_conv_dx.hip", "mx_conv_dw.hip",
+              "mx_winograd.hip", "mx_adamw.hip", "mx_util.hip"]
 EXT_SOURCES = ["backend.cpp", "ops_conv.cpp", "ops_gemm.cpp", "ops_adamw.cpp", "ops_plumbing.cpp"]
 
 
@@ -64,6 +65,34 @@ def run(cmd: list[str]) -> None:
         print(out)
 
 
+def compile_hip(cmd: list[str]) -> None:
+    """hipcc -c with the per-kernel resource remarks; a kernel that needs
+    scratch (private) memory fails the build: every kernel here keeps its
+    state in registers and LDS."""
+    res = subprocess.run(cmd + ["-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"], stdout=subprocess.PIPE,
+                         stderr=subprocess.STDOUT, text=True)
+    keep, scratch, fn = [], [], None
+    for line in res.stdout.splitlines():
+        if "packed-fp32-ops" in line:
+            continue
+        if "kernel-resource-usage" in line:
+            if "Function Name:" in line:
+                fn = line.split("Function Name:")[1].split("[")[0].strip()
+            elif "ScratchSize [bytes/lane]:" in line:
+                n = int(line.split("ScratchSize [bytes/lane]:")[1].split()[0])
+                if n:
+                    scratch.append(f"{fn} ({n} B/lane)")
+            continue
+        keep.append(line)
+    out = "\n".join(keep)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out)
+    if scratch:
+        raise RuntimeError("kernels using scratch memory:\n  " + "\n  ".join(scratch))
+
+
 def stale(target: Path, deps: list[Path]) -> bool:
     if not target.exists():
         return True
@@ -84,7 +113,7 @@ def build_mx(jobs: int, incremental: bool) -> Path:
         if not incremental or stale(obj, [CSRC / src] + headers):
             todo.append([cc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        for f in [ex.submit(run, c) for c in todo]:
+        for f in [ex.submit(compile_hip, c) for c in todo]:
             f.result()
     lib = OUT / "libmx.so"
     if not incremental or stale(lib, objs):

@@ -2,15 +2,23 @@
 // implicit-GEMM convolution kernels.
 //
 // A 256-thread workgroup (4 wave64) computes a BM x BN tile of C = A x B.
-// Operands are staged through LDS in double-buffered BK slabs laid out
-// row-major with k contiguous ([row][BK + pad]) for both A (rows = m) and
-// B (rows = n).  Each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile built
-// from 32x32 blocks of v_mfma_f32_32x32x2f32.  Inside a slab the k index is
-// permuted so that lane half h (lane / 32) handles k in [h*BK/2, (h+1)*BK/2):
-// a lane then fetches its BK/2 operand values with ds_read_b128 and issues
-// BK/2 MFMAs per 32x32 block, and the A/B fragments stay consistent because
-// both use the same permutation.  Summation order within a 32x32 block is the
-// MFMA's own (FP32 accumulate).
+// Operands are staged through LDS in double-buffered BK slabs.  Each operand
+// loader chooses its LDS layout: row-major with k contiguous ([row][BK + 4])
+// or k-major with rows contiguous ([k][ROWS + 4]), whichever its global
+// reads can fill with conflict-free 16-byte LDS stores (a row-contiguous
+// operand written row-major would be a strided transpose).  Each wave owns a
+// (BM/WAVES_M) x (BN/WAVES_N) sub-tile built from 32x32 blocks of
+// v_mfma_f32_32x32x2f32.  Inside a slab the k index is permuted so that lane
+// half h (lane / 32) handles k in [h*BK/2, (h+1)*BK/2): from a row-major
+// stage a lane fetches its BK/2 operand values with ds_read_b128, from a
+// k-major stage with one ds_read_b32 per k (32 consecutive rows per half
+// wave), and the A/B fragments stay consistent because both use the same
+// permutation.  Summation order within a 32x32 block is the MFMA's own (FP32
+// accumulate).
+//
+// Cfg::OCC is the register budget in waves per SIMD the kernels are compiled
+// for (amdgpu_waves_per_eu): 2 keeps a 128 x 128 tile in 256 registers so two
+// workgroups share a CU and hide each other's slab-load latency.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -25,22 +33,28 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 
-template <int BM_, int BN_, int BK_, int WAVES_M_>
+template <int BM_, int BN_, int BK_, int WAVES_M_, int OCC_ = 2>
 struct Cfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, OCC = OCC_;
   static constexpr int WAVES_M = WAVES_M_, WAVES_N = 4 / WAVES_M_;
   static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
   static constexpr int FM = WTM / 32, FN = WTN / 32;
   static constexpr int PAD = 4;
   static constexpr int LDK = BK + PAD;
   static constexpr int KH = BK / 2;
-  static constexpr int A_STAGE = BM * LDK, B_STAGE = BN * LDK;
+  // A stage holds either layout: [rows][BK + PAD] or [BK][rows + PAD].
+  static constexpr int A_STAGE = (BM * LDK > BK * (BM + PAD)) ? BM * LDK : BK * (BM + PAD);
+  static constexpr int B_STAGE = (BN * LDK > BK * (BN + PAD)) ? BN * LDK : BK * (BN + PAD);
   static constexpr int SMEM_FLOATS = 2 * (A_STAGE + B_STAGE);
   static constexpr int ACC_REGS = FM * FN * 16;
   static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert(BK % 8 == 0, "BK must be a multiple of 8");
 };
+
+// Qualifiers of a tile kernel compiled for configuration C.
+#define MX_TILE_KERNEL(C) \
+  __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(C::OCC, C::OCC)))
 
 template <class C>
 struct Acc {
@@ -57,37 +71,39 @@ __device__ __forceinline__ void acc_zero(Acc<C>& acc) {
       for (int r = 0; r < 16; ++r) acc.v[i][j][r] = 0.f;
 }
 
+// Operand fragment for one 32-row block: the KH k values (this lane's half of
+// the slab) of row `row` of a stage in either layout.
+template <class C, int ROWS, bool KMAJOR>
+__device__ __forceinline__ void load_frag(float (&f)[C::KH], const float* stage, int row, int h) {
+  if constexpr (KMAJOR) {
+    constexpr int LDR = ROWS + C::PAD;
+    const float* src = stage + h * C::KH * LDR + row;
+#pragma unroll
+    for (int q = 0; q < C::KH; ++q) f[q] = src[q * LDR];
+  } else {
+    const float* src = stage + row * C::LDK + h * C::KH;
+#pragma unroll
+    for (int q = 0; q < C::KH; q += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(src + q);
+      f[q + 0] = t[0];
+      f[q + 1] = t[1];
+      f[q + 2] = t[2];
+      f[q + 3] = t[3];
+    }
+  }
+}
+
 // One BK slab: fragments from LDS, BK/2 MFMA steps per 32x32 block.
-template <class C>
+template <class C, bool KMA, bool KMB>
 __device__ __forceinline__ void mma_slab(Acc<C>& acc, const float* As, const float* Bs, int wm,
                                          int wn, int lane) {
   const int r = lane & 31, h = lane >> 5;
   float a[C::FM][C::KH];
   float b[C::FN][C::KH];
 #pragma unroll
-  for (int i = 0; i < C::FM; ++i) {
-    const float* src = As + (wm * C::WTM + i * 32 + r) * C::LDK + h * C::KH;
+  for (int i = 0; i < C::FM; ++i) load_frag<C, C::BM, KMA>(a[i], As, wm * C::WTM + i * 32 + r, h);
 #pragma unroll
-    for (int q = 0; q < C::KH; q += 4) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(src + q);
-      a[i][q + 0] = t[0];
-      a[i][q + 1] = t[1];
-      a[i][q + 2] = t[2];
-      a[i][q + 3] = t[3];
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < C::FN; ++j) {
-    const float* src = Bs + (wn * C::WTN + j * 32 + r) * C::LDK + h * C::KH;
-#pragma unroll
-    for (int q = 0; q < C::KH; q += 4) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(src + q);
-      b[j][q + 0] = t[0];
-      b[j][q + 1] = t[1];
-      b[j][q + 2] = t[2];
-      b[j][q + 3] = t[3];
-    }
-  }
+  for (int j = 0; j < C::FN; ++j) load_frag<C, C::BN, KMB>(b[j], Bs, wn * C::WTN + j * 32 + r, h);
 #pragma unroll
   for (int s = 0; s < C::KH; ++s)
 #pragma unroll
@@ -98,7 +114,8 @@ __device__ __forceinline__ void mma_slab(Acc<C>& acc, const float* As, const flo
 }
 
 // Double-buffered main loop over nk slabs.  Loaders expose load() (global ->
-// registers for the next slab, advancing their k cursor) and store(lds).
+// registers for the next slab, advancing their k cursor), store(lds) and
+// KMAJOR (the LDS layout store() writes).
 template <class C, class LA, class LB>
 __device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la, LB& lb, int nk, float* smem) {
   float* As = smem;
@@ -119,7 +136,7 @@ __device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la, LB& lb, int nk, fl
       la.load();
       lb.load();
     }
-    mma_slab<C>(acc, As + cur * C::A_STAGE, Bs + cur * C::B_STAGE, wm, wn, lane);
+    mma_slab<C, LA::KMAJOR, LB::KMAJOR>(acc, As + cur * C::A_STAGE, Bs + cur * C::B_STAGE, wm, wn, lane);
     if (more) {
       la.store(As + (cur ^ 1) * C::A_STAGE);
       lb.store(Bs + (cur ^ 1) * C::B_STAGE);
@@ -148,6 +165,32 @@ __device__ __forceinline__ void for_each_acc(const Acc<C>& acc, F&& f) {
       }
 }
 
+// Same walk with the fragment column index j (0..FN) of each value: every
+// value of one j shares this lane's column.
+template <class C, class F>
+__device__ __forceinline__ void for_each_acc_j(const Acc<C>& acc, F&& f) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = wm * C::WTM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int col = wn * C::WTN + j * 32 + r;
+        f(row, col, j, acc.v[i][j][v]);
+      }
+}
+
+// This lane's column inside the tile for fragment column j.
+template <class C>
+__device__ __forceinline__ int acc_col(int j) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  return (wave % C::WAVES_N) * C::WTN + j * 32 + (lane & 31);
+}
+
 // Register-order index of accumulator (i, j, v) of this thread: partial tiles
 // are spilled and reloaded in this order, fully coalesced.
 template <class C>
@@ -170,6 +213,7 @@ struct StridedLoader;
 
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::KVEC> {
+  static constexpr bool KMAJOR = false;
   static constexpr int TPR = BK / 4;                 // threads per row
   static constexpr int RPP = kThreads / TPR;         // rows per pass
   static constexpr int PASSES = ROWS / RPP;
@@ -178,7 +222,7 @@ struct StridedLoader<ROWS, BK, Mode::KVEC> {
   const float* ptr[PASSES];
   bool ok[PASSES];
   int k, kmax, kq;
-  __device__ void init(const float* base, int64_t s_row, int64_t /*s_k*/, int row0, int R, int k0,
+  __device__ __forceinline__ void init(const float* base, int64_t s_row, int64_t /*s_k*/, int row0, int R, int k0,
                        int kmax_) {
     const int tid = threadIdx.x;
     kq = tid % TPR;
@@ -214,6 +258,9 @@ struct StridedLoader<ROWS, BK, Mode::KVEC> {
 
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::RVEC> {
+  // Rows are contiguous in memory: each thread reads 4 rows at one k with a
+  // 16-byte load and writes them unchanged into the k-major stage.
+  static constexpr bool KMAJOR = true;
   static constexpr int TPK = ROWS / 4;               // threads per k
   static constexpr int KPP = kThreads / TPK;         // k per pass
   static constexpr int PASSES = BK / KPP;
@@ -223,7 +270,7 @@ struct StridedLoader<ROWS, BK, Mode::RVEC> {
   int64_t s_k;
   bool ok;
   int k, kmax, kk;
-  __device__ void init(const float* base, int64_t /*s_row*/, int64_t s_k_, int row0, int R, int k0,
+  __device__ __forceinline__ void init(const float* base, int64_t /*s_row*/, int64_t s_k_, int row0, int R, int k0,
                        int kmax_) {
     const int tid = threadIdx.x;
     const int rq = tid % TPK;
@@ -248,17 +295,16 @@ struct StridedLoader<ROWS, BK, Mode::RVEC> {
   }
   __device__ __forceinline__ void store(float* lds) const {
     const int tid = threadIdx.x;
-    const int rq = tid % TPK;
-    constexpr int LDK = BK + 4;
+    constexpr int LDR = ROWS + 4;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) lds[(4 * rq + e) * LDK + kk + p * KPP] = v[p][e];
+      *reinterpret_cast<f32x4*>(lds + (kk + p * KPP) * LDR + 4 * (tid % TPK)) = v[p];
   }
 };
 
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
+  static constexpr bool KMAJOR = false;
   static constexpr int RPP = kThreads / BK;
   static constexpr int PASSES = ROWS / RPP;
   static_assert(PASSES >= 1 && ROWS % RPP == 0, "KSCALAR tiling");
@@ -267,7 +313,7 @@ struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
   bool ok[PASSES];
   int64_t s_k;
   int k, kmax, kk;
-  __device__ void init(const float* base, int64_t s_row, int64_t s_k_, int row0, int R, int k0, int kmax_) {
+  __device__ __forceinline__ void init(const float* base, int64_t s_row, int64_t s_k_, int row0, int R, int k0, int kmax_) {
     const int tid = threadIdx.x;
     kk = tid % BK;
     s_k = s_k_;
@@ -298,6 +344,7 @@ struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
 
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::RSCALAR> {
+  static constexpr bool KMAJOR = false;
   static_assert(kThreads % ROWS == 0 || ROWS % kThreads == 0, "RSCALAR tiling");
   static constexpr int EPT = ROWS * BK / kThreads;   // consecutive k per thread
   static_assert(ROWS <= kThreads, "RSCALAR expects ROWS <= 256");
@@ -306,7 +353,7 @@ struct StridedLoader<ROWS, BK, Mode::RSCALAR> {
   int64_t s_k;
   bool ok;
   int k, kmax, ks;
-  __device__ void init(const float* base, int64_t s_row, int64_t s_k_, int row0, int R, int k0, int kmax_) {
+  __device__ __forceinline__ void init(const float* base, int64_t s_row, int64_t s_k_, int row0, int R, int k0, int kmax_) {
     const int tid = threadIdx.x;
     const int r = tid % ROWS;
     ks = (tid / ROWS) * EPT;

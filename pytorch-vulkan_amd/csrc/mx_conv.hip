@@ -1,526 +1,29 @@
-// FP32 NCHW Conv2D on gfx950: validation, algorithm planner, implicit-GEMM
-// forward / dInput / dWeight(+dBias) on FP32 MFMA, direct kernels and the
-// dBias reduction.
+// FP32 NCHW Conv2D on gfx950: validation, algorithm selection, planning of
+// the implicit-GEMM launches (mx_conv_fwd.hip, mx_conv_dx.hip,
+// mx_conv_dw.hip), the direct kernels and the dBias reduction.
 //
 // Reference behaviour followed (mistrjirka/Pytorch-vulkan):
 //   validation + output shape  csrc/ops/convolution.cpp:101-156
 //   candidate menu / heuristic csrc/ops/convolution.cpp:357-482
 //   dWeight split-K plan       csrc/ops/convolution.cpp:204-238
-//   forward implicit GEMM      csrc/shaders/conv2d_tiled_body.glsl:1-87
-//   dInput implicit GEMM       csrc/shaders/conv2d_backward_input_tiled_body.glsl:1-95
-//   dWeight split + finalize   conv2d_backward_weight_tiled_body.glsl:1-71,
-//                              conv2d_backward_weight_finalize.comp:9-18
 //   direct kernels             conv2d_forward.comp:11-43, conv2d_backward_input.comp:10-47,
 //                              conv2d_backward_weight.comp:10-41
 //   dBias                      conv2d_backward_bias_reduce.comp:10-24
-//
-// GEMM views (per group g):
-//   forward : C[co, pos]        = W[co, (ci,kh,kw)]  x im2col(x)[(ci,kh,kw), pos]
-//   dInput  : C[ci, ipos]       = W^T[ci, (co,kh,kw)] x gather(dy)[(co,kh,kw), ipos]
-//   dWeight : C[co, (ci,kh,kw)] = dy[co, pos]        x im2col(x)^T[pos, (ci,kh,kw)]
-// The dWeight K dimension (all N*OH*OW positions) is split across workgroups;
-// partial tiles are summed in fixed split order by the last workgroup to
-// finish each tile (an atomic arrival counter), so the result is
-// deterministic and no separate finalize launch is needed.  dBias rides on
-// the dy operand already streamed by the dWeight tiles of column 0.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <climits>
 #include <cstring>
+#include <numeric>
 #include <string>
 
-#include "mfma_core.hpp"
-#include "mx_internal.hpp"
+#include "mx_conv_common.hpp"
 
 namespace mx {
 namespace {
 
-using namespace mfma;
-
-struct ConvArgs {
-  const float* x;
-  const float* w;
-  const float* bias;
-  const float* dy;
-  float* out;
-  float* db;
-  int N, Cin, H, W, Cout, KH, KW, OH, OW, sh, sw, ph, pw, dh, dw, G;
-  int Cin_g, Cout_g, KK, HW, OHOW;
-  int M, Ncols, K;
-  int tiles_m, tiles_n, splits, kps;
-  float* ws;
-  float* ws_db;
-  unsigned* counters;
-};
-
-// ------------------------------------------------------------------ loaders
-// Forward B operand: rows = output positions (img, oh, ow), k = (ci, kh, kw).
-// Consecutive lanes take consecutive positions (coalesced along ow).
-template <int ROWS, int BK>
-struct Im2colLoader {
-  static constexpr int EPT = ROWS * BK / kThreads;
-  static_assert(ROWS <= kThreads && EPT >= 1, "Im2colLoader tiling");
-  float v[EPT];
-  const float* xg;
-  int ih0, iw0, ks, k;
-  bool ok;
-  int K, KK, KH, KW, dh, dw, H, W, HW;
-  __device__ void init(const ConvArgs& p, int col0, int g) {
-    const int tid = threadIdx.x;
-    const int r = tid % ROWS;
-    ks = (tid / ROWS) * EPT;
-    const int pos = col0 + r;
-    ok = pos < p.Ncols;
-    const int pp = ok ? pos : 0;
-    const int img = pp / p.OHOW;
-    const int q = pp - img * p.OHOW;
-    const int oh = q / p.OW;
-    const int ow = q - oh * p.OW;
-    ih0 = oh * p.sh - p.ph;
-    iw0 = ow * p.sw - p.pw;
-    xg = p.x + (int64_t(img) * p.Cin + int64_t(g) * p.Cin_g) * p.HW;
-    K = p.K;
-    KK = p.KK;
-    KH = p.KH;
-    KW = p.KW;
-    dh = p.dh;
-    dw = p.dw;
-    H = p.H;
-    W = p.W;
-    HW = p.HW;
-    k = 0;
-  }
-  __device__ __forceinline__ void load() {
-    const int kb = k + ks;
-    int ci = kb / KK;
-    const int rem = kb - ci * KK;
-    int kh = rem / KW;
-    int kw = rem - kh * KW;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
-      const bool valid = ok && (kb + e) < K && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-      v[e] = valid ? xg[ci * HW + ih * W + iw] : 0.f;
-      if (++kw == KW) {
-        kw = 0;
-        if (++kh == KH) {
-          kh = 0;
-          ++ci;
-        }
-      }
-    }
-    k += BK;
-  }
-  __device__ __forceinline__ void store(float* lds) const {
-    constexpr int LDK = BK + 4;
-    const int tid = threadIdx.x;
-    float* dst = lds + (tid % ROWS) * LDK + ks;
-    if constexpr (EPT % 4 == 0) {
-#pragma unroll
-      for (int e = 0; e < EPT; e += 4)
-        *reinterpret_cast<f32x4*>(dst + e) = f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]};
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) dst[e] = v[e];
-    }
-  }
-};
-
-// dInput A operand: rows = ci, k = (co, kh, kw); element w[g*Cout_g+co][ci][kh][kw].
-template <int ROWS, int BK>
-struct WeightTLoader {
-  static constexpr int RPP = kThreads / BK;
-  static constexpr int PASSES = ROWS / RPP;
-  static_assert(PASSES >= 1 && ROWS % RPP == 0, "WeightTLoader tiling");
-  float v[PASSES];
-  int roff[PASSES];
-  bool ok[PASSES];
-  const float* wg;
-  int k, kk, K, KK, CKK;
-  __device__ void init(const ConvArgs& p, int row0, int g) {
-    const int tid = threadIdx.x;
-    kk = tid % BK;
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      const int ci = row0 + tid / BK + q * RPP;
-      ok[q] = ci < p.Cin_g;
-      roff[q] = ok[q] ? ci * p.KK : 0;
-    }
-    wg = p.w + int64_t(g) * p.Cout_g * p.Cin_g * p.KK;
-    K = p.K;
-    KK = p.KK;
-    CKK = p.Cin_g * p.KK;
-    k = 0;
-  }
-  __device__ __forceinline__ void load() {
-    const int kx = k + kk;
-    const bool kin = kx < K;
-    const int co = kx / KK;
-    const int base = co * CKK + (kx - co * KK);
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) v[q] = (ok[q] && kin) ? wg[base + roff[q]] : 0.f;
-    k += BK;
-  }
-  __device__ __forceinline__ void store(float* lds) const {
-    constexpr int LDK = BK + 4;
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) lds[(tid / BK + q * RPP) * LDK + kk] = v[q];
-  }
-};
-
-// dInput B operand: rows = input positions (img, ih, iw), k = (co, kh, kw);
-// element dy[img][co][oh][ow] with oh*sh = ih + ph - kh*dh (no zero insertion).
-template <int ROWS, int BK, bool UNIT>
-struct DyGatherLoader {
-  static constexpr int EPT = ROWS * BK / kThreads;
-  static_assert(ROWS <= kThreads && EPT >= 1, "DyGatherLoader tiling");
-  float v[EPT];
-  const float* dyg;
-  int ihp, iwp, ks, k;
-  bool ok;
-  int K, KK, KH, KW, dh, dw, sh, sw, OH, OW, OHOW;
-  __device__ void init(const ConvArgs& p, int col0, int g) {
-    const int tid = threadIdx.x;
-    const int r = tid % ROWS;
-    ks = (tid / ROWS) * EPT;
-    const int pos = col0 + r;
-    ok = pos < p.Ncols;
-    const int pp = ok ? pos : 0;
-    const int img = pp / p.HW;
-    const int q = pp - img * p.HW;
-    const int ih = q / p.W;
-    const int iw = q - ih * p.W;
-    ihp = ih + p.ph;
-    iwp = iw + p.pw;
-    dyg = p.dy + (int64_t(img) * p.Cout + int64_t(g) * p.Cout_g) * p.OHOW;
-    K = p.K;
-    KK = p.KK;
-    KH = p.KH;
-    KW = p.KW;
-    dh = p.dh;
-    dw = p.dw;
-    sh = p.sh;
-    sw = p.sw;
-    OH = p.OH;
-    OW = p.OW;
-    OHOW = p.OHOW;
-    k = 0;
-  }
-  __device__ __forceinline__ void load() {
-    const int kb = k + ks;
-    int co = kb / KK;
-    const int rem = kb - co * KK;
-    int kh = rem / KW;
-    int kw = rem - kh * KW;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int th = ihp - kh * dh, tw = iwp - kw * dw;
-      bool valid = ok && (kb + e) < K;
-      int off = 0;
-      if constexpr (UNIT) {
-        valid = valid && unsigned(th) < unsigned(OH) && unsigned(tw) < unsigned(OW);
-        off = co * OHOW + th * OW + tw;
-      } else {
-        valid = valid && th >= 0 && tw >= 0 && th % sh == 0 && tw % sw == 0;
-        const int oh = th / sh, ow = tw / sw;
-        valid = valid && oh < OH && ow < OW;
-        off = co * OHOW + oh * OW + ow;
-      }
-      v[e] = valid ? dyg[off] : 0.f;
-      if (++kw == KW) {
-        kw = 0;
-        if (++kh == KH) {
-          kh = 0;
-          ++co;
-        }
-      }
-    }
-    k += BK;
-  }
-  __device__ __forceinline__ void store(float* lds) const {
-    constexpr int LDK = BK + 4;
-    const int tid = threadIdx.x;
-    float* dst = lds + (tid % ROWS) * LDK + ks;
-    if constexpr (EPT % 4 == 0) {
-#pragma unroll
-      for (int e = 0; e < EPT; e += 4)
-        *reinterpret_cast<f32x4*>(dst + e) = f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]};
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) dst[e] = v[e];
-    }
-  }
-};
-
-// dWeight A operand: rows = co, k = output position; element dy[img][co][q].
-// Also keeps each thread's running row sums for dBias.
-template <int ROWS, int BK>
-struct DyRowsLoader {
-  static constexpr int RPP = kThreads / BK;
-  static constexpr int PASSES = ROWS / RPP;
-  static_assert(PASSES >= 1 && ROWS % RPP == 0, "DyRowsLoader tiling");
-  float v[PASSES];
-  float bsum[PASSES];
-  int coff[PASSES];
-  bool ok[PASSES];
-  const float* dyg;
-  int k, kk, kmax, OHOW, COHOW;
-  __device__ void init(const ConvArgs& p, int row0, int g, int k0, int kmax_) {
-    const int tid = threadIdx.x;
-    kk = tid % BK;
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      const int co = row0 + tid / BK + q * RPP;
-      ok[q] = co < p.Cout_g;
-      coff[q] = ok[q] ? co * p.OHOW : 0;
-      bsum[q] = 0.f;
-    }
-    dyg = p.dy + int64_t(g) * p.Cout_g * p.OHOW;
-    OHOW = p.OHOW;
-    COHOW = p.Cout * p.OHOW;
-    k = k0;
-    kmax = kmax_;
-  }
-  __device__ __forceinline__ void load() {
-    const int kx = k + kk;
-    const bool kin = kx < kmax;
-    const int img = kx / OHOW;
-    const int base = img * COHOW + (kx - img * OHOW);
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      v[q] = (ok[q] && kin) ? dyg[base + coff[q]] : 0.f;
-      bsum[q] += v[q];
-    }
-    k += BK;
-  }
-  __device__ __forceinline__ void store(float* lds) const {
-    constexpr int LDK = BK + 4;
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) lds[(tid / BK + q * RPP) * LDK + kk] = v[q];
-  }
-};
-
-// dWeight B operand: rows = (ci, kh, kw), k = output position;
-// element x[img][ci][oh*sh - ph + kh*dh][ow*sw - pw + kw*dw].
-template <int ROWS, int BK>
-struct XColsLoader {
-  static constexpr int RPP = kThreads / BK;
-  static constexpr int PASSES = ROWS / RPP;
-  static_assert(PASSES >= 1 && ROWS % RPP == 0, "XColsLoader tiling");
-  float v[PASSES];
-  int coff[PASSES];
-  int khd[PASSES];
-  int kwd[PASSES];
-  const float* xg;
-  int k, kk, kmax, OHOW, OW, sh, sw, H, W, CHW;
-  __device__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
-    const int tid = threadIdx.x;
-    kk = tid % BK;
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      const int n = col0 + tid / BK + q * RPP;
-      const bool ok = n < p.Ncols;
-      const int nn = ok ? n : 0;
-      const int ci = nn / p.KK;
-      const int r = nn - ci * p.KK;
-      const int kh = r / p.KW;
-      const int kw = r - kh * p.KW;
-      coff[q] = ci * p.HW;
-      // An invalid row gets an offset that always fails the bounds test.
-      khd[q] = ok ? kh * p.dh - p.ph : INT_MIN / 2;
-      kwd[q] = kw * p.dw - p.pw;
-    }
-    xg = p.x + int64_t(g) * p.Cin_g * p.HW;
-    OHOW = p.OHOW;
-    OW = p.OW;
-    sh = p.sh;
-    sw = p.sw;
-    H = p.H;
-    W = p.W;
-    CHW = p.Cin * p.HW;
-    k = k0;
-    kmax = kmax_;
-  }
-  __device__ __forceinline__ void load() {
-    const int kx = k + kk;
-    const bool kin = kx < kmax;
-    const int img = kx / OHOW;
-    const int q0 = kx - img * OHOW;
-    const int oh = q0 / OW;
-    const int ow = q0 - oh * OW;
-    const int ihb = oh * sh, iwb = ow * sw;
-    const float* xi = xg + int64_t(img) * CHW;
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      const int ih = ihb + khd[q], iw = iwb + kwd[q];
-      const bool valid = kin && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-      v[q] = valid ? xi[coff[q] + ih * W + iw] : 0.f;
-    }
-    k += BK;
-  }
-  __device__ __forceinline__ void store(float* lds) const {
-    constexpr int LDK = BK + 4;
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) lds[(tid / BK + q * RPP) * LDK + kk] = v[q];
-  }
-};
-
-// ------------------------------------------------------------------ kernels
-template <class C, Mode MA>
-__global__ __launch_bounds__(256) void conv_fwd_kernel(ConvArgs p) {
-  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
-  const int g = blockIdx.z;
-  int tm, tn;
-  tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
-  const int row0 = tm * C::BM, col0 = tn * C::BN;
-  StridedLoader<C::BM, C::BK, MA> la;
-  la.init(p.w + int64_t(g) * p.Cout_g * p.K, p.K, 1, row0, p.M, 0, p.K);
-  Im2colLoader<C::BN, C::BK> lb;
-  lb.init(p, col0, g);
-  Acc<C> acc;
-  mainloop<C>(acc, la, lb, (p.K + C::BK - 1) / C::BK, smem);
-  for_each_acc<C>(acc, [&](int r, int c, float v) {
-    const int co = row0 + r, pos = col0 + c;
-    if (co < p.M && pos < p.Ncols) {
-      const int img = pos / p.OHOW;
-      const int q = pos - img * p.OHOW;
-      const int oc = g * p.Cout_g + co;
-      p.out[(int64_t(img) * p.Cout + oc) * p.OHOW + q] = v + (p.bias ? p.bias[oc] : 0.f);
-    }
-  });
-}
-
-template <class C, bool UNIT>
-__global__ __launch_bounds__(256) void conv_dx_kernel(ConvArgs p) {
-  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
-  const int g = blockIdx.z;
-  int tm, tn;
-  tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
-  const int row0 = tm * C::BM, col0 = tn * C::BN;
-  WeightTLoader<C::BM, C::BK> la;
-  la.init(p, row0, g);
-  DyGatherLoader<C::BN, C::BK, UNIT> lb;
-  lb.init(p, col0, g);
-  Acc<C> acc;
-  mainloop<C>(acc, la, lb, (p.K + C::BK - 1) / C::BK, smem);
-  for_each_acc<C>(acc, [&](int r, int c, float v) {
-    const int ci = row0 + r, pos = col0 + c;
-    if (ci < p.M && pos < p.Ncols) {
-      const int img = pos / p.HW;
-      const int q = pos - img * p.HW;
-      p.out[(int64_t(img) * p.Cin + g * p.Cin_g + ci) * p.HW + q] = v;
-    }
-  });
-}
-
-// Sum of `v` over the BK consecutive lanes that share a row (fixed butterfly).
-template <int BK>
-__device__ __forceinline__ float row_lane_sum(float v) {
-#pragma unroll
-  for (int m = BK / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, BK);
-  return v;
-}
-
-template <class C>
-__global__ __launch_bounds__(256) void conv_dw_kernel(ConvArgs p) {
-  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
-  __shared__ int s_last;
-  const int g = blockIdx.z, split = blockIdx.y;
-  const int ntiles = p.tiles_m * p.tiles_n;
-  const int tile = xcd_remap(blockIdx.x, ntiles);
-  int tm, tn;
-  tile_coords(tile, p.tiles_m, p.tiles_n, tm, tn);
-  const int row0 = tm * C::BM, col0 = tn * C::BN;
-  const int k_begin = split * p.kps;
-  const int k_end = min(p.K, k_begin + p.kps);
-  DyRowsLoader<C::BM, C::BK> la;
-  la.init(p, row0, g, k_begin, k_end);
-  XColsLoader<C::BN, C::BK> lb;
-  lb.init(p, col0, g, k_begin, k_end);
-  Acc<C> acc;
-  mainloop<C>(acc, la, lb, (k_end - k_begin + C::BK - 1) / C::BK, smem);
-
-  const int tid = threadIdx.x;
-  const bool do_db = p.db != nullptr && tn == 0;
-  constexpr int RPP = kThreads / C::BK;
-  constexpr int PASSES = C::BM / RPP;
-  float* dwg = p.out + int64_t(g) * p.Cout_g * p.Ncols;
-
-  if (p.splits == 1) {
-    if (dwg != nullptr && p.out != nullptr)
-      for_each_acc<C>(acc, [&](int r, int c, float v) {
-        const int co = row0 + r, n = col0 + c;
-        if (co < p.M && n < p.Ncols) dwg[int64_t(co) * p.Ncols + n] = v;
-      });
-    if (do_db) {
-#pragma unroll
-      for (int q = 0; q < PASSES; ++q) {
-        const float s = row_lane_sum<C::BK>(la.bsum[q]);
-        const int co = row0 + tid / C::BK + q * RPP;
-        if (tid % C::BK == 0 && co < p.M) p.db[g * p.Cout_g + co] = s;
-      }
-    }
-    return;
-  }
-
-  // Partial tile -> workspace in register order; dBias partial per row.
-  constexpr int TILE = C::BM * C::BN;
-  const int64_t tile_id = int64_t(g) * ntiles + tile;
-  float* wsp = p.ws + (tile_id * p.splits + split) * TILE;
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) wsp[acc_slot<C>(i, j, v)] = acc.v[i][j][v];
-  if (do_db) {
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      const float s = row_lane_sum<C::BK>(la.bsum[q]);
-      const int rl = tid / C::BK + q * RPP;
-      if (tid % C::BK == 0)
-        p.ws_db[((int64_t(g) * p.tiles_m + tm) * p.splits + split) * C::BM + rl] = s;
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&p.counters[tile_id], 1u);
-    s_last = prev == unsigned(p.splits - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  // Last arrival: fixed-order sum over splits, then the epilogue.
-  const float* wst = p.ws + tile_id * p.splits * TILE;
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int slot = acc_slot<C>(i, j, v);
-        float s = 0.f;
-        for (int sp = 0; sp < p.splits; ++sp) s += wst[int64_t(sp) * TILE + slot];
-        acc.v[i][j][v] = s;
-      }
-  if (p.out != nullptr)
-    for_each_acc<C>(acc, [&](int r, int c, float v) {
-      const int co = row0 + r, n = col0 + c;
-      if (co < p.M && n < p.Ncols) dwg[int64_t(co) * p.Ncols + n] = v;
-    });
-  if (do_db && tid < C::BM && row0 + tid < p.M) {
-    const float* wdb = p.ws_db + (int64_t(g) * p.tiles_m + tm) * p.splits * C::BM;
-    float s = 0.f;
-    for (int sp = 0; sp < p.splits; ++sp) s += wdb[sp * C::BM + tid];
-    p.db[g * p.Cout_g + row0 + tid] = s;
-  }
-  if (tid == 0) p.counters[tile_id] = 0u;
-}
+using conv::ConvArgs;
+using mfma::Mode;
 
 // ----------------------------------------------------------- direct kernels
 __global__ void conv_fwd_direct_kernel(ConvArgs p) {
@@ -672,10 +175,6 @@ __global__ void conv_db_direct_kernel(ConvArgs p) {
 }
 
 // ------------------------------------------------------------------ host
-using TileL = Cfg<128, 128, 16, 2>;  // 128 x 128, waves 2 x 2 (64 x 64 each)
-using TileM = Cfg<64, 128, 16, 2>;   // 64 x 128, waves 2 x 2 (32 x 64 each)
-using TileS = Cfg<64, 64, 16, 2>;    // 64 x 64, waves 2 x 2 (32 x 32 each)
-
 int checked_desc(mx_conv2d_desc* d) {
   MX_REQUIRE(d, MX_ERR_INVALID, "conv2d: null descriptor");
   MX_REQUIRE(d->n > 0 && d->cin > 0 && d->cout > 0 && d->h > 0 && d->w > 0 && d->kh > 0 && d->kw > 0 &&
@@ -798,103 +297,123 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
   }
 }
 
-template <class C>
-void set_tiles(ConvArgs& p) {
-  p.tiles_m = (p.M + C::BM - 1) / C::BM;
-  p.tiles_n = (p.Ncols + C::BN - 1) / C::BN;
+// Per-tile figures for the planners: rows, columns, workgroups resident per
+// CU, and the measured MFMA throughput of a CU full of such tiles relative to
+// the 256 x 128 tile.
+struct TileInfo {
+  int bm, bn, per_cu;
+  double rate;
+  const char* name;
+};
+constexpr TileInfo kTileInfo[conv::NTILES] = {
+    {256, 128, 2, 1.0, "256x128x16"}, {128, 256, 2, 1.0, "128x256x16"}, {128, 128, 2, 0.94, "128x128x16"},
+    {64, 256, 2, 0.94, "64x256x16"},  {256, 64, 2, 0.94, "256x64x16"},  {64, 64, 4, 0.6, "64x64x16"}};
+
+// Single-pass GEMM (forward, dInput): rounds of resident tiles times the
+// time of one round (per_cu tiles per CU at the CU's relative rate).
+int pick_tile(int64_t M, int64_t Ncols, int64_t G) {
+  int best = conv::TALL;
+  double best_cost = 0;
+  for (int t = 0; t < conv::NTILES; ++t) {
+    if (t == conv::NARROW) continue;  // split-K (dWeight) only
+    const TileInfo& ti = kTileInfo[t];
+    const int64_t tiles = ((M + ti.bm - 1) / ti.bm) * ((Ncols + ti.bn - 1) / ti.bn) * G;
+    const int64_t slots = int64_t(cu_count()) * ti.per_cu;
+    const double cost = double((tiles + slots - 1) / slots) * ti.per_cu * ti.bm * ti.bn / ti.rate;
+    if (t == conv::TALL || cost < best_cost) {
+      best = t;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
-// Tile shape from the GEMM view (per group M x Ncols, times groups).
-int pick_tile(int M, int Ncols, int G) {
-  const int64_t big = int64_t((M + 127) / 128) * ((Ncols + 127) / 128) * G;
-  if (M > 64 && big >= cu_count()) return 0;
-  const int64_t mid = int64_t((M + 63) / 64) * ((Ncols + 127) / 128) * G;
-  if (mid >= cu_count()) return 1;
-  return 2;
+// Split-K GEMM (dWeight): the splits fill the machine, so only the padded
+// tile area at the tile's rate matters.
+int pick_tile_splitk(int64_t M, int64_t Ncols, bool gathers) {
+  int best = conv::SQ;
+  double best_cost = 0;
+  for (int t = 0; t < conv::NTILES; ++t) {
+    // Two scalar operands do not fit a 256-wide tile in the register budget.
+    if (gathers && (t == conv::TALL || t == conv::WIDE)) continue;
+    const TileInfo& ti = kTileInfo[t];
+    const double cost = double((M + ti.bm - 1) / ti.bm * ti.bm) * double((Ncols + ti.bn - 1) / ti.bn * ti.bn) / ti.rate;
+    if (t == (gathers ? conv::SQ : conv::TALL) || cost < best_cost) {
+      best = t;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
-template <class C>
-int launch_fwd(ConvArgs p, bool kvec, hipStream_t s) {
-  set_tiles<C>(p);
-  dim3 grid(p.tiles_m * p.tiles_n, 1, p.G);
-  if (kvec)
-    hipLaunchKernelGGL((conv_fwd_kernel<C, Mode::KVEC>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((conv_fwd_kernel<C, Mode::KSCALAR>), grid, dim3(256), 0, s, p);
-  MX_HIP(hipGetLastError());
-  return MX_OK;
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+bool unpadded_1x1(const ConvArgs& p) {
+  return p.KH == 1 && p.KW == 1 && p.sh == 1 && p.sw == 1 && p.ph == 0 && p.pw == 0;
 }
 
-template <class C>
-int launch_dx(ConvArgs p, bool unit, hipStream_t s) {
-  set_tiles<C>(p);
-  dim3 grid(p.tiles_m * p.tiles_n, 1, p.G);
-  if (unit)
-    hipLaunchKernelGGL((conv_dx_kernel<C, true>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((conv_dx_kernel<C, false>), grid, dim3(256), 0, s, p);
-  MX_HIP(hipGetLastError());
-  return MX_OK;
-}
+constexpr int kSplitBK = 16;          // K granularity of a dWeight split
+constexpr int kMinSplitSpan = 384;    // positions per split (partial-traffic bound)
 
 struct DwPlan {
-  int tile = 2;
+  int tile = conv::TALL;
   int splits = 1;
   int kps = 0;
   int64_t ws_bytes = 0;
   int64_t db_bytes = 0;
-  int64_t counters = 0;
 };
 
-template <class C>
-DwPlan plan_dw_cfg(const ConvArgs& p, int tile) {
+// dWeight plan: tile by padded area, then enough position splits to give
+// every CU its resident workgroups, keeping each split at least
+// kMinSplitSpan positions long (each split writes and the finalize re-reads
+// one full-size partial).
+DwPlan plan_dw(const ConvArgs& p, bool with_db, bool gathers) {
   DwPlan pl;
-  pl.tile = tile;
-  const int64_t tiles = int64_t((p.M + C::BM - 1) / C::BM) * ((p.Ncols + C::BN - 1) / C::BN);
-  const int64_t blocks = tiles * p.G;
-  const int64_t target = 2LL * cu_count();
-  const int64_t max_splits = std::max<int64_t>(1, (p.K + 4 * C::BK - 1) / (4 * C::BK));  // >= 4 slabs each
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(max_splits, (target + blocks - 1) / blocks));
+  pl.tile = pick_tile_splitk(p.M, p.Ncols, gathers);
+  const TileInfo& ti = kTileInfo[pl.tile];
+  const int64_t blocks = ((p.M + ti.bm - 1) / ti.bm) * ((p.Ncols + ti.bn - 1) / ti.bn) * p.G;
+  const int64_t slots = int64_t(cu_count()) * ti.per_cu;
+  const int64_t max_splits = std::max<int64_t>(1, p.K / kMinSplitSpan);
+  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(max_splits, (slots + blocks - 1) / blocks));
   splits = std::min<int64_t>(splits, 65535);
   int64_t kps = (p.K + splits - 1) / splits;
-  kps = (kps + C::BK - 1) / C::BK * C::BK;
+  kps = (kps + kSplitBK - 1) / kSplitBK * kSplitBK;
   splits = (p.K + kps - 1) / kps;
   pl.splits = int(splits);
   pl.kps = int(kps);
   if (splits > 1) {
-    pl.ws_bytes = blocks * splits * int64_t(C::BM) * C::BN * 4;
-    pl.db_bytes = int64_t(p.G) * ((p.M + C::BM - 1) / C::BM) * splits * C::BM * 4;
-    pl.counters = blocks;
+    pl.ws_bytes = splits * int64_t(p.G) * p.Cout_g * p.Ncols * 4;
+    pl.db_bytes = with_db ? splits * int64_t(p.Cout) * 4 : 0;
   }
   return pl;
 }
 
-DwPlan plan_dw(const ConvArgs& p) {
-  const int t = pick_tile(p.M, p.Ncols, p.G);
-  if (t == 0) return plan_dw_cfg<TileL>(p, 0);
-  if (t == 1) return plan_dw_cfg<TileM>(p, 1);
-  return plan_dw_cfg<TileS>(p, 2);
-}
+// dInput stride phases.  Along one axis, phase a (input index = a mod s) is
+// reached by the taps k with (a + pad - k*dil) % s == 0: k = k0 + t*step with
+// step = s / gcd(s, dil); tap t reads output index i + off0 - t*(dil / gcd).
+struct AxisPhase {
+  int len = 0;   // input positions in the phase
+  int taps = 0;
+  int k0 = 0, step = 1, off0 = 0, dstep = 0;
+};
 
-template <class C>
-int launch_dw(ConvArgs p, const DwPlan& pl, hipStream_t s) {
-  set_tiles<C>(p);
-  p.splits = pl.splits;
-  p.kps = pl.kps;
-  Scratch ws, wsdb;
-  if (pl.splits > 1) {
-    MX_TRY(ws.alloc(size_t(pl.ws_bytes), s));
-    p.ws = ws.as<float>();
-    if (p.db) {
-      MX_TRY(wsdb.alloc(size_t(pl.db_bytes), s));
-      p.ws_db = wsdb.as<float>();
+AxisPhase axis_phase(int a, int in, int k, int s, int pad, int dil) {
+  AxisPhase ph;
+  ph.len = a < in ? (in - a + s - 1) / s : 0;
+  const int gcd = std::gcd(s, dil);
+  ph.step = s / gcd;
+  ph.dstep = dil / gcd;
+  int k0 = -1;
+  for (int kk = 0; kk < std::min(k, ph.step); ++kk)
+    if (((a + pad - kk * dil) % s + s) % s == 0) {
+      k0 = kk;
+      break;
     }
-    MX_TRY(tile_counters(s, size_t(pl.counters), &p.counters));
-  }
-  dim3 grid(p.tiles_m * p.tiles_n, pl.splits, p.G);
-  hipLaunchKernelGGL((conv_dw_kernel<C>), grid, dim3(256), 0, s, p);
-  MX_HIP(hipGetLastError());
-  return MX_OK;
+  if (k0 < 0) return ph;
+  ph.k0 = k0;
+  ph.taps = (k - 1 - k0) / ph.step + 1;
+  ph.off0 = (a + pad - k0 * dil) / s;  // exact division
+  return ph;
 }
 
 }  // namespace
@@ -946,12 +465,9 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
   p.M = p.Cout_g;
   p.Ncols = p.N * p.OHOW;
   p.K = p.Cin_g * p.KK;
-  const bool kvec = (p.K % 4 == 0) && ((reinterpret_cast<uintptr_t>(w) & 15u) == 0);
-  switch (pick_tile(p.M, p.Ncols, p.G)) {
-    case 0: return launch_fwd<TileL>(p, kvec, s);
-    case 1: return launch_fwd<TileM>(p, kvec, s);
-    default: return launch_fwd<TileS>(p, kvec, s);
-  }
+  const Mode ma = (p.K % 4 == 0 && aligned16(w)) ? Mode::KVEC : Mode::KSCALAR;
+  const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
+  return conv::conv_fwd_launch(p, pick_tile(p.M, p.Ncols, p.G), ma, bmode, s);
   MX_ABI_END
 }
 
@@ -973,15 +489,47 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
     MX_HIP(hipGetLastError());
     return MX_OK;
   }
-  p.M = p.Cin_g;
-  p.Ncols = p.N * p.HW;
-  p.K = p.Cout_g * p.KK;
-  const bool unit = p.sh == 1 && p.sw == 1;
-  switch (pick_tile(p.M, p.Ncols, p.G)) {
-    case 0: return launch_dx<TileL>(p, unit, s);
-    case 1: return launch_dx<TileM>(p, unit, s);
-    default: return launch_dx<TileS>(p, unit, s);
+  // One GEMM per stride phase over exactly the taps that reach it.
+  const bool vec_a = p.Cin_g % 4 == 0;
+  Scratch wt;
+  MX_TRY(wt.alloc(size_t(p.Cout) * p.Cin_g * p.KK * 4, s));
+  p.wt = wt.as<float>();
+  for (int a = 0; a < p.sh; ++a) {
+    const AxisPhase ah = axis_phase(a, p.H, p.KH, p.sh, p.ph, p.dh);
+    for (int b = 0; b < p.sw; ++b) {
+      const AxisPhase aw = axis_phase(b, p.W, p.KW, p.sw, p.pw, p.dw);
+      if (ah.len == 0 || aw.len == 0) continue;
+      ConvArgs q = p;
+      q.pa = a;
+      q.pb = b;
+      q.Hp = ah.len;
+      q.Wp = aw.len;
+      q.HpWp = ah.len * aw.len;
+      q.nth = ah.taps;
+      q.ntw = aw.taps;
+      q.offh0 = ah.off0;
+      q.offw0 = aw.off0;
+      q.dsh = ah.dstep;
+      q.dsw = aw.dstep;
+      q.kh0 = ah.k0;
+      q.kw0 = aw.k0;
+      q.stph = ah.step;
+      q.stpw = aw.step;
+      if (ah.taps == 0 || aw.taps == 0) {
+        MX_TRY(conv::conv_dx_zero_phase(q, s));
+        continue;
+      }
+      q.M = p.Cin_g;
+      q.Ncols = p.N * q.HpWp;
+      q.K = p.Cout_g * q.nth * q.ntw;
+      MX_TRY(conv::conv_dx_pack_weights(q, wt.as<float>(), s));
+      const bool one_to_one = q.nth == 1 && q.ntw == 1 && q.offh0 == 0 && q.offw0 == 0 && q.Hp == p.OH &&
+                              q.Wp == p.OW && p.OHOW % 4 == 0 && aligned16(dy);
+      MX_TRY(conv::conv_dx_launch(q, pick_tile(q.M, q.Ncols, p.G), vec_a ? Mode::RVEC : Mode::RSCALAR,
+                                  one_to_one ? conv::B_VEC : conv::B_GATHER, s));
+    }
   }
+  return MX_OK;
   MX_ABI_END
 }
 
@@ -1036,12 +584,21 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
   p.M = p.Cout_g;
   p.Ncols = p.Cin_g * p.KK;
   p.K = p.N * p.OHOW;
-  const DwPlan pl = plan_dw(p);
-  switch (pl.tile) {
-    case 0: return launch_dw<TileL>(p, pl, s);
-    case 1: return launch_dw<TileM>(p, pl, s);
-    default: return launch_dw<TileS>(p, pl, s);
+  const int amode = (p.OHOW % 4 == 0 && aligned16(dy)) ? conv::B_VEC : conv::B_GATHER;
+  const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
+  const DwPlan pl = plan_dw(p, db != nullptr, amode == conv::B_GATHER && bmode == conv::B_GATHER);
+  p.splits = pl.splits;
+  p.kps = pl.kps;
+  if (pl.splits == 1) return conv::conv_dw_launch(p, pl.tile, amode, bmode, s);
+  Scratch ws, wsdb;
+  MX_TRY(ws.alloc(size_t(pl.ws_bytes), s));
+  p.ws = ws.as<float>();
+  if (db) {
+    MX_TRY(wsdb.alloc(size_t(pl.db_bytes), s));
+    p.ws_db = wsdb.as<float>();
   }
+  MX_TRY(conv::conv_dw_launch(p, pl.tile, amode, bmode, s));
+  return conv::conv_dw_finalize(p, dw, db, s);
   MX_ABI_END
 }
 
@@ -1052,7 +609,6 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
   int chosen = 0;
   MX_TRY(select_algo(d, phase, algo, &chosen));
   ConvArgs p = make_args(d);
-  static const char* tiles[] = {"128x128x16", "64x128x16", "64x64x16"};
   std::string name;
   if (phase == MX_CONV_DBIAS) {
     name = chosen == MX_CONV_ALGO_DIRECT ? "conv_db_direct_kernel" : "conv_db_reduce_kernel";
@@ -1064,14 +620,17 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
   } else if (chosen == MX_CONV_ALGO_REDUCE) {
     name = "conv_dw_reduce_kernel";
   } else if (phase == MX_CONV_FORWARD) {
-    name = cat("conv_fwd_kernel<", tiles[pick_tile(p.Cout_g, p.N * p.OHOW, p.G)], ">");
+    name = cat("conv_fwd_kernel<", kTileInfo[pick_tile(p.Cout_g, p.N * p.OHOW, p.G)].name, ">");
   } else if (phase == MX_CONV_DINPUT) {
-    name = cat("conv_dx_kernel<", tiles[pick_tile(p.Cin_g, p.N * p.HW, p.G)], ">");
+    // Tile of the stride phase (0, 0), the largest one.
+    const AxisPhase ah = axis_phase(0, p.H, p.KH, p.sh, p.ph, p.dh), aw = axis_phase(0, p.W, p.KW, p.sw, p.pw, p.dw);
+    name = cat("conv_dx_kernel<", kTileInfo[pick_tile(p.Cin_g, int64_t(p.N) * ah.len * aw.len, p.G)].name, ">");
   } else {
     p.M = p.Cout_g;
     p.Ncols = p.Cin_g * p.KK;
     p.K = p.N * p.OHOW;
-    name = cat("conv_dw_kernel<", tiles[plan_dw(p).tile], ">");
+    const bool gathers = p.OHOW % 4 != 0 && !(unpadded_1x1(p) && p.HW % 4 == 0);
+    name = cat("conv_dw_kernel<", kTileInfo[plan_dw(p, true, gathers).tile].name, ">");
   }
   if (len) {
     std::strncpy(buf, name.c_str(), len - 1);
@@ -1089,7 +648,8 @@ int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t*
   p.M = p.Cout_g;
   p.Ncols = p.Cin_g * p.KK;
   p.K = p.N * p.OHOW;
-  const DwPlan pl = plan_dw(p);
+  const bool gathers = p.OHOW % 4 != 0 && !(unpadded_1x1(p) && p.HW % 4 == 0);
+  const DwPlan pl = plan_dw(p, true, gathers);
   if (splits) *splits = pl.splits;
   if (span) *span = pl.kps;
   if (workspace_bytes) *workspace_bytes = pl.ws_bytes + pl.db_bytes;

@@ -1,0 +1,135 @@
+// Conv2D dWeight (+ fused dBias) as a split-K implicit GEMM on FP32 MFMA (gfx950).
+//
+// Reference behaviour followed: conv2d_backward_weight_tiled_body.glsl:1-71
+// (dW[co, (ci,kh,kw)] = sum over positions of dy[co, pos] * im2col(x)[pos, (ci,kh,kw)]),
+// conv2d_backward_weight_finalize.comp:9-18 (partials over position splits
+// summed in split order) and csrc/ops/convolution.cpp:204-238 (split plan).
+//
+// K = N*OH*OW is split over blockIdx.y.  With one split the tile is stored
+// directly; otherwise every split writes a full-size partial dW (and the
+// column-0 tiles a partial dBias, from row sums of the dy operand they already
+// stream) and conv_dw_finalize_kernel sums the partials in fixed split order,
+// so the result is deterministic for a given plan.
+#include <type_traits>
+
+#include "mx_conv_common.hpp"
+
+namespace mx {
+namespace conv {
+namespace {
+
+// Sum of `v` over the W consecutive lanes that share a row (fixed butterfly).
+template <int W>
+__device__ __forceinline__ float row_lane_sum(float v) {
+#pragma unroll
+  for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, W);
+  return v;
+}
+
+template <class C, class LA, class LB>
+MX_TILE_KERNEL(C) void conv_dw_kernel(ConvArgs p) {
+  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
+  const int g = blockIdx.z, split = blockIdx.y;
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
+  const int row0 = tm * C::BM, col0 = tn * C::BN;
+  const int k_begin = split * p.kps;
+  const int k_end = min(p.K, k_begin + p.kps);
+  LA la;
+  la.init(p, row0, g, k_begin, k_end);
+  LB lb;
+  lb.init(p, col0, g, k_begin, k_end);
+  Acc<C> acc;
+  mainloop<C>(acc, la, lb, (k_end - k_begin + C::BK - 1) / C::BK, smem);
+
+  const int64_t dw_elems = int64_t(p.G) * p.Cout_g * p.Ncols;
+  float* dst = (p.splits == 1 ? p.out : p.ws + split * dw_elems) + int64_t(g) * p.Cout_g * p.Ncols;
+  for_each_acc<C>(acc, [&](int r, int c, float v) {
+    const int co = row0 + r, n = col0 + c;
+    if (co < p.M && n < p.Ncols) dst[int64_t(co) * p.Ncols + n] = v;
+  });
+  if (p.db != nullptr && tn == 0) {
+    float* dbd = (p.splits == 1 ? p.db : p.ws_db + int64_t(split) * p.Cout) + g * p.Cout_g;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int q = 0; q < LA::PASSES; ++q) {
+      const float s = row_lane_sum<LA::LPR>(la.bsum[q]);
+      const int co = row0 + tid / LA::LPR + q * LA::RPP;
+      if (tid % LA::LPR == 0 && co < p.M) dbd[co] = s;
+    }
+  }
+}
+
+// dw[i] = sum over splits (in order) of ws[split][i]; same for db.
+__global__ void conv_dw_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ ws_db,
+                                        float* __restrict__ dw, float* __restrict__ db, int64_t n_dw, int n_db,
+                                        int splits) {
+  const int64_t total = n_dw + n_db;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    float s = 0.f;
+    if (idx < n_dw) {
+#pragma unroll 8
+      for (int sp = 0; sp < splits; ++sp) s += ws[sp * n_dw + idx];
+      dw[idx] = s;
+    } else {
+      const int64_t j = idx - n_dw;
+#pragma unroll 8
+      for (int sp = 0; sp < splits; ++sp) s += ws_db[sp * int64_t(n_db) + j];
+      db[j] = s;
+    }
+  }
+}
+
+template <class C, class LA>
+int launch_b(ConvArgs p, int bmode, hipStream_t s) {
+  p.tiles_m = (p.M + C::BM - 1) / C::BM;
+  p.tiles_n = (p.Ncols + C::BN - 1) / C::BN;
+  const dim3 grid(p.tiles_m * p.tiles_n, p.splits, p.G);
+  if (bmode == B_VEC) {
+    hipLaunchKernelGGL((conv_dw_kernel<C, LA, PosKLoader<C::BN, C::BK, false>>), grid, dim3(kThreads), 0, s, p);
+  } else {
+    // Two scalar gathers do not fit a 256-wide tile in registers; the planner
+    // never pairs them.
+    constexpr bool fits = LA::KMAJOR || C::BM * C::BN <= 128 * 128 || !std::is_same_v<LA, DyRowsLoader<C::BM, C::BK>>;
+    if constexpr (fits)
+      hipLaunchKernelGGL((conv_dw_kernel<C, LA, XColsLoader<C::BN, C::BK>>), grid, dim3(kThreads), 0, s, p);
+    else
+      return set_error(MX_ERR_INVALID, "conv2d dweight: tile too large for two gathered operands");
+  }
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+template <class C>
+int launch_a(const ConvArgs& p, int amode, int bmode, hipStream_t s) {
+  if (amode == B_VEC) return launch_b<C, PosKLoader<C::BM, C::BK, true>>(p, bmode, s);
+  return launch_b<C, DyRowsLoader<C::BM, C::BK>>(p, bmode, s);
+}
+
+}  // namespace
+
+int conv_dw_launch(const ConvArgs& p, int tile, int amode, int bmode, hipStream_t s) {
+  switch (tile) {
+    case TALL: return launch_a<TileTall>(p, amode, bmode, s);
+    case WIDE: return launch_a<TileWide>(p, amode, bmode, s);
+    case SQ: return launch_a<TileSq>(p, amode, bmode, s);
+    case FLAT: return launch_a<TileFlat>(p, amode, bmode, s);
+    case NARROW: return launch_a<TileNarrow>(p, amode, bmode, s);
+    default: return launch_a<TileSmall>(p, amode, bmode, s);
+  }
+}
+
+int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s) {
+  const int64_t n_dw = int64_t(p.G) * p.Cout_g * p.Ncols;
+  const int n_db = db ? p.Cout : 0;
+  const int64_t total = n_dw + n_db;
+  const int blocks = int(std::min<int64_t>((total + 255) / 256, 1 << 20));
+  hipLaunchKernelGGL(conv_dw_finalize_kernel, dim3(blocks), dim3(256), 0, s, p.ws, p.ws_db, dw, db, n_dw, n_db,
+                     p.splits);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+}  // namespace conv
+}  // namespace mx

@@ -1,0 +1,120 @@
+// Conv2D dInput as one implicit GEMM per stride phase on FP32 MFMA (gfx950).
+//
+// Reference behaviour followed: csrc/shaders/conv2d_backward_input_tiled_body.glsl:1-95
+// (dInput implicit GEMM: dx[ci, ipos] = sum over (co, kh, kw) of
+// w[co][ci][kh][kw] * dy[co][(ih + ph - kh*dh)/sh][(iw + pw - kw*dw)/sw] where
+// the division is exact) and csrc/ops/convolution.cpp:684-687.
+//
+// For stride s > 1 only the taps with (ih + ph - kh*dh) % sh == 0 contribute,
+// and which taps those are depends only on ih % sh.  The input positions are
+// therefore split into sh*sw phases (ih % sh, iw % sw); each phase is a dense
+// GEMM over exactly its taps (th, tw), so no zero-inserted term is ever
+// multiplied.  Phases no tap reaches are zero-filled.  Weights are first
+// packed per phase as Wt_p[g][co][th][tw][ci] so the A operand has ci
+// contiguous and loads 16 bytes per lane.
+#include "mx_conv_common.hpp"
+
+namespace mx {
+namespace conv {
+namespace {
+
+// Wt_p[g][co][th][tw][ci] = w[g*Cout_g + co][ci][kh0 + th*stph][kw0 + tw*stpw].
+__global__ void conv_dx_pack_kernel(ConvArgs p, float* wt) {
+  const int64_t total = int64_t(p.G) * p.Cout_g * p.nth * p.ntw * p.Cin_g;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int ci = int(idx % p.Cin_g);
+    int64_t rest = idx / p.Cin_g;
+    const int tw = int(rest % p.ntw);
+    rest /= p.ntw;
+    const int th = int(rest % p.nth);
+    const int oc = int(rest / p.nth);  // g * Cout_g + co
+    const int kh = p.kh0 + th * p.stph, kw = p.kw0 + tw * p.stpw;
+    wt[idx] = p.w[((int64_t(oc) * p.Cin_g + ci) * p.KH + kh) * p.KW + kw];
+  }
+}
+
+// dx = 0 at the input positions of a phase that no tap reaches.
+__global__ void conv_dx_zero_kernel(ConvArgs p) {
+  const int64_t total = int64_t(p.N) * p.Cin * p.HpWp;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int q = int(idx % p.HpWp);
+    const int64_t plane = idx / p.HpWp;  // img * Cin + c
+    const int i = q / p.Wp, j = q - (q / p.Wp) * p.Wp;
+    p.out[plane * p.HW + int64_t(p.pa + p.sh * i) * p.W + p.pb + p.sw * j] = 0.f;
+  }
+}
+
+template <class C, Mode MA, class LB>
+MX_TILE_KERNEL(C) void conv_dx_kernel(ConvArgs p) {
+  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
+  const int g = blockIdx.z;
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
+  const int row0 = tm * C::BM, col0 = tn * C::BN;
+  StridedLoader<C::BM, C::BK, MA> la;  // element (ci, k) = wt[g][k][ci]
+  la.init(p.wt + int64_t(g) * p.K * p.Cin_g, 1, p.Cin_g, row0, p.M, 0, p.K);
+  LB lb;
+  lb.init(p, col0, g);
+  Acc<C> acc;
+  mainloop<C>(acc, la, lb, (p.K + C::BK - 1) / C::BK, smem);
+  for_each_acc<C>(acc, [&](int r, int c, float v) {
+    const int ci = row0 + r, pos = col0 + c;
+    if (ci < p.M && pos < p.Ncols) {
+      const int img = pos / p.HpWp;
+      const int q = pos - img * p.HpWp;
+      const int i = q / p.Wp, j = q - (q / p.Wp) * p.Wp;
+      p.out[(int64_t(img) * p.Cin + g * p.Cin_g + ci) * p.HW + (p.pa + p.sh * i) * p.W + p.pb + p.sw * j] = v;
+    }
+  });
+}
+
+template <class C, Mode MA>
+int launch_b(ConvArgs p, int bmode, hipStream_t s) {
+  p.tiles_m = (p.M + C::BM - 1) / C::BM;
+  p.tiles_n = (p.Ncols + C::BN - 1) / C::BN;
+  const dim3 grid(p.tiles_m * p.tiles_n, 1, p.G);
+  if (bmode == B_VEC)
+    hipLaunchKernelGGL((conv_dx_kernel<C, MA, PosQuadLoader<C::BN, C::BK, true>>), grid, dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((conv_dx_kernel<C, MA, PhaseGatherLoader<C::BN, C::BK>>), grid, dim3(kThreads), 0, s, p);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+template <class C>
+int launch_a(const ConvArgs& p, Mode ma, int bmode, hipStream_t s) {
+  if (ma == Mode::RVEC) return launch_b<C, Mode::RVEC>(p, bmode, s);
+  return launch_b<C, Mode::RSCALAR>(p, bmode, s);
+}
+
+int grid_for(int64_t total) { return int(std::min<int64_t>((total + 255) / 256, 1 << 20)); }
+
+}  // namespace
+
+int conv_dx_pack_weights(const ConvArgs& p, float* wt, hipStream_t s) {
+  const int64_t total = int64_t(p.G) * p.Cout_g * p.nth * p.ntw * p.Cin_g;
+  hipLaunchKernelGGL(conv_dx_pack_kernel, dim3(grid_for(total)), dim3(256), 0, s, p, wt);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+int conv_dx_zero_phase(const ConvArgs& p, hipStream_t s) {
+  hipLaunchKernelGGL(conv_dx_zero_kernel, dim3(grid_for(int64_t(p.N) * p.Cin * p.HpWp)), dim3(256), 0, s, p);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+int conv_dx_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t s) {
+  switch (tile) {
+    case TALL: return launch_a<TileTall>(p, ma, bmode, s);
+    case WIDE: return launch_a<TileWide>(p, ma, bmode, s);
+    case SQ: return launch_a<TileSq>(p, ma, bmode, s);
+    case FLAT: return launch_a<TileFlat>(p, ma, bmode, s);
+    default: return launch_a<TileSmall>(p, ma, bmode, s);
+  }
+}
+
+}  // namespace conv
+}  // namespace mx

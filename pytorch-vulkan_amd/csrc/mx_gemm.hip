@@ -28,40 +28,50 @@ struct GemmArgs {
   int64_t b_sb, b_sk, b_sn;
   int64_t c_sb, ldc;
   int64_t bias_sm, bias_sn;
-  int M, N, K, batch;
+  int M, N, K, batch, batch0;
   int tiles_m, tiles_n;
   float alpha, beta;
   int bias_kind;
 };
 
 template <class C, Mode MA, Mode MB>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
+MX_TILE_KERNEL(C) void gemm_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
-  const int ntiles = p.tiles_m * p.tiles_n;
   int tm, tn;
-  tile_coords(xcd_remap(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, tm, tn);
+  tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
   const int row0 = tm * C::BM, col0 = tn * C::BN;
-  const int nk = (p.K + C::BK - 1) / C::BK;
-  for (int bz = blockIdx.z; bz < p.batch; bz += gridDim.z) {
-    StridedLoader<C::BM, C::BK, MA> la;
-    StridedLoader<C::BN, C::BK, MB> lb;
-    la.init(p.a + int64_t(bz) * p.a_sb, p.a_sm, p.a_sk, row0, p.M, 0, p.K);
-    lb.init(p.b + int64_t(bz) * p.b_sb, p.b_sn, p.b_sk, col0, p.N, 0, p.K);
-    Acc<C> acc;
-    mainloop<C>(acc, la, lb, nk, smem);
-    float* cb = p.c + int64_t(bz) * p.c_sb;
-    const bool use_bias = p.bias_kind != MX_BIAS_NONE && p.beta != 0.f;
+  const int64_t bz = int64_t(p.batch0) + blockIdx.z;
+  StridedLoader<C::BM, C::BK, MA> la;
+  StridedLoader<C::BN, C::BK, MB> lb;
+  la.init(p.a + bz * p.a_sb, p.a_sm, p.a_sk, row0, p.M, 0, p.K);
+  lb.init(p.b + bz * p.b_sb, p.b_sn, p.b_sk, col0, p.N, 0, p.K);
+  Acc<C> acc;
+  mainloop<C>(acc, la, lb, (p.K + C::BK - 1) / C::BK, smem);
+  float* __restrict__ cb = p.c + bz * p.c_sb;
+  const float alpha = p.alpha, beta = p.beta;
+  if (p.bias_kind == MX_BIAS_NONE || beta == 0.f) {
     for_each_acc<C>(acc, [&](int r, int c, float v) {
       const int row = row0 + r, col = col0 + c;
-      if (row < p.M && col < p.N) {
-        float out = p.alpha * v;
-        if (use_bias) {
-          const float bv = p.bias_kind == MX_BIAS_COL ? p.bias[int64_t(col) * p.bias_sn]
-                                                      : p.bias[int64_t(row) * p.bias_sm + int64_t(col) * p.bias_sn];
-          out += p.beta * bv;
-        }
-        cb[int64_t(row) * p.ldc + col] = out;
-      }
+      if (row < p.M && col < p.N) cb[int64_t(row) * p.ldc + col] = alpha * v;
+    });
+  } else if (p.bias_kind == MX_BIAS_COL) {
+    // One bias value per fragment column, loaded once.
+    float bcol[C::FN];
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      const int col = col0 + acc_col<C>(j);
+      bcol[j] = col < p.N ? beta * p.bias[int64_t(col) * p.bias_sn] : 0.f;
+    }
+    for_each_acc_j<C>(acc, [&](int r, int c, int j, float v) {
+      const int row = row0 + r, col = col0 + c;
+      if (row < p.M && col < p.N) cb[int64_t(row) * p.ldc + col] = alpha * v + bcol[j];
+    });
+  } else {
+    const float* __restrict__ bias = p.bias;
+    for_each_acc<C>(acc, [&](int r, int c, float v) {
+      const int row = row0 + r, col = col0 + c;
+      if (row < p.M && col < p.N)
+        cb[int64_t(row) * p.ldc + col] = alpha * v + beta * bias[int64_t(row) * p.bias_sm + int64_t(col) * p.bias_sn];
     });
   }
 }
@@ -99,11 +109,14 @@ Mode pick_mode(const float* base, int64_t s_row, int64_t s_k, int64_t s_batch, i
 }
 
 template <class C, Mode MA, Mode MB>
-int launch3(const GemmArgs& p, hipStream_t s) {
+int launch3(GemmArgs p, hipStream_t s) {
   const int ntiles = p.tiles_m * p.tiles_n;
-  dim3 grid(ntiles, 1, std::min(p.batch, 65535));
-  hipLaunchKernelGGL((gemm_kernel<C, MA, MB>), grid, dim3(256), 0, s, p);
-  MX_HIP(hipGetLastError());
+  for (int b0 = 0; b0 < p.batch; b0 += 65535) {
+    p.batch0 = b0;
+    const dim3 grid(ntiles, 1, std::min(p.batch - b0, 65535));
+    hipLaunchKernelGGL((gemm_kernel<C, MA, MB>), grid, dim3(kThreads), 0, s, p);
+    MX_HIP(hipGetLastError());
+  }
   return MX_OK;
 }
 
@@ -129,8 +142,49 @@ int launch1(GemmArgs p, Mode ma, Mode mb, hipStream_t s) {
   }
 }
 
-using BigTile = Cfg<128, 128, 16, 2>;
-using SmallTile = Cfg<64, 64, 16, 2>;
+// 256-row tiles are built for the 16-byte operand modes only (scalar modes
+// would need a register per row pass).
+template <class C>
+int launch1_vec(GemmArgs p, Mode ma, Mode mb, hipStream_t s) {
+  p.tiles_m = (p.M + C::BM - 1) / C::BM;
+  p.tiles_n = (p.N + C::BN - 1) / C::BN;
+  if (ma == Mode::KVEC)
+    return mb == Mode::KVEC ? launch3<C, Mode::KVEC, Mode::KVEC>(p, s) : launch3<C, Mode::KVEC, Mode::RVEC>(p, s);
+  return mb == Mode::KVEC ? launch3<C, Mode::RVEC, Mode::KVEC>(p, s) : launch3<C, Mode::RVEC, Mode::RVEC>(p, s);
+}
+
+bool is_vec(Mode m) { return m == Mode::KVEC || m == Mode::RVEC; }
+
+// Tile menu (BM x BN x BK, wave grid, waves per SIMD).  All keep two or more
+// workgroups resident per CU.
+using TileTall = Cfg<256, 128, 16, 2, 2>;  // 4 waves of 128 x 64
+using TileWide = Cfg<128, 256, 16, 2, 2>;  // 4 waves of 64 x 128
+using TileSq = Cfg<128, 128, 16, 2, 2>;    // 4 waves of 64 x 64
+using TileSmall = Cfg<64, 64, 16, 2, 4>;   // 4 waves of 32 x 32
+
+struct TileChoice {
+  int bm, bn, per_cu;
+  double rate;  // throughput of a CU full of such tiles, relative to 256 x 128
+};
+constexpr TileChoice kTiles[] = {{256, 128, 2, 1.0}, {128, 256, 2, 1.0}, {128, 128, 2, 0.94}, {64, 64, 4, 0.6}};
+
+// Cheapest tile by a wave-quantised cost model: rounds of resident tiles
+// times the time of one round (per_cu tiles per CU at the relative rate).
+int pick_gemm_tile(int64_t m, int64_t n, int64_t batch, bool vec) {
+  int best = 2;
+  double best_cost = 0;
+  for (int i = vec ? 0 : 2; i < 4; ++i) {
+    const TileChoice& t = kTiles[i];
+    const int64_t tiles = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn) * batch;
+    const int64_t slots = int64_t(cu_count()) * t.per_cu;
+    const double cost = double((tiles + slots - 1) / slots) * t.per_cu * t.bm * t.bn / t.rate;
+    if (i == (vec ? 0 : 2) || cost < best_cost) {
+      best = i;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
 
 }  // namespace
 }  // namespace mx
@@ -183,9 +237,12 @@ extern "C" int mx_gemm_f32(const mx_gemm_desc* d, const float* a, const float* b
   MX_REQUIRE(a && b, MX_ERR_INVALID, "mx_gemm_f32: null operand");
   const Mode ma = pick_mode(p.a, p.a_sm, p.a_sk, p.a_sb, p.batch, p.M, p.K);
   const Mode mb = pick_mode(p.b, p.b_sn, p.b_sk, p.b_sb, p.batch, p.N, p.K);
-  const int64_t big_tiles = ((d->m + 127) / 128) * ((d->n + 127) / 128) * d->batch;
   MX_REQUIRE(((d->m + 63) / 64) * ((d->n + 63) / 64) <= INT32_MAX, MX_ERR_INVALID, "mx_gemm_f32: too many tiles");
-  if (big_tiles >= cu_count()) return launch1<BigTile>(p, ma, mb, s);
-  return launch1<SmallTile>(p, ma, mb, s);
+  switch (pick_gemm_tile(d->m, d->n, d->batch, is_vec(ma) && is_vec(mb))) {
+    case 0: return launch1_vec<TileTall>(p, ma, mb, s);
+    case 1: return launch1_vec<TileWide>(p, ma, mb, s);
+    case 2: return launch1<TileSq>(p, ma, mb, s);
+    default: return launch1<TileSmall>(p, ma, mb, s);
+  }
   MX_ABI_END
 }

@@ -50,11 +50,6 @@ struct Scratch {
   }
 };
 
-// Zero-initialised uint32 counters for the split-K "last block reduces"
-// protocol.  Kernels return every counter they touch to zero, so the buffer
-// stays zeroed between launches on the same stream.
-int tile_counters(hipStream_t s, size_t count, unsigned** out);
-
 // Copies a small host table to device memory through a pinned ring buffer.
 // The returned device pointer is valid for work enqueued on `s` after this
 // call (the block is returned to the stream-ordered cache by `holder`).

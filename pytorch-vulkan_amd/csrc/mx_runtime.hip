@@ -453,41 +453,6 @@ int mx_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream) 
 
 namespace mx {
 
-// ----------------------------------------------------------- split-K counters
-static std::mutex g_counter_mu;
-struct CounterBuf {
-  unsigned* ptr = nullptr;
-  size_t count = 0;
-};
-static std::map<hipStream_t, CounterBuf> g_counters;
-
-__global__ void zero_u32_kernel(unsigned* p, size_t n) {
-  size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
-int tile_counters(hipStream_t s, size_t count, unsigned** out) {
-  std::lock_guard<std::mutex> lock(g_counter_mu);
-  auto& cb = g_counters[s];
-  if (cb.count < count) {
-    if (cb.ptr) mx_free(cb.ptr);
-    cb.ptr = nullptr;
-    cb.count = 0;
-    size_t n = std::max<size_t>(count, 4096);
-    void* p = nullptr;
-    MX_TRY(mx_malloc(&p, n * sizeof(unsigned), s));
-    // Cleared with a kernel (not hipMemsetAsync) so the sequence is
-    // graph-capture friendly.
-    hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                       static_cast<unsigned*>(p), n);
-    MX_HIP(hipGetLastError());
-    cb.ptr = static_cast<unsigned*>(p);
-    cb.count = n;
-  }
-  *out = cb.ptr;
-  return MX_OK;
-}
-
 // ----------------------------------------------------------- pinned upload ring
 namespace {
 constexpr size_t kRingBytes = size_t(8) << 20;

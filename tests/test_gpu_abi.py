@@ -122,6 +122,19 @@ CONV_CASES = [
     ((1, 9, 1, 257), 17, (1, 1), (1, 1), (0, 0), (1, 1), 1),
     ((2, 3, 32, 32), 16, (7, 7), (2, 2), (3, 3), (1, 1), 1),
     ((2, 128, 14, 14), 256, (1, 1), (2, 2), (0, 0), (1, 1), 1),
+    # 16-byte operand paths: unpadded 1x1 stride 1 with H*W % 4 == 0
+    ((3, 64, 12, 12), 128, (1, 1), (1, 1), (0, 0), (1, 1), 1),
+    ((2, 32, 8, 6), 48, (1, 1), (1, 1), (0, 0), (1, 1), 2),
+    ((4, 64, 28, 28), 64, (1, 1), (1, 1), (0, 0), (1, 1), 1),
+    ((2, 256, 14, 14), 512, (1, 1), (1, 1), (0, 0), (1, 1), 1),
+    # H*W % 4 != 0 and Cin % 4 != 0: scalar operand paths
+    ((2, 6, 7, 7), 10, (1, 1), (1, 1), (0, 0), (1, 1), 1),
+    # dInput stride phases: zero phases, one-to-one phase, 1/2-tap phases,
+    # stride 3 with dilation 2, stride 2 with dilation 2
+    ((2, 64, 16, 16), 128, (1, 1), (2, 2), (0, 0), (1, 1), 1),
+    ((2, 64, 16, 16), 64, (3, 3), (2, 2), (1, 1), (1, 1), 1),
+    ((1, 8, 20, 20), 8, (5, 5), (3, 3), (2, 2), (2, 2), 1),
+    ((1, 8, 15, 15), 8, (3, 3), (2, 2), (2, 2), (2, 2), 1),
 ]
 
 
@@ -152,6 +165,36 @@ def test_conv_all_phases(mx, case, algo):
     mx.conv2d_forward(d, X, W, B, y, A, stream())
     mx.conv2d_backward_input(d, DY, W, dx, A, stream())
     mx.conv2d_backward_weight(d, X, DY, dw, dbias, A if A != mx.ALGO_DIRECT else mx.ALGO_DIRECT, stream())
+    for name, got in (("y", y), ("dx", dx), ("dw", dw), ("db", dbias)):
+        ref, mag = refs[name]
+        close(got, ref, mag=mag, what=name)
+
+
+@pytest.mark.parametrize("case", [((3, 64, 12, 12), 128, (1, 1), (1, 1), (0, 0), (1, 1), 1),
+                                  ((2, 64, 16, 16), 64, (3, 3), (2, 2), (1, 1), (1, 1), 1)])
+def test_conv_unaligned_views(mx, case):
+    """Operands at a 4-byte offset from 16-byte alignment take the scalar paths."""
+    xs, cout, kernel, stride, padding, dilation, groups = case
+    x, w, b = conv_inputs(xs, cout, kernel, groups, seed=11)
+    d = mx.conv_desc(xs, w.shape, stride, padding, dilation, groups)
+    dy = torch.randn((xs[0], cout, d.oh, d.ow), generator=torch.Generator().manual_seed(6))
+    refs = conv_refs(x, w, b, dy, stride, padding, dilation, groups)
+
+    def shifted(t):
+        buf = torch.empty(t.numel() + 1, device="cuda")
+        buf[1:] = t.reshape(-1).to("cuda")
+        return buf[1:].view(t.shape)
+
+    X, W, DY = shifted(x), shifted(w), shifted(dy)
+    assert X.data_ptr() % 16 != 0
+    y = torch.empty(dy.shape, device="cuda")
+    dx = torch.empty(xs, device="cuda")
+    dw = torch.empty(w.shape, device="cuda")
+    dbias = torch.empty(cout, device="cuda")
+    A = mx.ALGO_IMPLICIT_GEMM
+    mx.conv2d_forward(d, X, W, dev(b), y, A, stream())
+    mx.conv2d_backward_input(d, DY, W, dx, A, stream())
+    mx.conv2d_backward_weight(d, X, DY, dw, dbias, A, stream())
     for name, got in (("y", y), ("dx", dx), ("dw", dw), ("db", dbias)):
         ref, mag = refs[name]
         close(got, ref, mag=mag, what=name)
