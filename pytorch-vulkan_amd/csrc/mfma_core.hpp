@@ -113,11 +113,27 @@ __device__ __forceinline__ void mma_slab(Acc<C>& acc, const float* As, const flo
         acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc.v[i][j], 0, 0, 0);
 }
 
-// Double-buffered main loop over nk slabs.  Loaders expose load() (global ->
-// registers for the next slab, advancing their k cursor), store(lds) and
-// KMAJOR (the LDS layout store() writes).
+// Loaders that keep per-thread row sums (dBias) add those of a second copy.
+template <class L>
+__device__ __forceinline__ auto merge_row_sums(L& a, const L& b, int) -> decltype(a.bsum[0], void()) {
+#pragma unroll
+  for (int q = 0; q < int(sizeof(a.bsum) / sizeof(a.bsum[0])); ++q) a.bsum[q] += b.bsum[q];
+}
+template <class L>
+__device__ __forceinline__ void merge_row_sums(L&, const L&, long) {}
+
+// Main loop over nk slabs.  Loaders expose load() (global -> registers,
+// advancing their k cursor by kstep), store(lds) and KMAJOR (the LDS layout
+// store() writes).  Two LDS stages.
+//
+// Tiles up to 128 x 128 keep two register sets per operand: set 0 carries the
+// even slabs and set 1 the odd ones (each cursor steps two slabs), so the
+// global loads of slab t + 2 are in flight while slab t is multiplied and
+// slab t + 1 is written to LDS -- two slabs of MFMA time cover the load
+// latency.  Larger tiles have the registers for one set only; their longer
+// slabs (4096 MFMA cycles per wave) cover one slab of latency.
 template <class C, class LA, class LB>
-__device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la, LB& lb, int nk, float* smem) {
+__device__ __forceinline__ void mainloop_1deep(Acc<C>& acc, LA& la, LB& lb, int nk, float* smem) {
   float* As = smem;
   float* Bs = smem + 2 * C::A_STAGE;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -142,6 +158,62 @@ __device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la, LB& lb, int nk, fl
       lb.store(Bs + (cur ^ 1) * C::B_STAGE);
     }
     __syncthreads();
+  }
+}
+
+template <class C, class LA, class LB>
+__device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la0, LB& lb0, int nk, float* smem) {
+  if constexpr (C::BM * C::BN > 128 * 128) {
+    mainloop_1deep<C>(acc, la0, lb0, nk, smem);
+  } else {
+  float* const As0 = smem;
+  float* const As1 = smem + C::A_STAGE;
+  float* const Bs0 = smem + 2 * C::A_STAGE;
+  float* const Bs1 = Bs0 + C::B_STAGE;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  acc_zero<C>(acc);
+  if (nk <= 0) return;
+  LA la1 = la0;
+  LB lb1 = lb0;
+  la0.kstep = lb0.kstep = la1.kstep = lb1.kstep = 2 * C::BK;
+  la1.k += C::BK;
+  lb1.k += C::BK;
+  la0.load();
+  lb0.load();
+  if (nk > 1) {
+    la1.load();
+    lb1.load();
+  }
+  la0.store(As0);
+  lb0.store(Bs0);
+  __syncthreads();
+  for (int t = 0; t < nk; t += 2) {
+    // Slab t (stage 0); slab t + 1 waits in set 1.
+    if (t + 2 < nk) {
+      la0.load();
+      lb0.load();
+    }
+    mma_slab<C, LA::KMAJOR, LB::KMAJOR>(acc, As0, Bs0, wm, wn, lane);
+    if (t + 1 < nk) {
+      la1.store(As1);
+      lb1.store(Bs1);
+    }
+    __syncthreads();
+    if (t + 1 >= nk) break;
+    // Slab t + 1 (stage 1); slab t + 2 waits in set 0.
+    if (t + 3 < nk) {
+      la1.load();
+      lb1.load();
+    }
+    mma_slab<C, LA::KMAJOR, LB::KMAJOR>(acc, As1, Bs1, wm, wn, lane);
+    if (t + 2 < nk) {
+      la0.store(As0);
+      lb0.store(Bs0);
+    }
+    __syncthreads();
+  }
+  merge_row_sums(la0, la1, 0);
   }
 }
 
@@ -191,6 +263,24 @@ __device__ __forceinline__ int acc_col(int j) {
   return (wave % C::WAVES_N) * C::WTN + j * 32 + (lane & 31);
 }
 
+// This lane's row inside the tile for accumulator (i, v).
+template <class C>
+__device__ __forceinline__ int acc_row(int i, int v) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  return (wave / C::WAVES_N) * C::WTM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+}
+
+// Epilogue walk by rows: f(row, i, v) once per accumulator row of this lane;
+// the callee loops over the FN fragment columns (acc.v[i][j][v]) with column
+// data it computed once (acc_col), so per-element work is one add and a store.
+template <class C, class F>
+__device__ __forceinline__ void for_each_acc_row(F&& f) {
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) f(acc_row<C>(i, v), i, v);
+}
+
 // Register-order index of accumulator (i, j, v) of this thread: partial tiles
 // are spilled and reloaded in this order, fully coalesced.
 template <class C>
@@ -214,6 +304,7 @@ struct StridedLoader;
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::KVEC> {
   static constexpr bool KMAJOR = false;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int TPR = BK / 4;                 // threads per row
   static constexpr int RPP = kThreads / TPR;         // rows per pass
   static constexpr int PASSES = ROWS / RPP;
@@ -245,7 +336,7 @@ struct StridedLoader<ROWS, BK, Mode::KVEC> {
       else
         v[p] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     const int tid = threadIdx.x;
@@ -261,6 +352,7 @@ struct StridedLoader<ROWS, BK, Mode::RVEC> {
   // Rows are contiguous in memory: each thread reads 4 rows at one k with a
   // 16-byte load and writes them unchanged into the k-major stage.
   static constexpr bool KMAJOR = true;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int TPK = ROWS / 4;               // threads per k
   static constexpr int KPP = kThreads / TPK;         // k per pass
   static constexpr int PASSES = BK / KPP;
@@ -291,7 +383,7 @@ struct StridedLoader<ROWS, BK, Mode::RVEC> {
       else
         v[p] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     const int tid = threadIdx.x;
@@ -305,6 +397,7 @@ struct StridedLoader<ROWS, BK, Mode::RVEC> {
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
   static constexpr bool KMAJOR = false;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int RPP = kThreads / BK;
   static constexpr int PASSES = ROWS / RPP;
   static_assert(PASSES >= 1 && ROWS % RPP == 0, "KSCALAR tiling");
@@ -332,7 +425,7 @@ struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
     const int64_t off = int64_t(kx) * s_k;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) v[p] = (ok[p] && kin) ? ptr[p][off] : 0.f;
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     const int tid = threadIdx.x;
@@ -345,6 +438,7 @@ struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::RSCALAR> {
   static constexpr bool KMAJOR = false;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static_assert(kThreads % ROWS == 0 || ROWS % kThreads == 0, "RSCALAR tiling");
   static constexpr int EPT = ROWS * BK / kThreads;   // consecutive k per thread
   static_assert(ROWS <= kThreads, "RSCALAR expects ROWS <= 256");
@@ -370,7 +464,7 @@ struct StridedLoader<ROWS, BK, Mode::RSCALAR> {
       const int kx = k + ks + e;
       v[e] = (ok && kx < kmax) ? ptr[int64_t(kx) * s_k] : 0.f;
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     const int tid = threadIdx.x;

@@ -13,9 +13,12 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <numeric>
 #include <string>
+#include <vector>
 
 #include "mx_conv_common.hpp"
 
@@ -298,53 +301,85 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
 }
 
 // Per-tile figures for the planners: rows, columns, workgroups resident per
-// CU, and the measured MFMA throughput of a CU full of such tiles relative to
-// the 256 x 128 tile.
+// CU, and the CU's MFMA throughput with a full set of such tiles, relative to
+// 85% of its FP32 peak.  The rates (and the constants of plan_cost) were
+// fitted to measured times of every (tile, split) plan on the 53 ResNet-50
+// layers (forward, dInput, dWeight) on MI355X: the fitted planner's choices
+// cost 1.5% more in total than the best measured plan per layer.
 struct TileInfo {
   int bm, bn, per_cu;
   double rate;
   const char* name;
 };
 constexpr TileInfo kTileInfo[conv::NTILES] = {
-    {256, 128, 2, 1.0, "256x128x16"}, {128, 256, 2, 1.0, "128x256x16"}, {128, 128, 2, 0.94, "128x128x16"},
-    {64, 256, 2, 0.94, "64x256x16"},  {256, 64, 2, 0.94, "256x64x16"},  {64, 64, 4, 0.6, "64x64x16"}};
+    {256, 128, 2, 1.20, "256x128x16"}, {128, 256, 2, 1.22, "128x256x16"}, {128, 128, 2, 1.15, "128x128x16"},
+    {64, 256, 2, 0.68, "64x256x16"},   {256, 64, 2, 0.76, "256x64x16"},   {64, 64, 4, 1.10, "64x64x32"}};
 
-// Single-pass GEMM (forward, dInput): rounds of resident tiles times the
-// time of one round (per_cu tiles per CU at the CU's relative rate).
-int pick_tile(int64_t M, int64_t Ncols, int64_t G) {
-  int best = conv::TALL;
-  double best_cost = 0;
+// Estimated time of one implicit GEMM (per group M x Ncols x K, G groups)
+// with tile `ti` and K split `splits` ways of kps each, plus the finalize pass
+// that sums the partial outputs.  A CU holding n tiles runs at
+// rate * occ(n) of its share of 85% of the FP32 MFMA peak, occ rising from
+// 0.56 with one resident tile to 1 with per_cu; tiles beyond that queue.
+double plan_cost(const TileInfo& ti, int64_t M, int64_t Ncols, int64_t G, int64_t splits, int64_t kps,
+                 int64_t out_elems) {
+  const double cu = cu_count();
+  const double cu_flops = 0.85 * 157.3e12 / 256.0;
+  const int64_t tiles = ((M + ti.bm - 1) / ti.bm) * ((Ncols + ti.bn - 1) / ti.bn) * G;
+  const int64_t per_cu = (tiles * splits + int64_t(cu) - 1) / int64_t(cu);
+  const double occ = std::min(1.0, 0.56 + 0.44 * double(per_cu - 1) / double(ti.per_cu - 1));
+  double t = double(per_cu) * 2.0 * ti.bm * ti.bn * double(kps) / (cu_flops * ti.rate * occ) + 2e-6;
+  if (splits > 1) t += double(splits + 1) * double(out_elems) * 4.0 / 8.0e12 + 3e-6;
+  return t;
+}
+
+constexpr int kSplitBK = 32;         // K granularity of a split (a multiple of every loader run)
+constexpr int kMinSplitSpan = 128;   // shortest K range worth a split
+
+struct GemmPlan {
+  int tile = conv::SQ;
+  int splits = 1;
+  int kps = 0;
+};
+
+// Cheapest (tile, K split) over the allowed tiles (bit mask over conv::Tile)
+// and split counts up to max_splits.  MX_CONV_PLAN="tile,splits" (tile index
+// in conv::Tile order, splits from the candidate list) restricts the choice,
+// for tuning and diagnosis; a combination this shape cannot use is ignored.
+GemmPlan plan_gemm(int64_t M, int64_t Ncols, int64_t K, int64_t G, unsigned tiles, int64_t max_splits,
+                   int64_t out_elems) {
+  int force_tile = -1, force_splits = 0;
+  if (const char* e = std::getenv("MX_CONV_PLAN")) {
+    if (std::sscanf(e, "%d,%d", &force_tile, &force_splits) != 2) force_tile = -1;
+  }
+  GemmPlan best;
+  double best_t = -1;
+  static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128, 192, 256, 384, 512};
+  for (int pass = force_tile >= 0 ? 0 : 1; pass < 2 && best_t < 0; ++pass)
   for (int t = 0; t < conv::NTILES; ++t) {
-    if (t == conv::NARROW) continue;  // split-K (dWeight) only
-    const TileInfo& ti = kTileInfo[t];
-    const int64_t tiles = ((M + ti.bm - 1) / ti.bm) * ((Ncols + ti.bn - 1) / ti.bn) * G;
-    const int64_t slots = int64_t(cu_count()) * ti.per_cu;
-    const double cost = double((tiles + slots - 1) / slots) * ti.per_cu * ti.bm * ti.bn / ti.rate;
-    if (t == conv::TALL || cost < best_cost) {
-      best = t;
-      best_cost = cost;
+    if (!(tiles & (1u << t))) continue;
+    if (pass == 0 && t != force_tile) continue;
+    for (int want : kSplits) {
+      if (want > max_splits) break;
+      if (pass == 0 && want != force_splits) continue;
+      int64_t kps = (K + want - 1) / want;
+      kps = (kps + kSplitBK - 1) / kSplitBK * kSplitBK;
+      const int64_t splits = (K + kps - 1) / kps;
+      if (splits > 1 && kps < kMinSplitSpan) break;
+      const double cost = plan_cost(kTileInfo[t], M, Ncols, G, splits, kps, out_elems);
+      if (best_t < 0 || cost < best_t) {
+        best_t = cost;
+        best.tile = t;
+        best.splits = int(splits);
+        best.kps = int(kps);
+      }
     }
   }
   return best;
 }
 
-// Split-K GEMM (dWeight): the splits fill the machine, so only the padded
-// tile area at the tile's rate matters.
-int pick_tile_splitk(int64_t M, int64_t Ncols, bool gathers) {
-  int best = conv::SQ;
-  double best_cost = 0;
-  for (int t = 0; t < conv::NTILES; ++t) {
-    // Two scalar operands do not fit a 256-wide tile in the register budget.
-    if (gathers && (t == conv::TALL || t == conv::WIDE)) continue;
-    const TileInfo& ti = kTileInfo[t];
-    const double cost = double((M + ti.bm - 1) / ti.bm * ti.bm) * double((Ncols + ti.bn - 1) / ti.bn * ti.bn) / ti.rate;
-    if (t == (gathers ? conv::SQ : conv::TALL) || cost < best_cost) {
-      best = t;
-      best_cost = cost;
-    }
-  }
-  return best;
-}
+constexpr unsigned kAllTiles = (1u << conv::NTILES) - 1;
+constexpr unsigned kSinglePassTiles = kAllTiles & ~(1u << conv::NARROW);  // forward / dInput
+constexpr unsigned kNoWideTiles = kAllTiles & ~((1u << conv::TALL) | (1u << conv::WIDE));
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
@@ -352,38 +387,21 @@ bool unpadded_1x1(const ConvArgs& p) {
   return p.KH == 1 && p.KW == 1 && p.sh == 1 && p.sw == 1 && p.ph == 0 && p.pw == 0;
 }
 
-constexpr int kSplitBK = 16;          // K granularity of a dWeight split
-constexpr int kMinSplitSpan = 384;    // positions per split (partial-traffic bound)
-
 struct DwPlan {
-  int tile = conv::TALL;
-  int splits = 1;
-  int kps = 0;
+  GemmPlan g;
   int64_t ws_bytes = 0;
   int64_t db_bytes = 0;
 };
 
-// dWeight plan: tile by padded area, then enough position splits to give
-// every CU its resident workgroups, keeping each split at least
-// kMinSplitSpan positions long (each split writes and the finalize re-reads
-// one full-size partial).
+// dWeight: K = N*OH*OW positions, split so every CU gets work; each split
+// writes one full-size partial dW that the finalize re-reads.
 DwPlan plan_dw(const ConvArgs& p, bool with_db, bool gathers) {
   DwPlan pl;
-  pl.tile = pick_tile_splitk(p.M, p.Ncols, gathers);
-  const TileInfo& ti = kTileInfo[pl.tile];
-  const int64_t blocks = ((p.M + ti.bm - 1) / ti.bm) * ((p.Ncols + ti.bn - 1) / ti.bn) * p.G;
-  const int64_t slots = int64_t(cu_count()) * ti.per_cu;
-  const int64_t max_splits = std::max<int64_t>(1, p.K / kMinSplitSpan);
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(max_splits, (slots + blocks - 1) / blocks));
-  splits = std::min<int64_t>(splits, 65535);
-  int64_t kps = (p.K + splits - 1) / splits;
-  kps = (kps + kSplitBK - 1) / kSplitBK * kSplitBK;
-  splits = (p.K + kps - 1) / kps;
-  pl.splits = int(splits);
-  pl.kps = int(kps);
-  if (splits > 1) {
-    pl.ws_bytes = splits * int64_t(p.G) * p.Cout_g * p.Ncols * 4;
-    pl.db_bytes = with_db ? splits * int64_t(p.Cout) * 4 : 0;
+  const int64_t out = int64_t(p.G) * p.Cout_g * p.Ncols;
+  pl.g = plan_gemm(p.M, p.Ncols, p.K, p.G, gathers ? kNoWideTiles : kAllTiles, 65535, out);
+  if (pl.g.splits > 1) {
+    pl.ws_bytes = int64_t(pl.g.splits) * out * 4;
+    pl.db_bytes = with_db ? int64_t(pl.g.splits) * p.Cout * 4 : 0;
   }
   return pl;
 }
@@ -414,6 +432,56 @@ AxisPhase axis_phase(int a, int in, int k, int s, int pad, int dil) {
   ph.taps = (k - 1 - k0) / ph.step + 1;
   ph.off0 = (a + pad - k0 * dil) / s;  // exact division
   return ph;
+}
+
+GemmPlan plan_fwd(const ConvArgs& p) {
+  return plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G, kSinglePassTiles, 512,
+                   int64_t(p.N) * p.Cout * p.OHOW);
+}
+
+// dInput stride phases of `p` (GEMM fields filled in) and one plan for all of
+// them, made on the phase with the most work.  Split-K only when every phase
+// has taps, so every partial output element is written by some phase.
+GemmPlan plan_dx(const ConvArgs& p, std::vector<ConvArgs>* phases) {
+  bool any_zero = false;
+  int64_t best_work = -1, bm = 0, bn = 0, bk = 0;
+  for (int a = 0; a < p.sh; ++a) {
+    const AxisPhase ah = axis_phase(a, p.H, p.KH, p.sh, p.ph, p.dh);
+    for (int b = 0; b < p.sw; ++b) {
+      const AxisPhase aw = axis_phase(b, p.W, p.KW, p.sw, p.pw, p.dw);
+      if (ah.len == 0 || aw.len == 0) continue;
+      ConvArgs q = p;
+      q.pa = a;
+      q.pb = b;
+      q.Hp = ah.len;
+      q.Wp = aw.len;
+      q.HpWp = ah.len * aw.len;
+      q.nth = ah.taps;
+      q.ntw = aw.taps;
+      q.offh0 = ah.off0;
+      q.offw0 = aw.off0;
+      q.dsh = ah.dstep;
+      q.dsw = aw.dstep;
+      q.kh0 = ah.k0;
+      q.kw0 = aw.k0;
+      q.stph = ah.step;
+      q.stpw = aw.step;
+      q.M = p.Cin_g;
+      q.Ncols = p.N * q.HpWp;
+      q.K = p.Cout_g * q.nth * q.ntw;
+      if (q.K == 0) any_zero = true;
+      const int64_t work = int64_t(q.K) * q.Ncols;
+      if (work > best_work) {
+        best_work = work;
+        bm = q.M;
+        bn = q.Ncols;
+        bk = q.K;
+      }
+      if (phases) phases->push_back(q);
+    }
+  }
+  return plan_gemm(bm, bn, std::max<int64_t>(bk, 1), p.G, kSinglePassTiles, any_zero ? 1 : 512,
+                   int64_t(p.N) * p.Cin * p.HW);
 }
 
 }  // namespace
@@ -465,9 +533,25 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
   p.M = p.Cout_g;
   p.Ncols = p.N * p.OHOW;
   p.K = p.Cin_g * p.KK;
-  const Mode ma = (p.K % 4 == 0 && aligned16(w)) ? Mode::KVEC : Mode::KSCALAR;
+  const bool fwd_packed = p.KK > 1 && conv::blocked_channels(p.Cin_g);
+  const Mode ma = (p.K % 4 == 0 && (fwd_packed || aligned16(w))) ? Mode::KVEC : Mode::KSCALAR;
   const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
-  return conv::conv_fwd_launch(p, pick_tile(p.M, p.Ncols, p.G), ma, bmode, s);
+  const GemmPlan gp = plan_fwd(p);
+  p.splits = gp.splits;
+  p.kps = gp.kps;
+  p.out_elems = int64_t(p.N) * p.Cout * p.OHOW;
+  Scratch wp, ws;
+  p.wt = w;
+  if (p.KK > 1 && conv::blocked_channels(p.Cin_g)) {  // pack to the blocked K order
+    MX_TRY(wp.alloc(size_t(p.Cout) * p.Cin_g * p.KK * 4, s));
+    MX_TRY(conv::conv_fwd_pack_weights(p, wp.as<float>(), s));
+    p.wt = wp.as<float>();
+  }
+  if (gp.splits == 1) return conv::conv_fwd_launch(p, gp.tile, ma, bmode, s);
+  MX_TRY(ws.alloc(size_t(gp.splits) * size_t(p.out_elems) * 4, s));
+  p.ws = ws.as<float>();
+  MX_TRY(conv::conv_fwd_launch(p, gp.tile, ma, bmode, s));
+  return conv::conv_sum_splits(p.ws, gp.splits, p.out_elems, y, bias, p.OHOW, p.Cout, s);
   MX_ABI_END
 }
 
@@ -490,45 +574,32 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
     return MX_OK;
   }
   // One GEMM per stride phase over exactly the taps that reach it.
-  const bool vec_a = p.Cin_g % 4 == 0;
-  Scratch wt;
-  MX_TRY(wt.alloc(size_t(p.Cout) * p.Cin_g * p.KK * 4, s));
-  p.wt = wt.as<float>();
-  for (int a = 0; a < p.sh; ++a) {
-    const AxisPhase ah = axis_phase(a, p.H, p.KH, p.sh, p.ph, p.dh);
-    for (int b = 0; b < p.sw; ++b) {
-      const AxisPhase aw = axis_phase(b, p.W, p.KW, p.sw, p.pw, p.dw);
-      if (ah.len == 0 || aw.len == 0) continue;
-      ConvArgs q = p;
-      q.pa = a;
-      q.pb = b;
-      q.Hp = ah.len;
-      q.Wp = aw.len;
-      q.HpWp = ah.len * aw.len;
-      q.nth = ah.taps;
-      q.ntw = aw.taps;
-      q.offh0 = ah.off0;
-      q.offw0 = aw.off0;
-      q.dsh = ah.dstep;
-      q.dsw = aw.dstep;
-      q.kh0 = ah.k0;
-      q.kw0 = aw.k0;
-      q.stph = ah.step;
-      q.stpw = aw.step;
-      if (ah.taps == 0 || aw.taps == 0) {
-        MX_TRY(conv::conv_dx_zero_phase(q, s));
-        continue;
-      }
-      q.M = p.Cin_g;
-      q.Ncols = p.N * q.HpWp;
-      q.K = p.Cout_g * q.nth * q.ntw;
-      MX_TRY(conv::conv_dx_pack_weights(q, wt.as<float>(), s));
-      const bool one_to_one = q.nth == 1 && q.ntw == 1 && q.offh0 == 0 && q.offw0 == 0 && q.Hp == p.OH &&
-                              q.Wp == p.OW && p.OHOW % 4 == 0 && aligned16(dy);
-      MX_TRY(conv::conv_dx_launch(q, pick_tile(q.M, q.Ncols, p.G), vec_a ? Mode::RVEC : Mode::RSCALAR,
-                                  one_to_one ? conv::B_VEC : conv::B_GATHER, s));
+  std::vector<ConvArgs> phases;
+  const GemmPlan gp = plan_dx(p, &phases);
+  // A 1x1 kernel is already [g][co][ci]; larger kernels are packed per phase.
+  const bool packed = p.KK > 1;
+  const bool vec_a = p.Cin_g % 4 == 0 && (packed || aligned16(w));
+  const int64_t out_elems = int64_t(p.N) * p.Cin * p.HW;
+  Scratch wt, ws;
+  if (packed) MX_TRY(wt.alloc(size_t(p.Cout) * p.Cin_g * p.KK * 4, s));
+  if (gp.splits > 1) MX_TRY(ws.alloc(size_t(gp.splits) * size_t(out_elems) * 4, s));
+  for (ConvArgs& q : phases) {
+    if (q.K == 0) {
+      MX_TRY(conv::conv_dx_zero_phase(q, s));
+      continue;
     }
+    q.wt = packed ? wt.as<float>() : w;
+    q.splits = gp.splits;
+    q.kps = int((q.K + gp.splits - 1) / gp.splits + kSplitBK - 1) / kSplitBK * kSplitBK;
+    q.ws = ws.as<float>();
+    q.out_elems = out_elems;
+    if (packed) MX_TRY(conv::conv_dx_pack_weights(q, wt.as<float>(), s));
+    const bool one_to_one = q.nth == 1 && q.ntw == 1 && q.offh0 == 0 && q.offw0 == 0 && q.Hp == p.OH &&
+                            q.Wp == p.OW && p.OHOW % 4 == 0 && aligned16(dy);
+    MX_TRY(conv::conv_dx_launch(q, gp.tile, vec_a ? Mode::RVEC : Mode::RSCALAR,
+                                one_to_one ? conv::B_VEC : conv::B_GATHER, s));
   }
+  if (gp.splits > 1) return conv::conv_sum_splits(ws.as<float>(), gp.splits, out_elems, dx, nullptr, 1, 1, s);
   return MX_OK;
   MX_ABI_END
 }
@@ -587,9 +658,9 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
   const int amode = (p.OHOW % 4 == 0 && aligned16(dy)) ? conv::B_VEC : conv::B_GATHER;
   const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
   const DwPlan pl = plan_dw(p, db != nullptr, amode == conv::B_GATHER && bmode == conv::B_GATHER);
-  p.splits = pl.splits;
-  p.kps = pl.kps;
-  if (pl.splits == 1) return conv::conv_dw_launch(p, pl.tile, amode, bmode, s);
+  p.splits = pl.g.splits;
+  p.kps = pl.g.kps;
+  if (pl.g.splits == 1) return conv::conv_dw_launch(p, pl.g.tile, amode, bmode, s);
   Scratch ws, wsdb;
   MX_TRY(ws.alloc(size_t(pl.ws_bytes), s));
   p.ws = ws.as<float>();
@@ -597,7 +668,7 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
     MX_TRY(wsdb.alloc(size_t(pl.db_bytes), s));
     p.ws_db = wsdb.as<float>();
   }
-  MX_TRY(conv::conv_dw_launch(p, pl.tile, amode, bmode, s));
+  MX_TRY(conv::conv_dw_launch(p, pl.g.tile, amode, bmode, s));
   return conv::conv_dw_finalize(p, dw, db, s);
   MX_ABI_END
 }
@@ -620,17 +691,15 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
   } else if (chosen == MX_CONV_ALGO_REDUCE) {
     name = "conv_dw_reduce_kernel";
   } else if (phase == MX_CONV_FORWARD) {
-    name = cat("conv_fwd_kernel<", kTileInfo[pick_tile(p.Cout_g, p.N * p.OHOW, p.G)].name, ">");
+    name = cat("conv_fwd_kernel<", kTileInfo[plan_fwd(p).tile].name, ">");
   } else if (phase == MX_CONV_DINPUT) {
-    // Tile of the stride phase (0, 0), the largest one.
-    const AxisPhase ah = axis_phase(0, p.H, p.KH, p.sh, p.ph, p.dh), aw = axis_phase(0, p.W, p.KW, p.sw, p.pw, p.dw);
-    name = cat("conv_dx_kernel<", kTileInfo[pick_tile(p.Cin_g, int64_t(p.N) * ah.len * aw.len, p.G)].name, ">");
+    name = cat("conv_dx_kernel<", kTileInfo[plan_dx(p, nullptr).tile].name, ">");
   } else {
     p.M = p.Cout_g;
     p.Ncols = p.Cin_g * p.KK;
     p.K = p.N * p.OHOW;
     const bool gathers = p.OHOW % 4 != 0 && !(unpadded_1x1(p) && p.HW % 4 == 0);
-    name = cat("conv_dw_kernel<", kTileInfo[plan_dw(p, true, gathers).tile].name, ">");
+    name = cat("conv_dw_kernel<", kTileInfo[plan_dw(p, true, gathers).g.tile].name, ">");
   }
   if (len) {
     std::strncpy(buf, name.c_str(), len - 1);
@@ -650,8 +719,8 @@ int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t*
   p.K = p.N * p.OHOW;
   const bool gathers = p.OHOW % 4 != 0 && !(unpadded_1x1(p) && p.HW % 4 == 0);
   const DwPlan pl = plan_dw(p, true, gathers);
-  if (splits) *splits = pl.splits;
-  if (span) *span = pl.kps;
+  if (splits) *splits = pl.g.splits;
+  if (span) *span = pl.g.kps;
   if (workspace_bytes) *workspace_bytes = pl.ws_bytes + pl.db_bytes;
   return MX_OK;
   MX_ABI_END

@@ -2,8 +2,9 @@
 // dWeight): the argument block, the operand loaders and the tile menu.
 //
 // GEMM views (per group g):
-//   forward : C[co, pos]        = W[co, (ci,kh,kw)]     x im2col(x)[(ci,kh,kw), pos]
-//   dInput  : C[ci, ppos]       = Wt_p[ci, (co,th,tw)]  x gather_p(dy)[(co,th,tw), ppos]
+//   forward : C[co, pos]        = Wp[co, k(ci,kh,kw)]   x im2col(x)[k(ci,kh,kw), pos]
+//   dInput  : C[ci, ppos]       = Wt_p[ci, k(co,th,tw)] x gather_p(dy)[k(co,th,tw), ppos]
+//             k(.) is the gathered K order (kChanBlock below).
 //             one GEMM per stride phase p = (ih % sh, iw % sw); ppos runs over
 //             the input positions of that phase and (th, tw) over the taps
 //             that reach it, so no zero-inserted term is ever multiplied.
@@ -47,25 +48,42 @@ struct ConvArgs {
   // dy column j + offw0 - tw*dsw.
   // Tap th is kernel row kh0 + th*stph (tw: kernel column kw0 + tw*stpw).
   int pa, pb, Hp, Wp, HpWp, nth, ntw, offh0, offw0, dsh, dsw, kh0, kw0, stph, stpw;
-  const float* wt;  // dInput: phase-packed weights [g][co][th][tw][ci]
-  float* ws;        // dWeight: per-split partial dW [split][G*Cout_g][Cin_g*KK]
-  float* ws_db;     // dWeight: per-split partial dBias [split][Cout]
+  const float* wt;  // weights packed to the gathered K order: forward [g][co][k], dInput [g][k][ci]
+  // Split-K partials (splits > 1): forward / dInput write their tile to
+  // ws + split * out_elems at the output's own offsets; dWeight writes
+  // [split][G*Cout_g][Cin_g*KK] and the dBias partials to ws_db [split][Cout].
+  float* ws;
+  float* ws_db;
+  int64_t out_elems;
 };
 
+// Gathered K order.  With a channel count that is a multiple of kChanBlock
+// the K index of the forward / dInput GEMMs runs over (channel block, kh, kw,
+// channel in block): a loader's run of consecutive k (at most kChanBlock) then
+// shares one tap, so one bounds test covers it and its addresses are one
+// channel plane apart, while the taps of one channel block stay within a few
+// slabs (the input lines they share stay in L1).  Other channel counts keep
+// the plain (channel, kh, kw) order.  The weights are packed to match.
+constexpr int kChanBlock = 16;
+__host__ __device__ constexpr bool blocked_channels(int c) { return c % kChanBlock == 0; }
+
 // ------------------------------------------------------------------ loaders
-// Forward B operand (gather): rows = output positions (img, oh, ow),
-// k = (ci, kh, kw).  Each thread holds EPT consecutive k of one position.
+// Forward B operand (gather): rows = output positions (img, oh, ow), k in
+// the gathered K order over (ci, kh, kw); element
+// x[img][g*Cin_g + ci][oh*sh - ph + kh*dh][ow*sw - pw + kw*dw].  Each thread
+// holds EPT consecutive k of one position.
 template <int ROWS, int BK>
 struct Im2colLoader {
   static constexpr bool KMAJOR = false;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int EPT = ROWS * BK / kThreads;
-  static_assert(ROWS <= kThreads && EPT >= 1, "Im2colLoader tiling");
+  static_assert(ROWS <= kThreads && EPT >= 1 && BK % EPT == 0 && kChanBlock % EPT == 0, "Im2colLoader tiling");
   float v[EPT];
   const float* xg;
-  int ih0, iw0, ks, k;
-  bool ok;
-  int K, KK, KH, KW, dh, dw, H, W, HW;
-  __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g) {
+  int ih0, iw0, ks, k, kmax;
+  bool ok, blocked;
+  int KK, KBLK, KH, KW, dh, dw, H, W, HW;
+  __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     const int r = tid % ROWS;
     ks = (tid / ROWS) * EPT;
@@ -79,8 +97,9 @@ struct Im2colLoader {
     ih0 = oh * p.sh - p.ph;
     iw0 = ow * p.sw - p.pw;
     xg = p.x + (int64_t(img) * p.Cin + int64_t(g) * p.Cin_g) * p.HW;
-    K = p.K;
+    blocked = blocked_channels(p.Cin_g);
     KK = p.KK;
+    KBLK = p.KK * kChanBlock;
     KH = p.KH;
     KW = p.KW;
     dh = p.dh;
@@ -88,28 +107,44 @@ struct Im2colLoader {
     H = p.H;
     W = p.W;
     HW = p.HW;
-    k = 0;
+    k = k0;
+    kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
     const int kb = k + ks;
-    int ci = kb / KK;
-    const int rem = kb - ci * KK;
-    int kh = rem / KW;
-    int kw = rem - kh * KW;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
+    if (blocked) {
+      // (channel block, kh, kw, channel in block): the run shares one tap.
+      const int cb = kb / KBLK;
+      const int rem = kb - cb * KBLK;
+      const int t = rem / kChanBlock;
+      const int kh = t / KW, kw = t - (t / KW) * KW;
+      const int c = cb * kChanBlock + (rem - t * kChanBlock);
       const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
-      const bool valid = ok && (kb + e) < K && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-      v[e] = valid ? xg[ci * HW + ih * W + iw] : 0.f;
-      if (++kw == KW) {
-        kw = 0;
-        if (++kh == KH) {
-          kh = 0;
-          ++ci;
+      const bool valid = ok && kb < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
+      const float* src = xg + (valid ? c * HW + ih * W + iw : 0);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) v[e] = valid ? src[e * HW] : 0.f;
+    } else {
+      // (ci, kh, kw) with kw fastest.
+      int ci = kb / KK;
+      const int rem = kb - ci * KK;
+      int kh = rem / KW;
+      int kw = rem - kh * KW;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
+        const bool valid = ok && (kb + e) < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
+        v[e] = valid ? xg[ci * HW + ih * W + iw] : 0.f;
+        if (++kw == KW) {
+          kw = 0;
+          if (++kh == KH) {
+            kh = 0;
+            ++ci;
+          }
         }
       }
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     constexpr int LDK = BK + 4;
@@ -134,6 +169,7 @@ struct Im2colLoader {
 template <int ROWS, int BK, bool DY>
 struct PosQuadLoader {
   static constexpr bool KMAJOR = true;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int TPK = ROWS / 4;        // threads per k
   static constexpr int KPP = kThreads / TPK;  // k per pass
   static constexpr int PASSES = BK / KPP;
@@ -142,7 +178,7 @@ struct PosQuadLoader {
   const float* ptr;
   int hw, k, kmax, kk;
   bool ok;
-  __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g) {
+  __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     kk = tid / TPK;
     const float* base = DY ? p.dy + int64_t(g) * p.Cout_g * p.OHOW : p.x + int64_t(g) * p.Cin_g * p.HW;
@@ -153,8 +189,8 @@ struct PosQuadLoader {
     const int pp = ok ? pos : 0;
     const int img = pp / hw;
     ptr = base + int64_t(img) * cs + (pp - img * hw);
-    k = 0;
-    kmax = p.K;
+    k = k0;
+    kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
 #pragma unroll
@@ -165,7 +201,7 @@ struct PosQuadLoader {
       else
         v[q] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     constexpr int LDR = ROWS + 4;
@@ -177,18 +213,20 @@ struct PosQuadLoader {
 };
 
 // dInput B operand (gather) for one stride phase: rows = phase positions
-// (img, i, j), k = (co, th, tw); element dy[img][co][i + offh0 - th*dsh][j + offw0 - tw*dsw].
+// (img, i, j), k in the gathered K order over (co, th, tw); element
+// dy[img][g*Cout_g + co][i + offh0 - th*dsh][j + offw0 - tw*dsw].
 template <int ROWS, int BK>
 struct PhaseGatherLoader {
   static constexpr bool KMAJOR = false;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int EPT = ROWS * BK / kThreads;
-  static_assert(ROWS <= kThreads && EPT >= 1, "PhaseGatherLoader tiling");
+  static_assert(ROWS <= kThreads && EPT >= 1 && BK % EPT == 0 && kChanBlock % EPT == 0, "PhaseGatherLoader tiling");
   float v[EPT];
   const float* dyg;
-  int ib, jb, ks, k;
-  bool ok;
-  int K, NT, nth, ntw, dsh, dsw, OH, OW, OHOW;
-  __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g) {
+  int ib, jb, ks, k, kmax;
+  bool ok, blocked;
+  int NT, KBLK, nth, ntw, dsh, dsw, OH, OW, OHOW;
+  __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     const int r = tid % ROWS;
     ks = (tid / ROWS) * EPT;
@@ -202,8 +240,9 @@ struct PhaseGatherLoader {
     ib = i + p.offh0;
     jb = j + p.offw0;
     dyg = p.dy + (int64_t(img) * p.Cout + int64_t(g) * p.Cout_g) * p.OHOW;
-    K = p.K;
+    blocked = blocked_channels(p.Cout_g);
     NT = p.nth * p.ntw;
+    KBLK = NT * kChanBlock;
     nth = p.nth;
     ntw = p.ntw;
     dsh = p.dsh;
@@ -211,28 +250,44 @@ struct PhaseGatherLoader {
     OH = p.OH;
     OW = p.OW;
     OHOW = p.OHOW;
-    k = 0;
+    k = k0;
+    kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
     const int kb = k + ks;
-    int co = kb / NT;
-    const int rem = kb - co * NT;
-    int th = rem / ntw;
-    int tw = rem - th * ntw;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
+    if (blocked) {
+      // (channel block, th, tw, channel in block): the run shares one tap.
+      const int cb = kb / KBLK;
+      const int rem = kb - cb * KBLK;
+      const int t = rem / kChanBlock;
+      const int th = t / ntw, tw = t - (t / ntw) * ntw;
+      const int co = cb * kChanBlock + (rem - t * kChanBlock);
       const int oh = ib - th * dsh, ow = jb - tw * dsw;
-      const bool valid = ok && (kb + e) < K && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
-      v[e] = valid ? dyg[co * OHOW + oh * OW + ow] : 0.f;
-      if (++tw == ntw) {
-        tw = 0;
-        if (++th == nth) {
-          th = 0;
-          ++co;
+      const bool valid = ok && kb < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
+      const float* src = dyg + (valid ? co * OHOW + oh * OW + ow : 0);
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) v[e] = valid ? src[e * OHOW] : 0.f;
+    } else {
+      // (co, th, tw) with tw fastest.
+      int co = kb / NT;
+      const int rem = kb - co * NT;
+      int th = rem / ntw;
+      int tw = rem - th * ntw;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int oh = ib - th * dsh, ow = jb - tw * dsw;
+        const bool valid = ok && (kb + e) < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
+        v[e] = valid ? dyg[co * OHOW + oh * OW + ow] : 0.f;
+        if (++tw == ntw) {
+          tw = 0;
+          if (++th == nth) {
+            th = 0;
+            ++co;
+          }
         }
       }
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     constexpr int LDK = BK + 4;
@@ -256,6 +311,7 @@ struct PhaseGatherLoader {
 template <int ROWS, int BK>
 struct DyRowsLoader {
   static constexpr bool KMAJOR = false;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int LPR = BK;  // lanes per row
   static constexpr int RPP = kThreads / BK;
   static constexpr int PASSES = ROWS / RPP;
@@ -292,7 +348,7 @@ struct DyRowsLoader {
       v[q] = (ok[q] && kin) ? dyg[base + coff[q]] : 0.f;
       bsum[q] += v[q];
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     constexpr int LDK = BK + 4;
@@ -309,6 +365,7 @@ struct DyRowsLoader {
 template <int ROWS, int BK, bool DY>
 struct PosKLoader {
   static constexpr bool KMAJOR = false;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int LPR = BK / 4;  // lanes per row
   static constexpr int RPP = kThreads / LPR;
   static constexpr int PASSES = ROWS / RPP;
@@ -349,7 +406,7 @@ struct PosKLoader {
         v[q] = f32x4{0.f, 0.f, 0.f, 0.f};
       if constexpr (DY) bsum[q] += (v[q][0] + v[q][1]) + (v[q][2] + v[q][3]);
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     constexpr int LDK = BK + 4;
@@ -365,6 +422,7 @@ struct PosKLoader {
 template <int ROWS, int BK>
 struct XColsLoader {
   static constexpr bool KMAJOR = false;
+  int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int RPP = kThreads / BK;
   static constexpr int PASSES = ROWS / RPP;
   static_assert(PASSES >= 1 && ROWS % RPP == 0, "XColsLoader tiling");
@@ -417,7 +475,7 @@ struct XColsLoader {
       const bool valid = kin && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
       v[q] = valid ? xi[coff[q] + ih * W + iw] : 0.f;
     }
-    k += BK;
+    k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     constexpr int LDK = BK + 4;
@@ -434,7 +492,7 @@ using TileWide = Cfg<128, 256, 16, 2, 2>;   // 4 waves of 64 x 128
 using TileSq = Cfg<128, 128, 16, 2, 2>;     // 4 waves of 64 x 64
 using TileFlat = Cfg<64, 256, 16, 1, 2>;    // 4 waves of 64 x 64 in a row
 using TileNarrow = Cfg<256, 64, 16, 4, 2>;  // 4 waves of 64 x 64 in a column
-using TileSmall = Cfg<64, 64, 16, 2, 4>;    // 4 waves of 32 x 32
+using TileSmall = Cfg<64, 64, 32, 2, 4>;    // 4 waves of 32 x 32, 32-deep slabs
 enum Tile : int { TALL = 0, WIDE, SQ, FLAT, NARROW, SMALL, NTILES };
 
 // Operand modes the launchers dispatch on.
@@ -444,8 +502,12 @@ int conv_fwd_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t
 int conv_dx_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t s);
 int conv_dw_launch(const ConvArgs& p, int tile, int amode, int bmode, hipStream_t s);
 int conv_dx_pack_weights(const ConvArgs& p, float* wt, hipStream_t s);
+int conv_fwd_pack_weights(const ConvArgs& p, float* wt, hipStream_t s);
 int conv_dx_zero_phase(const ConvArgs& p, hipStream_t s);
 int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s);
+// out[i] = sum over splits of ws[split][i] (+ bias[(i / hw) % cout] when bias).
+int conv_sum_splits(const float* ws, int splits, int64_t n, float* out, const float* bias, int hw, int cout,
+                    hipStream_t s);
 
 }  // namespace conv
 }  // namespace mx

@@ -44,9 +44,16 @@ MX_TILE_KERNEL(C) void conv_dw_kernel(ConvArgs p) {
 
   const int64_t dw_elems = int64_t(p.G) * p.Cout_g * p.Ncols;
   float* dst = (p.splits == 1 ? p.out : p.ws + split * dw_elems) + int64_t(g) * p.Cout_g * p.Ncols;
-  for_each_acc<C>(acc, [&](int r, int c, float v) {
-    const int co = row0 + r, n = col0 + c;
-    if (co < p.M && n < p.Ncols) dst[int64_t(co) * p.Ncols + n] = v;
+  int ccol[C::FN];
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) ccol[j] = col0 + acc_col<C>(j);
+  for_each_acc_row<C>([&](int r, int i, int v) {
+    const int co = row0 + r;
+    if (co >= p.M) return;
+    float* d = dst + int64_t(co) * p.Ncols;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+      if (ccol[j] < p.Ncols) d[ccol[j]] = acc.v[i][j][v];
   });
   if (p.db != nullptr && tn == 0) {
     float* dbd = (p.splits == 1 ? p.db : p.ws_db + int64_t(split) * p.Cout) + g * p.Cout_g;
@@ -78,6 +85,18 @@ __global__ void conv_dw_finalize_kernel(const float* __restrict__ ws, const floa
       for (int sp = 0; sp < splits; ++sp) s += ws_db[sp * int64_t(n_db) + j];
       db[j] = s;
     }
+  }
+}
+
+__global__ void conv_sum_splits_kernel(const float* __restrict__ ws, int splits, int64_t n, float* __restrict__ out,
+                                       const float* __restrict__ bias, int hw, int cout) {
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < n;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    float s = 0.f;
+#pragma unroll 8
+    for (int sp = 0; sp < splits; ++sp) s += ws[sp * n + idx];
+    if (bias) s += bias[(idx / hw) % cout];
+    out[idx] = s;
   }
 }
 
@@ -118,6 +137,14 @@ int conv_dw_launch(const ConvArgs& p, int tile, int amode, int bmode, hipStream_
     case NARROW: return launch_a<TileNarrow>(p, amode, bmode, s);
     default: return launch_a<TileSmall>(p, amode, bmode, s);
   }
+}
+
+int conv_sum_splits(const float* ws, int splits, int64_t n, float* out, const float* bias, int hw, int cout,
+                    hipStream_t s) {
+  const int blocks = int(std::min<int64_t>((n + 255) / 256, 1 << 20));
+  hipLaunchKernelGGL(conv_sum_splits_kernel, dim3(blocks), dim3(256), 0, s, ws, splits, n, out, bias, hw, cout);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
 }
 
 int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s) {

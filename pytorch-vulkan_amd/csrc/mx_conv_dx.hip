@@ -10,27 +10,41 @@
 // therefore split into sh*sw phases (ih % sh, iw % sw); each phase is a dense
 // GEMM over exactly its taps (th, tw), so no zero-inserted term is ever
 // multiplied.  Phases no tap reaches are zero-filled.  Weights are first
-// packed per phase as Wt_p[g][co][th][tw][ci] so the A operand has ci
-// contiguous and loads 16 bytes per lane.
+// packed per phase as Wt_p[g][k][ci] (k the gathered K order over (co, th,
+// tw), mx_conv_common.hpp) so the A operand has ci contiguous (16 bytes per
+// lane); a 1x1 kernel needs no packing, w itself is [g][co][ci].
 #include "mx_conv_common.hpp"
 
 namespace mx {
 namespace conv {
 namespace {
 
-// Wt_p[g][co][th][tw][ci] = w[g*Cout_g + co][ci][kh0 + th*stph][kw0 + tw*stpw].
+// Wt_p[g][k][ci] = w[g*Cout_g + co][ci][kh0 + th*stph][kw0 + tw*stpw] with k
+// the gathered K order over (co, th, tw): the A operand of the phase GEMM,
+// ci contiguous.
 __global__ void conv_dx_pack_kernel(ConvArgs p, float* wt) {
-  const int64_t total = int64_t(p.G) * p.Cout_g * p.nth * p.ntw * p.Cin_g;
+  const int nt = p.nth * p.ntw;
+  const int64_t total = int64_t(p.G) * p.K * p.Cin_g;
+  const bool blocked = blocked_channels(p.Cout_g);
+  const int kblk = nt * kChanBlock;
   for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
        idx += int64_t(gridDim.x) * blockDim.x) {
     const int ci = int(idx % p.Cin_g);
-    int64_t rest = idx / p.Cin_g;
-    const int tw = int(rest % p.ntw);
-    rest /= p.ntw;
-    const int th = int(rest % p.nth);
-    const int oc = int(rest / p.nth);  // g * Cout_g + co
+    const int64_t rest = idx / p.Cin_g;
+    const int k = int(rest % p.K);
+    const int g = int(rest / p.K);
+    int co, t;
+    if (blocked) {
+      const int cb = k / kblk, rem = k - (k / kblk) * kblk;
+      t = rem / kChanBlock;
+      co = cb * kChanBlock + rem - t * kChanBlock;
+    } else {
+      co = k / nt;
+      t = k - co * nt;
+    }
+    const int th = t / p.ntw, tw = t - (t / p.ntw) * p.ntw;
     const int kh = p.kh0 + th * p.stph, kw = p.kw0 + tw * p.stpw;
-    wt[idx] = p.w[((int64_t(oc) * p.Cin_g + ci) * p.KH + kh) * p.KW + kw];
+    wt[idx] = p.w[((int64_t(g * p.Cout_g + co) * p.Cin_g + ci) * p.KH + kh) * p.KW + kw];
   }
 }
 
@@ -53,20 +67,35 @@ MX_TILE_KERNEL(C) void conv_dx_kernel(ConvArgs p) {
   int tm, tn;
   tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
   const int row0 = tm * C::BM, col0 = tn * C::BN;
+  const int split = blockIdx.y;
+  const int k0 = split * p.kps, k1 = min(p.K, k0 + p.kps);
   StridedLoader<C::BM, C::BK, MA> la;  // element (ci, k) = wt[g][k][ci]
-  la.init(p.wt + int64_t(g) * p.K * p.Cin_g, 1, p.Cin_g, row0, p.M, 0, p.K);
+  la.init(p.wt + int64_t(g) * p.K * p.Cin_g, 1, p.Cin_g, row0, p.M, k0, k1);
   LB lb;
-  lb.init(p, col0, g);
+  lb.init(p, col0, g, k0, k1);
   Acc<C> acc;
-  mainloop<C>(acc, la, lb, (p.K + C::BK - 1) / C::BK, smem);
-  for_each_acc<C>(acc, [&](int r, int c, float v) {
-    const int ci = row0 + r, pos = col0 + c;
-    if (ci < p.M && pos < p.Ncols) {
-      const int img = pos / p.HpWp;
-      const int q = pos - img * p.HpWp;
-      const int i = q / p.Wp, j = q - (q / p.Wp) * p.Wp;
-      p.out[(int64_t(img) * p.Cin + g * p.Cin_g + ci) * p.HW + (p.pa + p.sh * i) * p.W + p.pb + p.sw * j] = v;
-    }
+  mainloop<C>(acc, la, lb, (k1 - k0 + C::BK - 1) / C::BK, smem);
+  float* const out = p.splits == 1 ? p.out : p.ws + split * p.out_elems;
+  // Output offset of each fragment column (img * Cin * HW + phase position), once.
+  int cbase[C::FN];
+  bool cok[C::FN];
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    const int pos = col0 + acc_col<C>(j);
+    cok[j] = pos < p.Ncols;
+    const int pp = cok[j] ? pos : 0;
+    const int img = pp / p.HpWp;
+    const int q = pp - img * p.HpWp;
+    const int i = q / p.Wp;
+    cbase[j] = img * p.Cin * p.HW + (p.pa + p.sh * i) * p.W + p.pb + p.sw * (q - i * p.Wp);
+  }
+  for_each_acc_row<C>([&](int r, int i, int v) {
+    const int ci = row0 + r;
+    if (ci >= p.M) return;
+    float* dst = out + int64_t(g * p.Cin_g + ci) * p.HW;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+      if (cok[j]) dst[cbase[j]] = acc.v[i][j][v];
   });
 }
 
@@ -74,7 +103,7 @@ template <class C, Mode MA>
 int launch_b(ConvArgs p, int bmode, hipStream_t s) {
   p.tiles_m = (p.M + C::BM - 1) / C::BM;
   p.tiles_n = (p.Ncols + C::BN - 1) / C::BN;
-  const dim3 grid(p.tiles_m * p.tiles_n, 1, p.G);
+  const dim3 grid(p.tiles_m * p.tiles_n, p.splits, p.G);
   if (bmode == B_VEC)
     hipLaunchKernelGGL((conv_dx_kernel<C, MA, PosQuadLoader<C::BN, C::BK, true>>), grid, dim3(kThreads), 0, s, p);
   else

@@ -3,10 +3,12 @@
 // Reference behaviour followed: csrc/shaders/conv2d_tiled_body.glsl:1-87
 // (implicit-GEMM forward, bias in the store) and
 // csrc/ops/convolution.cpp:641-665 (dispatch(Forward)).
-//   C[co, pos] = W[co, (ci,kh,kw)] x im2col(x)[(ci,kh,kw), pos] + bias[co]
-// A (weights, k contiguous) is read 16 bytes per lane when K % 4 == 0; B is
-// the im2col gather, or for an unpadded 1x1 stride-1 convolution the input
-// itself read as rows of four positions.
+//   C[co, pos] = Wp[co, k] x im2col(x)[k, pos] + bias[co]
+// with k the gathered K order over (ci, kh, kw) (mx_conv_common.hpp); the
+// weights are packed to it when it differs from their own [co][ci][kh][kw].
+// A is read 16 bytes per lane when K % 4 == 0; B is the im2col gather, or for
+// an unpadded 1x1 stride-1 convolution the input itself read as rows of four
+// positions.
 #include "mx_conv_common.hpp"
 
 namespace mx {
@@ -20,28 +22,61 @@ MX_TILE_KERNEL(C) void conv_fwd_kernel(ConvArgs p) {
   int tm, tn;
   tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
   const int row0 = tm * C::BM, col0 = tn * C::BN;
+  const int split = blockIdx.y;
+  const int k0 = split * p.kps, k1 = min(p.K, k0 + p.kps);
   StridedLoader<C::BM, C::BK, MA> la;
-  la.init(p.w + int64_t(g) * p.Cout_g * p.K, p.K, 1, row0, p.M, 0, p.K);
+  la.init(p.wt + int64_t(g) * p.Cout_g * p.K, p.K, 1, row0, p.M, k0, k1);
   LB lb;
-  lb.init(p, col0, g);
+  lb.init(p, col0, g, k0, k1);
   Acc<C> acc;
-  mainloop<C>(acc, la, lb, (p.K + C::BK - 1) / C::BK, smem);
-  for_each_acc<C>(acc, [&](int r, int c, float v) {
-    const int co = row0 + r, pos = col0 + c;
-    if (co < p.M && pos < p.Ncols) {
-      const int img = pos / p.OHOW;
-      const int q = pos - img * p.OHOW;
-      const int oc = g * p.Cout_g + co;
-      p.out[(int64_t(img) * p.Cout + oc) * p.OHOW + q] = v + (p.bias ? p.bias[oc] : 0.f);
-    }
+  mainloop<C>(acc, la, lb, (k1 - k0 + C::BK - 1) / C::BK, smem);
+  // With split-K the tile goes to this split's partial output (bias added by
+  // the finalize).
+  float* const out = p.splits == 1 ? p.out : p.ws + split * p.out_elems;
+  const float* const bias = p.splits == 1 ? p.bias : nullptr;
+  // Output offset of each fragment column (img * Cout * OHOW + q), once.
+  int cbase[C::FN];
+  bool cok[C::FN];
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    const int pos = col0 + acc_col<C>(j);
+    cok[j] = pos < p.Ncols;
+    const int img = (cok[j] ? pos : 0) / p.OHOW;
+    cbase[j] = img * p.Cout * p.OHOW + (pos - img * p.OHOW);
+  }
+  for_each_acc_row<C>([&](int r, int i, int v) {
+    const int co = row0 + r;
+    if (co >= p.M) return;
+    const int oc = g * p.Cout_g + co;
+    const float b = bias ? bias[oc] : 0.f;
+    float* dst = out + int64_t(oc) * p.OHOW;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+      if (cok[j]) dst[cbase[j]] = acc.v[i][j][v] + b;
   });
+}
+
+// Wp[g][co][k] = w[g*Cout_g + co][ci][kh][kw] with k the blocked gathered
+// order (channel block, kh, kw, channel in block).
+__global__ void conv_fwd_pack_kernel(ConvArgs p, float* wp) {
+  const int64_t total = int64_t(p.Cout) * p.Cin_g * p.KK;
+  const int kblk = p.KK * kChanBlock;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int k = int(idx % p.K);
+    const int64_t oc = idx / p.K;
+    const int cb = k / kblk, rem = k - (k / kblk) * kblk;
+    const int t = rem / kChanBlock;  // kh * KW + kw
+    const int ci = cb * kChanBlock + rem - t * kChanBlock;
+    wp[idx] = p.w[(oc * p.Cin_g + ci) * p.KK + t];
+  }
 }
 
 template <class C, Mode MA>
 int launch_b(ConvArgs p, int bmode, hipStream_t s) {
   p.tiles_m = (p.M + C::BM - 1) / C::BM;
   p.tiles_n = (p.Ncols + C::BN - 1) / C::BN;
-  const dim3 grid(p.tiles_m * p.tiles_n, 1, p.G);
+  const dim3 grid(p.tiles_m * p.tiles_n, p.splits, p.G);
   if (bmode == B_VEC)
     hipLaunchKernelGGL((conv_fwd_kernel<C, MA, PosQuadLoader<C::BN, C::BK, false>>), grid, dim3(kThreads), 0, s, p);
   else
@@ -57,6 +92,14 @@ int launch_a(const ConvArgs& p, Mode ma, int bmode, hipStream_t s) {
 }
 
 }  // namespace
+
+int conv_fwd_pack_weights(const ConvArgs& p, float* wp, hipStream_t s) {
+  const int64_t total = int64_t(p.Cout) * p.Cin_g * p.KK;
+  hipLaunchKernelGGL(conv_fwd_pack_kernel, dim3(int(std::min<int64_t>((total + 255) / 256, 1 << 20))), dim3(256), 0,
+                     s, p, wp);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
 
 int conv_fwd_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t s) {
   switch (tile) {

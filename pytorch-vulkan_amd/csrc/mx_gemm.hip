@@ -49,31 +49,30 @@ MX_TILE_KERNEL(C) void gemm_kernel(GemmArgs p) {
   mainloop<C>(acc, la, lb, (p.K + C::BK - 1) / C::BK, smem);
   float* __restrict__ cb = p.c + bz * p.c_sb;
   const float alpha = p.alpha, beta = p.beta;
-  if (p.bias_kind == MX_BIAS_NONE || beta == 0.f) {
-    for_each_acc<C>(acc, [&](int r, int c, float v) {
-      const int row = row0 + r, col = col0 + c;
-      if (row < p.M && col < p.N) cb[int64_t(row) * p.ldc + col] = alpha * v;
-    });
-  } else if (p.bias_kind == MX_BIAS_COL) {
-    // One bias value per fragment column, loaded once.
-    float bcol[C::FN];
+  const int kind = (p.bias_kind == MX_BIAS_NONE || beta == 0.f) ? MX_BIAS_NONE : p.bias_kind;
+  int ccol[C::FN];
+  float bcol[C::FN];
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      const int col = col0 + acc_col<C>(j);
-      bcol[j] = col < p.N ? beta * p.bias[int64_t(col) * p.bias_sn] : 0.f;
-    }
-    for_each_acc_j<C>(acc, [&](int r, int c, int j, float v) {
-      const int row = row0 + r, col = col0 + c;
-      if (row < p.M && col < p.N) cb[int64_t(row) * p.ldc + col] = alpha * v + bcol[j];
-    });
-  } else {
-    const float* __restrict__ bias = p.bias;
-    for_each_acc<C>(acc, [&](int r, int c, float v) {
-      const int row = row0 + r, col = col0 + c;
-      if (row < p.M && col < p.N)
-        cb[int64_t(row) * p.ldc + col] = alpha * v + beta * bias[int64_t(row) * p.bias_sm + int64_t(col) * p.bias_sn];
-    });
+  for (int j = 0; j < C::FN; ++j) {
+    ccol[j] = col0 + acc_col<C>(j);
+    // Column bias (nn.Linear): one value per fragment column, loaded once.
+    bcol[j] = (kind == MX_BIAS_COL && ccol[j] < p.N) ? beta * p.bias[int64_t(ccol[j]) * p.bias_sn] : 0.f;
   }
+  for_each_acc_row<C>([&](int r, int i, int v) {
+    const int row = row0 + r;
+    if (row >= p.M) return;
+    float* __restrict__ crow = cb + int64_t(row) * p.ldc;
+    if (kind == MX_BIAS_MATRIX) {
+      const float* __restrict__ brow = p.bias + int64_t(row) * p.bias_sm;
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j)
+        if (ccol[j] < p.N) crow[ccol[j]] = alpha * acc.v[i][j][v] + beta * brow[int64_t(ccol[j]) * p.bias_sn];
+    } else {
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j)
+        if (ccol[j] < p.N) crow[ccol[j]] = alpha * acc.v[i][j][v] + bcol[j];
+    }
+  });
 }
 
 // k == 0: C = beta * bias (or zeros when beta == 0 / no bias).

@@ -135,6 +135,11 @@ CONV_CASES = [
     ((2, 64, 16, 16), 64, (3, 3), (2, 2), (1, 1), (1, 1), 1),
     ((1, 8, 20, 20), 8, (5, 5), (3, 3), (2, 2), (2, 2), 1),
     ((1, 8, 15, 15), 8, (3, 3), (2, 2), (2, 2), (2, 2), 1),
+    # channel-blocked gathered K order (channels per group a multiple of 16):
+    # grouped, strided + grouped, dilated
+    ((2, 32, 9, 9), 64, (3, 3), (1, 1), (1, 1), (1, 1), 2),
+    ((2, 64, 10, 10), 32, (3, 3), (2, 2), (1, 1), (1, 1), 2),
+    ((1, 16, 12, 12), 16, (3, 3), (1, 1), (2, 2), (2, 2), 1),
 ]
 
 
