@@ -4,9 +4,11 @@
 // (fused_adamw_step_batch_impl csrc/ops/adamw.cpp:78-284,
 // adamw_multitensor{4,8}[_amsgrad].comp, multitensor::partition
 // csrc/ops/multitensor_plan.h:22-48): one persistent launch walks a device
-// table of every tensor, each workgroup taking a contiguous run of 1024-element
-// chunks, with 128-bit loads/stores where the four (five) streams are 16-byte
-// aligned.  There is no 8-tensor or 65,535-workgroup cap; a new launch starts
+// table of every tensor in 4096-element chunks dealt round-robin to the
+// workgroups.  Where the four (five) streams are 16-byte aligned a thread issues
+// all 16 (20) of its 128-bit loads for a chunk before any arithmetic -- the
+// kernel is HBM-bound, so bytes in flight per CU set its speed -- and every
+// access is non-temporal (each byte is touched once per step).  There is no 8-tensor or 65,535-workgroup cap; a new launch starts
 // only where an entry writes memory an earlier entry of the same launch uses
 // (the reference's alias-conflict predicate, csrc/ops/adamw.cpp:207-215).
 //
@@ -29,7 +31,9 @@
 namespace mx {
 namespace {
 
-constexpr int kChunk = 1024;  // elements per chunk: 256 threads x 4
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kVec = 4;                    // float4 per stream per thread per chunk
+constexpr int kChunk = 256 * 4 * kVec;      // elements per chunk
 
 struct AdamEntry {
   float* p;
@@ -115,52 +119,68 @@ template <bool AMS>
 __global__ __launch_bounds__(256) void adamw_kernel(const AdamEntry* __restrict__ tab, AdamHP hp) {
   if (hp.found_inf && *hp.found_inf != 0.f) return;
   const float scale = hp.grad_scale ? *hp.grad_scale : 1.f;
-  const int64_t per = (hp.total_chunks + gridDim.x - 1) / gridDim.x;
-  const int64_t c0 = int64_t(blockIdx.x) * per;
-  const int64_t c1 = min(hp.total_chunks, c0 + per);
-  if (c0 >= c1) return;
-  int lo = 0, hi = hp.ntens - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (tab[mid].chunk_begin <= c0) lo = mid;
-    else hi = mid - 1;
-  }
-  int t = lo;
-  AdamEntry e = tab[t];
-  int64_t e_end = e.chunk_begin + (e.numel + kChunk - 1) / kChunk;
+  // Chunks are dealt round-robin (chunk = blockIdx.x + i * gridDim.x), so the
+  // workgroups in flight stream through neighbouring memory; each finds its
+  // tensor by binary search over the table's chunk offsets.
+  AdamEntry e = tab[0];
+  int64_t e_end = (e.numel + kChunk - 1) / kChunk;
   Coef c = coefficients(e, hp);
-  for (int64_t ch = c0; ch < c1; ++ch) {
-    while (ch >= e_end) {
-      e = tab[++t];
+  for (int64_t ch = blockIdx.x; ch < hp.total_chunks; ch += gridDim.x) {
+    if (ch >= e_end || ch < e.chunk_begin) {
+      int lo = 0, hi = hp.ntens - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tab[mid].chunk_begin <= ch) lo = mid;
+        else hi = mid - 1;
+      }
+      e = tab[lo];
       e_end = e.chunk_begin + (e.numel + kChunk - 1) / kChunk;
       c = coefficients(e, hp);
     }
-    const int64_t i0 = (ch - e.chunk_begin) * kChunk + int64_t(threadIdx.x) * 4;
-    if (e.vec && i0 + 3 < e.numel) {
-      float4 p4 = *reinterpret_cast<const float4*>(e.p + i0);
-      const float4 g4 = *reinterpret_cast<const float4*>(e.g + i0);
-      float4 m4 = *reinterpret_cast<const float4*>(e.m + i0);
-      float4 v4 = *reinterpret_cast<const float4*>(e.v + i0);
-      float4 x4 = make_float4(0.f, 0.f, 0.f, 0.f);
-      if constexpr (AMS) x4 = *reinterpret_cast<const float4*>(e.vmax + i0);
-      update<AMS>(p4.x, g4.x, m4.x, v4.x, &x4.x, c, hp, scale);
-      update<AMS>(p4.y, g4.y, m4.y, v4.y, &x4.y, c, hp, scale);
-      update<AMS>(p4.z, g4.z, m4.z, v4.z, &x4.z, c, hp, scale);
-      update<AMS>(p4.w, g4.w, m4.w, v4.w, &x4.w, c, hp, scale);
-      *reinterpret_cast<float4*>(e.p + i0) = p4;
-      *reinterpret_cast<float4*>(e.m + i0) = m4;
-      *reinterpret_cast<float4*>(e.v + i0) = v4;
-      if constexpr (AMS) *reinterpret_cast<float4*>(e.vmax + i0) = x4;
-    } else {
-      for (int64_t i = i0; i < min(i0 + 4, e.numel); ++i) {
-        float p = e.p[i], m = e.m[i], v = e.v[i];
-        float x = AMS ? e.vmax[i] : 0.f;
-        update<AMS>(p, e.g[i], m, v, &x, c, hp, scale);
-        e.p[i] = p;
-        e.m[i] = m;
-        e.v[i] = v;
-        if constexpr (AMS) e.vmax[i] = x;
+    const int64_t base = (ch - e.chunk_begin) * kChunk + int64_t(threadIdx.x) * 4;
+    if (e.vec && base + (kVec - 1) * 1024 + 3 < e.numel) {
+      // Element base + u * 1024 + (0..3): each load instruction covers 4 KiB
+      // contiguous per wave.
+      f32x4 p4[kVec], g4[kVec], m4[kVec], v4[kVec], x4[kVec];
+#pragma unroll
+      for (int u = 0; u < kVec; ++u) {
+        const int64_t i = base + u * 1024;
+        p4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.p + i));
+        g4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.g + i));
+        m4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.m + i));
+        v4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.v + i));
+        if constexpr (AMS) x4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.vmax + i));
       }
+#pragma unroll
+      for (int u = 0; u < kVec; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float pp = p4[u][j], mm = m4[u][j], vv = v4[u][j], xx = AMS ? x4[u][j] : 0.f;
+          update<AMS>(pp, g4[u][j], mm, vv, &xx, c, hp, scale);
+          p4[u][j] = pp;
+          m4[u][j] = mm;
+          v4[u][j] = vv;
+          if constexpr (AMS) x4[u][j] = xx;
+        }
+#pragma unroll
+      for (int u = 0; u < kVec; ++u) {
+        const int64_t i = base + u * 1024;
+        __builtin_nontemporal_store(p4[u], reinterpret_cast<f32x4*>(e.p + i));
+        __builtin_nontemporal_store(m4[u], reinterpret_cast<f32x4*>(e.m + i));
+        __builtin_nontemporal_store(v4[u], reinterpret_cast<f32x4*>(e.v + i));
+        if constexpr (AMS) __builtin_nontemporal_store(x4[u], reinterpret_cast<f32x4*>(e.vmax + i));
+      }
+    } else {
+      for (int u = 0; u < kVec; ++u)
+        for (int64_t i = base + u * 1024; i < min(base + u * 1024 + 4, e.numel); ++i) {
+          float p = e.p[i], m = e.m[i], v = e.v[i];
+          float x = AMS ? e.vmax[i] : 0.f;
+          update<AMS>(p, e.g[i], m, v, &x, c, hp, scale);
+          e.p[i] = p;
+          e.m[i] = m;
+          e.v[i] = v;
+          if constexpr (AMS) e.vmax[i] = x;
+        }
     }
   }
 }
@@ -275,7 +295,7 @@ extern "C" int mx_adamw_step(const mx_adamw_tensor* tensors, int64_t count, cons
       hp.total_chunks = chunks;
       Scratch dtab;
       MX_TRY(upload(tab.data(), tab.size() * sizeof(AdamEntry), s, dtab));
-      const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(chunks, int64_t(cu_count()) * 8));
+      const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(chunks, int64_t(cu_count()) * 16));
       if (ams)
         hipLaunchKernelGGL(adamw_kernel<true>, dim3(unsigned(grid)), dim3(256), 0, s, dtab.as<AdamEntry>(), hp);
       else
