@@ -1,7 +1,9 @@
 #!/usr/bin/env python
 """Benchmark of the MI355X FP32 conv / GEMM / fused-AdamW path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1|copy] [--no-cpu-baseline]
+    python bench.py --pmc-summary FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR
+    python bench.py --trace-summary KERNEL_TRACE_CSV BENCH_LOG
 
 Prints ONE JSON line.  The headline (`value`) is BASELINE.json's Conv2D
 fwd+bwd FP32 TFLOP/s on its largest single-GPU Conv2D configuration, C3: the
@@ -17,6 +19,13 @@ tensors only provide device memory and the stream.  `roofline` is measured
 live with HIP events around every launch of the timed steps, on the stream the
 kernels run on; `cpu_baseline` is CPU PyTorch (the reference's CPU
 implementation of these ops) on a bounded sample of the same workload.
+
+`roofline.traffic` (HBM bytes per launch of the dominant kernel) comes from
+two rocprofv3 PMC passes over this script (FETCH_SIZE, then WRITE_SIZE, KiB
+per dispatch), each scaled by what the same counter reads for a plain copy of
+known size (`--workload copy`); `--pmc-summary` turns the four passes into
+profiles/traffic_c3.json, which the headline run reads.  Without that file
+traffic is null.
 """
 from __future__ import annotations
 
@@ -33,6 +42,8 @@ sys.path.insert(0, os.path.join(REPO, "pytorch-vulkan_amd"))
 
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_c3.json")
+COPY_FLOATS = 256 * 1024 * 1024  # calibration copy: 1 GiB read, 1 GiB written
 METRIC = "Conv2D fwd+bwd FP32 TFLOP/s & % MFMA peak; fused AdamW GB/s; 1 MI355X"
 
 
@@ -263,16 +274,140 @@ def cpu_conv_stack(torch, batch, reps):
     return total / times[len(times) // 2] / 1e12, total, times
 
 
+# ------------------------------------------------------------------ HBM traffic (PMC)
+def kernel_class(name: str) -> str:
+    """Demangled dispatch name -> the label bench uses for its launch class."""
+    import re
+    for kind in ("conv_fwd_kernel", "conv_dx_kernel", "conv_dw_kernel"):
+        if kind in name:
+            m = re.search(r"Cfg<(\d+), (\d+), (\d+),", name)
+            return f"{kind}<{m.group(1)}x{m.group(2)}x{m.group(3)}>" if m else kind
+    m = re.search(r"(?:mx::)?(?:\(anonymous namespace\)::)?(\w+_kernel)", name)
+    return m.group(1) if m else name[:60]
+
+
+def read_pmc(directory: str, counter: str):
+    """[(dispatch id, kernel name, KiB)] from a rocprofv3 --pmc CSV directory."""
+    import csv
+    import glob
+    rows = []
+    for path in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir):
+    """Per launch class: mean HBM bytes read and written per dispatch, each
+    scaled so the calibration copy reads/writes exactly its 1 GiB."""
+    copy_bytes = COPY_FLOATS * 4
+    cf = [kib for _, name, kib in read_pmc(copy_fetch_dir, "FETCH_SIZE") if "copy" in name.lower()]
+    cw = [kib for _, name, kib in read_pmc(copy_write_dir, "WRITE_SIZE") if "copy" in name.lower()]
+    f_scale = copy_bytes / (1024.0 * max(cf)) if cf else 1.0
+    w_scale = copy_bytes / (1024.0 * max(cw)) if cw else 1.0
+    agg = defaultdict(lambda: [0, 0.0, 0, 0.0])
+    for _, name, kib in read_pmc(fetch_dir, "FETCH_SIZE"):
+        a = agg[kernel_class(name)]
+        a[0] += 1
+        a[1] += kib * 1024.0 * f_scale
+    for _, name, kib in read_pmc(write_dir, "WRITE_SIZE"):
+        a = agg[kernel_class(name)]
+        a[2] += 1
+        a[3] += kib * 1024.0 * w_scale
+    out = {"fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "kernels": {}}
+    for label, (nf, fb, nw, wb) in sorted(agg.items(), key=lambda kv: -(kv[1][1] + kv[1][3])):
+        if nf and nw:
+            out["kernels"][label] = {"dispatches": nf, "read_bytes": round(fb / nf), "write_bytes": round(wb / nw),
+                                     "bytes_per_launch": round(fb / nf + wb / nw)}
+    return out
+
+
+WINOGRAD_KERNELS = ("wino_filter_kernel", "wino_input_kernel", "wino_output_kernel", "gemm_kernel")
+BEFORE_HELPERS = ("conv_fwd_pack_kernel", "conv_dx_pack_kernel")       # run before their tile kernel
+AFTER_HELPERS = ("conv_dw_finalize_kernel", "conv_sum_splits_kernel")   # run after it
+
+
+def trace_summary(trace_csv, bench_log):
+    """Per bench launch class: the kernel time of one ABI call from a rocprofv3
+    --kernel-trace CSV of a bench.py run, comparable with that run's live
+    `avg_us`.  An ABI call can issue several dispatches (weight packing, one
+    GEMM per dInput stride phase, zero phases, the split-K sum); helper
+    dispatches are charged to the call's tile kernel (packing to the next one,
+    split sums and zero phases to the previous one), Winograd's four kernels to
+    "winograd_forward", and the class total is divided by the number of calls
+    the run made (warm-up + untimed + event-timed steps)."""
+    import csv
+    res = [json.loads(l) for l in open(bench_log) if l.startswith("{")][-1]
+    steps_run = res["warmup"] + 2 * res["steps"]
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    seq = [(kernel_class(r["Kernel_Name"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+           for r in rows]
+    owner = [None] * len(seq)
+    last_tile = None
+    for i, (label, _) in enumerate(seq):
+        if label in WINOGRAD_KERNELS:
+            owner[i] = "winograd_forward"
+        elif label in AFTER_HELPERS or label == "conv_dx_zero_kernel":
+            owner[i] = last_tile
+        elif label not in BEFORE_HELPERS:
+            owner[i] = last_tile = label
+    nxt = None
+    for i in range(len(seq) - 1, -1, -1):
+        label = seq[i][0]
+        if label in BEFORE_HELPERS or (label == "conv_dx_zero_kernel" and owner[i] is None):
+            owner[i] = nxt
+        elif owner[i] is not None and owner[i] != "winograd_forward":
+            nxt = owner[i]
+    agg = defaultdict(float)
+    for (label, us), own in zip(seq, owner):
+        agg[own or label] += us
+    out = {}
+    for label, live in res["kernels"].items():
+        calls = live["launches"] // res["steps"] * steps_run
+        if label in agg and calls:
+            out[label] = {"calls": calls, "trace_total_us": round(agg[label], 1),
+                          "trace_avg_us_per_call": round(agg[label] / calls, 2), "live_avg_us": live["avg_us"]}
+    return out
+
+
+def run_copy(torch, steps, warmup):
+    x = torch.ones(COPY_FLOATS, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(warmup):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"workload": "copy: 1 GiB device-to-device (PMC calibration)", "ms_per_step": round(dt * 1e3, 4),
+            "value": round(2 * 4 * COPY_FLOATS / dt / 1e9, 1), "unit": "GB/s"}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["c3", "c1"], default="c3")
+    ap.add_argument("--workload", choices=["c3", "c1", "copy"], default="c3")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                    help="summarise four rocprofv3 --pmc output directories into per-kernel HBM bytes")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_LOG"),
+                    help="kernel time per ABI call of each launch class from a rocprofv3 kernel trace of a "
+                         "bench.py run, next to that run's live per-call time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 forwards to implicit GEMM")
     args = ap.parse_args(argv)
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return 0
+    if args.trace_summary:
+        print(json.dumps(trace_summary(*args.trace_summary), indent=1))
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the multi-GPU "
               "sharding is a design (DESIGN.md), not a measured path.", file=sys.stderr)
@@ -286,6 +421,10 @@ def main(argv=None):
     stream = torch.cuda.current_stream().cuda_stream
     L = Launcher(mx, stream)
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
+
+    if args.workload == "copy":
+        print(json.dumps(run_copy(torch, args.steps, args.warmup)), flush=True)
+        return 0
 
     # ---------------- headline
     if args.workload == "c3":
@@ -305,6 +444,11 @@ def main(argv=None):
     log(f"headline: {ms_step:.3f} ms/step, {value:.2f} TFLOP/s")
     _, agg = run_steps(torch, L, calls, args.steps, 0, timing=True)
     roof = roofline_from(agg, "mfma")
+    if args.workload == "c3" and not args.no_winograd and os.path.exists(TRAFFIC_FILE):
+        traffic = json.load(open(TRAFFIC_FILE)).get("kernels", {}).get(roof["kernel"])
+        if traffic:
+            roof["traffic"] = traffic["bytes_per_launch"]
+            roof["traffic_source"] = os.path.relpath(TRAFFIC_FILE, REPO)
     result = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
