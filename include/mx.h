@@ -184,8 +184,9 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
 /* dw = sum over positions dy x im2col(x); db = sum over positions of dy.
  * Either dw or db may be NULL.  dispatch(Weight) + dispatch(Bias)
  * (csrc/ops/convolution.cpp:688-695, conv2d_backward_weight_tiled_body.glsl,
- * conv2d_backward_weight_finalize.comp, conv2d_backward_bias_reduce.comp),
- * fused into one launch with a deterministic split-K reduction. */
+ * conv2d_backward_weight_finalize.comp, conv2d_backward_bias_reduce.comp):
+ * dBias rides on the dWeight GEMM's dy operand; K splits are summed in split
+ * order by a finalize launch, so the result is deterministic. */
 int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const float* dy,
                               float* dw, float* db, int algo, void* stream);
 
@@ -198,8 +199,8 @@ int mx_conv2d_backward_bias(const mx_conv2d_desc* desc, const float* dy, float* 
 int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t* span,
                            int64_t* workspace_bytes);
 
-/* Name of the (first) kernel a conv call with these arguments launches, e.g.
- * "conv_dw_kernel<64x64x16>": matches the kernel-trace names of a profiler and
+/* Name of the main kernel a conv call with these arguments launches, e.g.
+ * "conv_dw_kernel<64x64x32>": matches the kernel-trace names of a profiler and
  * keys per-kernel timing (the reference's gpu_timing_stats() per shader,
  * csrc/vulkan_context.cpp:368-404). */
 int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char* buf, size_t len);
