@@ -227,6 +227,7 @@ typedef struct mx_gemm_desc {
   int64_t bias_offset, bias_stride_m, bias_stride_n;
   float alpha, beta;
   int bias_kind;
+  int64_t bias_stride_b; /* bias batch stride (0 = one bias for every batch); ABI >= 2 */
 } mx_gemm_desc;
 
 int mx_gemm_f32(const mx_gemm_desc* desc, const float* a, const float* b, const float* bias,

@@ -27,7 +27,7 @@ struct GemmArgs {
   int64_t a_sb, a_sm, a_sk;
   int64_t b_sb, b_sk, b_sn;
   int64_t c_sb, ldc;
-  int64_t bias_sm, bias_sn;
+  int64_t bias_sb, bias_sm, bias_sn;
   int M, N, K, batch, batch0;
   int tiles_m, tiles_n;
   float alpha, beta;
@@ -48,6 +48,7 @@ MX_TILE_KERNEL(C) void gemm_kernel(GemmArgs p) {
   Acc<C> acc;
   mainloop<C>(acc, la, lb, (p.K + C::BK - 1) / C::BK, smem);
   float* __restrict__ cb = p.c + bz * p.c_sb;
+  const float* __restrict__ bias = p.bias ? p.bias + bz * p.bias_sb : nullptr;
   const float alpha = p.alpha, beta = p.beta;
   const int kind = (p.bias_kind == MX_BIAS_NONE || beta == 0.f) ? MX_BIAS_NONE : p.bias_kind;
   int ccol[C::FN];
@@ -56,14 +57,14 @@ MX_TILE_KERNEL(C) void gemm_kernel(GemmArgs p) {
   for (int j = 0; j < C::FN; ++j) {
     ccol[j] = col0 + acc_col<C>(j);
     // Column bias (nn.Linear): one value per fragment column, loaded once.
-    bcol[j] = (kind == MX_BIAS_COL && ccol[j] < p.N) ? beta * p.bias[int64_t(ccol[j]) * p.bias_sn] : 0.f;
+    bcol[j] = (kind == MX_BIAS_COL && ccol[j] < p.N) ? beta * bias[int64_t(ccol[j]) * p.bias_sn] : 0.f;
   }
   for_each_acc_row<C>([&](int r, int i, int v) {
     const int row = row0 + r;
     if (row >= p.M) return;
     float* __restrict__ crow = cb + int64_t(row) * p.ldc;
     if (kind == MX_BIAS_MATRIX) {
-      const float* __restrict__ brow = p.bias + int64_t(row) * p.bias_sm;
+      const float* __restrict__ brow = bias + int64_t(row) * p.bias_sm;
 #pragma unroll
       for (int j = 0; j < C::FN; ++j)
         if (ccol[j] < p.N) crow[ccol[j]] = alpha * acc.v[i][j][v] + beta * brow[int64_t(ccol[j]) * p.bias_sn];
@@ -86,8 +87,9 @@ __global__ void gemm_k0_kernel(GemmArgs p) {
     const int bz = int(rest / p.M);
     float out = 0.f;
     if (p.bias_kind != MX_BIAS_NONE && p.beta != 0.f) {
-      const float bv = p.bias_kind == MX_BIAS_COL ? p.bias[int64_t(col) * p.bias_sn]
-                                                  : p.bias[int64_t(row) * p.bias_sm + int64_t(col) * p.bias_sn];
+      const float* bias = p.bias + int64_t(bz) * p.bias_sb;
+      const float bv = p.bias_kind == MX_BIAS_COL ? bias[int64_t(col) * p.bias_sn]
+                                                  : bias[int64_t(row) * p.bias_sm + int64_t(col) * p.bias_sn];
       out = p.beta * bv;
     }
     p.c[int64_t(bz) * p.c_sb + int64_t(row) * p.ldc + col] = out;
@@ -217,6 +219,7 @@ extern "C" int mx_gemm_f32(const mx_gemm_desc* d, const float* a, const float* b
   p.b_sn = d->b_stride_n;
   p.c_sb = d->c_stride_b;
   p.ldc = d->ldc;
+  p.bias_sb = d->bias_stride_b;
   p.bias_sm = d->bias_stride_m;
   p.bias_sn = d->bias_stride_n;
   p.M = int(d->m);

@@ -1,5 +1,6 @@
-// mm / mm.out / addmm / bmm / bmm.out for the PrivateUse1 device on the
-// MFMA GEMM of the C ABI (mx_gemm_f32).
+// mm / mm.out / addmm / bmm / bmm.out / baddbmm / addbmm (+ out= and in-place
+// forms) for the PrivateUse1 device on the MFMA GEMM of the C ABI
+// (mx_gemm_f32).
 //
 // Reference counterparts: mm_impl / mm_out csrc/ops/mm.cpp:244-383,
 // vulkan_addmm / addmm_bias_vulkan csrc/ops/mm.cpp:835-917, bmm_impl /
@@ -48,13 +49,15 @@ void run_gemm(const at::Tensor& a, const at::Tensor& b, at::Tensor& out, int64_t
   const float* bias_ptr = nullptr;
   if (bias && bias->defined() && beta != 0.f) {
     if (bias->dim() == 1 && bias->size(0) == N) {
-      d.bias_kind = MX_BIAS_COL;
+      d.bias_kind = MX_BIAS_COL;  // one row for every batch
       d.bias_stride_n = bias->stride(0);
     } else {
-      const at::Tensor e = bias->expand({M, N});
+      // Anything broadcastable to [M, N] (or [batch, M, N]); broadcast dims get stride 0.
+      const at::Tensor e = batched ? bias->expand({batch, M, N}) : bias->expand({M, N});
       d.bias_kind = MX_BIAS_MATRIX;
-      d.bias_stride_m = e.stride(0);
-      d.bias_stride_n = e.stride(1);
+      d.bias_stride_m = e.stride(-2);
+      d.bias_stride_n = e.stride(-1);
+      d.bias_stride_b = batched ? e.stride(0) : 0;
     }
     d.bias_offset = bias->storage_offset();
     bias_ptr = static_cast<const float*>(bias->storage().data());
@@ -181,10 +184,103 @@ at::Tensor& bmm_out(const at::Tensor& a, const at::Tensor& b, at::Tensor& out) {
   return out;
 }
 
+// baddbmm: out[b] = beta * self[b] + alpha * batch1[b] x batch2[b], self
+// broadcast to the product shape; beta == 0 ignores self (NaN included), as
+// baddbmm_native (csrc/ops/tensor_selection.cpp:92) and torch.  One launch:
+// the product and the scaled bias are combined in the GEMM epilogue.
+at::Tensor baddbmm(const at::Tensor& self, const at::Tensor& batch1, const at::Tensor& batch2, const at::Scalar& beta,
+                   const at::Scalar& alpha) {
+  TORCH_CHECK(batch1.dim() == 3 && batch2.dim() == 3, "baddbmm: batch1 and batch2 must be 3-D tensors");
+  TORCH_CHECK(batch1.size(0) == batch2.size(0) && batch1.size(2) == batch2.size(1),
+              "baddbmm: expected matching batch dimensions and contraction size, got ", batch1.sizes(), " and ",
+              batch2.sizes());
+  TORCH_CHECK(self.device() == batch1.device() && self.device() == batch2.device(),
+              "baddbmm: all tensors must be on the same device");
+  TORCH_CHECK(self.scalar_type() == batch1.scalar_type() && self.scalar_type() == batch2.scalar_type(),
+              "baddbmm: all tensors must have the same dtype");
+  const std::vector<int64_t> shape = {batch1.size(0), batch1.size(1), batch2.size(2)};
+  const at::Tensor bias = self.expand(shape);  // broadcast check even when beta == 0
+  if (!gemm_native(self) || !gemm_native(batch1) || !gemm_native(batch2)) {
+    note_cpu_fallback("baddbmm (non-FP32)");
+    return at::baddbmm(self.cpu(), batch1.cpu(), batch2.cpu(), beta, alpha).to(self.device());
+  }
+  c10::DeviceGuard guard(self.device());
+  at::Tensor out = at::empty(shape, batch1.options());
+  if (out.numel() == 0) return out;
+  const at::Tensor bias_arg = self.dim() == 1 && self.size(0) == shape[2] ? self : bias;
+  run_gemm(batch1, batch2, out, shape[0], &bias_arg, alpha.toFloat(), beta.toFloat());
+  return out;
+}
+
+// addbmm: out = beta * self + alpha * sum_b batch1[b] x batch2[b]
+// (addbmm_general, csrc/ops/tensor_selection.cpp:102).  The batch sum is
+// accumulated in the output: the first GEMM stores beta * self + alpha * P0,
+// each later one adds alpha * Pb with the output as its own bias (every
+// element is read and written by the same thread), in batch order.
+at::Tensor addbmm(const at::Tensor& self, const at::Tensor& batch1, const at::Tensor& batch2, const at::Scalar& beta,
+                  const at::Scalar& alpha) {
+  TORCH_CHECK(batch1.dim() == 3 && batch2.dim() == 3 && batch1.size(0) == batch2.size(0),
+              "addbmm expects matching batches");
+  TORCH_CHECK(batch1.size(2) == batch2.size(1), "addbmm: contraction sizes differ, got ", batch1.sizes(), " and ",
+              batch2.sizes());
+  TORCH_CHECK(self.device() == batch1.device() && self.device() == batch2.device(),
+              "addbmm: all tensors must be on the same device");
+  TORCH_CHECK(self.scalar_type() == batch1.scalar_type() && self.scalar_type() == batch2.scalar_type(),
+              "addbmm: all tensors must have the same dtype");
+  const std::vector<int64_t> shape = {batch1.size(1), batch2.size(2)};
+  const at::Tensor bias = self.expand(shape);
+  if (!gemm_native(self) || !gemm_native(batch1) || !gemm_native(batch2)) {
+    note_cpu_fallback("addbmm (non-FP32)");
+    return at::addbmm(self.cpu(), batch1.cpu(), batch2.cpu(), beta, alpha).to(self.device());
+  }
+  c10::DeviceGuard guard(self.device());
+  at::Tensor out = at::empty(shape, batch1.options());
+  if (out.numel() == 0) return out;
+  const float a = alpha.toFloat(), b = beta.toFloat();
+  if (batch1.size(0) == 0) {  // empty sum
+    if (b == 0.f) return out.zero_();
+    return out.copy_(at::mul(bias, beta));
+  }
+  const at::Tensor bias_arg = self.dim() == 1 && self.size(0) == shape[1] ? self : bias;
+  run_gemm(batch1.select(0, 0), batch2.select(0, 0), out, 1, &bias_arg, a, b);
+  for (int64_t i = 1; i < batch1.size(0); ++i) run_gemm(batch1.select(0, i), batch2.select(0, i), out, 1, &out, a, 1.f);
+  return out;
+}
+
+// out= and in-place forms: compute, then resize/copy into the destination.
+template <at::Tensor (*F)(const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Scalar&,
+                          const at::Scalar&)>
+at::Tensor& into_out(const at::Tensor& self, const at::Tensor& b1, const at::Tensor& b2, const at::Scalar& beta,
+                     const at::Scalar& alpha, at::Tensor& out) {
+  at::Tensor value = F(self, b1, b2, beta, alpha);
+  TORCH_CHECK(c10::canCast(value.scalar_type(), out.scalar_type()),
+              "result type cannot be cast to the desired output type");
+  at::native::resize_output(out, value.sizes());
+  out.copy_(value);
+  return out;
+}
+
+template <at::Tensor (*F)(const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Scalar&,
+                          const at::Scalar&)>
+at::Tensor& in_place(at::Tensor& self, const at::Tensor& b1, const at::Tensor& b2, const at::Scalar& beta,
+                     const at::Scalar& alpha) {
+  at::Tensor value = F(self, b1, b2, beta, alpha);
+  TORCH_CHECK(value.sizes().equals(self.sizes()), "in-place result of shape ", value.sizes(),
+              " does not match self of shape ", self.sizes());
+  self.copy_(value);
+  return self;
+}
+
 }  // namespace
 }  // namespace tvk
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+  m.impl("baddbmm", TORCH_FN(tvk::baddbmm));
+  m.impl("baddbmm.out", TORCH_FN(tvk::into_out<tvk::baddbmm>));
+  m.impl("baddbmm_", TORCH_FN(tvk::in_place<tvk::baddbmm>));
+  m.impl("addbmm", TORCH_FN(tvk::addbmm));
+  m.impl("addbmm.out", TORCH_FN(tvk::into_out<tvk::addbmm>));
+  m.impl("addbmm_", TORCH_FN(tvk::in_place<tvk::addbmm>));
   m.impl("mm", TORCH_FN(tvk::mm));
   m.impl("mm.out", TORCH_FN(tvk::mm_out));
   m.impl("addmm", TORCH_FN(tvk::addmm));

@@ -23,6 +23,7 @@ MX_COPY_H2D, MX_COPY_D2H, MX_COPY_D2D = 1, 2, 3
 MX_CONV_FORWARD, MX_CONV_DINPUT, MX_CONV_DWEIGHT, MX_CONV_DBIAS = range(4)
 ALGO_AUTO, ALGO_DIRECT, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_REDUCE = range(5)
 BIAS_NONE, BIAS_COL, BIAS_MATRIX = range(3)
+ABI_VERSION = 2  # struct layouts of include/mx.h
 
 # Every entry point declared in include/mx.h (checked by the CPU test suite).
 EXPORTS = [
@@ -53,7 +54,7 @@ class GemmDesc(C.Structure):
                 ("batch", "m", "n", "k", "a_offset", "a_stride_b", "a_stride_m", "a_stride_k",
                  "b_offset", "b_stride_b", "b_stride_k", "b_stride_n", "c_offset", "c_stride_b", "ldc",
                  "bias_offset", "bias_stride_m", "bias_stride_n")] + [
-                ("alpha", C.c_float), ("beta", C.c_float), ("bias_kind", C.c_int)]
+                ("alpha", C.c_float), ("beta", C.c_float), ("bias_kind", C.c_int), ("bias_stride_b", C.c_int64)]
 
 
 class AdamWTensor(C.Structure):
@@ -133,6 +134,8 @@ def lib() -> C.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = res
+        if L.mx_abi_version() != ABI_VERSION:
+            raise ImportError(f"{_LIB_PATH} has ABI {L.mx_abi_version()}, this binding expects {ABI_VERSION}; rebuild")
         _lib = L
     return _lib
 
@@ -196,10 +199,14 @@ def gemm(a, b, c, *, bias=None, alpha=1.0, beta=0.0, bias_kind=None, stream=None
         d.bias_kind = bias_kind
         d.bias_offset = bias.storage_offset()
         if bias_kind == BIAS_COL:
-            d.bias_stride_n = bias.stride(0)
+            d.bias_stride_n = bias.stride(-1)
+            if batched and bias.dim() == 3:
+                d.bias_stride_b = bias.stride(0)
         else:
-            e = bias.expand(m, n)
-            d.bias_stride_m, d.bias_stride_n = e.stride(0), e.stride(1)
+            e = bias.expand(a.shape[0], m, n) if batched else bias.expand(m, n)
+            d.bias_stride_m, d.bias_stride_n = e.stride(-2), e.stride(-1)
+            if batched:
+                d.bias_stride_b = e.stride(0)
         bias_base = bias.untyped_storage().data_ptr()
     assert c.stride(-1) == 1, "output rows must be contiguous"
     check(lib().mx_gemm_f32(C.byref(d), a.untyped_storage().data_ptr(), b.untyped_storage().data_ptr(), bias_base,

@@ -96,6 +96,23 @@ def test_bmm_strided(mx, bsz, m, k, n):
     close(c, a.double() @ bt.double().transpose(1, 2), mag=gemm_mag(a, bt.transpose(1, 2)))
 
 
+@pytest.mark.parametrize("bias_shape", [(6, 40, 24), (1, 40, 24), (6, 1, 24), (24,)])
+def test_bmm_batched_bias_stride(mx, bias_shape):
+    """MX_BIAS_MATRIX / COL with a bias batch stride (0 when broadcast), incl. K = 0."""
+    g = torch.Generator().manual_seed(len(bias_shape) + bias_shape[0])
+    a, b = torch.randn(6, 40, 19, generator=g), torch.randn(6, 19, 24, generator=g)
+    bias = torch.randn(bias_shape, generator=g)
+    c = torch.empty(6, 40, 24, device="cuda")
+    kind = mx.BIAS_COL if len(bias_shape) == 1 else mx.BIAS_MATRIX
+    mx.gemm(dev(a), dev(b), c, bias=dev(bias), alpha=0.5, beta=-2.0, bias_kind=kind, stream=stream())
+    ref = -2.0 * bias.double() + 0.5 * (a.double() @ b.double())
+    close(c, ref.expand(6, 40, 24), mag=2.0 * bias.double().abs().expand(6, 40, 24) + 0.5 * gemm_mag(a, b))
+    c0 = torch.empty(6, 40, 24, device="cuda")
+    mx.gemm(torch.empty(6, 40, 0, device="cuda"), torch.empty(6, 0, 24, device="cuda"), c0, bias=dev(bias),
+            beta=3.0, bias_kind=kind, stream=stream())
+    assert torch.allclose(c0.cpu(), (3.0 * bias).expand(6, 40, 24))
+
+
 def test_gemm_offset_view(mx):
     big = torch.randn(300, 200)
     a = big[7:107, 3:67]

@@ -286,6 +286,75 @@ def test_sdpa_style_attention_through_bmm(no_fallback):
     assert_close_mag(o, ref @ v.double(), ref.abs() @ v.double().abs(), rtol=2e-4, what="av")
 
 
+# ------------------------------------------------------- baddbmm / addbmm
+def test_baddbmm_beta_zero_ignores_nan_bias(no_fallback):
+    # tests/test_opinfo_regressions.py:808-811 of the reference
+    m, n = torch.randn(2, 3, 4), torch.randn(2, 4, 5)
+    bias = torch.full((5,), float("nan"))
+    got = torch.baddbmm(bias.to("vulkan"), m.to("vulkan"), n.to("vulkan"), beta=0, alpha=.5)
+    torch.testing.assert_close(got.cpu(), torch.baddbmm(bias, m, n, beta=0, alpha=.5))
+
+
+@pytest.mark.parametrize("bias_shape", [(7, 5, 9), (5, 9), (1, 9), (9,), (7, 1, 1)])
+@pytest.mark.parametrize("coefficients", [(1.0, 1.0), (0.25, -1.5)])
+def test_baddbmm_broadcast_bias_and_autograd(bias_shape, coefficients, no_fallback):
+    g = torch.Generator().manual_seed(sum(bias_shape))
+    beta, alpha = coefficients
+    a, b = torch.randn(7, 5, 33, generator=g), torch.randn(7, 9, 33, generator=g).transpose(1, 2)
+    bias = torch.randn(bias_shape, generator=g)
+    av, bv, cv = (t.to("vulkan").requires_grad_() for t in (a, b, bias))
+    out = torch.baddbmm(cv, av, bv, beta=beta, alpha=alpha)
+    ref = beta * bias.double() + alpha * (a.double() @ b.double())
+    mag = abs(beta) * bias.double().abs().expand(7, 5, 9) + abs(alpha) * (a.double().abs() @ b.double().abs())
+    assert_close_mag(out, ref, mag, what="baddbmm")
+    grad = torch.randn(7, 5, 9, generator=g)
+    ga, gb, gc = torch.autograd.grad(out, (av, bv, cv), grad.to("vulkan"))
+    assert_close_mag(ga, alpha * (grad.double() @ b.double().transpose(1, 2)),
+                     abs(alpha) * (grad.double().abs() @ b.double().abs().transpose(1, 2)), what="d batch1")
+    assert_close_mag(gb, alpha * (a.double().transpose(1, 2) @ grad.double()),
+                     abs(alpha) * (a.double().abs().transpose(1, 2) @ grad.double().abs()), what="d batch2")
+    gc_ref = (beta * grad.double()).sum_to_size(bias_shape)
+    assert_close_mag(gc, gc_ref, (abs(beta) * grad.double().abs()).sum_to_size(bias_shape), what="d self")
+
+
+@pytest.mark.parametrize("bias_shape", [(6, 10), (10,), (1, 1)])
+@pytest.mark.parametrize("coefficients", [(1.0, 1.0), (0.0, 0.75), (-0.5, 2.0)])
+def test_addbmm_sums_batches_in_order(bias_shape, coefficients, no_fallback):
+    g = torch.Generator().manual_seed(len(bias_shape))
+    beta, alpha = coefficients
+    a, b = torch.randn(4, 6, 17, generator=g), torch.randn(4, 17, 10, generator=g)
+    bias = torch.randn(bias_shape, generator=g)
+    if beta == 0:
+        bias = torch.full(bias_shape, float("nan"))
+    out = torch.addbmm(bias.to("vulkan"), a.to("vulkan"), b.to("vulkan"), beta=beta, alpha=alpha)
+    prod = (a.double() @ b.double()).sum(0)
+    ref = alpha * prod + (beta * bias.double() if beta != 0 else 0)
+    mag = abs(alpha) * (a.double().abs() @ b.double().abs()).sum(0) + (abs(beta) * bias.double().abs() if beta else 0)
+    assert_close_mag(out, ref, torch.as_tensor(mag).expand(6, 10), what="addbmm")
+
+
+def test_baddbmm_addbmm_out_and_in_place(no_fallback):
+    g = torch.Generator().manual_seed(9)
+    a, b = torch.randn(3, 4, 8, generator=g), torch.randn(3, 8, 5, generator=g)
+    c3, c2 = torch.randn(3, 4, 5, generator=g), torch.randn(4, 5, generator=g)
+    av, bv = a.to("vulkan"), b.to("vulkan")
+    out3 = torch.empty(0, device="vulkan")
+    torch.baddbmm(c3.to("vulkan"), av, bv, beta=0.5, alpha=2.0, out=out3)
+    torch.testing.assert_close(out3.cpu(), torch.baddbmm(c3, a, b, beta=0.5, alpha=2.0), rtol=1e-4, atol=1e-5)
+    inp = c3.to("vulkan")
+    inp.baddbmm_(av, bv, alpha=-1.0)
+    torch.testing.assert_close(inp.cpu(), c3.baddbmm(a, b, alpha=-1.0), rtol=1e-4, atol=1e-5)
+    out2 = torch.empty(4, 5, device="vulkan")
+    torch.addbmm(c2.to("vulkan"), av, bv, out=out2)
+    torch.testing.assert_close(out2.cpu(), torch.addbmm(c2, a, b), rtol=1e-4, atol=1e-5)
+    inp2 = c2.to("vulkan")
+    inp2.addbmm_(av, bv, beta=3.0)
+    torch.testing.assert_close(inp2.cpu(), c2.addbmm(a, b, beta=3.0), rtol=1e-4, atol=1e-5)
+    empty = torch.addbmm(c2.to("vulkan"), torch.empty(0, 4, 8, device="vulkan"), torch.empty(0, 8, 5, device="vulkan"),
+                         beta=0.5)
+    torch.testing.assert_close(empty.cpu(), 0.5 * c2)
+
+
 # --------------------------------------------------------------------- AdamW
 @pytest.mark.parametrize("shape", [(3,), (4, 5), (137, 351), (256, 1024)])
 def test_fused_adamw_matches_pytorch_cpu(shape, vk, no_fallback):
