@@ -61,6 +61,18 @@ struct Acc {
   f32x16 v[C::FM][C::FN];
 };
 
+// Branch-free guarded loads: a masked element reads a zero from kZeroPage
+// instead of its own address, so the loop has no control flow and no
+// instruction touches a loaded value before it is stored to LDS one slab
+// later.  (A branch or a select right after the load makes the compiler wait
+// for every load in flight, prefetched slabs included.)
+static __device__ __attribute__((aligned(16))) float kZeroPage[4];  // zero-initialised, never written
+
+__device__ __forceinline__ float load_or_zero(const float* p, bool ok) { return *(ok ? p : kZeroPage); }
+__device__ __forceinline__ f32x4 load4_or_zero(const float* p, bool ok) {
+  return *reinterpret_cast<const f32x4*>(ok ? p : kZeroPage);
+}
+
 template <class C>
 __device__ __forceinline__ void acc_zero(Acc<C>& acc) {
 #pragma unroll
@@ -104,6 +116,9 @@ __device__ __forceinline__ void mma_slab(Acc<C>& acc, const float* As, const flo
   for (int i = 0; i < C::FM; ++i) load_frag<C, C::BM, KMA>(a[i], As, wm * C::WTM + i * 32 + r, h);
 #pragma unroll
   for (int j = 0; j < C::FN; ++j) load_frag<C, C::BN, KMB>(b[j], Bs, wn * C::WTN + j * 32 + r, h);
+  // All fragment reads are in flight before the first MFMA; the MFMAs then
+  // wait only on their own operands (LDS returns in order).
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < C::KH; ++s)
 #pragma unroll
@@ -130,8 +145,9 @@ __device__ __forceinline__ void merge_row_sums(L&, const L&, long) {}
 // even slabs and set 1 the odd ones (each cursor steps two slabs), so the
 // global loads of slab t + 2 are in flight while slab t is multiplied and
 // slab t + 1 is written to LDS -- two slabs of MFMA time cover the load
-// latency.  Larger tiles have the registers for one set only; their longer
-// slabs (4096 MFMA cycles per wave) cover one slab of latency.
+// latency.  Larger tiles (and scalar strided operands) have the registers for
+// one set only; the 256-wide tiles' longer slabs (4096 MFMA cycles per wave)
+// cover one slab of latency.
 template <class C, class LA, class LB>
 __device__ __forceinline__ void mainloop_1deep(Acc<C>& acc, LA& la, LB& lb, int nk, float* smem) {
   float* As = smem;
@@ -145,25 +161,30 @@ __device__ __forceinline__ void mainloop_1deep(Acc<C>& acc, LA& la, LB& lb, int 
   la.store(As);
   lb.store(Bs);
   __syncthreads();
+  // Loads past the last slab read zeros (the loaders mask k >= kmax) into a
+  // stage nobody reads; issuing them unconditionally keeps the loop free of
+  // branches.
   for (int t = 0; t < nk; ++t) {
     const int cur = t & 1;
-    const bool more = t + 1 < nk;
-    if (more) {
-      la.load();
-      lb.load();
-    }
+    la.load();
+    lb.load();
     mma_slab<C, LA::KMAJOR, LB::KMAJOR>(acc, As + cur * C::A_STAGE, Bs + cur * C::B_STAGE, wm, wn, lane);
-    if (more) {
-      la.store(As + (cur ^ 1) * C::A_STAGE);
-      lb.store(Bs + (cur ^ 1) * C::B_STAGE);
-    }
+    la.store(As + (cur ^ 1) * C::A_STAGE);
+    lb.store(Bs + (cur ^ 1) * C::B_STAGE);
     __syncthreads();
   }
 }
 
+// Loaders declare DEEP = false when a second register set would not fit
+// (scalar strided modes hold a 64-bit pointer per row pass).
+template <class L>
+constexpr auto deep_ok(int) -> decltype(L::DEEP, bool()) { return L::DEEP; }
+template <class L>
+constexpr bool deep_ok(long) { return true; }
+
 template <class C, class LA, class LB>
 __device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la0, LB& lb0, int nk, float* smem) {
-  if constexpr (C::BM * C::BN > 128 * 128) {
+  if constexpr (C::BM * C::BN > 128 * 128 || !deep_ok<LA>(0) || !deep_ok<LB>(0)) {
     mainloop_1deep<C>(acc, la0, lb0, nk, smem);
   } else {
   float* const As0 = smem;
@@ -179,38 +200,32 @@ __device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la0, LB& lb0, int nk, 
   la0.kstep = lb0.kstep = la1.kstep = lb1.kstep = 2 * C::BK;
   la1.k += C::BK;
   lb1.k += C::BK;
+  // Loads past the last slab read zeros (the loaders mask k >= kmax) into a
+  // stage nobody reads; issuing loads and stores unconditionally keeps the
+  // loop free of branches, so the waits before each store cover only the
+  // older register set.
   la0.load();
   lb0.load();
-  if (nk > 1) {
-    la1.load();
-    lb1.load();
-  }
+  la1.load();
+  lb1.load();
   la0.store(As0);
   lb0.store(Bs0);
   __syncthreads();
   for (int t = 0; t < nk; t += 2) {
     // Slab t (stage 0); slab t + 1 waits in set 1.
-    if (t + 2 < nk) {
-      la0.load();
-      lb0.load();
-    }
+    la0.load();
+    lb0.load();
     mma_slab<C, LA::KMAJOR, LB::KMAJOR>(acc, As0, Bs0, wm, wn, lane);
-    if (t + 1 < nk) {
-      la1.store(As1);
-      lb1.store(Bs1);
-    }
+    la1.store(As1);
+    lb1.store(Bs1);
     __syncthreads();
     if (t + 1 >= nk) break;
     // Slab t + 1 (stage 1); slab t + 2 waits in set 0.
-    if (t + 3 < nk) {
-      la1.load();
-      lb1.load();
-    }
+    la1.load();
+    lb1.load();
     mma_slab<C, LA::KMAJOR, LB::KMAJOR>(acc, As1, Bs1, wm, wn, lane);
-    if (t + 2 < nk) {
-      la0.store(As0);
-      lb0.store(Bs0);
-    }
+    la0.store(As0);
+    lb0.store(Bs0);
     __syncthreads();
   }
   merge_row_sums(la0, la1, 0);
@@ -330,12 +345,7 @@ struct StridedLoader<ROWS, BK, Mode::KVEC> {
     const int kk = k + 4 * kq;
     const bool kin = kk < kmax;
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      if (ok[p] && kin)
-        v[p] = *reinterpret_cast<const f32x4*>(ptr[p] + k);
-      else
-        v[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int p = 0; p < PASSES; ++p) v[p] = load4_or_zero(ptr[p] + k, ok[p] && kin);
     k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
@@ -378,10 +388,7 @@ struct StridedLoader<ROWS, BK, Mode::RVEC> {
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       const int kx = k + kk + p * KPP;
-      if (ok && kx < kmax)
-        v[p] = *reinterpret_cast<const f32x4*>(ptr + int64_t(kx) * s_k);
-      else
-        v[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+      v[p] = load4_or_zero(ptr + int64_t(kx) * s_k, ok && kx < kmax);
     }
     k += kstep;
   }
@@ -397,6 +404,7 @@ struct StridedLoader<ROWS, BK, Mode::RVEC> {
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
   static constexpr bool KMAJOR = false;
+  static constexpr bool DEEP = false;
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int RPP = kThreads / BK;
   static constexpr int PASSES = ROWS / RPP;
@@ -424,7 +432,7 @@ struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
     const bool kin = kx < kmax;
     const int64_t off = int64_t(kx) * s_k;
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) v[p] = (ok[p] && kin) ? ptr[p][off] : 0.f;
+    for (int p = 0; p < PASSES; ++p) v[p] = load_or_zero(ptr[p] + off, ok[p] && kin);
     k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
@@ -438,6 +446,7 @@ struct StridedLoader<ROWS, BK, Mode::KSCALAR> {
 template <int ROWS, int BK>
 struct StridedLoader<ROWS, BK, Mode::RSCALAR> {
   static constexpr bool KMAJOR = false;
+  static constexpr bool DEEP = false;
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static_assert(kThreads % ROWS == 0 || ROWS % kThreads == 0, "RSCALAR tiling");
   static constexpr int EPT = ROWS * BK / kThreads;   // consecutive k per thread
@@ -462,7 +471,7 @@ struct StridedLoader<ROWS, BK, Mode::RSCALAR> {
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const int kx = k + ks + e;
-      v[e] = (ok && kx < kmax) ? ptr[int64_t(kx) * s_k] : 0.f;
+      v[e] = load_or_zero(ptr + int64_t(kx) * s_k, ok && kx < kmax);
     }
     k += kstep;
   }

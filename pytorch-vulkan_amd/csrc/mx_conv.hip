@@ -379,7 +379,6 @@ GemmPlan plan_gemm(int64_t M, int64_t Ncols, int64_t K, int64_t G, unsigned tile
 
 constexpr unsigned kAllTiles = (1u << conv::NTILES) - 1;
 constexpr unsigned kSinglePassTiles = kAllTiles & ~(1u << conv::NARROW);  // forward / dInput
-constexpr unsigned kNoWideTiles = kAllTiles & ~((1u << conv::TALL) | (1u << conv::WIDE));
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
@@ -395,10 +394,17 @@ struct DwPlan {
 
 // dWeight: K = N*OH*OW positions, split so every CU gets work; each split
 // writes one full-size partial dW that the finalize re-reads.
-DwPlan plan_dw(const ConvArgs& p, bool with_db, bool gathers) {
+// `x_gather`: the x operand is the column gather (any kernel but an unpadded
+// 1x1 stride-1 one with 4-aligned planes); `dy_gather`: dy is read as scalar
+// rows (OH*OW % 4 != 0).  Gathers over 256 columns (and a 256-wide tile with
+// both gathers) are not built.
+DwPlan plan_dw(const ConvArgs& p, bool with_db, bool x_gather, bool dy_gather) {
   DwPlan pl;
   const int64_t out = int64_t(p.G) * p.Cout_g * p.Ncols;
-  pl.g = plan_gemm(p.M, p.Ncols, p.K, p.G, gathers ? kNoWideTiles : kAllTiles, 65535, out);
+  unsigned tiles = kAllTiles;
+  if (x_gather) tiles &= ~((1u << conv::WIDE) | (1u << conv::FLAT));
+  if (x_gather && dy_gather) tiles &= ~(1u << conv::TALL);
+  pl.g = plan_gemm(p.M, p.Ncols, p.K, p.G, tiles, 65535, out);
   if (pl.g.splits > 1) {
     pl.ws_bytes = int64_t(pl.g.splits) * out * 4;
     pl.db_bytes = with_db ? int64_t(pl.g.splits) * p.Cout * 4 : 0;
@@ -434,8 +440,12 @@ AxisPhase axis_phase(int a, int in, int k, int s, int pad, int dil) {
   return ph;
 }
 
+// Forward plan.  With K % 4 != 0 the weights load as scalars, for which no
+// 256-row tile is built.
 GemmPlan plan_fwd(const ConvArgs& p) {
-  return plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G, kSinglePassTiles, 512,
+  const bool scalar_w = (int64_t(p.Cin_g) * p.KK) % 4 != 0;
+  return plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G,
+                   scalar_w ? kSinglePassTiles & ~(1u << conv::TALL) : kSinglePassTiles, 512,
                    int64_t(p.N) * p.Cout * p.OHOW);
 }
 
@@ -657,7 +667,7 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
   p.K = p.N * p.OHOW;
   const int amode = (p.OHOW % 4 == 0 && aligned16(dy)) ? conv::B_VEC : conv::B_GATHER;
   const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
-  const DwPlan pl = plan_dw(p, db != nullptr, amode == conv::B_GATHER && bmode == conv::B_GATHER);
+  const DwPlan pl = plan_dw(p, db != nullptr, bmode == conv::B_GATHER, amode == conv::B_GATHER);
   p.splits = pl.g.splits;
   p.kps = pl.g.kps;
   if (pl.g.splits == 1) return conv::conv_dw_launch(p, pl.g.tile, amode, bmode, s);
@@ -698,8 +708,7 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
     p.M = p.Cout_g;
     p.Ncols = p.Cin_g * p.KK;
     p.K = p.N * p.OHOW;
-    const bool gathers = p.OHOW % 4 != 0 && !(unpadded_1x1(p) && p.HW % 4 == 0);
-    name = cat("conv_dw_kernel<", kTileInfo[plan_dw(p, true, gathers).g.tile].name, ">");
+    name = cat("conv_dw_kernel<", kTileInfo[plan_dw(p, true, !(unpadded_1x1(p) && p.HW % 4 == 0), p.OHOW % 4 != 0).g.tile].name, ">");
   }
   if (len) {
     std::strncpy(buf, name.c_str(), len - 1);
@@ -717,8 +726,7 @@ int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t*
   p.M = p.Cout_g;
   p.Ncols = p.Cin_g * p.KK;
   p.K = p.N * p.OHOW;
-  const bool gathers = p.OHOW % 4 != 0 && !(unpadded_1x1(p) && p.HW % 4 == 0);
-  const DwPlan pl = plan_dw(p, true, gathers);
+  const DwPlan pl = plan_dw(p, true, !(unpadded_1x1(p) && p.HW % 4 == 0), p.OHOW % 4 != 0);
   if (splits) *splits = pl.g.splits;
   if (span) *span = pl.g.kps;
   if (workspace_bytes) *workspace_bytes = pl.ws_bytes + pl.db_bytes;

@@ -75,6 +75,7 @@ __host__ __device__ constexpr bool blocked_channels(int c) { return c % kChanBlo
 template <int ROWS, int BK>
 struct Im2colLoader {
   static constexpr bool KMAJOR = false;
+  static constexpr bool DEEP = false;  // its per-thread state leaves no room for a second set at 64x64
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int EPT = ROWS * BK / kThreads;
   static_assert(ROWS <= kThreads && EPT >= 1 && BK % EPT == 0 && kChanBlock % EPT == 0, "Im2colLoader tiling");
@@ -121,9 +122,9 @@ struct Im2colLoader {
       const int c = cb * kChanBlock + (rem - t * kChanBlock);
       const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
       const bool valid = ok && kb < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-      const float* src = xg + (valid ? c * HW + ih * W + iw : 0);
+      const float* src = xg + (c * HW + ih * W + iw);
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) v[e] = valid ? src[e * HW] : 0.f;
+      for (int e = 0; e < EPT; ++e) v[e] = load_or_zero(src + e * HW, valid);
     } else {
       // (ci, kh, kw) with kw fastest.
       int ci = kb / KK;
@@ -134,7 +135,7 @@ struct Im2colLoader {
       for (int e = 0; e < EPT; ++e) {
         const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
         const bool valid = ok && (kb + e) < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-        v[e] = valid ? xg[ci * HW + ih * W + iw] : 0.f;
+        v[e] = load_or_zero(xg + ci * HW + ih * W + iw, valid);
         if (++kw == KW) {
           kw = 0;
           if (++kh == KH) {
@@ -196,10 +197,7 @@ struct PosQuadLoader {
 #pragma unroll
     for (int q = 0; q < PASSES; ++q) {
       const int kx = k + kk + q * KPP;
-      if (ok && kx < kmax)
-        v[q] = *reinterpret_cast<const f32x4*>(ptr + int64_t(kx) * hw);
-      else
-        v[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+      v[q] = load4_or_zero(ptr + int64_t(kx) * hw, ok && kx < kmax);
     }
     k += kstep;
   }
@@ -264,9 +262,9 @@ struct PhaseGatherLoader {
       const int co = cb * kChanBlock + (rem - t * kChanBlock);
       const int oh = ib - th * dsh, ow = jb - tw * dsw;
       const bool valid = ok && kb < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
-      const float* src = dyg + (valid ? co * OHOW + oh * OW + ow : 0);
+      const float* src = dyg + (co * OHOW + oh * OW + ow);
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) v[e] = valid ? src[e * OHOW] : 0.f;
+      for (int e = 0; e < EPT; ++e) v[e] = load_or_zero(src + e * OHOW, valid);
     } else {
       // (co, th, tw) with tw fastest.
       int co = kb / NT;
@@ -277,7 +275,7 @@ struct PhaseGatherLoader {
       for (int e = 0; e < EPT; ++e) {
         const int oh = ib - th * dsh, ow = jb - tw * dsw;
         const bool valid = ok && (kb + e) < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
-        v[e] = valid ? dyg[co * OHOW + oh * OW + ow] : 0.f;
+        v[e] = load_or_zero(dyg + co * OHOW + oh * OW + ow, valid);
         if (++tw == ntw) {
           tw = 0;
           if (++th == nth) {
@@ -311,6 +309,7 @@ struct PhaseGatherLoader {
 template <int ROWS, int BK>
 struct DyRowsLoader {
   static constexpr bool KMAJOR = false;
+  static constexpr bool DEEP = false;  // a pointer offset, flag and row sum per pass: one register set
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int LPR = BK;  // lanes per row
   static constexpr int RPP = kThreads / BK;
@@ -339,13 +338,17 @@ struct DyRowsLoader {
     kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
+    // One register set (DEEP = false): clamped 32-bit offsets and a select.
     const int kx = k + kk;
     const bool kin = kx < kmax;
-    const int img = kx / OHOW;
-    const int base = img * COHOW + (kx - img * OHOW);
+    const int kc = kin ? kx : 0;
+    const int img = kc / OHOW;
+    const int base = img * COHOW + (kc - img * OHOW);
 #pragma unroll
     for (int q = 0; q < PASSES; ++q) {
-      v[q] = (ok[q] && kin) ? dyg[base + coff[q]] : 0.f;
+      const bool use = ok[q] && kin;
+      const float t = dyg[use ? base + coff[q] : 0];
+      v[q] = use ? t : 0.f;
       bsum[q] += v[q];
     }
     k += kstep;
@@ -400,10 +403,7 @@ struct PosKLoader {
     const float* src = base + int64_t(img) * cs + (kx - img * hw);
 #pragma unroll
     for (int q = 0; q < PASSES; ++q) {
-      if (ok[q] && kin)
-        v[q] = *reinterpret_cast<const f32x4*>(src + roff[q]);
-      else
-        v[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+      v[q] = load4_or_zero(src + roff[q], ok[q] && kin);
       if constexpr (DY) bsum[q] += (v[q][0] + v[q][1]) + (v[q][2] + v[q][3]);
     }
     k += kstep;
@@ -422,6 +422,7 @@ struct PosKLoader {
 template <int ROWS, int BK>
 struct XColsLoader {
   static constexpr bool KMAJOR = false;
+  static constexpr bool DEEP = false;  // three per-pass offsets: one register set
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int RPP = kThreads / BK;
   static constexpr int PASSES = ROWS / RPP;
@@ -461,10 +462,12 @@ struct XColsLoader {
     kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
+    // One register set (DEEP = false): clamped 32-bit offsets and a select.
     const int kx = k + kk;
     const bool kin = kx < kmax;
-    const int img = kx / OHOW;
-    const int q0 = kx - img * OHOW;
+    const int kc = kin ? kx : 0;
+    const int img = kc / OHOW;
+    const int q0 = kc - img * OHOW;
     const int oh = q0 / OW;
     const int ow = q0 - oh * OW;
     const int ihb = oh * sh, iwb = ow * sw;
@@ -473,7 +476,8 @@ struct XColsLoader {
     for (int q = 0; q < PASSES; ++q) {
       const int ih = ihb + khd[q], iw = iwb + kwd[q];
       const bool valid = kin && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-      v[q] = valid ? xi[coff[q] + ih * W + iw] : 0.f;
+      const float t = xi[valid ? coff[q] + ih * W + iw : 0];
+      v[q] = valid ? t : 0.f;
     }
     k += kstep;
   }

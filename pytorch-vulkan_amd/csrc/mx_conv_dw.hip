@@ -108,9 +108,11 @@ int launch_b(ConvArgs p, int bmode, hipStream_t s) {
   if (bmode == B_VEC) {
     hipLaunchKernelGGL((conv_dw_kernel<C, LA, PosKLoader<C::BN, C::BK, false>>), grid, dim3(kThreads), 0, s, p);
   } else {
-    // Two scalar gathers do not fit a 256-wide tile in registers; the planner
-    // never pairs them.
-    constexpr bool fits = LA::KMAJOR || C::BM * C::BN <= 128 * 128 || !std::is_same_v<LA, DyRowsLoader<C::BM, C::BK>>;
+    // The x-column gather over 256 columns, or paired with the scalar dy rows
+    // on a 256-wide tile, does not fit the register budget; the planner never
+    // picks those.
+    constexpr bool dy_rows = std::is_same_v<LA, DyRowsLoader<C::BM, C::BK>>;
+    constexpr bool fits = C::BN <= 128 && (C::BM * C::BN <= 128 * 128 || !dy_rows);
     if constexpr (fits)
       hipLaunchKernelGGL((conv_dw_kernel<C, LA, XColsLoader<C::BN, C::BK>>), grid, dim3(kThreads), 0, s, p);
     else

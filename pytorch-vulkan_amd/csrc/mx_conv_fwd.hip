@@ -88,7 +88,10 @@ int launch_b(ConvArgs p, int bmode, hipStream_t s) {
 template <class C>
 int launch_a(const ConvArgs& p, Mode ma, int bmode, hipStream_t s) {
   if (ma == Mode::KVEC) return launch_b<C, Mode::KVEC>(p, bmode, s);
-  return launch_b<C, Mode::KSCALAR>(p, bmode, s);
+  // Scalar weights (K % 4 != 0) keep a pointer per row pass: not built for
+  // 256-row tiles, which the planner does not pick for them.
+  if constexpr (C::BM <= 128) return launch_b<C, Mode::KSCALAR>(p, bmode, s);
+  return set_error(MX_ERR_INVALID, "conv2d forward: 256-row tile with scalar weight loads");
 }
 
 }  // namespace

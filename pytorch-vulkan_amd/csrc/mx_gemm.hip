@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "mfma_core.hpp"
 #include "mx_internal.hpp"
@@ -171,7 +172,13 @@ constexpr TileChoice kTiles[] = {{256, 128, 2, 1.0}, {128, 256, 2, 1.0}, {128, 1
 
 // Cheapest tile by a wave-quantised cost model: rounds of resident tiles
 // times the time of one round (per_cu tiles per CU at the relative rate).
+// MX_GEMM_TILE=<index into kTiles> forces a tile (tuning and diagnosis; the
+// 256-wide tiles only for 16-byte operand modes).
 int pick_gemm_tile(int64_t m, int64_t n, int64_t batch, bool vec) {
+  if (const char* e = std::getenv("MX_GEMM_TILE")) {
+    const int t = std::atoi(e);
+    if (t >= (vec ? 0 : 2) && t < 4) return t;
+  }
   int best = 2;
   double best_cost = 0;
   for (int i = vec ? 0 : 2; i < 4; ++i) {
