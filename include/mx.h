@@ -271,6 +271,92 @@ typedef struct mx_adamw_hparams {
 int mx_adamw_step(const mx_adamw_tensor* tensors, int64_t count, const mx_adamw_hparams* hp,
                   int64_t* launches, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Normalisation, activation, resampling, softmax, loss and concatenation   */
+/* of the C3/C4 training steps (FP32, contiguous NCHW; rows r = n*C + c of  */
+/* hw = H*W elements).  Results follow torch's CPU operators, the parity     */
+/* target of the reference's kernels for the same ops.                       */
+/* ------------------------------------------------------------------------ */
+
+/* native_group_norm (csrc/ops/group_norm.cpp:73-107, group_norm_forward.comp):
+ * y = (x - mean[n,g]) * rstd[n,g] * gamma[c] + beta[c]; mean / rstd are
+ * [n, groups] (rstd = 1/sqrt(var + eps), biased variance).  gamma and beta may
+ * be NULL (1 and 0).  n == 0 is a no-op. */
+int mx_group_norm_forward(const float* x, const float* gamma, const float* beta, int64_t n, int64_t c,
+                          int64_t hw, int64_t groups, float eps, float* y, float* mean, float* rstd,
+                          void* stream);
+/* native_group_norm_backward (csrc/ops/group_norm.cpp:109-153,
+ * group_norm_backward_input.comp, group_norm_backward_affine.comp) from the
+ * saved mean / rstd.  Any of dx, dgamma, dbeta may be NULL (not computed);
+ * n == 0 writes zero dgamma / dbeta. */
+int mx_group_norm_backward(const float* dy, const float* x, const float* mean, const float* rstd,
+                           const float* gamma, int64_t n, int64_t c, int64_t hw, int64_t groups, float* dx,
+                           float* dgamma, float* dbeta, void* stream);
+
+/* native_batch_norm (csrc/ops/batch_norm.cpp:21-82, batch_norm_forward.comp).
+ * training: batch statistics over (n, hw) per channel into save_mean /
+ * save_invstd (invstd 0 when var == eps == 0), running statistics (element
+ * strides rm_stride / rv_stride; NULL to skip) updated with momentum and the
+ * unbiased variance.  evaluation: running statistics normalise.  gamma / beta
+ * may be NULL. */
+int mx_batch_norm_forward(const float* x, const float* gamma, const float* beta, float* running_mean,
+                          int64_t rm_stride, float* running_var, int64_t rv_stride, int64_t n, int64_t c,
+                          int64_t hw, int training, float momentum, float eps, float* y, float* save_mean,
+                          float* save_invstd, void* stream);
+/* native_batch_norm_backward (csrc/ops/batch_norm.cpp:83-110,
+ * batch_norm_backward.comp).  training: `mean` / `invstd_or_var` are the saved
+ * batch mean and inverse std; evaluation: the running mean and variance
+ * (contiguous).  dx, dgamma, dbeta may be NULL. */
+int mx_batch_norm_backward(const float* dy, const float* x, const float* gamma, const float* mean,
+                           const float* invstd_or_var, int64_t n, int64_t c, int64_t hw, int training, float eps,
+                           float* dx, float* dgamma, float* dbeta, void* stream);
+
+/* Pointwise ops on `count` contiguous floats.  SiLU: x / (1 + exp(-x))
+ * (csrc/ops/diffusion_unary.cpp:143, diffusion_unary.comp op 0); ReLU:
+ * x <= 0 ? 0 : x, NaN kept (csrc/ops/mm.cpp:475-480). */
+enum mx_unary_op { MX_UNARY_SILU = 0, MX_UNARY_RELU = 1 };
+int mx_unary_f32(int op, const float* x, float* y, int64_t count, void* stream);
+/* silu_backward: dy * s * (1 + x * (1 - s)), s = sigmoid(x)
+ * (csrc/ops/diffusion_unary.cpp:151, diffusion_unary_backward.comp);
+ * threshold_backward: x <= threshold ? 0 : dy (csrc/ops/mm.cpp:484-495). */
+enum mx_unary_grad_op { MX_UNARY_SILU_GRAD = 0, MX_UNARY_THRESHOLD_GRAD = 1 };
+int mx_unary_backward_f32(int op, const float* dy, const float* x, float threshold, float* dx,
+                          int64_t count, void* stream);
+
+/* upsample_nearest2d over `planes` = N*C planes (csrc/ops/upsample.cpp:7-45,
+ * upsample_nearest2d.comp): source index = o for equal sizes, o >> 1 for
+ * exact doubling, else min(floor(o * s), in - 1) with s = (float)(1/scale)
+ * when scale > 0, else (float)in / out. */
+int mx_upsample_nearest2d(const float* x, int64_t planes, int64_t ih, int64_t iw, int64_t oh, int64_t ow,
+                          double scale_h, double scale_w, float* y, void* stream);
+/* upsample_nearest2d_backward (csrc/ops/upsample.cpp:46-56): each input pixel
+ * sums the output gradients that read it, in row-major output order. */
+int mx_upsample_nearest2d_backward(const float* dy, int64_t planes, int64_t ih, int64_t iw, int64_t oh,
+                                   int64_t ow, double scale_h, double scale_w, float* dx, void* stream);
+
+/* _softmax over the middle axis of a contiguous [outer, axis, inner] view
+ * (csrc/ops/mm.cpp:1100, softmax_axis.comp): exp(x - max) * (1 / sum). */
+int mx_softmax_f32(const float* x, int64_t outer, int64_t axis, int64_t inner, float* y, void* stream);
+/* _softmax_backward_data (csrc/ops/softmax_axis_backward.cpp:11-38):
+ * dx = y * (dy - sum(dy * y)). */
+int mx_softmax_backward_f32(const float* dy, const float* y, int64_t outer, int64_t axis, int64_t inner,
+                            float* dx, void* stream);
+
+/* mse_loss (csrc/ops/loss_primitives.cpp:349-352): reduction NONE writes
+ * (x - t)^2 elementwise, MEAN / SUM one float (mean of nothing is NaN). */
+enum mx_reduction { MX_REDUCE_NONE = 0, MX_REDUCE_MEAN = 1, MX_REDUCE_SUM = 2 };
+int mx_mse_loss_f32(const float* x, const float* t, int64_t count, int reduction, float* out, void* stream);
+/* mse_loss_backward (csrc/ops/loss_primitives.cpp:353-356):
+ * dx = norm * (x - t) * dy, norm = 2/count for MEAN else 2; dy is one device
+ * float for MEAN / SUM and `count` floats for NONE. */
+int mx_mse_loss_backward_f32(const float* dy, const float* x, const float* t, int64_t count, int reduction,
+                             float* dx, void* stream);
+
+/* Copy `rows` rows of `row_bytes` bytes between pitched buffers: one input's
+ * slab of cat along any axis (csrc/ops/cat.cpp:44-55, cat_copy.comp). */
+int mx_copy_rows(void* dst, int64_t dst_pitch, const void* src, int64_t src_pitch, int64_t row_bytes,
+                 int64_t rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

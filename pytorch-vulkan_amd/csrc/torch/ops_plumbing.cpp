@@ -221,8 +221,16 @@ at::Tensor& zero_(at::Tensor& self) { return fill_scalar(self, 0); }
 
 bool is_host_scalar(const at::Tensor& t) { return t.device().is_cpu() && t.dim() == 0; }
 
+// A 0-dim CPU operand (a Python number arrives as a wrapped double) joins an
+// FP32 device tensor on the device when the result stays FP32.
+bool f32_with_host_scalar(const at::Tensor& dev_t, const at::Tensor& oth) {
+  return dev_t.scalar_type() == at::kFloat && is_host_scalar(oth) && !oth.is_complex() &&
+         at::result_type(dev_t, oth) == at::kFloat;
+}
+
 at::Tensor add_tensor(const at::Tensor& self, const at::Tensor& other, const at::Scalar& alpha) {
-  const bool f32 = self.scalar_type() == at::kFloat && other.scalar_type() == at::kFloat;
+  const bool f32 = (self.scalar_type() == at::kFloat && other.scalar_type() == at::kFloat) ||
+                   f32_with_host_scalar(self, other);
   if (f32 && is_vk(self) && !self.is_neg() && (is_host_scalar(other) || (is_vk(other) && !other.is_neg()))) {
     c10::DeviceGuard guard(self.device());
     if (is_host_scalar(other)) {
@@ -248,9 +256,10 @@ at::Tensor add_tensor(const at::Tensor& self, const at::Tensor& other, const at:
 }
 
 at::Tensor mul_tensor(const at::Tensor& self, const at::Tensor& other) {
-  const bool f32 = self.scalar_type() == at::kFloat && other.scalar_type() == at::kFloat;
   const at::Tensor& dev_t = is_vk(self) ? self : other;
   const at::Tensor& oth = is_vk(self) ? other : self;
+  const bool f32 = (self.scalar_type() == at::kFloat && other.scalar_type() == at::kFloat) ||
+                   f32_with_host_scalar(dev_t, oth);
   if (f32 && is_vk(dev_t) && !dev_t.is_neg() && (is_host_scalar(oth) || (is_vk(oth) && !oth.is_neg()))) {
     c10::DeviceGuard guard(dev_t.device());
     if (is_host_scalar(oth)) {

@@ -12,6 +12,7 @@ the same HIP runtime (torch/lib/libamdhip64.so).
 from __future__ import annotations
 
 import ctypes as C
+import math
 import os
 
 import torch  # noqa: F401  (HIP runtime first, see module docstring)
@@ -35,6 +36,9 @@ EXPORTS = [
     "mx_add_f32", "mx_scale_f32", "mx_mul_f32", "mx_sum_f32", "mx_foreach_add_scalar_f32", "mx_conv2d_check",
     "mx_conv2d_select", "mx_conv2d_forward", "mx_conv2d_backward_input", "mx_conv2d_backward_weight",
     "mx_conv2d_backward_bias", "mx_conv2d_dweight_plan", "mx_conv2d_kernel_name", "mx_gemm_f32", "mx_adamw_step",
+    "mx_group_norm_forward", "mx_group_norm_backward", "mx_batch_norm_forward", "mx_batch_norm_backward",
+    "mx_unary_f32", "mx_unary_backward_f32", "mx_upsample_nearest2d", "mx_upsample_nearest2d_backward",
+    "mx_softmax_f32", "mx_softmax_backward_f32", "mx_mse_loss_f32", "mx_mse_loss_backward_f32", "mx_copy_rows",
 ]
 
 
@@ -129,6 +133,20 @@ def lib() -> C.CDLL:
             "mx_conv2d_kernel_name": ([C.POINTER(ConvDesc), i32, i32, C.c_char_p, C.c_size_t], i32),
             "mx_gemm_f32": ([C.POINTER(GemmDesc), vp, vp, vp, vp, vp], i32),
             "mx_adamw_step": ([C.POINTER(AdamWTensor), i64, C.POINTER(AdamWHParams), C.POINTER(i64), vp], i32),
+            "mx_group_norm_forward": ([vp, vp, vp, i64, i64, i64, i64, C.c_float, vp, vp, vp, vp], i32),
+            "mx_group_norm_backward": ([vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp], i32),
+            "mx_batch_norm_forward": ([vp, vp, vp, vp, i64, vp, i64, i64, i64, i64, i32, C.c_float, C.c_float,
+                                       vp, vp, vp, vp], i32),
+            "mx_batch_norm_backward": ([vp, vp, vp, vp, vp, i64, i64, i64, i32, C.c_float, vp, vp, vp, vp], i32),
+            "mx_unary_f32": ([i32, vp, vp, i64, vp], i32),
+            "mx_unary_backward_f32": ([i32, vp, vp, C.c_float, vp, i64, vp], i32),
+            "mx_upsample_nearest2d": ([vp, i64, i64, i64, i64, i64, C.c_double, C.c_double, vp, vp], i32),
+            "mx_upsample_nearest2d_backward": ([vp, i64, i64, i64, i64, i64, C.c_double, C.c_double, vp, vp], i32),
+            "mx_softmax_f32": ([vp, i64, i64, i64, vp, vp], i32),
+            "mx_softmax_backward_f32": ([vp, vp, i64, i64, i64, vp, vp], i32),
+            "mx_mse_loss_f32": ([vp, vp, i64, i32, vp, vp], i32),
+            "mx_mse_loss_backward_f32": ([vp, vp, vp, i64, i32, vp, vp], i32),
+            "mx_copy_rows": ([vp, i64, vp, i64, i64, i64, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -237,6 +255,97 @@ def adamw_step(params, grads, exp_avgs, exp_avg_sqs, *, lr, beta1, beta2, eps, w
 
 def sum_mid(out, src, outer, reduce, inner, stream=None) -> None:
     check(lib().mx_sum_f32(ptr(out), ptr(src), outer, reduce, inner, stream))
+
+
+UNARY_SILU, UNARY_RELU = 0, 1
+UNARY_SILU_GRAD, UNARY_THRESHOLD_GRAD = 0, 1
+REDUCE_NONE, REDUCE_MEAN, REDUCE_SUM = 0, 1, 2
+
+
+def group_norm_forward(x, gamma, beta, groups, eps, y, mean, rstd, stream=None) -> None:
+    """x [N, C, *] contiguous FP32; mean / rstd [N, groups]."""
+    n, c = x.shape[0], x.shape[1]
+    hw = math.prod(x.shape[2:])
+    check(lib().mx_group_norm_forward(ptr(x), ptr(gamma), ptr(beta), n, c, hw, groups, eps, ptr(y), ptr(mean),
+                                      ptr(rstd), stream))
+
+
+def group_norm_backward(dy, x, mean, rstd, gamma, groups, dx, dgamma, dbeta, stream=None) -> None:
+    n, c = x.shape[0], x.shape[1]
+    hw = math.prod(x.shape[2:])
+    check(lib().mx_group_norm_backward(ptr(dy), ptr(x), ptr(mean), ptr(rstd), ptr(gamma), n, c, hw, groups,
+                                       ptr(dx), ptr(dgamma), ptr(dbeta), stream))
+
+
+def batch_norm_forward(x, gamma, beta, running_mean, running_var, training, momentum, eps, y, save_mean,
+                       save_invstd, stream=None) -> None:
+    n, c = x.shape[0], x.shape[1]
+    hw = math.prod(x.shape[2:])
+    rms = running_mean.stride(0) if running_mean is not None else 0
+    rvs = running_var.stride(0) if running_var is not None else 0
+    check(lib().mx_batch_norm_forward(ptr(x), ptr(gamma), ptr(beta), ptr(running_mean), rms, ptr(running_var), rvs,
+                                      n, c, hw, 1 if training else 0, momentum, eps, ptr(y), ptr(save_mean),
+                                      ptr(save_invstd), stream))
+
+
+def batch_norm_backward(dy, x, gamma, mean, invstd_or_var, training, eps, dx, dgamma, dbeta, stream=None) -> None:
+    n, c = x.shape[0], x.shape[1]
+    hw = math.prod(x.shape[2:])
+    check(lib().mx_batch_norm_backward(ptr(dy), ptr(x), ptr(gamma), ptr(mean), ptr(invstd_or_var), n, c, hw,
+                                       1 if training else 0, eps, ptr(dx), ptr(dgamma), ptr(dbeta), stream))
+
+
+def unary(op, x, y, stream=None) -> None:
+    check(lib().mx_unary_f32(op, ptr(x), ptr(y), x.numel(), stream))
+
+
+def unary_backward(op, dy, x, dx, threshold=0.0, stream=None) -> None:
+    check(lib().mx_unary_backward_f32(op, ptr(dy), ptr(x), threshold, ptr(dx), x.numel(), stream))
+
+
+def upsample_nearest2d(x, y, scale_h=0.0, scale_w=0.0, stream=None) -> None:
+    n, c, ih, iw = x.shape
+    check(lib().mx_upsample_nearest2d(ptr(x), n * c, ih, iw, y.shape[2], y.shape[3], scale_h or 0.0, scale_w or 0.0,
+                                      ptr(y), stream))
+
+
+def upsample_nearest2d_backward(dy, dx, scale_h=0.0, scale_w=0.0, stream=None) -> None:
+    n, c, ih, iw = dx.shape
+    check(lib().mx_upsample_nearest2d_backward(ptr(dy), n * c, ih, iw, dy.shape[2], dy.shape[3], scale_h or 0.0,
+                                               scale_w or 0.0, ptr(dx), stream))
+
+
+def _axis_split(shape, dim):
+    outer = inner = 1
+    for i, s in enumerate(shape):
+        if i < dim:
+            outer *= s
+        elif i > dim:
+            inner *= s
+    return outer, (shape[dim] if shape else 1), inner
+
+
+def softmax(x, dim, y, stream=None) -> None:
+    o, a, i = _axis_split(tuple(x.shape), dim % max(1, x.dim()))
+    check(lib().mx_softmax_f32(ptr(x), o, a, i, ptr(y), stream))
+
+
+def softmax_backward(dy, y, dim, dx, stream=None) -> None:
+    o, a, i = _axis_split(tuple(y.shape), dim % max(1, y.dim()))
+    check(lib().mx_softmax_backward_f32(ptr(dy), ptr(y), o, a, i, ptr(dx), stream))
+
+
+def mse_loss(x, t, reduction, out, stream=None) -> None:
+    check(lib().mx_mse_loss_f32(ptr(x), ptr(t), x.numel(), reduction, ptr(out), stream))
+
+
+def mse_loss_backward(dy, x, t, reduction, dx, stream=None) -> None:
+    check(lib().mx_mse_loss_backward_f32(ptr(dy), ptr(x), ptr(t), x.numel(), reduction, ptr(dx), stream))
+
+
+def copy_rows(dst, dst_pitch, src, src_pitch, row_bytes, rows, stream=None) -> None:
+    """Pitches and row length in bytes; dst / src are raw device addresses."""
+    check(lib().mx_copy_rows(dst, dst_pitch, src, src_pitch, row_bytes, rows, stream))
 
 
 def conv2d_kernel_name(d: ConvDesc, phase: int, algo: int = ALGO_AUTO) -> str:
