@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """Benchmark of the MI355X FP32 conv / GEMM / fused-AdamW path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1|copy] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1|c4|copy] [--no-cpu-baseline]
     python bench.py --pmc-summary FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR
     python bench.py --trace-summary KERNEL_TRACE_CSV BENCH_LOG
 
@@ -11,8 +11,10 @@ fwd+bwd FP32 TFLOP/s on its largest single-GPU Conv2D configuration, C3: the
 dInput + dWeight (the stem needs no dInput), 3x3 stride-1 forwards routed to
 Winograd F(2x2,3x3) as the configuration states.  A "step" is one pass of
 every layer; inputs are resident in HBM before timing.  `components` holds
-C1 (single conv layer fwd+dX+dW+dB), C2 (Linear addmm fwd+bwd, 8192x4096x4096)
-and C5 (multi-tensor AdamW, 250 tensors, GB/s).
+C1 (single conv layer fwd+dX+dW+dB), C2 (Linear addmm fwd+bwd, 8192x4096x4096),
+C5 (multi-tensor AdamW, 250 tensors, GB/s), C4 (the diffusion U-Net training
+step on the "vulkan" device, TFLOP/s of its convolutions and bmm over the
+whole step) and c4_ops (its normalisation / activation kernels, GB/s).
 
 Every kernel runs through the C ABI (libmx.so, include/mx.h); torch ROCm
 tensors only provide device memory and the stream.  `roofline` is measured
@@ -195,6 +197,88 @@ def build_c5(torch, mx, L):
     for _ in range(10):  # warm the moments as the configuration states
         step()
     return [("adamw_kernel", 0, 28.0 * numel, step)], numel
+
+
+def build_c4_ops(torch, mx, L):
+    """The normalisation / activation / resampling / softmax kernels of the C4
+    step at its largest shapes, each launch priced at its algorithmic HBM
+    bytes (every input read once, every output written once)."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    st = L.stream
+    big = (16, 128, 64, 64)  # level-0 activations
+    n = math.prod(big)
+    x = torch.randn(big, device="cuda", generator=g) * 2 + 0.5
+    dy = torch.randn(big, device="cuda", generator=g)
+    y = torch.empty_like(x)
+    dx = torch.empty_like(x)
+    gamma = torch.rand(128, device="cuda", generator=g) + 0.5
+    beta = torch.randn(128, device="cuda", generator=g)
+    mean = torch.empty(16, 32, device="cuda")
+    rstd = torch.empty(16, 32, device="cuda")
+    dg = torch.empty(128, device="cuda")
+    db = torch.empty(128, device="cuda")
+    up_in = torch.randn(16, 256, 32, 32, device="cuda", generator=g)  # upsample into level 0
+    up_out = torch.empty(16, 256, 64, 64, device="cuda")
+    up_grad = torch.empty_like(up_in)
+    att = torch.randn(64, 256, 256, device="cuda", generator=g) * 3  # attention scores at 16x16
+    att_y = torch.empty_like(att)
+    att_dx = torch.empty_like(att)
+    att_dy = torch.randn(64, 256, 256, device="cuda", generator=g)
+    mx.group_norm_forward(x, gamma, beta, 32, 1e-5, y, mean, rstd, stream=st)
+    calls = [
+        ("group_norm_forward", 0, 8.0 * n,
+         lambda: mx.group_norm_forward(x, gamma, beta, 32, 1e-5, y, mean, rstd, stream=st)),
+        ("group_norm_backward", 0, 12.0 * n,
+         lambda: mx.group_norm_backward(dy, x, mean, rstd, gamma, 32, dx, dg, db, stream=st)),
+        ("silu_forward", 0, 8.0 * n, lambda: mx.unary(mx.UNARY_SILU, x, y, stream=st)),
+        ("silu_backward", 0, 12.0 * n, lambda: mx.unary_backward(mx.UNARY_SILU_GRAD, dy, x, dx, stream=st)),
+        ("upsample_nearest2d", 0, 4.0 * (up_in.numel() + up_out.numel()),
+         lambda: mx.upsample_nearest2d(up_in, up_out, 2.0, 2.0, stream=st)),
+        ("upsample_nearest2d_backward", 0, 4.0 * (up_in.numel() + up_out.numel()),
+         lambda: mx.upsample_nearest2d_backward(up_out, up_grad, 2.0, 2.0, stream=st)),
+        ("softmax_forward", 0, 8.0 * att.numel(), lambda: mx.softmax(att, -1, att_y, stream=st)),
+        ("softmax_backward", 0, 12.0 * att.numel(), lambda: mx.softmax_backward(att_dy, att_y, -1, att_dx, stream=st)),
+    ]
+    return calls
+
+
+def run_c4(torch, steps, warmup, log):
+    """The C4 U-Net training step (forward, MSE loss, backward, fused AdamW) on
+    the "vulkan" device at batch 16, 64x64; GEMM FLOPs of convolutions and
+    attention bmm over the whole step time."""
+    import torch_vulkan as tv
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import unet_c4 as U
+    model = U.make_model().to("vulkan")
+    x, t = U.make_inputs()
+    x, t = x.to("vulkan"), t.to("vulkan")
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.01, fused=True)
+    flops = U.step_flops(model, x)
+
+    def step():
+        U.train_step_loss(model, x, t)
+        opt.step()
+
+    for _ in range(warmup):
+        step()
+    tv.synchronize()
+    before = tv.execution_stats()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    tv.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    after = tv.execution_stats()
+    fallbacks = after["cpu_fallback_calls"] - before["cpu_fallback_calls"]
+    reads = after["host_reads"] - before["host_reads"]
+    params = sum(p.numel() for p in model.parameters())
+    out = {"workload": "C4: diffusion U-Net training step (GroupNorm32/SiLU ResBlocks, width 128 x (1,2,2,4), "
+                       "4-head bmm attention at 16x16, MSE, fused AdamW), batch 16, 3x64x64, on the vulkan device",
+           "ms_per_step": round(dt * 1e3, 3), "value": round(flops / dt / 1e12, 3), "unit": "TFLOP/s",
+           "gflop_per_step": round(flops / 1e9, 1), "params": params,
+           "cpu_fallback_calls_per_step": fallbacks / steps, "host_reads_per_step": reads / steps}
+    del model, opt, x, t
+    return out
 
 
 def run_steps(torch, L, calls, steps, warmup, timing):
@@ -392,7 +476,8 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["c3", "c1", "copy"], default="c3")
+    ap.add_argument("--workload", choices=["c3", "c1", "c4", "copy"], default="c3",
+                    help="c4 runs only the U-Net step component (for profiling); the headline stays C3")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="summarise four rocprofv3 --pmc output directories into per-kernel HBM bytes")
     ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_LOG"),
@@ -424,6 +509,9 @@ def main(argv=None):
 
     if args.workload == "copy":
         print(json.dumps(run_copy(torch, args.steps, args.warmup)), flush=True)
+        return 0
+    if args.workload == "c4":
+        print(json.dumps(run_c4(torch, args.steps, args.warmup, log)), flush=True)
         return 0
 
     # ---------------- headline
@@ -481,6 +569,22 @@ def main(argv=None):
             log(key, comps[key]["value"], comps[key]["unit"])
             del calls_c, built
             torch.cuda.empty_cache()
+        calls_c = build_c4_ops(torch, mx, L)
+        dt, _ = run_steps(torch, L, calls_c, 20, 3, timing=False)
+        _, agg_c = run_steps(torch, L, calls_c, 20, 0, timing=True)
+        ops = {}
+        for label, (n_l, ms_l, _, nbytes) in agg_c.items():
+            gbs = nbytes / n_l / (ms_l / n_l * 1e-3) / 1e9
+            ops[label] = {"avg_us": round(1000 * ms_l / n_l, 2), "algorithmic_gb_s": round(gbs, 1),
+                          "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        comps["c4_ops"] = {"workload": "C4 normalisation / activation kernels at the step's largest shapes: "
+                                       "GroupNorm32 and SiLU on 16x128x64x64, 2x nearest 16x256x32x32->64x64, "
+                                       "softmax over 64x256x256 scores", "ops": ops}
+        log("c4_ops", {k: v["algorithmic_gb_s"] for k, v in ops.items()})
+        del calls_c
+        torch.cuda.empty_cache()
+        comps["c4"] = run_c4(torch, max(3, min(args.steps, 10)), 3, log)
+        log("c4", comps["c4"]["ms_per_step"], "ms/step", comps["c4"]["value"], "TFLOP/s")
         result["components"] = comps
 
     # ---------------- CPU baseline (bounded sample)

@@ -258,9 +258,12 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
         *algo = requested;
         return MX_OK;
       }
+      // Small-channel layers (a 3-channel stem or output head) still go to
+      // the MFMA implicit GEMM: a mostly-empty tile row is cheaper than the
+      // direct kernel's per-output loop once the GEMM has real depth.
       if (winograd_applicable(d) && d.groups >= 4 && cin_g >= 16 && cout_g >= 16 && rows >= 2048)
         *algo = MX_CONV_ALGO_WINOGRAD;
-      else if (cout_g >= 8 && cols >= 16 && rows >= 32)
+      else if (cols >= 8 && rows >= 32 && cout_g * cols >= 64)
         *algo = MX_CONV_ALGO_IMPLICIT_GEMM;
       else
         *algo = MX_CONV_ALGO_DIRECT;
@@ -272,8 +275,10 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
         *algo = requested;
         return MX_OK;
       }
-      *algo = (cin_g >= 2 && cout_g >= 8 && d.n * d.h * d.w >= 32) ? MX_CONV_ALGO_IMPLICIT_GEMM
-                                                                   : MX_CONV_ALGO_DIRECT;
+      *algo = (cin_g >= 2 && cout_g * d.kh * d.kw >= 8 && cin_g * cout_g * d.kh * d.kw >= 64 &&
+               d.n * d.h * d.w >= 32)
+                  ? MX_CONV_ALGO_IMPLICIT_GEMM
+                  : MX_CONV_ALGO_DIRECT;
       return MX_OK;
     case MX_CONV_DWEIGHT:
       MX_REQUIRE(requested != MX_CONV_ALGO_WINOGRAD, MX_ERR_UNSUPPORTED, "winograd is forward only");
@@ -281,7 +286,7 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
         *algo = requested;
         return MX_OK;
       }
-      if (cout_g >= 8 && cols >= 16 && cols * d.cout > 4096)
+      if (rows >= 64 && cout_g * cols >= 64)
         *algo = MX_CONV_ALGO_IMPLICIT_GEMM;
       else if (rows >= 128)
         *algo = MX_CONV_ALGO_REDUCE;

@@ -15,7 +15,9 @@
 //   MSE loss    csrc/ops/loss_primitives.cpp:349-356
 //   cat         csrc/ops/cat.cpp:8-58 (cat_copy.comp)
 //
-// GroupNorm and BatchNorm share one structure.  The tensor is seen as rows
+// GroupNorm runs one workgroup per (sample, group) when a group has at most
+// 1024 channels (gn_fwd_fused_kernel / gn_bwd_fused_kernel); wider groups and
+// BatchNorm share the row structure below.  The tensor is seen as rows
 // r = n*C + c of HW contiguous elements.  Statistics are gathered per row by
 // one wave (a centred two-pass over the row, so the second read comes from the
 // cache), merged per group / channel with Chan's pairwise formula (exact for
@@ -218,6 +220,173 @@ __global__ void gn_affine_kernel(const float* __restrict__ sdy, const float* __r
   }
   if (dgamma) dgamma[c] = dw;
   if (dbeta) dbeta[c] = db;
+}
+
+// One workgroup per (n, g) for the common GroupNorm shapes (at most
+// kGnMaxCpg channels per group): the group's cpg*hw elements are contiguous,
+// so the statistics, the normalisation and, in the backward, the per-channel
+// sums all come from one block of memory that stays in L2 / the Infinity Cache
+// between passes.  Forward is one launch, backward two (the second sums the
+// per-sample affine partials over n).
+constexpr int kGnMaxCpg = 1024;
+
+// Sum of one value per thread over the block, the same result in every
+// thread (fixed order: wave trees, then waves 0..3).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void gn_fwd_fused_kernel(const float* __restrict__ x,
+                                                                const float* __restrict__ gamma,
+                                                                const float* __restrict__ beta, int C, int G, int hw,
+                                                                float eps, float* __restrict__ y,
+                                                                float* __restrict__ mean, float* __restrict__ rstd) {
+  __shared__ float red[kWavesPerBlock];
+  const int ng = blockIdx.x;
+  const int n = ng / G, g = ng - (ng / G) * G, cpg = C / G;
+  const int count = cpg * hw;
+  const int64_t base = (int64_t(n) * C + int64_t(g) * cpg) * hw;
+  const float* p = x + base;
+  float* q = y + base;
+  float s = 0.f;
+  if (VEC) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    for (int i = threadIdx.x; i < count / 4; i += kThreads) {
+      const float4 v = p4[i];
+      s += (v.x + v.y) + (v.z + v.w);
+    }
+  } else {
+    for (int i = threadIdx.x; i < count; i += kThreads) s += p[i];
+  }
+  const float m = block_sum(s, red) / float(count);
+  float sq = 0.f;
+  if (VEC) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    for (int i = threadIdx.x; i < count / 4; i += kThreads) {
+      const float4 v = p4[i];
+      const float a = v.x - m, b = v.y - m, c = v.z - m, d = v.w - m;
+      sq += (a * a + b * b) + (c * c + d * d);
+    }
+  } else {
+    for (int i = threadIdx.x; i < count; i += kThreads) {
+      const float a = p[i] - m;
+      sq += a * a;
+    }
+  }
+  const float inv = 1.f / sqrtf(block_sum(sq, red) / float(count) + eps);
+  if (threadIdx.x == 0) {
+    mean[ng] = m;
+    rstd[ng] = inv;
+  }
+  const int c0 = g * cpg;
+  if (VEC) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    float4* q4 = reinterpret_cast<float4*>(q);
+    for (int i = threadIdx.x; i < count / 4; i += kThreads) {
+      const int c = c0 + (4 * i) / hw;
+      const float a = gamma ? inv * gamma[c] : inv, b = beta ? beta[c] : 0.f;
+      const float4 v = p4[i];
+      q4[i] = make_float4((v.x - m) * a + b, (v.y - m) * a + b, (v.z - m) * a + b, (v.w - m) * a + b);
+    }
+  } else {
+    for (int i = threadIdx.x; i < count; i += kThreads) {
+      const int c = c0 + i / hw;
+      const float a = gamma ? inv * gamma[c] : inv, b = beta ? beta[c] : 0.f;
+      q[i] = (p[i] - m) * a + b;
+    }
+  }
+}
+
+// Per (n, g): per-channel sum(dy) and sum(dy * (x - mean)) (waves over the
+// group's channels, lanes over the channel's plane), written to the affine
+// partials [n][c]; the group totals of v = gamma_c * dy and v * (x - mean) in
+// channel order; then dx = p_c * dy + k * (x - mean) + q (see gn_grad_merge_kernel).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void gn_bwd_fused_kernel(const float* __restrict__ dy,
+                                                                const float* __restrict__ x,
+                                                                const float* __restrict__ mean,
+                                                                const float* __restrict__ rstd,
+                                                                const float* __restrict__ gamma, int C, int G, int hw,
+                                                                float* __restrict__ dx, float* __restrict__ part_dy,
+                                                                float* __restrict__ part_dyx) {
+  __shared__ float sdy[kGnMaxCpg], sdyx[kGnMaxCpg];
+  __shared__ float tot[2];
+  const int ng = blockIdx.x;
+  const int n = ng / G, g = ng - (ng / G) * G, cpg = C / G;
+  const int64_t base = (int64_t(n) * C + int64_t(g) * cpg) * hw;
+  const float mu = mean[ng], inv = rstd[ng];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int ci = wave; ci < cpg; ci += kWavesPerBlock) {
+    const float* pg = dy + base + int64_t(ci) * hw;
+    const float* px = x + base + int64_t(ci) * hw;
+    float a = 0.f, b = 0.f;
+    if (VEC) {
+      const float4* g4 = reinterpret_cast<const float4*>(pg);
+      const float4* x4 = reinterpret_cast<const float4*>(px);
+      for (int i = lane; i < hw / 4; i += 64) {
+        const float4 gv = g4[i], v = x4[i];
+        a += (gv.x + gv.y) + (gv.z + gv.w);
+        b += (gv.x * (v.x - mu) + gv.y * (v.y - mu)) + (gv.z * (v.z - mu) + gv.w * (v.w - mu));
+      }
+    } else {
+      for (int i = lane; i < hw; i += 64) {
+        const float gv = pg[i];
+        a += gv;
+        b += gv * (px[i] - mu);
+      }
+    }
+    a = wave_sum(a);
+    b = wave_sum(b);
+    if (lane == 0) {
+      sdy[ci] = a;
+      sdyx[ci] = b;
+      const int64_t r = int64_t(n) * C + int64_t(g) * cpg + ci;
+      part_dy[r] = a;
+      part_dyx[r] = b;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sv = 0.f, svx = 0.f;
+    for (int ci = 0; ci < cpg; ++ci) {
+      const float w = gamma ? gamma[g * cpg + ci] : 1.f;
+      sv += w * sdy[ci];
+      svx += w * sdyx[ci];
+    }
+    tot[0] = sv;
+    tot[1] = svx;
+  }
+  __syncthreads();
+  if (!dx) return;
+  const int count = cpg * hw;
+  const float cnt = float(count);
+  const float k = -inv * inv * inv * (tot[1] / cnt);
+  const float q = -inv * (tot[0] / cnt);
+  const int c0 = g * cpg;
+  if (VEC) {
+    const float4* g4 = reinterpret_cast<const float4*>(dy + base);
+    const float4* x4 = reinterpret_cast<const float4*>(x + base);
+    float4* d4 = reinterpret_cast<float4*>(dx + base);
+    for (int i = threadIdx.x; i < count / 4; i += kThreads) {
+      const int c = c0 + (4 * i) / hw;
+      const float pc = gamma ? inv * gamma[c] : inv;
+      const float4 gv = g4[i], v = x4[i];
+      d4[i] = make_float4(pc * gv.x + k * (v.x - mu) + q, pc * gv.y + k * (v.y - mu) + q,
+                          pc * gv.z + k * (v.z - mu) + q, pc * gv.w + k * (v.w - mu) + q);
+    }
+  } else {
+    for (int i = threadIdx.x; i < count; i += kThreads) {
+      const int c = c0 + i / hw;
+      const float pc = gamma ? inv * gamma[c] : inv;
+      dx[base + i] = pc * dy[base + i] + k * (x[base + i] - mu) + q;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- BatchNorm
@@ -656,6 +825,18 @@ int mx_group_norm_forward(const float* x, const float* gamma, const float* beta,
   if (n == 0) return MX_OK;
   MX_REQUIRE(x && y && mean && rstd, MX_ERR_INVALID, "mx_group_norm_forward: null tensor");
   hipStream_t s = resolve_stream(stream);
+  const int64_t cpg64 = c / groups;
+  if (cpg64 <= kGnMaxCpg && cpg64 * hw <= INT32_MAX && n * groups <= INT32_MAX) {
+    const bool vec4 = hw % 4 == 0 && aligned16(x) && aligned16(y);
+    if (vec4)
+      hipLaunchKernelGGL(gn_fwd_fused_kernel<true>, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, x, gamma, beta,
+                         int(c), int(groups), int(hw), eps, y, mean, rstd);
+    else
+      hipLaunchKernelGGL(gn_fwd_fused_kernel<false>, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, x, gamma,
+                         beta, int(c), int(groups), int(hw), eps, y, mean, rstd);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
   const int64_t rows = n * c;
   Scratch stats, coef;
   MX_TRY(stats.alloc(size_t(rows) * 2 * sizeof(float), s));
@@ -709,6 +890,21 @@ int mx_group_norm_backward(const float* dy, const float* x, const float* mean, c
   float* sdyx = sdy + rows;
   const bool vec = hw % 4 == 0 && aligned16(x) && aligned16(dy) && (!dx || aligned16(dx));
   const int cpg = int(c / groups);
+  if (cpg <= kGnMaxCpg && int64_t(cpg) * hw <= INT32_MAX && n * groups <= INT32_MAX) {
+    if (vec)
+      hipLaunchKernelGGL(gn_bwd_fused_kernel<true>, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, dy, x, mean,
+                         rstd, gamma, int(c), int(groups), int(hw), dx, sdy, sdyx);
+    else
+      hipLaunchKernelGGL(gn_bwd_fused_kernel<false>, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, dy, x, mean,
+                         rstd, gamma, int(c), int(groups), int(hw), dx, sdy, sdyx);
+    MX_HIP(hipGetLastError());
+    if (dgamma || dbeta) {
+      hipLaunchKernelGGL(gn_affine_kernel, dim3(int((c + 255) / 256)), dim3(256), 0, s, sdy, sdyx, rstd, int(n),
+                         int(c), int(groups), dgamma, dbeta);
+      MX_HIP(hipGetLastError());
+    }
+    return MX_OK;
+  }
   if (vec)
     hipLaunchKernelGGL(row_grad_kernel<true>, dim3(launch_rows(rows)), dim3(kThreads), 0, s, dy, x, mean, rows,
                        int(hw), int(c), int(groups), cpg, sdy, sdyx);

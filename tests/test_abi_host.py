@@ -66,6 +66,11 @@ def test_planner_mirrors_reference_heuristic(mx):
     assert mx.conv2d_select(grouped, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
     tiny = mx.conv_desc((1, 1, 4, 4), (2, 1, 1, 1))
     assert mx.conv2d_select(tiny, mx.MX_CONV_FORWARD) == mx.ALGO_DIRECT
+    # 3-channel input conv and output head: every phase on the MFMA GEMM
+    for x_shape, w_shape in (((16, 3, 64, 64), (128, 3, 3, 3)), ((16, 128, 64, 64), (3, 128, 3, 3))):
+        d = mx.conv_desc(x_shape, w_shape, (1, 1), (1, 1))
+        for phase in (mx.MX_CONV_FORWARD, mx.MX_CONV_DINPUT, mx.MX_CONV_DWEIGHT):
+            assert mx.conv2d_select(d, phase) == mx.ALGO_IMPLICIT_GEMM
 
 
 def test_forced_inapplicable_algorithm_raises(mx):

@@ -157,6 +157,9 @@ CONV_CASES = [
     ((2, 32, 9, 9), 64, (3, 3), (1, 1), (1, 1), (1, 1), 2),
     ((2, 64, 10, 10), 32, (3, 3), (2, 2), (1, 1), (1, 1), 2),
     ((1, 16, 12, 12), 16, (3, 3), (1, 1), (2, 2), (2, 2), 1),
+    # small-channel layers of the C4 U-Net: 3-channel input conv and output head
+    ((2, 3, 64, 64), 128, (3, 3), (1, 1), (1, 1), (1, 1), 1),
+    ((2, 128, 64, 64), 3, (3, 3), (1, 1), (1, 1), (1, 1), 1),
 ]
 
 

@@ -36,10 +36,29 @@ def vk():
     return torch_vulkan
 
 
+class _OnDeviceStream:
+    """torch_vulkan.mx with every kernel call issued on the "vulkan" device's
+    current stream, the stream the test's tensors were produced on (the
+    device's streams are non-blocking, so the HIP NULL stream would race)."""
+
+    CALLS = {"group_norm_forward", "group_norm_backward", "batch_norm_forward", "batch_norm_backward", "unary",
+             "unary_backward", "upsample_nearest2d", "upsample_nearest2d_backward", "softmax", "softmax_backward",
+             "mse_loss", "mse_loss_backward", "copy_rows"}
+
+    def __init__(self, mx, vk):
+        self._mx, self._vk = mx, vk
+
+    def __getattr__(self, name):
+        f = getattr(self._mx, name)
+        if name in self.CALLS:
+            return lambda *a, **k: f(*a, stream=self._vk._C._current_stream_ptr(), **k)
+        return f
+
+
 @pytest.fixture(scope="module")
 def mx(vk):
     from torch_vulkan import mx
-    return mx
+    return _OnDeviceStream(mx, vk)
 
 
 @pytest.fixture
@@ -69,7 +88,10 @@ def close(actual, ref, mag=None, rtol=RTOL, atol=ATOL, what=""):
 
 # ------------------------------------------------------- C ABI vs the oracle
 GN_CASES = [((2, 8, 4, 5), 4), ((1, 12, 3, 7), 3), ((2, 16, 8), 8), ((2, 4, 1, 1), 2),
-            ((2, 64, 16, 16), 32), ((4, 128, 32, 32), 32), ((2, 512, 8, 8), 32), ((1, 32, 6, 6), 32)]
+            ((2, 64, 16, 16), 32), ((4, 128, 32, 32), 32), ((2, 512, 8, 8), 32), ((1, 32, 6, 6), 32),
+            ((2, 256, 64, 64), 32),
+            # more than 1024 channels per group: the row-statistics path
+            ((1, 2048, 2, 2), 1), ((2, 1030, 3, 1), 1)]
 
 
 @pytest.mark.parametrize("shape,groups", GN_CASES)

@@ -141,27 +141,32 @@ def train_step_loss(model, x, target):
     return loss
 
 
-def conv_flops(model, x) -> float:
-    """Forward+dInput+dWeight FLOPs of the model's convolutions and bmm products
-    for one training step on input x (2 FLOPs per multiply-add, 3 GEMM-sized
-    passes per convolution and per bmm).  Counted from the shapes seen in a
-    forward pass on the CPU at the same size."""
+def step_flops(model, x) -> float:
+    """GEMM FLOPs of one training step on input x (2 per multiply-add):
+    every convolution three times (forward, dInput, dWeight) except conv_in,
+    whose input needs no gradient (two), and every attention bmm three times
+    (forward and the two operand gradients).  Shapes are read by forward hooks
+    in one no-grad forward pass, so this runs wherever the model lives."""
     total = [0.0]
     hooks = []
 
     def conv_hook(mod, inp, out):
         k = mod.weight.shape[1] * mod.weight.shape[2] * mod.weight.shape[3]
-        total[0] += 3 * 2.0 * out.numel() * k
+        total[0] += (2 if mod is model.conv_in else 3) * 2.0 * out.numel() * k
+
+    def attn_hook(mod, inp, out):
+        b, c, h, w = inp[0].shape
+        n = h * w
+        # scores = q^T k and out = v attn^T, each 2*(b*heads)*n*n*d FLOPs
+        total[0] += 3 * 2 * (2.0 * b * mod.heads * n * n * (c // mod.heads))
 
     for m in model.modules():
         if isinstance(m, nn.Conv2d):
             hooks.append(m.register_forward_hook(conv_hook))
+        elif isinstance(m, Attention):
+            hooks.append(m.register_forward_hook(attn_hook))
     with torch.no_grad():
         model(x)
     for h in hooks:
         h.remove()
-    # Attention: per block two bmm of (b*heads) x HW x HW x d each way.
-    for m in model.modules():
-        if isinstance(m, Attention):
-            pass
     return total[0]
