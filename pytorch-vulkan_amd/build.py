@@ -90,7 +90,23 @@ def compile_hip(cmd: list[str]) -> None:
     if out.strip():
         print(out)
     if scratch:
-        raise RuntimeError("kernels using scratch memory:\n  " + "\n  ".join(scratch))
+        # Drop the object so an incremental build compiles (and checks) it again.
+        obj = Path(cmd[cmd.index("-o") + 1])
+        obj.unlink(missing_ok=True)
+        raise RuntimeError(f"{obj.name}: kernels using scratch memory:\n  " + "\n  ".join(scratch))
+
+
+def wait_all(futures) -> None:
+    """Waits for every job and raises the first failure after all have ended
+    (a failing compile must not hide another job's result)."""
+    errors = []
+    for f in futures:
+        try:
+            f.result()
+        except Exception as e:  # noqa: BLE001 (reported below)
+            errors.append(e)
+    if errors:
+        raise RuntimeError("\n\n".join(str(e) for e in errors))
 
 
 def stale(target: Path, deps: list[Path]) -> bool:
@@ -113,8 +129,7 @@ def build_mx(jobs: int, incremental: bool) -> Path:
         if not incremental or stale(obj, [CSRC / src] + headers):
             todo.append([cc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        for f in [ex.submit(compile_hip, c) for c in todo]:
-            f.result()
+        wait_all([ex.submit(compile_hip, c) for c in todo])
     lib = OUT / "libmx.so"
     if not incremental or stale(lib, objs):
         tmp = OUT / "libmx.so.tmp"
@@ -150,8 +165,7 @@ def build_ext(jobs: int, incremental: bool) -> Path:
         if not incremental or stale(obj, [path] + headers):
             todo.append([cxx, *flags, "-c", str(path), "-o", str(obj)])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        for f in [ex.submit(run, c) for c in todo]:
-            f.result()
+        wait_all([ex.submit(run, c) for c in todo])
     so = OUT / "_C.so"
     if not incremental or stale(so, objs + [OUT / "libmx.so"]):
         tmp = OUT / "_C.so.tmp"

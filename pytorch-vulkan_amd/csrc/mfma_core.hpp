@@ -73,6 +73,53 @@ __device__ __forceinline__ f32x4 load4_or_zero(const float* p, bool ok) {
   return *reinterpret_cast<const f32x4*>(ok ? p : kZeroPage);
 }
 
+// Raw buffer loads.  An operand tensor becomes one buffer resource (base,
+// byte extent) held in scalar registers; a lane supplies a 32-bit byte offset
+// and the per-element stride goes in the scalar offset, so a run of loads
+// costs no vector ALU work beyond its first offset.  The hardware range check
+// returns zero for an offset at or past the extent: a masked lane uses
+// kOffNone, which needs every operand to end below 2^31 bytes (kBufMaxBytes,
+// enforced by the host, which splits larger batches).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+extern "C" __device__ float mx_raw_buffer_load_f32(i32x4 rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.buffer.load.f32");
+extern "C" __device__ f32x4 mx_raw_buffer_load_v4f32(i32x4 rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.buffer.load.v4f32");
+
+constexpr uint32_t kOffNone = 0x80000000u;
+constexpr int64_t kBufMaxBytes = 0x7FFF0000;
+
+// Word 3 = 0x00020000: 32-bit data format, raw (stride 0) addressing.
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(int(uint32_t(a)));
+  r.y = __builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32) & 0xFFFFu));
+  r.z = __builtin_amdgcn_readfirstlane(int(uint32_t(bytes)));
+  r.w = 0x00020000;
+  return r;
+}
+__device__ __forceinline__ float bload(const i32x4& r, uint32_t voff, uint32_t soff) {
+  return mx_raw_buffer_load_f32(r, int(voff), int(soff), 0);
+}
+__device__ __forceinline__ f32x4 bload4(const i32x4& r, uint32_t voff, uint32_t soff) {
+  return mx_raw_buffer_load_v4f32(r, int(voff), int(soff), 0);
+}
+
+// n / d for n < 2^31 by multiply-high (m, l from fast_div(d) on the host):
+// (umulhi(n, m) + n) >> l with l = ceil(log2 d), m = 2^32 (2^l - d) / d + 1.
+struct FastDiv {
+  uint32_t m;
+  uint32_t l;
+};
+inline FastDiv fast_div(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1;
+  return FastDiv{uint32_t(m), l};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) { return (__umulhi(n, f.m) + n) >> f.l; }
+
 template <class C>
 __device__ __forceinline__ void acc_zero(Acc<C>& acc) {
 #pragma unroll

@@ -228,10 +228,36 @@ ConvArgs make_args(const mx_conv2d_desc& d) {
   p.KK = p.KH * p.KW;
   p.HW = p.H * p.W;
   p.OHOW = p.OH * p.OW;
+  p.f_ohow = conv::fast_div(uint32_t(p.OHOW));
+  p.f_ow = conv::fast_div(uint32_t(p.OW));
+  p.f_hw = conv::fast_div(uint32_t(p.HW));
+  p.f_kblk = conv::fast_div(uint32_t(p.KK * conv::kChanBlock));
+  p.f_tapw = conv::fast_div(uint32_t(p.KW));
   return p;
 }
 
 int linear_blocks(int64_t total) { return int(std::min<int64_t>((total + 255) / 256, 1 << 20)); }
+
+// Images per launch of the implicit-GEMM kernels: their loaders address each
+// activation tensor with 32-bit byte offsets below kBufMaxBytes, so a larger
+// batch runs as several launches over image chunks.  MX_CONV_BUFFER_LIMIT
+// (bytes) lowers the bound, which lets the tests run the chunked path on small
+// tensors.  Returns 0 when a single image does not fit.
+int64_t images_per_launch(const mx_conv2d_desc& d) {
+  int64_t limit = conv::kBufMaxBytes;
+  if (const char* e = std::getenv("MX_CONV_BUFFER_LIMIT")) {
+    const long long v = std::atoll(e);
+    if (v > 0 && v < limit) limit = v;
+  }
+  const int64_t per_img = std::max(d.cin * d.h * d.w, d.cout * d.oh * d.ow) * 4;
+  return std::min<int64_t>(d.n, limit / per_img);
+}
+
+mx_conv2d_desc batch_slice(const mx_conv2d_desc& d, int64_t n) {
+  mx_conv2d_desc c = d;
+  c.n = n;
+  return c;
+}
 
 bool winograd_applicable(const mx_conv2d_desc& d) {
   return d.kh == 3 && d.kw == 3 && d.sh == 1 && d.sw == 1 && d.dh == 1 && d.dw == 1;
@@ -535,6 +561,18 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
   MX_TRY(select_algo(d, MX_CONV_FORWARD, algo, &chosen));
   hipStream_t s = resolve_stream(stream);
   if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_forward(d, x, w, bias, y, s);
+  if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM) {
+    const int64_t nc = images_per_launch(d);
+    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d forward: one image exceeds the 2 GiB operand bound");
+    if (nc < d.n) {
+      for (int64_t n0 = 0; n0 < d.n; n0 += nc) {
+        const mx_conv2d_desc c = batch_slice(d, std::min(nc, d.n - n0));
+        MX_TRY(mx_conv2d_forward(&c, x + n0 * d.cin * d.h * d.w, w, bias, y + n0 * d.cout * d.oh * d.ow,
+                                 MX_CONV_ALGO_IMPLICIT_GEMM, stream));
+      }
+      return MX_OK;
+    }
+  }
   ConvArgs p = make_args(d);
   p.x = x;
   p.w = w;
@@ -579,6 +617,18 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
   int chosen = 0;
   MX_TRY(select_algo(d, MX_CONV_DINPUT, algo, &chosen));
   hipStream_t s = resolve_stream(stream);
+  if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM) {
+    const int64_t nc = images_per_launch(d);
+    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d dinput: one image exceeds the 2 GiB operand bound");
+    if (nc < d.n) {
+      for (int64_t n0 = 0; n0 < d.n; n0 += nc) {
+        const mx_conv2d_desc c = batch_slice(d, std::min(nc, d.n - n0));
+        MX_TRY(mx_conv2d_backward_input(&c, dy + n0 * d.cout * d.oh * d.ow, w, dx + n0 * d.cin * d.h * d.w,
+                                        MX_CONV_ALGO_IMPLICIT_GEMM, stream));
+      }
+      return MX_OK;
+    }
+  }
   ConvArgs p = make_args(d);
   p.dy = dy;
   p.w = w;
@@ -604,6 +654,8 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
       continue;
     }
     q.wt = packed ? wt.as<float>() : w;
+    q.f_kblk = conv::fast_div(uint32_t(q.nth * q.ntw * conv::kChanBlock));
+    q.f_tapw = conv::fast_div(uint32_t(q.ntw));
     q.splits = gp.splits;
     q.kps = int((q.K + gp.splits - 1) / gp.splits + kSplitBK - 1) / kSplitBK * kSplitBK;
     q.ws = ws.as<float>();
@@ -666,12 +718,39 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
     if (db) return mx_conv2d_backward_bias(desc, dy, db, stream);
     return MX_OK;
   }
+  {
+    const int64_t nc = images_per_launch(d);
+    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d dweight: one image exceeds the 2 GiB operand bound");
+    if (nc < d.n) {
+      // Sum of the chunks' gradients: the first chunk writes dw / db, the
+      // others go through a scratch copy added in chunk order.
+      const int64_t nw = d.cout * (d.cin / d.groups) * d.kh * d.kw;
+      Scratch tmp;
+      MX_TRY(tmp.alloc(size_t(nw + (db ? d.cout : 0)) * 4, s));
+      float* tw = tmp.as<float>();
+      float* tb = db ? tw + nw : nullptr;
+      for (int64_t n0 = 0; n0 < d.n; n0 += nc) {
+        const mx_conv2d_desc c = batch_slice(d, std::min(nc, d.n - n0));
+        const float* xc = x + n0 * d.cin * d.h * d.w;
+        const float* dyc = dy + n0 * d.cout * d.oh * d.ow;
+        if (n0 == 0) {
+          MX_TRY(mx_conv2d_backward_weight(&c, xc, dyc, dw, db, MX_CONV_ALGO_IMPLICIT_GEMM, stream));
+        } else {
+          MX_TRY(mx_conv2d_backward_weight(&c, xc, dyc, tw, tb, MX_CONV_ALGO_IMPLICIT_GEMM, stream));
+          MX_TRY(mx_add_f32(dw, dw, tw, 1.f, nw, stream));
+          if (db) MX_TRY(mx_add_f32(db, db, tb, 1.f, d.cout, stream));
+        }
+      }
+      return MX_OK;
+    }
+  }
   p.db = db;
   p.M = p.Cout_g;
   p.Ncols = p.Cin_g * p.KK;
   p.K = p.N * p.OHOW;
   const int amode = (p.OHOW % 4 == 0 && aligned16(dy)) ? conv::B_VEC : conv::B_GATHER;
   const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
+  p.cols_blocked = bmode == conv::B_GATHER && conv::blocked_channels(p.Cin_g) ? 1 : 0;
   const DwPlan pl = plan_dw(p, db != nullptr, bmode == conv::B_GATHER, amode == conv::B_GATHER);
   p.splits = pl.g.splits;
   p.kps = pl.g.kps;

@@ -55,6 +55,17 @@ struct ConvArgs {
   float* ws;
   float* ws_db;
   int64_t out_elems;
+  // Per-lane divisions of the loaders' inner loops: position -> image
+  // (OH*OW), row (OW) and, for the 16-byte k loaders, image of a k index (hw
+  // of the operand read along k).
+  FastDiv f_ohow, f_ow, f_hw;
+  // Blocked K walk of the forward / dInput gathers: k -> (channel block,
+  // tap) by taps * kChanBlock, tap -> (row, column) by the tap-grid width
+  // (forward: KK * 16 and KW; dInput phase: nth * ntw * 16 and ntw).
+  FastDiv f_kblk, f_tapw;
+  // dWeight: the B gather runs its columns in the channel-blocked order
+  // (channel block, kh, kw, channel in block); the epilogue maps them back.
+  int cols_blocked;
 };
 
 // Gathered K order.  With a channel count that is a multiple of kChanBlock
@@ -68,26 +79,39 @@ constexpr int kChanBlock = 16;
 __host__ __device__ constexpr bool blocked_channels(int c) { return c % kChanBlock == 0; }
 
 // ------------------------------------------------------------------ loaders
+// All activation operands are read through buffer resources (mfma_core.hpp):
+// a lane computes one 32-bit byte offset per run of elements (kOffNone when
+// masked, which reads zeros), the run's stride is a scalar offset, and no
+// instruction touches a loaded value before store() writes it to LDS, so the
+// loads of the next slabs stay in flight behind the MFMAs.  K decompositions
+// that are the same for a whole wave are made wave-uniform
+// (readfirstlane) and run on the scalar unit.
+
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 // Forward B operand (gather): rows = output positions (img, oh, ow), k in
 // the gathered K order over (ci, kh, kw); element
 // x[img][g*Cin_g + ci][oh*sh - ph + kh*dh][ow*sw - pw + kw*dw].  Each thread
-// holds EPT consecutive k of one position.
-template <int ROWS, int BK>
+// holds EPT consecutive k of one position; a wave's 64 threads share their
+// k run (ROWS is a multiple of 64), so the (ci, kh, kw) walk is scalar.
+template <int ROWS, int BK, bool BLOCKED>
 struct Im2colLoader {
   static constexpr bool KMAJOR = false;
-  static constexpr bool DEEP = false;  // its per-thread state leaves no room for a second set at 64x64
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int EPT = ROWS * BK / kThreads;
-  static_assert(ROWS <= kThreads && EPT >= 1 && BK % EPT == 0 && kChanBlock % EPT == 0, "Im2colLoader tiling");
+  static_assert(ROWS % 64 == 0 && ROWS <= kThreads && EPT >= 1 && BK % EPT == 0 && kChanBlock % EPT == 0,
+                "Im2colLoader tiling");
   float v[EPT];
-  const float* xg;
+  i32x4 rs;
+  uint32_t xoff;  // bytes to (img, first channel of the group, 0, 0)
   int ih0, iw0, ks, k, kmax;
-  bool ok, blocked;
+  bool ok;
+  FastDiv f_kblk, f_kw;
   int KK, KBLK, KH, KW, dh, dw, H, W, HW;
   __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     const int r = tid % ROWS;
-    ks = (tid / ROWS) * EPT;
+    ks = wave_uniform((tid / ROWS) * EPT);
     const int pos = col0 + r;
     ok = pos < p.Ncols;
     const int pp = ok ? pos : 0;
@@ -97,8 +121,10 @@ struct Im2colLoader {
     const int ow = q - oh * p.OW;
     ih0 = oh * p.sh - p.ph;
     iw0 = ow * p.sw - p.pw;
-    xg = p.x + (int64_t(img) * p.Cin + int64_t(g) * p.Cin_g) * p.HW;
-    blocked = blocked_channels(p.Cin_g);
+    xoff = uint32_t((int64_t(img) * p.Cin + int64_t(g) * p.Cin_g) * p.HW * 4);
+    rs = buffer_rsrc(p.x, int64_t(p.N) * p.Cin * p.HW * 4);
+    f_kblk = p.f_kblk;
+    f_kw = p.f_tapw;
     KK = p.KK;
     KBLK = p.KK * kChanBlock;
     KH = p.KH;
@@ -112,21 +138,23 @@ struct Im2colLoader {
     kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
-    const int kb = k + ks;
-    if (blocked) {
+    const int kb = k + ks;  // wave-uniform
+    if constexpr (BLOCKED) {
       // (channel block, kh, kw, channel in block): the run shares one tap.
-      const int cb = kb / KBLK;
+      const int cb = int(fdiv(uint32_t(kb), f_kblk));
       const int rem = kb - cb * KBLK;
       const int t = rem / kChanBlock;
-      const int kh = t / KW, kw = t - (t / KW) * KW;
+      const int kh = int(fdiv(uint32_t(t), f_kw));
+      const int kw = t - kh * KW;
       const int c = cb * kChanBlock + (rem - t * kChanBlock);
       const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
       const bool valid = ok && kb < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-      const float* src = xg + (c * HW + ih * W + iw);
+      const uint32_t voff = valid ? xoff + uint32_t(ih * W + iw) * 4u : kOffNone;
+      const uint32_t s0 = uint32_t(c) * uint32_t(HW) * 4u;
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) v[e] = load_or_zero(src + e * HW, valid);
+      for (int e = 0; e < EPT; ++e) v[e] = bload(rs, voff, s0 + uint32_t(e * HW) * 4u);
     } else {
-      // (ci, kh, kw) with kw fastest.
+      // (ci, kh, kw) with kw fastest; the walk is wave-uniform.
       int ci = kb / KK;
       const int rem = kb - ci * KK;
       int kh = rem / KW;
@@ -135,7 +163,7 @@ struct Im2colLoader {
       for (int e = 0; e < EPT; ++e) {
         const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
         const bool valid = ok && (kb + e) < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-        v[e] = load_or_zero(xg + ci * HW + ih * W + iw, valid);
+        v[e] = bload(rs, valid ? xoff + uint32_t(ih * W + iw) * 4u : kOffNone, uint32_t(ci) * uint32_t(HW) * 4u);
         if (++kw == KW) {
           kw = 0;
           if (++kh == KH) {
@@ -176,20 +204,22 @@ struct PosQuadLoader {
   static constexpr int PASSES = BK / KPP;
   static_assert(PASSES >= 1 && BK % KPP == 0, "PosQuadLoader tiling");
   f32x4 v[PASSES];
-  const float* ptr;
-  int hw, k, kmax, kk;
-  bool ok;
+  i32x4 rs;
+  uint32_t voff, hw4;
+  int k, kmax, kk;
   __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     kk = tid / TPK;
-    const float* base = DY ? p.dy + int64_t(g) * p.Cout_g * p.OHOW : p.x + int64_t(g) * p.Cin_g * p.HW;
     const int cs = DY ? p.Cout * p.OHOW : p.Cin * p.HW;
-    hw = DY ? p.OHOW : p.HW;
+    const int hw = DY ? p.OHOW : p.HW;
+    const int64_t gbase = DY ? int64_t(g) * p.Cout_g * p.OHOW : int64_t(g) * p.Cin_g * p.HW;
+    rs = buffer_rsrc(DY ? p.dy : p.x, int64_t(p.N) * cs * 4);
     const int pos = col0 + 4 * (tid % TPK);
-    ok = pos < p.Ncols;
+    const bool ok = pos < p.Ncols;
     const int pp = ok ? pos : 0;
     const int img = pp / hw;
-    ptr = base + int64_t(img) * cs + (pp - img * hw);
+    voff = ok ? uint32_t((gbase + int64_t(img) * cs + (pp - img * hw) + int64_t(kk) * hw) * 4) : kOffNone;
+    hw4 = uint32_t(hw) * 4u;
     k = k0;
     kmax = kmax_;
   }
@@ -197,7 +227,7 @@ struct PosQuadLoader {
 #pragma unroll
     for (int q = 0; q < PASSES; ++q) {
       const int kx = k + kk + q * KPP;
-      v[q] = load4_or_zero(ptr + int64_t(kx) * hw, ok && kx < kmax);
+      v[q] = bload4(rs, kx < kmax ? voff : kOffNone, uint32_t(k + q * KPP) * hw4);
     }
     k += kstep;
   }
@@ -212,22 +242,26 @@ struct PosQuadLoader {
 
 // dInput B operand (gather) for one stride phase: rows = phase positions
 // (img, i, j), k in the gathered K order over (co, th, tw); element
-// dy[img][g*Cout_g + co][i + offh0 - th*dsh][j + offw0 - tw*dsw].
-template <int ROWS, int BK>
+// dy[img][g*Cout_g + co][i + offh0 - th*dsh][j + offw0 - tw*dsw].  The k run
+// of a wave is shared, as in Im2colLoader.
+template <int ROWS, int BK, bool BLOCKED>
 struct PhaseGatherLoader {
   static constexpr bool KMAJOR = false;
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int EPT = ROWS * BK / kThreads;
-  static_assert(ROWS <= kThreads && EPT >= 1 && BK % EPT == 0 && kChanBlock % EPT == 0, "PhaseGatherLoader tiling");
+  static_assert(ROWS % 64 == 0 && ROWS <= kThreads && EPT >= 1 && BK % EPT == 0 && kChanBlock % EPT == 0,
+                "PhaseGatherLoader tiling");
   float v[EPT];
-  const float* dyg;
+  i32x4 rs;
+  uint32_t doff;  // bytes to (img, first channel of the group, 0, 0)
   int ib, jb, ks, k, kmax;
-  bool ok, blocked;
+  bool ok;
+  FastDiv f_kblk, f_tw;
   int NT, KBLK, nth, ntw, dsh, dsw, OH, OW, OHOW;
   __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     const int r = tid % ROWS;
-    ks = (tid / ROWS) * EPT;
+    ks = wave_uniform((tid / ROWS) * EPT);
     const int pos = col0 + r;
     ok = pos < p.Ncols;
     const int pp = ok ? pos : 0;
@@ -237,8 +271,10 @@ struct PhaseGatherLoader {
     const int j = q - i * p.Wp;
     ib = i + p.offh0;
     jb = j + p.offw0;
-    dyg = p.dy + (int64_t(img) * p.Cout + int64_t(g) * p.Cout_g) * p.OHOW;
-    blocked = blocked_channels(p.Cout_g);
+    doff = uint32_t((int64_t(img) * p.Cout + int64_t(g) * p.Cout_g) * p.OHOW * 4);
+    rs = buffer_rsrc(p.dy, int64_t(p.N) * p.Cout * p.OHOW * 4);
+    f_kblk = p.f_kblk;
+    f_tw = p.f_tapw;
     NT = p.nth * p.ntw;
     KBLK = NT * kChanBlock;
     nth = p.nth;
@@ -252,21 +288,23 @@ struct PhaseGatherLoader {
     kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
-    const int kb = k + ks;
-    if (blocked) {
+    const int kb = k + ks;  // wave-uniform
+    if constexpr (BLOCKED) {
       // (channel block, th, tw, channel in block): the run shares one tap.
-      const int cb = kb / KBLK;
+      const int cb = int(fdiv(uint32_t(kb), f_kblk));
       const int rem = kb - cb * KBLK;
       const int t = rem / kChanBlock;
-      const int th = t / ntw, tw = t - (t / ntw) * ntw;
+      const int th = int(fdiv(uint32_t(t), f_tw));
+      const int tw = t - th * ntw;
       const int co = cb * kChanBlock + (rem - t * kChanBlock);
       const int oh = ib - th * dsh, ow = jb - tw * dsw;
       const bool valid = ok && kb < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
-      const float* src = dyg + (co * OHOW + oh * OW + ow);
+      const uint32_t voff = valid ? doff + uint32_t(oh * OW + ow) * 4u : kOffNone;
+      const uint32_t s0 = uint32_t(co) * uint32_t(OHOW) * 4u;
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) v[e] = load_or_zero(src + e * OHOW, valid);
+      for (int e = 0; e < EPT; ++e) v[e] = bload(rs, voff, s0 + uint32_t(e * OHOW) * 4u);
     } else {
-      // (co, th, tw) with tw fastest.
+      // (co, th, tw) with tw fastest; the walk is wave-uniform.
       int co = kb / NT;
       const int rem = kb - co * NT;
       int th = rem / ntw;
@@ -275,7 +313,7 @@ struct PhaseGatherLoader {
       for (int e = 0; e < EPT; ++e) {
         const int oh = ib - th * dsh, ow = jb - tw * dsw;
         const bool valid = ok && (kb + e) < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
-        v[e] = load_or_zero(dyg + co * OHOW + oh * OW + ow, valid);
+        v[e] = bload(rs, valid ? doff + uint32_t(oh * OW + ow) * 4u : kOffNone, uint32_t(co) * uint32_t(OHOW) * 4u);
         if (++tw == ntw) {
           tw = 0;
           if (++th == nth) {
@@ -303,61 +341,59 @@ struct PhaseGatherLoader {
 };
 
 // dWeight operands with k = output position.  Every loader exposes the
-// thread -> row map (rows tid / LPR + q * RPP) used by the dBias row sums.
+// thread -> row map (rows tid / LPR + q * RPP) used by the dBias row sums,
+// which store() accumulates (after the loads have landed).
 //
 // dy rows (A, rows = co), scalar: element dy[img][co][q]; lanes along k.
 template <int ROWS, int BK>
 struct DyRowsLoader {
   static constexpr bool KMAJOR = false;
-  static constexpr bool DEEP = false;  // a pointer offset, flag and row sum per pass: one register set
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int LPR = BK;  // lanes per row
   static constexpr int RPP = kThreads / BK;
   static constexpr int PASSES = ROWS / RPP;
   static_assert(PASSES >= 1 && ROWS % RPP == 0, "DyRowsLoader tiling");
   float v[PASSES];
-  float bsum[PASSES];
-  int coff[PASSES];
-  bool ok[PASSES];
-  const float* dyg;
-  int k, kk, kmax, OHOW, COHOW;
+  mutable float bsum[PASSES];
+  bool rok[PASSES];
+  i32x4 rs;
+  uint32_t roff, pass4, cohow4;
+  FastDiv f_ohow;
+  int k, kk, kmax, OHOW;
   __device__ __forceinline__ void init(const ConvArgs& p, int row0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     kk = tid % BK;
 #pragma unroll
     for (int q = 0; q < PASSES; ++q) {
-      const int co = row0 + tid / BK + q * RPP;
-      ok[q] = co < p.Cout_g;
-      coff[q] = ok[q] ? co * p.OHOW : 0;
+      rok[q] = row0 + tid / BK + q * RPP < p.Cout_g;
       bsum[q] = 0.f;
     }
-    dyg = p.dy + int64_t(g) * p.Cout_g * p.OHOW;
+    rs = buffer_rsrc(p.dy, int64_t(p.N) * p.Cout * p.OHOW * 4);
+    roff = uint32_t((int64_t(g) * p.Cout_g + row0 + tid / BK) * p.OHOW * 4);
+    pass4 = uint32_t(RPP) * uint32_t(p.OHOW) * 4u;
+    cohow4 = uint32_t(p.Cout) * uint32_t(p.OHOW) * 4u;
+    f_ohow = p.f_ohow;
     OHOW = p.OHOW;
-    COHOW = p.Cout * p.OHOW;
     k = k0;
     kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
-    // One register set (DEEP = false): clamped 32-bit offsets and a select.
     const int kx = k + kk;
     const bool kin = kx < kmax;
-    const int kc = kin ? kx : 0;
-    const int img = kc / OHOW;
-    const int base = img * COHOW + (kc - img * OHOW);
+    const uint32_t img = fdiv(uint32_t(kx), f_ohow);
+    const uint32_t base = kin ? img * cohow4 + roff + (uint32_t(kx) - img * uint32_t(OHOW)) * 4u : kOffNone;
 #pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      const bool use = ok[q] && kin;
-      const float t = dyg[use ? base + coff[q] : 0];
-      v[q] = use ? t : 0.f;
-      bsum[q] += v[q];
-    }
+    for (int q = 0; q < PASSES; ++q) v[q] = bload(rs, rok[q] ? base : kOffNone, uint32_t(q) * pass4);
     k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     constexpr int LDK = BK + 4;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int q = 0; q < PASSES; ++q) lds[(tid / BK + q * RPP) * LDK + kk] = v[q];
+    for (int q = 0; q < PASSES; ++q) {
+      lds[(tid / BK + q * RPP) * LDK + kk] = v[q];
+      bsum[q] += v[q];
+    }
   }
 };
 
@@ -374,110 +410,142 @@ struct PosKLoader {
   static constexpr int PASSES = ROWS / RPP;
   static_assert(PASSES >= 1 && ROWS % RPP == 0, "PosKLoader tiling");
   f32x4 v[PASSES];
-  float bsum[PASSES];
-  int roff[PASSES];
-  bool ok[PASSES];
-  const float* base;
-  int k, kq, kmax, hw, cs;
+  mutable float bsum[PASSES];
+  bool rok[PASSES];
+  i32x4 rs;
+  uint32_t roff, pass4, cs4;
+  FastDiv f_hw;
+  int k, kq, kmax, hw;
   __device__ __forceinline__ void init(const ConvArgs& p, int row0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     kq = tid % LPR;
-    base = DY ? p.dy + int64_t(g) * p.Cout_g * p.OHOW : p.x + int64_t(g) * p.Cin_g * p.HW;
-    cs = DY ? p.Cout * p.OHOW : p.Cin * p.HW;
+    const int cs = DY ? p.Cout * p.OHOW : p.Cin * p.HW;
     hw = DY ? p.OHOW : p.HW;
+    const int64_t gbase = DY ? int64_t(g) * p.Cout_g : int64_t(g) * p.Cin_g;
+    f_hw = DY ? p.f_ohow : p.f_hw;
     const int R = DY ? p.Cout_g : p.Ncols;
 #pragma unroll
     for (int q = 0; q < PASSES; ++q) {
-      const int row = row0 + tid / LPR + q * RPP;
-      ok[q] = row < R;
-      roff[q] = ok[q] ? row * hw : 0;
+      rok[q] = row0 + tid / LPR + q * RPP < R;
       bsum[q] = 0.f;
     }
+    rs = buffer_rsrc(DY ? p.dy : p.x, int64_t(p.N) * cs * 4);
+    roff = uint32_t((gbase + row0 + tid / LPR) * hw * 4);
+    pass4 = uint32_t(RPP) * uint32_t(hw) * 4u;
+    cs4 = uint32_t(cs) * 4u;
     k = k0;
     kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
     const int kx = k + 4 * kq;
     const bool kin = kx < kmax;
-    const int img = kx / hw;
-    const float* src = base + int64_t(img) * cs + (kx - img * hw);
+    const uint32_t img = fdiv(uint32_t(kx), f_hw);
+    const uint32_t base = kin ? img * cs4 + roff + (uint32_t(kx) - img * uint32_t(hw)) * 4u : kOffNone;
 #pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      v[q] = load4_or_zero(src + roff[q], ok[q] && kin);
-      if constexpr (DY) bsum[q] += (v[q][0] + v[q][1]) + (v[q][2] + v[q][3]);
-    }
+    for (int q = 0; q < PASSES; ++q) v[q] = bload4(rs, rok[q] ? base : kOffNone, uint32_t(q) * pass4);
     k += kstep;
   }
   __device__ __forceinline__ void store(float* lds) const {
     constexpr int LDK = BK + 4;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int q = 0; q < PASSES; ++q)
+    for (int q = 0; q < PASSES; ++q) {
       *reinterpret_cast<f32x4*>(lds + (tid / LPR + q * RPP) * LDK + 4 * kq) = v[q];
+      if constexpr (DY) bsum[q] += (v[q][0] + v[q][1]) + (v[q][2] + v[q][3]);
+    }
   }
 };
 
 // dWeight B operand (gather): rows = (ci, kh, kw), k = output position;
-// element x[img][ci][oh*sh - ph + kh*dh][ow*sw - pw + kw*dw].
-template <int ROWS, int BK>
+// element x[img][ci][oh*sh - ph + kh*dh][ow*sw - pw + kw*dw].  Lanes run along
+// k (one position each); a thread's PASSES rows are consecutive.  With a
+// channel count that is a multiple of kChanBlock the rows are taken in the
+// channel-blocked order (channel block, kh, kw, channel in block), so a
+// thread's rows share one tap: one bounds test and one offset, the channels a
+// plane apart in the scalar offset (ConvArgs::cols_blocked tells the epilogue
+// to map the columns back).  Other channel counts test each row.
+template <int ROWS, int BK, bool BLOCKED>
 struct XColsLoader {
   static constexpr bool KMAJOR = false;
-  static constexpr bool DEEP = false;  // three per-pass offsets: one register set
+  // Per-row offsets of the plain order leave room for one register set only.
+  static constexpr bool DEEP = BLOCKED;
   int kstep = BK;  // k advance per load(); the main loop may set 2 * BK
   static constexpr int RPP = kThreads / BK;
   static constexpr int PASSES = ROWS / RPP;
-  static_assert(PASSES >= 1 && ROWS % RPP == 0, "XColsLoader tiling");
+  static constexpr int NR = BLOCKED ? 1 : PASSES;  // rows with their own tap / channel
+  static_assert(PASSES >= 1 && ROWS % RPP == 0 && kChanBlock % PASSES == 0, "XColsLoader tiling");
   float v[PASSES];
-  int coff[PASSES];
-  int khd[PASSES];
-  int kwd[PASSES];
-  const float* xg;
-  int k, kk, kmax, OHOW, OW, sh, sw, H, W, CHW;
+  i32x4 rs;
+  uint32_t coff[NR];  // bytes to the row's channel plane (blocked: the run's first channel)
+  int khd[NR], kwd[NR];
+  FastDiv f_ohow, f_ow;
+  uint32_t chw4, hw4;
+  int k, kk, kmax, OHOW, OW, sh, sw, H, W;
   __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
     kk = tid % BK;
+    const int n0 = col0 + (tid / BK) * PASSES;
+    if constexpr (BLOCKED) {
+      // The PASSES rows n0.. lie in one 16-channel block and share tap t.
+      const int kblk = p.KK * kChanBlock;
+      const int cb = n0 / kblk, rem = n0 - cb * kblk;
+      const int t = rem / kChanBlock;
+      const int ci0 = cb * kChanBlock + (rem - t * kChanBlock);
+      const int kh = t / p.KW, kw = t - (t / p.KW) * p.KW;
+      coff[0] = uint32_t((int64_t(g) * p.Cin_g + ci0) * p.HW * 4);
+      // A run past the last column gets a tap offset that always fails the bounds test.
+      khd[0] = n0 < p.Ncols ? kh * p.dh - p.ph : INT_MIN / 2;
+      kwd[0] = kw * p.dw - p.pw;
+    } else {
 #pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      const int n = col0 + tid / BK + q * RPP;
-      const bool ok = n < p.Ncols;
-      const int nn = ok ? n : 0;
-      const int ci = nn / p.KK;
-      const int r = nn - ci * p.KK;
-      const int kh = r / p.KW;
-      const int kw = r - kh * p.KW;
-      coff[q] = ci * p.HW;
-      // An invalid row gets an offset that always fails the bounds test.
-      khd[q] = ok ? kh * p.dh - p.ph : INT_MIN / 2;
-      kwd[q] = kw * p.dw - p.pw;
+      for (int q = 0; q < PASSES; ++q) {
+        const int n = n0 + q;
+        const bool ok = n < p.Ncols;
+        const int nn = ok ? n : 0;
+        const int ci = nn / p.KK;
+        const int r = nn - ci * p.KK;
+        const int kh = r / p.KW;
+        const int kw = r - kh * p.KW;
+        coff[q] = uint32_t((int64_t(g) * p.Cin_g + ci) * p.HW * 4);
+        khd[q] = ok ? kh * p.dh - p.ph : INT_MIN / 2;
+        kwd[q] = kw * p.dw - p.pw;
+      }
     }
-    xg = p.x + int64_t(g) * p.Cin_g * p.HW;
+    rs = buffer_rsrc(p.x, int64_t(p.N) * p.Cin * p.HW * 4);
+    f_ohow = p.f_ohow;
+    f_ow = p.f_ow;
+    chw4 = uint32_t(p.Cin) * uint32_t(p.HW) * 4u;
+    hw4 = uint32_t(p.HW) * 4u;
     OHOW = p.OHOW;
     OW = p.OW;
     sh = p.sh;
     sw = p.sw;
     H = p.H;
     W = p.W;
-    CHW = p.Cin * p.HW;
     k = k0;
     kmax = kmax_;
   }
   __device__ __forceinline__ void load() {
-    // One register set (DEEP = false): clamped 32-bit offsets and a select.
     const int kx = k + kk;
     const bool kin = kx < kmax;
-    const int kc = kin ? kx : 0;
-    const int img = kc / OHOW;
-    const int q0 = kc - img * OHOW;
-    const int oh = q0 / OW;
-    const int ow = q0 - oh * OW;
-    const int ihb = oh * sh, iwb = ow * sw;
-    const float* xi = xg + int64_t(img) * CHW;
-#pragma unroll
-    for (int q = 0; q < PASSES; ++q) {
-      const int ih = ihb + khd[q], iw = iwb + kwd[q];
+    const uint32_t img = fdiv(uint32_t(kx), f_ohow);
+    const uint32_t q0 = uint32_t(kx) - img * uint32_t(OHOW);
+    const uint32_t oh = fdiv(q0, f_ow);
+    const int ihb = int(oh) * sh, iwb = int(q0 - oh * uint32_t(OW)) * sw;
+    const uint32_t ibase = img * chw4;
+    if constexpr (BLOCKED) {
+      const int ih = ihb + khd[0], iw = iwb + kwd[0];
       const bool valid = kin && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-      const float t = xi[valid ? coff[q] + ih * W + iw : 0];
-      v[q] = valid ? t : 0.f;
+      const uint32_t voff = valid ? ibase + coff[0] + uint32_t(ih * W + iw) * 4u : kOffNone;
+#pragma unroll
+      for (int q = 0; q < PASSES; ++q) v[q] = bload(rs, voff, uint32_t(q) * hw4);
+    } else {
+#pragma unroll
+      for (int q = 0; q < PASSES; ++q) {
+        const int ih = ihb + khd[q], iw = iwb + kwd[q];
+        const bool valid = kin && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
+        v[q] = bload(rs, valid ? ibase + coff[q] + uint32_t(ih * W + iw) * 4u : kOffNone, 0u);
+      }
     }
     k += kstep;
   }
@@ -485,7 +553,7 @@ struct XColsLoader {
     constexpr int LDK = BK + 4;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int q = 0; q < PASSES; ++q) lds[(tid / BK + q * RPP) * LDK + kk] = v[q];
+    for (int q = 0; q < PASSES; ++q) lds[((tid / BK) * PASSES + q) * LDK + kk] = v[q];
   }
 };
 

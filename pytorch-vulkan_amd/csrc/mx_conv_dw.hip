@@ -44,16 +44,30 @@ MX_TILE_KERNEL(C) void conv_dw_kernel(ConvArgs p) {
 
   const int64_t dw_elems = int64_t(p.G) * p.Cout_g * p.Ncols;
   float* dst = (p.splits == 1 ? p.out : p.ws + split * dw_elems) + int64_t(g) * p.Cout_g * p.Ncols;
+  // Column n of the GEMM is weight column n, or with channel-blocked columns
+  // (channel block cb, tap t, channel in block c) weight column (16cb + c)*KK + t.
   int ccol[C::FN];
+  bool cok[C::FN];
+  const int kblk = p.KK * kChanBlock;
 #pragma unroll
-  for (int j = 0; j < C::FN; ++j) ccol[j] = col0 + acc_col<C>(j);
+  for (int j = 0; j < C::FN; ++j) {
+    const int n = col0 + acc_col<C>(j);
+    cok[j] = n < p.Ncols;
+    if (p.cols_blocked) {
+      const int cb = n / kblk, rem = n - cb * kblk;
+      const int t = rem / kChanBlock;
+      ccol[j] = cb * kblk + (rem - t * kChanBlock) * p.KK + t;
+    } else {
+      ccol[j] = n;
+    }
+  }
   for_each_acc_row<C>([&](int r, int i, int v) {
     const int co = row0 + r;
     if (co >= p.M) return;
     float* d = dst + int64_t(co) * p.Ncols;
 #pragma unroll
     for (int j = 0; j < C::FN; ++j)
-      if (ccol[j] < p.Ncols) d[ccol[j]] = acc.v[i][j][v];
+      if (cok[j]) d[ccol[j]] = acc.v[i][j][v];
   });
   if (p.db != nullptr && tn == 0) {
     float* dbd = (p.splits == 1 ? p.db : p.ws_db + int64_t(split) * p.Cout) + g * p.Cout_g;
@@ -113,10 +127,14 @@ int launch_b(ConvArgs p, int bmode, hipStream_t s) {
     // picks those.
     constexpr bool dy_rows = std::is_same_v<LA, DyRowsLoader<C::BM, C::BK>>;
     constexpr bool fits = C::BN <= 128 && (C::BM * C::BN <= 128 * 128 || !dy_rows);
-    if constexpr (fits)
-      hipLaunchKernelGGL((conv_dw_kernel<C, LA, XColsLoader<C::BN, C::BK>>), grid, dim3(kThreads), 0, s, p);
-    else
+    if constexpr (fits) {
+      if (p.cols_blocked)
+        hipLaunchKernelGGL((conv_dw_kernel<C, LA, XColsLoader<C::BN, C::BK, true>>), grid, dim3(kThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((conv_dw_kernel<C, LA, XColsLoader<C::BN, C::BK, false>>), grid, dim3(kThreads), 0, s, p);
+    } else {
       return set_error(MX_ERR_INVALID, "conv2d dweight: tile too large for two gathered operands");
+    }
   }
   MX_HIP(hipGetLastError());
   return MX_OK;

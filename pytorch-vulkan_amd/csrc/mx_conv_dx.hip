@@ -106,8 +106,10 @@ int launch_b(ConvArgs p, int bmode, hipStream_t s) {
   const dim3 grid(p.tiles_m * p.tiles_n, p.splits, p.G);
   if (bmode == B_VEC)
     hipLaunchKernelGGL((conv_dx_kernel<C, MA, PosQuadLoader<C::BN, C::BK, true>>), grid, dim3(kThreads), 0, s, p);
+  else if (blocked_channels(p.Cout_g))
+    hipLaunchKernelGGL((conv_dx_kernel<C, MA, PhaseGatherLoader<C::BN, C::BK, true>>), grid, dim3(kThreads), 0, s, p);
   else
-    hipLaunchKernelGGL((conv_dx_kernel<C, MA, PhaseGatherLoader<C::BN, C::BK>>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((conv_dx_kernel<C, MA, PhaseGatherLoader<C::BN, C::BK, false>>), grid, dim3(kThreads), 0, s, p);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }

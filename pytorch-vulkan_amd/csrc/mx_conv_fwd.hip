@@ -77,10 +77,18 @@ int launch_b(ConvArgs p, int bmode, hipStream_t s) {
   p.tiles_m = (p.M + C::BM - 1) / C::BM;
   p.tiles_n = (p.Ncols + C::BN - 1) / C::BN;
   const dim3 grid(p.tiles_m * p.tiles_n, p.splits, p.G);
-  if (bmode == B_VEC)
+  if (bmode == B_VEC) {
     hipLaunchKernelGGL((conv_fwd_kernel<C, MA, PosQuadLoader<C::BN, C::BK, false>>), grid, dim3(kThreads), 0, s, p);
-  else
-    hipLaunchKernelGGL((conv_fwd_kernel<C, MA, Im2colLoader<C::BN, C::BK>>), grid, dim3(kThreads), 0, s, p);
+  } else if constexpr (MA == Mode::KVEC) {
+    if (blocked_channels(p.Cin_g))
+      hipLaunchKernelGGL((conv_fwd_kernel<C, MA, Im2colLoader<C::BN, C::BK, true>>), grid, dim3(kThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((conv_fwd_kernel<C, MA, Im2colLoader<C::BN, C::BK, false>>), grid, dim3(kThreads), 0, s, p);
+  } else {
+    // Scalar weight rows mean unpacked weights: channels not blocked, or a
+    // 1x1 kernel, whose blocked and plain K orders are the same.
+    hipLaunchKernelGGL((conv_fwd_kernel<C, MA, Im2colLoader<C::BN, C::BK, false>>), grid, dim3(kThreads), 0, s, p);
+  }
   MX_HIP(hipGetLastError());
   return MX_OK;
 }

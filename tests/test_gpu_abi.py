@@ -225,6 +225,34 @@ def test_conv_unaligned_views(mx, case):
         close(got, ref, mag=mag, what=name)
 
 
+@pytest.mark.parametrize("case", [((5, 32, 12, 10), 48, (3, 3), (1, 1), (1, 1), (1, 1), 1),
+                                  ((5, 6, 9, 9), 10, (3, 3), (2, 2), (1, 1), (1, 1), 1),
+                                  ((5, 64, 8, 8), 32, (1, 1), (1, 1), (0, 0), (1, 1), 1)])
+def test_conv_batch_chunks(mx, case, monkeypatch):
+    """Operands past the loaders' 32-bit byte range run as several launches over
+    image chunks (dWeight summed over chunks); MX_CONV_BUFFER_LIMIT lowers that
+    range so 5 images split 2 + 2 + 1."""
+    xs, cout, kernel, stride, padding, dilation, groups = case
+    x, w, b = conv_inputs(xs, cout, kernel, groups, seed=21)
+    d = mx.conv_desc(xs, w.shape, stride, padding, dilation, groups)
+    dy = torch.randn((xs[0], cout, d.oh, d.ow), generator=torch.Generator().manual_seed(8))
+    refs = conv_refs(x, w, b, dy, stride, padding, dilation, groups)
+    per_img = 4 * max(xs[1] * xs[2] * xs[3], cout * d.oh * d.ow)
+    monkeypatch.setenv("MX_CONV_BUFFER_LIMIT", str(2 * per_img + 3))
+    X, W, B, DY = dev(x), dev(w), dev(b), dev(dy)
+    y = torch.empty(dy.shape, device="cuda")
+    dx = torch.empty(xs, device="cuda")
+    dw = torch.empty(w.shape, device="cuda")
+    dbias = torch.empty(cout, device="cuda")
+    A = mx.ALGO_IMPLICIT_GEMM
+    mx.conv2d_forward(d, X, W, B, y, A, stream())
+    mx.conv2d_backward_input(d, DY, W, dx, A, stream())
+    mx.conv2d_backward_weight(d, X, DY, dw, dbias, A, stream())
+    for name, got in (("y", y), ("dx", dx), ("dw", dw), ("db", dbias)):
+        ref, mag = refs[name]
+        close(got, ref, mag=mag, what=name)
+
+
 @pytest.mark.parametrize("case", [CONV_CASES[0], ((2, 16, 9, 11), 24, (3, 3), (1, 1), (1, 1), (1, 1), 1),
                                   ((1, 32, 8, 8), 32, (3, 3), (1, 1), (0, 0), (1, 1), 4)])
 def test_conv_winograd_forward(mx, case):
