@@ -537,6 +537,175 @@ struct StridedLoader<ROWS, BK, Mode::RSCALAR> {
   }
 };
 
+// The same operand views through a buffer resource over [base, base + bytes)
+// (bytes < kBufMaxBytes, 32-bit element strides): per-lane byte offsets are
+// fixed at init, the k cursor moves the scalar offset, and masked elements
+// read zero through the range check.  Used for convolution weights; the
+// general GEMM keeps StridedLoader (its operands may exceed the 2^31 range).
+template <int ROWS, int BK, Mode MODE>
+struct BufStridedLoader;
+
+template <int ROWS, int BK>
+struct BufStridedLoader<ROWS, BK, Mode::KVEC> {
+  static constexpr bool KMAJOR = false;
+  int kstep = BK;
+  static constexpr int TPR = BK / 4;
+  static constexpr int RPP = kThreads / TPR;
+  static constexpr int PASSES = ROWS / RPP;
+  static_assert(PASSES >= 1 && ROWS % RPP == 0, "KVEC tiling");
+  f32x4 v[PASSES];
+  i32x4 rs;
+  uint32_t off[PASSES];
+  int k, kmax, kq;
+  __device__ __forceinline__ void init(const float* base, int64_t bytes, int s_row, int /*s_k*/, int row0, int R,
+                                       int k0, int kmax_) {
+    const int tid = threadIdx.x;
+    kq = tid % TPR;
+    rs = buffer_rsrc(base, bytes);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = row0 + tid / TPR + p * RPP;
+      off[p] = row < R ? uint32_t(row * s_row + 4 * kq) * 4u : kOffNone;
+    }
+    k = k0;
+    kmax = kmax_;
+  }
+  __device__ __forceinline__ void load() {
+    const bool kin = k + 4 * kq < kmax;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) v[p] = bload4(rs, kin ? off[p] : kOffNone, uint32_t(k) * 4u);
+    k += kstep;
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    const int tid = threadIdx.x;
+    constexpr int LDK = BK + 4;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+      *reinterpret_cast<f32x4*>(lds + (tid / TPR + p * RPP) * LDK + 4 * kq) = v[p];
+  }
+};
+
+template <int ROWS, int BK>
+struct BufStridedLoader<ROWS, BK, Mode::RVEC> {
+  static constexpr bool KMAJOR = true;
+  int kstep = BK;
+  static constexpr int TPK = ROWS / 4;
+  static constexpr int KPP = kThreads / TPK;
+  static constexpr int PASSES = BK / KPP;
+  static_assert(PASSES >= 1 && BK % KPP == 0, "RVEC tiling");
+  f32x4 v[PASSES];
+  i32x4 rs;
+  uint32_t off, sk4;
+  int k, kmax, kk;
+  __device__ __forceinline__ void init(const float* base, int64_t bytes, int /*s_row*/, int s_k, int row0, int R,
+                                       int k0, int kmax_) {
+    const int tid = threadIdx.x;
+    kk = tid / TPK;
+    const int row = row0 + 4 * (tid % TPK);
+    rs = buffer_rsrc(base, bytes);
+    off = row < R ? uint32_t(row + kk * s_k) * 4u : kOffNone;
+    sk4 = uint32_t(s_k) * 4u;
+    k = k0;
+    kmax = kmax_;
+  }
+  __device__ __forceinline__ void load() {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+      v[p] = bload4(rs, k + kk + p * KPP < kmax ? off : kOffNone, uint32_t(k + p * KPP) * sk4);
+    k += kstep;
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    const int tid = threadIdx.x;
+    constexpr int LDR = ROWS + 4;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+      *reinterpret_cast<f32x4*>(lds + (kk + p * KPP) * LDR + 4 * (tid % TPK)) = v[p];
+  }
+};
+
+template <int ROWS, int BK>
+struct BufStridedLoader<ROWS, BK, Mode::KSCALAR> {
+  static constexpr bool KMAJOR = false;
+  int kstep = BK;
+  static constexpr int RPP = kThreads / BK;
+  static constexpr int PASSES = ROWS / RPP;
+  static_assert(PASSES >= 1 && ROWS % RPP == 0, "KSCALAR tiling");
+  float v[PASSES];
+  i32x4 rs;
+  uint32_t off[PASSES], sk4;
+  int k, kmax, kk;
+  __device__ __forceinline__ void init(const float* base, int64_t bytes, int s_row, int s_k, int row0, int R, int k0,
+                                       int kmax_) {
+    const int tid = threadIdx.x;
+    kk = tid % BK;
+    rs = buffer_rsrc(base, bytes);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = row0 + tid / BK + p * RPP;
+      off[p] = row < R ? uint32_t(row * s_row + kk * s_k) * 4u : kOffNone;
+    }
+    sk4 = uint32_t(s_k) * 4u;
+    k = k0;
+    kmax = kmax_;
+  }
+  __device__ __forceinline__ void load() {
+    const bool kin = k + kk < kmax;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) v[p] = bload(rs, kin ? off[p] : kOffNone, uint32_t(k) * sk4);
+    k += kstep;
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    const int tid = threadIdx.x;
+    constexpr int LDK = BK + 4;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) lds[(tid / BK + p * RPP) * LDK + kk] = v[p];
+  }
+};
+
+template <int ROWS, int BK>
+struct BufStridedLoader<ROWS, BK, Mode::RSCALAR> {
+  static constexpr bool KMAJOR = false;
+  int kstep = BK;
+  static_assert(ROWS % 64 == 0 && ROWS <= kThreads, "RSCALAR tiling");
+  static constexpr int EPT = ROWS * BK / kThreads;  // consecutive k per thread (wave-uniform run)
+  float v[EPT];
+  i32x4 rs;
+  uint32_t off, sk4;
+  int k, kmax, ks;
+  __device__ __forceinline__ void init(const float* base, int64_t bytes, int s_row, int s_k, int row0, int R, int k0,
+                                       int kmax_) {
+    const int tid = threadIdx.x;
+    ks = __builtin_amdgcn_readfirstlane((tid / ROWS) * EPT);
+    const int row = row0 + tid % ROWS;
+    rs = buffer_rsrc(base, bytes);
+    off = row < R ? uint32_t(row * s_row) * 4u : kOffNone;
+    sk4 = uint32_t(s_k) * 4u;
+    k = k0;
+    kmax = kmax_;
+  }
+  __device__ __forceinline__ void load() {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int kx = k + ks + e;  // wave-uniform
+      v[e] = bload(rs, kx < kmax ? off : kOffNone, uint32_t(kx) * sk4);
+    }
+    k += kstep;
+  }
+  __device__ __forceinline__ void store(float* lds) const {
+    const int tid = threadIdx.x;
+    constexpr int LDK = BK + 4;
+    float* dst = lds + (tid % ROWS) * LDK + ks;
+    if constexpr (EPT % 4 == 0) {
+#pragma unroll
+      for (int e = 0; e < EPT; e += 4)
+        *reinterpret_cast<f32x4*>(dst + e) = f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) dst[e] = v[e];
+    }
+  }
+};
+
 // Bijective block remap so that consecutive logical tiles land on the same
 // XCD (hardware dispatches workgroup b to XCD b % 8): tiles that share an
 // operand panel then share that XCD's L2.

@@ -244,6 +244,8 @@ int linear_blocks(int64_t total) { return int(std::min<int64_t>((total + 255) / 
 // (bytes) lowers the bound, which lets the tests run the chunked path on small
 // tensors.  Returns 0 when a single image does not fit.
 int64_t images_per_launch(const mx_conv2d_desc& d) {
+  // The weights are one buffer too (they cannot be split).
+  if (d.cout * (d.cin / d.groups) * d.kh * d.kw * 4 >= conv::kBufMaxBytes) return 0;
   int64_t limit = conv::kBufMaxBytes;
   if (const char* e = std::getenv("MX_CONV_BUFFER_LIMIT")) {
     const long long v = std::atoll(e);
@@ -563,7 +565,7 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
   if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_forward(d, x, w, bias, y, s);
   if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM) {
     const int64_t nc = images_per_launch(d);
-    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d forward: one image exceeds the 2 GiB operand bound");
+    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d forward: one image or the weights exceed the 2 GiB operand bound");
     if (nc < d.n) {
       for (int64_t n0 = 0; n0 < d.n; n0 += nc) {
         const mx_conv2d_desc c = batch_slice(d, std::min(nc, d.n - n0));
@@ -619,7 +621,7 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
   hipStream_t s = resolve_stream(stream);
   if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM) {
     const int64_t nc = images_per_launch(d);
-    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d dinput: one image exceeds the 2 GiB operand bound");
+    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d dinput: one image or the weights exceed the 2 GiB operand bound");
     if (nc < d.n) {
       for (int64_t n0 = 0; n0 < d.n; n0 += nc) {
         const mx_conv2d_desc c = batch_slice(d, std::min(nc, d.n - n0));
@@ -720,7 +722,7 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
   }
   {
     const int64_t nc = images_per_launch(d);
-    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d dweight: one image exceeds the 2 GiB operand bound");
+    MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d dweight: one image or the weights exceed the 2 GiB operand bound");
     if (nc < d.n) {
       // Sum of the chunks' gradients: the first chunk writes dw / db, the
       // others go through a scratch copy added in chunk order.

@@ -69,8 +69,8 @@ MX_TILE_KERNEL(C) void conv_dx_kernel(ConvArgs p) {
   const int row0 = tm * C::BM, col0 = tn * C::BN;
   const int split = blockIdx.y;
   const int k0 = split * p.kps, k1 = min(p.K, k0 + p.kps);
-  StridedLoader<C::BM, C::BK, MA> la;  // element (ci, k) = wt[g][k][ci]
-  la.init(p.wt + int64_t(g) * p.K * p.Cin_g, 1, p.Cin_g, row0, p.M, k0, k1);
+  BufStridedLoader<C::BM, C::BK, MA> la;  // element (ci, k) = wt[g][k][ci]
+  la.init(p.wt + int64_t(g) * p.K * p.Cin_g, int64_t(p.K) * p.Cin_g * 4, 1, p.Cin_g, row0, p.M, k0, k1);
   LB lb;
   lb.init(p, col0, g, k0, k1);
   Acc<C> acc;

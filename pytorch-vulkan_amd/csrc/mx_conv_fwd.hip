@@ -24,8 +24,8 @@ MX_TILE_KERNEL(C) void conv_fwd_kernel(ConvArgs p) {
   const int row0 = tm * C::BM, col0 = tn * C::BN;
   const int split = blockIdx.y;
   const int k0 = split * p.kps, k1 = min(p.K, k0 + p.kps);
-  StridedLoader<C::BM, C::BK, MA> la;
-  la.init(p.wt + int64_t(g) * p.Cout_g * p.K, p.K, 1, row0, p.M, k0, k1);
+  BufStridedLoader<C::BM, C::BK, MA> la;
+  la.init(p.wt + int64_t(g) * p.Cout_g * p.K, int64_t(p.Cout_g) * p.K * 4, p.K, 1, row0, p.M, k0, k1);
   LB lb;
   lb.init(p, col0, g, k0, k1);
   Acc<C> acc;
