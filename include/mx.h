@@ -352,6 +352,33 @@ int mx_mse_loss_f32(const float* x, const float* t, int64_t count, int reduction
 int mx_mse_loss_backward_f32(const float* dy, const float* x, const float* t, int64_t count, int reduction,
                              float* dx, void* stream);
 
+/* Multi-tensor pointwise ops on contiguous FP32 tensors, one launch per list
+ * (torch.optim's foreach path and the per-tensor lerp / addcmul / addcdiv /
+ * maximum / minimum of csrc/ops/optimizer_primitives.cpp:12-202,
+ * optimizer_pointwise.comp).  Entry i computes out[i] = f(a, b, c, scalar)
+ * elementwise over numel elements (out may equal a: in place):
+ *   MUL_SCALAR a*s   ADD_SCALAR a+s   DIV_SCALAR a/s   SQRT sqrt(a)
+ *   LERP_SCALAR lerp(a, b, s)   LERP_TENSOR lerp(a, b, c)   (torch's two-branch lerp)
+ *   ADDCMUL fma(s*b, c, a)   ADDCDIV a + (s*b)/c   ADD_LIST fma(b, s, a)
+ *   MAXIMUM / MINIMUM of a and b (NaN propagates; a tie of signed zeros gives b).
+ * Entries that write memory an earlier entry of the list touches start a new
+ * launch, so repeated tensors update in list order.  *launches (optional)
+ * receives the launch count. */
+enum mx_foreach_op {
+  MX_FOREACH_MUL_SCALAR = 0, MX_FOREACH_ADD_SCALAR = 1, MX_FOREACH_DIV_SCALAR = 2, MX_FOREACH_LERP_SCALAR = 3,
+  MX_FOREACH_LERP_TENSOR = 4, MX_FOREACH_ADDCMUL = 5, MX_FOREACH_ADDCDIV = 6, MX_FOREACH_MAXIMUM = 7,
+  MX_FOREACH_MINIMUM = 8, MX_FOREACH_SQRT = 9, MX_FOREACH_ADD_LIST = 10
+};
+typedef struct mx_foreach_tensor {
+  float* out;
+  const float* a;
+  const float* b; /* NULL unless the op reads it */
+  const float* c;
+  int64_t numel;
+  double scalar;
+} mx_foreach_tensor;
+int mx_foreach_f32(int op, const mx_foreach_tensor* tensors, int64_t count, int64_t* launches, void* stream);
+
 /* Copy `rows` rows of `row_bytes` bytes between pitched buffers: one input's
  * slab of cat along any axis (csrc/ops/cat.cpp:44-55, cat_copy.comp). */
 int mx_copy_rows(void* dst, int64_t dst_pitch, const void* src, int64_t src_pitch, int64_t row_bytes,

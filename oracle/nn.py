@@ -25,6 +25,10 @@ What pins each function (tests/test_oracle_nn.py):
                                    and its autograd; finite differences.
   mse_loss / mse_loss_backward     closed forms and torch.nn.functional.mse_loss.
   cat                              np.concatenate.
+  lerp / addcmul / addcdiv / add_alpha / maximum / minimum (float32, the
+  foreach ops)                     torch.lerp / addcmul / addcdiv / add(alpha) /
+                                   maximum / minimum on the CPU, bit for bit
+                                   (signed zeros and NaN included).
 """
 from __future__ import annotations
 
@@ -238,3 +242,55 @@ def cat(xs, dim: int):
     """csrc/ops/cat.cpp:8-58: concatenation, 1-D empty inputs skipped."""
     keep = [np.asarray(v) for v in xs if not (np.asarray(v).ndim == 1 and np.asarray(v).size == 0)]
     return np.concatenate(keep, axis=dim)
+
+
+# ------------------------------------------------------------- foreach ops
+def _f32(x):
+    return np.asarray(x, np.float32).astype(np.float64)
+
+
+def fma32(a, b, c):
+    """float32 fused multiply-add: the exact a*b + c rounded once (float64 holds
+    the product of two float32 exactly)."""
+    return (_f32(a) * _f32(b) + _f32(c)).astype(np.float32)
+
+
+def lerp(a, b, w):
+    """torch's vectorised CPU lerp (ATen/native/Lerp.h, cpu/LerpKernel.cpp):
+    |w| < 0.5 ? fma(w, b - a, a) : fma(w - 1, b - a, b), in float32.
+    The reference's optimizer_pointwise op 0/1 (csrc/ops/optimizer_primitives.cpp:50-51)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    w = np.broadcast_to(np.asarray(w, np.float32), a.shape)
+    d = (b - a).astype(np.float32)
+    return np.where(np.abs(w) < 0.5, fma32(w, d, a), fma32((w - np.float32(1)).astype(np.float32), d, b))
+
+
+def addcmul(a, t1, t2, v):
+    """fma(v * t1, t2, a) in float32: torch's CPU addcmul (one fused
+    multiply-add after the scalar product; csrc/ops/optimizer_primitives.cpp:52)."""
+    v = np.float32(v)
+    return fma32((v * np.asarray(t1, np.float32)).astype(np.float32), t2, a)
+
+
+def add_alpha(a, b, alpha):
+    """fma(b, alpha, a) in float32: torch's CPU add with alpha."""
+    return fma32(b, np.float32(alpha), a)
+
+
+def addcdiv(a, t1, t2, v):
+    """a + (v * t1) / t2 in float32 (csrc/ops/optimizer_primitives.cpp:53)."""
+    v = np.float32(v)
+    return (np.asarray(a, np.float32) + (v * np.asarray(t1, np.float32)) / np.asarray(t2, np.float32)).astype(np.float32)
+
+
+def maximum(a, b):
+    """NaN-propagating maximum as torch's vectorised CPU kernel (max_ps: the
+    second operand unless the first is greater, so max(-0, +0) = +0)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return np.where(np.isnan(a) | np.isnan(b), np.float32(np.nan), np.where(a > b, a, b))
+
+
+def minimum(a, b):
+    """NaN-propagating minimum (min_ps: the second operand unless the first is smaller)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return np.where(np.isnan(a) | np.isnan(b), np.float32(np.nan), np.where(a < b, a, b))

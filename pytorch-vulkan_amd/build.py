@@ -39,8 +39,8 @@ HIP_FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 MX_SOURCES = ["mx_runtime.hip", "mx_gemm.hip", "mx_conv.hip", "mx_conv_fwd.hip", "mx_conv_dx.hip", "mx_conv_dw.hip",
-              "mx_winograd.hip", "mx_adamw.hip", "mx_util.hip", "mx_nn.hip"]
-EXT_SOURCES = ["backend.cpp", "ops_conv.cpp", "ops_gemm.cpp", "ops_adamw.cpp", "ops_plumbing.cpp", "ops_nn.cpp"]
+              "mx_winograd.hip", "mx_adamw.hip", "mx_util.hip", "mx_nn.hip", "mx_foreach.hip"]
+EXT_SOURCES = ["backend.cpp", "ops_conv.cpp", "ops_gemm.cpp", "ops_adamw.cpp", "ops_plumbing.cpp", "ops_nn.cpp", "ops_foreach.cpp"]
 
 
 def torch_paths():

@@ -39,6 +39,7 @@ EXPORTS = [
     "mx_group_norm_forward", "mx_group_norm_backward", "mx_batch_norm_forward", "mx_batch_norm_backward",
     "mx_unary_f32", "mx_unary_backward_f32", "mx_upsample_nearest2d", "mx_upsample_nearest2d_backward",
     "mx_softmax_f32", "mx_softmax_backward_f32", "mx_mse_loss_f32", "mx_mse_loss_backward_f32", "mx_copy_rows",
+    "mx_foreach_f32",
 ]
 
 
@@ -71,6 +72,11 @@ class AdamWHParams(C.Structure):
     _fields_ = [("lr", C.c_double), ("beta1", C.c_double), ("beta2", C.c_double), ("eps", C.c_double),
                 ("weight_decay", C.c_double), ("amsgrad", C.c_int), ("maximize", C.c_int),
                 ("lr_dev", C.c_void_p), ("grad_scale", C.c_void_p), ("found_inf", C.c_void_p)]
+
+
+class ForeachTensor(C.Structure):
+    _fields_ = [("out", C.c_void_p), ("a", C.c_void_p), ("b", C.c_void_p), ("c", C.c_void_p),
+                ("numel", C.c_int64), ("scalar", C.c_double)]
 
 
 class MemoryStats(C.Structure):
@@ -147,6 +153,7 @@ def lib() -> C.CDLL:
             "mx_mse_loss_f32": ([vp, vp, i64, i32, vp, vp], i32),
             "mx_mse_loss_backward_f32": ([vp, vp, vp, i64, i32, vp, vp], i32),
             "mx_copy_rows": ([vp, i64, vp, i64, i64, i64, vp], i32),
+            "mx_foreach_f32": ([i32, C.POINTER(ForeachTensor), i64, C.POINTER(i64), vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -346,6 +353,24 @@ def mse_loss_backward(dy, x, t, reduction, dx, stream=None) -> None:
 def copy_rows(dst, dst_pitch, src, src_pitch, row_bytes, rows, stream=None) -> None:
     """Pitches and row length in bytes; dst / src are raw device addresses."""
     check(lib().mx_copy_rows(dst, dst_pitch, src, src_pitch, row_bytes, rows, stream))
+
+
+(FE_MUL_SCALAR, FE_ADD_SCALAR, FE_DIV_SCALAR, FE_LERP_SCALAR, FE_LERP_TENSOR, FE_ADDCMUL, FE_ADDCDIV,
+ FE_MAXIMUM, FE_MINIMUM, FE_SQRT, FE_ADD_LIST) = range(11)
+
+
+def foreach(op, outs, a, b=None, c=None, scalars=0.0, stream=None) -> int:
+    """One multi-tensor pointwise call; scalars is one number or one per tensor.
+    Returns the number of launches."""
+    n = len(outs)
+    arr = (ForeachTensor * max(1, n))()
+    for i in range(n):
+        s = scalars[i] if isinstance(scalars, (list, tuple)) else scalars
+        arr[i] = ForeachTensor(ptr(outs[i]), ptr(a[i]), ptr(b[i]) if b is not None else None,
+                               ptr(c[i]) if c is not None else None, outs[i].numel(), float(s))
+    launches = C.c_int64(0)
+    check(lib().mx_foreach_f32(op, arr, n, C.byref(launches), stream))
+    return launches.value
 
 
 def conv2d_kernel_name(d: ConvDesc, phase: int, algo: int = ALGO_AUTO) -> str:

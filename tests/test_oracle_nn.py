@@ -202,3 +202,40 @@ def test_cat_matches_concatenate_and_skips_legacy_empty():
     a, b = np.ones((2, 3, 4)), np.zeros((2, 5, 4))
     np.testing.assert_array_equal(O.cat([a, np.zeros(0), b], 1), np.concatenate([a, b], 1))
     np.testing.assert_array_equal(O.cat([a, a], -1), torch.cat([t64(a), t64(a)], -1).numpy())
+
+
+# ------------------------------------------------------------- foreach ops
+def _ulp_close(a, b, ulps=0):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    both_nan = np.isnan(a) & np.isnan(b)
+    diff = np.abs(a.astype(np.float64) - b.astype(np.float64))
+    tol = ulps * np.spacing(np.maximum(np.abs(a), np.abs(b)).astype(np.float32)).astype(np.float64)
+    assert np.all(both_nan | (diff <= tol)), float(np.max(np.where(both_nan, 0, diff - tol)))
+
+
+@pytest.mark.parametrize("w", [0.1, 0.49, 0.5, 0.9, -0.3, 1.7])
+def test_lerp_matches_torch_cpu(w):
+    rng = np.random.default_rng(31)
+    a, b = (rng.standard_normal(1000) * 3).astype(np.float32), rng.standard_normal(1000).astype(np.float32)
+    _ulp_close(O.lerp(a, b, w), torch.lerp(torch.from_numpy(a), torch.from_numpy(b), w).numpy())
+    wt = rng.uniform(-1, 2, 1000).astype(np.float32)
+    _ulp_close(O.lerp(a, b, wt), torch.lerp(torch.from_numpy(a), torch.from_numpy(b), torch.from_numpy(wt)).numpy())
+    assert np.array_equal(O.lerp(a, b, 0.0), a) and np.array_equal(O.lerp(a, b, 1.0), b)
+
+
+def test_addcmul_addcdiv_extrema_match_torch_cpu():
+    rng = np.random.default_rng(32)
+    a, t1, t2 = (rng.standard_normal((3, 1000)) * 2).astype(np.float32)
+    t2 = np.abs(t2) + np.float32(0.1)
+    A, T1, T2 = map(torch.from_numpy, (a, t1, t2))
+    _ulp_close(O.addcmul(a, t1, t2, -0.37), torch.addcmul(A, T1, T2, value=-0.37).numpy())
+    _ulp_close(O.addcdiv(a, t1, t2, 1.9), torch.addcdiv(A, T1, T2, value=1.9).numpy())
+    _ulp_close(O.add_alpha(a, t1, -0.71), torch.add(A, T1, alpha=-0.71).numpy())
+    # 64 elements so torch takes its vectorised path throughout
+    x = np.resize(np.array([1.0, np.nan, -0.0, 0.0, 3.0, -2.0, 0.5, 7.0], np.float32), 64)
+    y = np.resize(np.array([2.0, 1.0, 0.0, -0.0, np.nan, -5.0, 0.5, -7.0], np.float32), 64)
+    for f, t in ((O.maximum, torch.maximum), (O.minimum, torch.minimum)):
+        got, want = f(x, y), t(torch.from_numpy(x), torch.from_numpy(y)).numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+        assert np.array_equal(np.signbit(got[~np.isnan(got)]), np.signbit(want[~np.isnan(want)]))
