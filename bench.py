@@ -4,6 +4,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1|c4|copy] [--no-cpu-baseline]
     python bench.py --pmc-summary FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR
     python bench.py --trace-summary KERNEL_TRACE_CSV BENCH_LOG
+    python bench.py --stats-table KERNEL_STATS_OR_TRACE_CSV STEPS_RUN
 
 Prints ONE JSON line.  The headline (`value`) is BASELINE.json's Conv2D
 fwd+bwd FP32 TFLOP/s on its largest single-GPU Conv2D configuration, C3: the
@@ -413,6 +414,53 @@ BEFORE_HELPERS = ("conv_fwd_pack_kernel", "conv_dx_pack_kernel")       # run bef
 AFTER_HELPERS = ("conv_dw_finalize_kernel", "conv_sum_splits_kernel")   # run after it
 
 
+PHASE_MARKER = "spin_kernel"   # torch.cuda._sleep's kernel, issued once between the headline and the components
+
+
+def stats_table(stats_csv, steps_run, top=25):
+    """Markdown tables from a rocprofv3 --stats kernel_stats.csv (or from a
+    --kernel-trace CSV, up to the headline's end marker): time per step of
+    each launch class (all instantiations of a kernel template together), then
+    the top kernel instantiations."""
+    import csv
+    import re
+    rows = list(csv.DictReader(open(stats_csv)))
+    if rows and "Start_Timestamp" in rows[0]:
+        # a --kernel-trace CSV: the headline phase only, aggregated per kernel
+        rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+        agg = defaultdict(lambda: [0, 0])
+        for r in rows:
+            if PHASE_MARKER in r["Kernel_Name"]:
+                break
+            a = agg[r["Kernel_Name"]]
+            a[0] += 1
+            a[1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        rows = [{"Name": k, "Calls": str(n), "TotalDurationNs": str(t)} for k, (n, t) in agg.items()]
+    steps_run = float(steps_run)
+    cls = defaultdict(lambda: [0, 0.0])
+    for r in rows:
+        c = cls[kernel_class(r["Name"]).split("<")[0]]
+        c[0] += int(r["Calls"])
+        c[1] += float(r["TotalDurationNs"])
+    total = sum(t for _, t in cls.values())
+    out = [f"Kernel time {total / 1e6 / steps_run:.3f} ms per step over {steps_run:g} steps.", "",
+           "| launch class | ms/step | calls/step | avg us | % |", "|---|---:|---:|---:|---:|"]
+    for k, (n, t) in sorted(cls.items(), key=lambda kv: -kv[1][1])[:top]:
+        out.append(f"| `{k}` | {t / 1e6 / steps_run:.3f} | {n / steps_run:.1f} | {t / n / 1e3:.1f} | "
+                   f"{100 * t / total:.2f} |")
+
+    def short(n):
+        n = re.sub(r"mx::(conv::|mfma::)?(\(anonymous namespace\)::)?", "", n).replace("void ", "")
+        n = re.sub(r"\((ConvArgs|GemmArgs|WinoArgs)\)$", "", n)
+        return ("torch: " + n.split("<")[0].split("(")[0]) if "at::native" in n else n[:120]
+    out += ["", "| kernel | calls | total us | avg us | % |", "|---|---:|---:|---:|---:|"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:top]:
+        t = float(r["TotalDurationNs"])
+        out.append(f"| `{short(r['Name'])}` | {r['Calls']} | {t / 1e3:.1f} | {t / int(r['Calls']) / 1e3:.2f} | "
+                   f"{100 * t / total:.2f} |")
+    return "\n".join(out)
+
+
 def trace_summary(trace_csv, bench_log):
     """Per bench launch class: the kernel time of one ABI call from a rocprofv3
     --kernel-trace CSV of a bench.py run, comparable with that run's live
@@ -426,6 +474,9 @@ def trace_summary(trace_csv, bench_log):
     res = [json.loads(l) for l in open(bench_log) if l.startswith("{")][-1]
     steps_run = res["warmup"] + 2 * res["steps"]
     rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    # the headline phase ends at the marker dispatch main() issues before the components
+    end = next((i for i, r in enumerate(rows) if PHASE_MARKER in r["Kernel_Name"]), len(rows))
+    rows = rows[:end]
     seq = [(kernel_class(r["Kernel_Name"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
            for r in rows]
     owner = [None] * len(seq)
@@ -483,6 +534,8 @@ def main(argv=None):
     ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_LOG"),
                     help="kernel time per ABI call of each launch class from a rocprofv3 kernel trace of a "
                          "bench.py run, next to that run's live per-call time")
+    ap.add_argument("--stats-table", nargs=2, metavar=("KERNEL_STATS_CSV", "STEPS_RUN"),
+                    help="markdown tables (per launch class, per kernel) from a rocprofv3 --stats CSV")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 forwards to implicit GEMM")
@@ -492,6 +545,9 @@ def main(argv=None):
         return 0
     if args.trace_summary:
         print(json.dumps(trace_summary(*args.trace_summary), indent=1))
+        return 0
+    if args.stats_table:
+        print(stats_table(*args.stats_table))
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the multi-GPU "
@@ -546,6 +602,7 @@ def main(argv=None):
     }
     del calls
     torch.cuda.empty_cache()
+    torch.cuda._sleep(1)   # marks the end of the headline phase in a kernel trace (PHASE_MARKER)
 
     # ---------------- components
     if not args.no_components:

@@ -250,9 +250,24 @@ def _f32(x):
 
 
 def fma32(a, b, c):
-    """float32 fused multiply-add: the exact a*b + c rounded once (float64 holds
-    the product of two float32 exactly)."""
-    return (_f32(a) * _f32(b) + _f32(c)).astype(np.float32)
+    """float32 fused multiply-add: the exact a*b + c rounded once to nearest
+    even.  float64 holds the product of two float32 exactly; the float64 sum s
+    is one rounding away from the exact value s + e (e recovered exactly by
+    Knuth's TwoSum), and rounding s to float32 gives the correctly rounded
+    result except when s lands exactly on a float32 midpoint with e != 0: then
+    the neighbour on e's side is the answer."""
+    p, c64 = _f32(a) * _f32(b), _f32(c)
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = p + c64
+        bv = s - p
+        e = (p - (s - bv)) + (c64 - bv)
+        f = s.astype(np.float32)
+        g = np.where(s > f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf)))
+        tie = np.isfinite(s) & (f.astype(np.float64) != s) & \
+            ((f.astype(np.float64) + g.astype(np.float64)) * 0.5 == s) & (e != 0) & np.isfinite(e)
+        up = np.maximum(f, g)
+        dn = np.minimum(f, g)
+        return np.where(tie, np.where(e > 0, up, dn), f).astype(np.float32)
 
 
 def lerp(a, b, w):

@@ -239,3 +239,70 @@ def test_addcmul_addcdiv_extrema_match_torch_cpu():
         assert np.array_equal(np.isnan(got), np.isnan(want))
         assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
         assert np.array_equal(np.signbit(got[~np.isnan(got)]), np.signbit(want[~np.isnan(want)]))
+
+
+# ---------------------------------------------------------------- fma32 exactness and planted mistakes
+def _round_f32_exact(v):
+    """Correctly rounded float32 (nearest, ties to even) of an exact rational."""
+    from fractions import Fraction
+    f0 = np.float32(float(v))
+    cands = [f0, np.nextafter(f0, np.float32(np.inf)), np.nextafter(f0, np.float32(-np.inf))]
+    best = min(cands, key=lambda f: (abs(Fraction(float(f)) - v), int(np.float32(f).view(np.int32)) & 1))
+    return np.float32(best)
+
+
+def _fma_exact(a, b, c):
+    from fractions import Fraction
+    return np.array([_round_f32_exact(Fraction(float(x)) * Fraction(float(y)) + Fraction(float(z)))
+                     for x, y, z in zip(a, b, c)], np.float32)
+
+
+# a*b lies 2^-70 below the float32 midpoint 1 + 2^-23 + 2^-24: one float64
+# rounding lands on the midpoint, and ties-to-even would then round up.
+TIE = (np.float32(1 + 2 ** -23), np.float32(2 ** -24 - 2 ** -47), np.float32(1 + 2 ** -23))
+
+
+def test_fma32_is_correctly_rounded():
+    rng = np.random.default_rng(41)
+    a = (rng.standard_normal(3000) * 2).astype(np.float32)
+    b = (rng.standard_normal(3000) * 2).astype(np.float32)
+    c = (rng.standard_normal(3000) * 4).astype(np.float32)
+    a, b, c = (np.append(x, t) for x, t in zip((a, b, c), TIE))
+    assert np.array_equal(O.fma32(a, b, c), _fma_exact(a, b, c))
+    assert O.fma32(*TIE) == np.float32(1 + 2 ** -23)
+
+
+def test_planted_mistakes_are_caught():
+    """Each planted variant of an oracle function fails a check above."""
+    # fma by one float64 sum then a float32 cast (double rounding): the tie vector
+    naive = lambda x, y, z: (_f64(x) * _f64(y) + _f64(z)).astype(np.float32)  # noqa: E731
+    assert naive(*TIE) != _fma_exact(*[np.array([t]) for t in TIE])[0]
+    rng = np.random.default_rng(43)
+    a, t1, t2 = (rng.standard_normal((3, 4096)) * 2).astype(np.float32)
+    A, T1, T2 = map(torch.from_numpy, (a, t1, t2))
+    # addcmul as two roundings (v*t1*t2 + a)
+    two = ((np.float32(-0.37) * t1 * t2).astype(np.float32) + a).astype(np.float32)
+    assert not np.array_equal(two, torch.addcmul(A, T1, T2, value=-0.37).numpy())
+    # lerp without the w >= 0.5 branch
+    one_branch = O.fma32(np.float32(0.9), (t1 - a).astype(np.float32), a)
+    assert not np.array_equal(one_branch, torch.lerp(A, T1, 0.9).numpy())
+    # GroupNorm variance with the n-1 denominator: the variance-1 invariant fails
+    x = rng.standard_normal((2, 6, 3, 3)) * 3 + 7
+    v = x.reshape(2, 3, -1)
+    z = (v - v.mean(axis=2, keepdims=True)) / np.sqrt(v.var(axis=2, ddof=1, keepdims=True))
+    assert not np.allclose(z.var(axis=2), 1, rtol=1e-10)
+    # GroupNorm backward without the mean(dy) term: finite differences disagree
+    w = rng.standard_normal(6)
+    g = rng.standard_normal(x.shape)
+    _, mean, rstd = O.group_norm_forward(x, w, None, 3, 1e-3)
+    dx, _, _ = O.group_norm_backward(g, x, mean, rstd, w, 3)
+    vg = (g * w[None, :, None, None]).reshape(2, 3, -1)
+    wrong = dx + np.repeat(rstd, 2, axis=1)[:, :, None, None] * \
+        np.repeat(vg.mean(axis=2), 2, axis=1)[:, :, None, None]
+    fd = fd_grad(lambda u: O.group_norm_forward(u, w, None, 3, 1e-3)[0], x.copy(), g)
+    np.testing.assert_allclose(dx, fd, rtol=1e-5, atol=1e-6)
+    assert not np.allclose(wrong, fd, rtol=1e-5, atol=1e-6)
+
+
+def _f64(x):
+    return np.asarray(x, np.float32).astype(np.float64)
