@@ -15,7 +15,8 @@ every layer; inputs are resident in HBM before timing.  `components` holds
 C1 (single conv layer fwd+dX+dW+dB), C2 (Linear addmm fwd+bwd, 8192x4096x4096),
 C5 (multi-tensor AdamW, 250 tensors, GB/s), C4 (the diffusion U-Net training
 step on the "vulkan" device, TFLOP/s of its convolutions and bmm over the
-whole step) and c4_ops (its normalisation / activation kernels, GB/s).
+whole step), c4_ops (its normalisation / activation kernels, GB/s) and
+streams (copy / compute overlap across HIP streams on the "vulkan" device).
 
 Every kernel runs through the C ABI (libmx.so, include/mx.h); torch ROCm
 tensors only provide device memory and the stream.  `roofline` is measured
@@ -279,6 +280,56 @@ def run_c4(torch, steps, warmup, log):
            "gflop_per_step": round(flops / 1e9, 1), "params": params,
            "cpu_fallback_calls_per_step": fallbacks / steps, "host_reads_per_step": reads / steps}
     del model, opt, x, t
+    return out
+
+
+def run_streams(torch, reps=5):
+    """Copy / compute overlap on the "vulkan" device: a 256 MiB upload from
+    page-locked host memory (non_blocking) on a copy stream beside two one-tile
+    GEMMs (64x64 output, K = 2^19: one workgroup for milliseconds) on a
+    compute stream, then two such GEMMs on two streams.  Each figure is the
+    best of `reps` runs timed on the host between device synchronisations."""
+    import torch_vulkan as tv
+
+    def timed(fn):
+        best = float("inf")
+        for _ in range(reps):
+            tv.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            tv.synchronize()
+            best = min(best, time.perf_counter() - t0)
+        return 1e3 * best
+
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(64, 1 << 19, generator=g).to("vulkan")
+    b = torch.randn(1 << 19, 64, generator=g).to("vulkan")
+    host = torch.randn(64 << 20, generator=g).pin_memory()
+    dst = torch.empty(64 << 20, device="vulkan")
+    s1, s2 = tv.Stream(), tv.Stream()
+    for s in (s1, s2):
+        s.wait_stream(tv.current_stream())
+
+    def upload():
+        with tv.stream(s2):
+            dst.copy_(host, non_blocking=True)
+
+    def gemms(streams):
+        for s in streams:
+            with tv.stream(s):
+                a @ b
+
+    t_copy = timed(upload)
+    t_gemm = timed(lambda: gemms((s1, s1)))
+    t_both = timed(lambda: (upload(), gemms((s1, s1))))
+    t_two = timed(lambda: gemms((s1, s2)))
+    out = {"workload": "stream overlap: 256 MiB non_blocking upload from pinned memory on a copy stream beside "
+                       "two one-tile GEMMs (64x64, K=2^19) on a compute stream; then the two GEMMs on two streams",
+           "copy_ms": round(t_copy, 3), "h2d_gb_s": round(4 * (64 << 20) / (t_copy * 1e-3) / 1e9, 1),
+           "gemms_one_stream_ms": round(t_gemm, 3), "copy_beside_gemms_ms": round(t_both, 3),
+           "copy_hidden_frac": round((t_copy + t_gemm - t_both) / t_copy, 3),
+           "gemms_two_streams_ms": round(t_two, 3), "two_stream_speedup": round(t_gemm / t_two, 3)}
+    del a, b, host, dst
     return out
 
 
@@ -642,6 +693,8 @@ def main(argv=None):
         torch.cuda.empty_cache()
         comps["c4"] = run_c4(torch, max(3, min(args.steps, 10)), 3, log)
         log("c4", comps["c4"]["ms_per_step"], "ms/step", comps["c4"]["value"], "TFLOP/s")
+        comps["streams"] = run_streams(torch)
+        log("streams", comps["streams"])
         result["components"] = comps
 
     # ---------------- CPU baseline (bounded sample)

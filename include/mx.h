@@ -94,6 +94,21 @@ enum mx_copy_kind { MX_COPY_H2D = 1, MX_COPY_D2H = 2, MX_COPY_D2D = 3 };
  * complete on return (as the reference's ensure_host_read,
  * csrc/vulkan_context.cpp:98-112). */
 int mx_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream);
+/* *pinned = 1 when `ptr` lies in page-locked host memory HIP knows
+ * (hipHostMalloc, including torch's pinned-memory allocator), else 0.  The
+ * reference has no pinned memory (csrc/ops/mm.cpp:664 rejects pin_memory);
+ * this serves non_blocking copies (torch's Tensor.to(non_blocking=True)). */
+int mx_host_is_pinned(const void* ptr, int* pinned);
+/* Page-locked host memory (hipHostMalloc), cached by rounded size and
+ * returned to the cache by mx_host_free (released by mx_empty_cache): the
+ * PrivateUse1 pinned-memory allocator behind Tensor.pin_memory(). */
+int mx_host_malloc(void** ptr, size_t bytes);
+int mx_host_free(void* ptr);
+/* H2D / D2H copy on `stream` that returns before the copy runs (no host
+ * staging).  The host side must be page-locked over its whole range (else
+ * MX_ERR_INVALID) and stay alive and untouched until the stream reaches the
+ * copy (record an event after it). */
+int mx_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Elementwise / layout plumbing used by the operator surface                */

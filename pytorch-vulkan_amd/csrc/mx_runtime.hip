@@ -152,6 +152,8 @@ void release_cached(int dev) {
 
 }  // namespace
 
+void release_host_cache();  // the page-locked host block cache, below
+
 }  // namespace mx
 
 using namespace mx;
@@ -419,6 +421,7 @@ int mx_empty_cache(void) {
   process_pending(g_pools[dev]);
   release_cached(dev);
   g_stats.cached_blocks = 0;
+  release_host_cache();
   return MX_OK;
   MX_ABI_END
 }
@@ -445,6 +448,104 @@ int mx_memcpy(void* dst, const void* src, size_t bytes, int kind, void* stream) 
   MX_HIP(hipMemcpyAsync(dst, src, bytes, k, s));
   // Host buffers may be pageable and are reused by the caller on return.
   if (kind != MX_COPY_D2D) MX_HIP(hipStreamSynchronize(s));
+  return MX_OK;
+  MX_ABI_END
+}
+
+}  // extern "C"
+
+namespace mx {
+namespace {
+// Page-locked host blocks, cached by rounded size.  A freed block is reusable
+// at once: the PyTorch layer keeps a host storage alive until every
+// asynchronous copy that reads or writes it has completed, and host code is
+// synchronous.
+std::mutex g_host_mu;
+std::unordered_map<void*, size_t> g_host_live;        // pointer -> rounded size
+std::multimap<size_t, void*> g_host_free;             // rounded size -> cached block
+
+size_t host_round(size_t bytes) {
+  if (bytes <= (size_t(1) << 20)) {
+    size_t r = 512;
+    while (r < bytes) r <<= 1;
+    return r;
+  }
+  const size_t g = size_t(2) << 20;
+  return (bytes + g - 1) / g * g;
+}
+}  // namespace
+
+void release_host_cache() {
+  std::lock_guard<std::mutex> lock(g_host_mu);
+  for (auto& kv : g_host_free) (void)hipHostFree(kv.second);
+  g_host_free.clear();
+}
+}  // namespace mx
+
+extern "C" {
+
+int mx_host_malloc(void** ptr, size_t bytes) {
+  MX_ABI_BEGIN
+  *ptr = nullptr;
+  if (bytes == 0) return MX_OK;
+  const size_t r = host_round(bytes);
+  std::lock_guard<std::mutex> lock(g_host_mu);
+  auto it = g_host_free.find(r);
+  void* p = nullptr;
+  if (it != g_host_free.end()) {
+    p = it->second;
+    g_host_free.erase(it);
+  } else {
+    MX_HIP(hipHostMalloc(&p, r, hipHostMallocDefault));
+  }
+  g_host_live[p] = r;
+  *ptr = p;
+  return MX_OK;
+  MX_ABI_END
+}
+
+int mx_host_free(void* ptr) {
+  MX_ABI_BEGIN
+  if (!ptr) return MX_OK;
+  std::lock_guard<std::mutex> lock(g_host_mu);
+  auto it = g_host_live.find(ptr);
+  MX_REQUIRE(it != g_host_live.end(), MX_ERR_INVALID, "mx_host_free: pointer not from mx_host_malloc");
+  g_host_free.emplace(it->second, ptr);
+  g_host_live.erase(it);
+  return MX_OK;
+  MX_ABI_END
+}
+
+int mx_host_is_pinned(const void* ptr, int* pinned) {
+  MX_ABI_BEGIN
+  *pinned = 0;
+  if (!ptr) return MX_OK;
+  hipPointerAttribute_t attr;
+  std::memset(&attr, 0, sizeof(attr));
+  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess) {
+    (void)hipGetLastError();  // memory HIP does not know: pageable, not an error
+    return MX_OK;
+  }
+  *pinned = attr.type == hipMemoryTypeHost ? 1 : 0;
+  return MX_OK;
+  MX_ABI_END
+}
+
+int mx_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream) {
+  MX_ABI_BEGIN
+  if (!bytes) return MX_OK;
+  if (kind != MX_COPY_H2D && kind != MX_COPY_D2H)
+    return set_error(MX_ERR_INVALID, cat("mx_memcpy_async: kind must be H2D or D2H, got ", kind));
+  const char* host = static_cast<const char*>(kind == MX_COPY_H2D ? src : dst);
+  int first = 0, last = 0;
+  int rc = mx_host_is_pinned(host, &first);
+  if (rc != MX_OK) return rc;
+  rc = mx_host_is_pinned(host + bytes - 1, &last);
+  if (rc != MX_OK) return rc;
+  if (!first || !last)
+    return set_error(MX_ERR_INVALID, "mx_memcpy_async: the host buffer is not page-locked (hipHostMalloc) memory");
+  MX_HIP(hipMemcpyAsync(dst, src, bytes, kind == MX_COPY_H2D ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost,
+                        resolve_stream(stream)));
   return MX_OK;
   MX_ABI_END
 }

@@ -134,6 +134,28 @@ struct VkAllocator final : public c10::Allocator {
 
 VkAllocator g_allocator;
 
+void host_delete(void* p) {
+  if (p) mx_host_free(p);
+}
+
+// Tensor.pin_memory() for this device: page-locked host memory from the
+// library's cache (CPU tensors, usable by non_blocking copies).
+struct PinnedAllocator final : public c10::Allocator {
+  c10::DataPtr allocate(size_t n) override {
+    void* p = nullptr;
+    if (n) {
+      const int rc = mx_host_malloc(&p, n);
+      TORCH_CHECK_WITH(OutOfMemoryError, rc == MX_OK, "vulkan: cannot allocate ", n, " bytes of pinned memory: ",
+                       mx_last_error());
+    }
+    return {p, p, &host_delete, c10::Device(c10::DeviceType::CPU)};
+  }
+  c10::DeleterFnPtr raw_deleter() const override { return &host_delete; }
+  void copy_data(void* dest, const void* src, std::size_t count) const override { std::memcpy(dest, src, count); }
+};
+
+PinnedAllocator g_pinned_allocator;
+
 }  // namespace
 
 c10::Allocator* allocator() { return &g_allocator; }
@@ -313,6 +335,11 @@ struct VkHooks final : public at::PrivateUse1HooksInterface {
     return c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(cur_dev()));
   }
   bool hasPrimaryContext(c10::DeviceIndex) const override { return true; }
+  at::Allocator* getPinnedMemoryAllocator() const override { return &g_pinned_allocator; }
+  bool isPinnedPtr(const void* data) const override {
+    int pinned = 0;
+    return mx_host_is_pinned(data, &pinned) == MX_OK && pinned != 0;
+  }
   c10::DeviceIndex deviceCount() const override {
     int n = 0;
     if (mx_device_count(&n) != MX_OK) return 0;
@@ -357,6 +384,8 @@ py::dict execution_stats() {
   d["host_reads"] = c.host_reads.load();
   d["kernel_launches"] = c.kernel_launches.load();
   d["adamw_launches"] = c.adamw_launches.load();
+  d["async_copies"] = c.async_copies.load();
+  d["pending_host_copies"] = tvk::pending_host_copies();
   return d;
 }
 
@@ -366,6 +395,7 @@ void reset_execution_stats() {
   c.host_reads = 0;
   c.kernel_launches = 0;
   c.adamw_launches = 0;
+  c.async_copies = 0;
 }
 
 py::dict memory_stats() {

@@ -39,7 +39,12 @@ struct Counters {
   std::atomic<uint64_t> host_reads{0};
   std::atomic<uint64_t> kernel_launches{0};
   std::atomic<uint64_t> adamw_launches{0};
+  std::atomic<uint64_t> async_copies{0};  // non_blocking copies to / from page-locked host memory
 };
+
+// Asynchronous host copies whose host storage is still held (completed ones
+// are released first).
+size_t pending_host_copies();
 Counters& counters();
 
 // Conv algorithm selections (conv_dispatch_stats()).

@@ -14,6 +14,8 @@
 #include <torch/library.h>
 
 #include <cstring>
+#include <deque>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -73,6 +75,64 @@ void d2d_copy(const at::Tensor& dst, const at::Tensor& src) {
   counters().kernel_launches++;
 }
 
+// ----------------------------------------------------- non_blocking copies
+// A non_blocking copy between the device and page-locked host memory is
+// queued on the current stream and returns at once (the reference has no
+// pinned memory and always waits).  The host storage is held here until an
+// event recorded after the copy has completed, so freeing the host tensor
+// right after the call cannot hand its pages to another allocation while the
+// copy still reads or writes them.
+struct PendingHost {
+  void* event;
+  c10::Storage storage;
+};
+std::mutex g_pending_mu;
+std::deque<PendingHost> g_pending;   // in issue order
+std::vector<void*> g_event_pool;     // completed events, reused
+
+void reap_pending_locked() {
+  while (!g_pending.empty()) {
+    int done = 0;
+    TVK_MX(mx_event_query(g_pending.front().event, &done));
+    if (!done) break;
+    g_event_pool.push_back(g_pending.front().event);
+    g_pending.pop_front();
+  }
+}
+
+bool host_pinned(const at::Tensor& t) {
+  int pinned = 0;
+  TVK_MX(mx_host_is_pinned(t.data_ptr(), &pinned));
+  return pinned != 0;
+}
+
+void copy_async(void* dst, const void* src, size_t bytes, int kind, const c10::Storage& host) {
+  std::lock_guard<std::mutex> lock(g_pending_mu);
+  reap_pending_locked();
+  void* stream = current_stream();
+  TVK_MX(mx_memcpy_async(dst, src, bytes, kind, stream));
+  void* ev = nullptr;
+  if (!g_event_pool.empty()) {
+    ev = g_event_pool.back();
+    g_event_pool.pop_back();
+  } else {
+    TVK_MX(mx_event_create(&ev, 0));
+  }
+  TVK_MX(mx_event_record(ev, stream));
+  g_pending.push_back({ev, host});
+  counters().async_copies++;
+}
+
+}  // namespace
+
+size_t pending_host_copies() {
+  std::lock_guard<std::mutex> lock(g_pending_mu);
+  reap_pending_locked();
+  return g_pending.size();
+}
+
+namespace {
+
 at::Tensor& copy_impl(at::Tensor& self, const at::Tensor& src, bool non_blocking) {
   TORCH_CHECK(self.defined() && src.defined(), "copy_: undefined tensor");
   if (self.numel() == 0) return self;
@@ -106,7 +166,10 @@ at::Tensor& copy_impl(at::Tensor& self, const at::Tensor& src, bool non_blocking
     if (host.is_neg()) host = host.resolve_neg();
     if (host.is_conj()) host = host.resolve_conj();
     if (self.is_contiguous()) {
-      TVK_MX(mx_memcpy(self.data_ptr(), host.data_ptr(), host.nbytes(), MX_COPY_H2D, current_stream()));
+      if (non_blocking && host_pinned(host))
+        copy_async(self.data_ptr(), host.data_ptr(), host.nbytes(), MX_COPY_H2D, host.storage());
+      else
+        TVK_MX(mx_memcpy(self.data_ptr(), host.data_ptr(), host.nbytes(), MX_COPY_H2D, current_stream()));
     } else {
       at::Tensor tmp = at::empty(self.sizes(), self.options().memory_format(at::MemoryFormat::Contiguous));
       TVK_MX(mx_memcpy(tmp.data_ptr(), host.data_ptr(), host.nbytes(), MX_COPY_H2D, current_stream()));
@@ -118,6 +181,12 @@ at::Tensor& copy_impl(at::Tensor& self, const at::Tensor& src, bool non_blocking
   TORCH_CHECK(is_vk(s), "copy_: expected a vulkan tensor on one side");
   c10::DeviceGuard guard(s.device());
   at::Tensor dense = s.is_contiguous() ? s : s.contiguous();
+  if (non_blocking && self.is_contiguous() && self.scalar_type() == dense.scalar_type() && !self.is_neg() &&
+      !self.is_conj() && host_pinned(self)) {
+    copy_async(self.data_ptr(), dense.data_ptr(), self.nbytes(), MX_COPY_D2H, self.storage());
+    counters().host_reads++;
+    return self;
+  }
   at::Tensor host = at::empty(dense.sizes(), dense.options().device(at::kCPU));
   TVK_MX(mx_memcpy(host.data_ptr(), dense.data_ptr(), host.nbytes(), MX_COPY_D2H, current_stream()));
   counters().host_reads++;
@@ -378,10 +447,20 @@ void foreach_add_scalar(at::TensorList self, const at::Scalar& scalar) {
   counters().kernel_launches++;
 }
 
+// Tensor.record_stream: the storage's block is not reused until the work
+// queued on `s` at the time the tensor is freed has completed.
+void record_stream_vk(at::Tensor& self, at::Stream s) {
+  TORCH_CHECK(s.device_type() == c10::DeviceType::PrivateUse1, "record_stream: expected a vulkan stream, got ",
+              s.device_type());
+  void* base = self.storage().mutable_data();
+  if (base) TVK_MX(mx_record_stream(base, stream_for_id(s.device_index(), s.id())));
+}
+
 }  // namespace
 }  // namespace tvk
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+  m.impl("record_stream", TORCH_FN(tvk::record_stream_vk));
   m.impl("empty.memory_format", TORCH_FN(tvk::empty_memory_format));
   m.impl("empty_strided", TORCH_FN(tvk::empty_strided));
   m.impl("_copy_from", TORCH_FN(tvk::copy_from));

@@ -32,7 +32,8 @@ EXPORTS = [
     "mx_device_name", "mx_device_synchronize", "mx_default_stream", "mx_stream_create", "mx_stream_destroy",
     "mx_stream_synchronize", "mx_stream_query", "mx_stream_wait_event", "mx_event_create", "mx_event_destroy",
     "mx_event_record", "mx_event_query", "mx_event_synchronize", "mx_event_elapsed_ms", "mx_malloc", "mx_free",
-    "mx_record_stream", "mx_empty_cache", "mx_memory_stats_get", "mx_memcpy", "mx_fill", "mx_copy_strided",
+    "mx_record_stream", "mx_empty_cache", "mx_memory_stats_get", "mx_memcpy", "mx_host_is_pinned",
+    "mx_memcpy_async", "mx_host_malloc", "mx_host_free", "mx_fill", "mx_copy_strided",
     "mx_add_f32", "mx_scale_f32", "mx_mul_f32", "mx_sum_f32", "mx_foreach_add_scalar_f32", "mx_conv2d_check",
     "mx_conv2d_select", "mx_conv2d_forward", "mx_conv2d_backward_input", "mx_conv2d_backward_weight",
     "mx_conv2d_backward_bias", "mx_conv2d_dweight_plan", "mx_conv2d_kernel_name", "mx_gemm_f32", "mx_adamw_step",
@@ -122,6 +123,10 @@ def lib() -> C.CDLL:
             "mx_empty_cache": ([], i32),
             "mx_memory_stats_get": ([C.POINTER(MemoryStats)], i32),
             "mx_memcpy": ([vp, vp, C.c_size_t, i32, vp], i32),
+            "mx_host_is_pinned": ([vp, C.POINTER(i32)], i32),
+            "mx_memcpy_async": ([vp, vp, C.c_size_t, i32, vp], i32),
+            "mx_host_malloc": ([C.POINTER(vp), C.c_size_t], i32),
+            "mx_host_free": ([vp], i32),
             "mx_fill": ([vp, i64, i32, C.c_uint64, vp], i32),
             "mx_copy_strided": ([vp, vp, i32, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64), i64, i64, i32, vp], i32),
             "mx_add_f32": ([vp, vp, vp, C.c_float, i64, vp], i32),
