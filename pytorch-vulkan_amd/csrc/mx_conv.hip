@@ -562,19 +562,19 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
   int chosen = 0;
   MX_TRY(select_algo(d, MX_CONV_FORWARD, algo, &chosen));
   hipStream_t s = resolve_stream(stream);
-  if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_forward(d, x, w, bias, y, s);
-  if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM) {
+  if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM || chosen == MX_CONV_ALGO_WINOGRAD) {
     const int64_t nc = images_per_launch(d);
     MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d forward: one image or the weights exceed the 2 GiB operand bound");
     if (nc < d.n) {
       for (int64_t n0 = 0; n0 < d.n; n0 += nc) {
         const mx_conv2d_desc c = batch_slice(d, std::min(nc, d.n - n0));
-        MX_TRY(mx_conv2d_forward(&c, x + n0 * d.cin * d.h * d.w, w, bias, y + n0 * d.cout * d.oh * d.ow,
-                                 MX_CONV_ALGO_IMPLICIT_GEMM, stream));
+        MX_TRY(mx_conv2d_forward(&c, x + n0 * d.cin * d.h * d.w, w, bias, y + n0 * d.cout * d.oh * d.ow, chosen,
+                                 stream));
       }
       return MX_OK;
     }
   }
+  if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_forward(d, x, w, bias, y, s);
   ConvArgs p = make_args(d);
   p.x = x;
   p.w = w;

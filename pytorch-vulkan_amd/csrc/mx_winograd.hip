@@ -6,14 +6,29 @@
 //   U = G g G^T,  G = [[1,0,0],[1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]]
 //   V = B^T d B,  B^T = [[1,0,-1,0],[0,1,1,0],[0,-1,1,0],[0,1,0,-1]]
 //   Y = A^T M A + bias,  A^T = [[1,1,1,0],[0,1,-1,-1]]
-// on 4x4 input tiles at stride 2.  The 16 products M_t = U_t V_t (one per
-// transform coordinate t, every group) run as a single batched FP32 MFMA GEMM
-// of batch 16*groups.  Layouts: U [16*G][Cout_g][Cin_g], V [16*G][Cin_g][T],
+// on 4x4 input tiles at stride 2, M_t = U_t V_t for each of the 16 transform
+// coordinates t.
+//
+// Fused kernel (the default): one workgroup computes 64 output channels x 32
+// tiles for all 16 coordinates.  Per slab of 8 input channels it stages the
+// transformed filter U (precomputed once per call, [G][16][Cpad][Opad], output
+// channels contiguous, zero padded) and transforms the 4x4 input patches it
+// loads straight into LDS, so V never goes to HBM; the 16 products run as
+// v_mfma_f32_16x16x4f32 with each wave holding all 16 coordinates of a 32
+// channel x 16 tile block, so the output transform A^T M A and the bias are
+// applied in registers and M never goes to HBM either.
+//
+// Unfused kernels (launches with few tiles, or MX_WINOGRAD_FUSED=0): the
+// filter, input and output
+// transforms run as separate passes around one batched MFMA GEMM of batch
+// 16*groups over U [16*G][Cout_g][Cin_g], V [16*G][Cin_g][T],
 // M [16*G][Cout_g][T] with T = N * ceil(OH/2) * ceil(OW/2).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 
+#include "mfma_core.hpp"
 #include "mx_internal.hpp"
 
 namespace mx {
@@ -120,9 +135,256 @@ __global__ void wino_output_kernel(WinoArgs p) {
 
 int blocks_for(int64_t total) { return int(std::min<int64_t>((total + 255) / 256, 1 << 20)); }
 
+// ------------------------------------------------------------ fused kernel
+namespace fused {
+using mfma::f32x4;
+using mfma::i32x4;
+using mfma::kOffNone;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int BO = 64;  // output channels per workgroup
+constexpr int BT = 32;  // tiles per workgroup
+constexpr int BK = 8;   // input channels per slab
+// A 16x16x4 MFMA step takes k index kq = lane / 16 of its four; a lane runs
+// two steps per slab, so it needs slab channels 2 kq and 2 kq + 1.  Both
+// stages keep those two adjacent: A [coord][kq][o][2], B [coord][kq][t][2],
+// and a lane's fragments for one coordinate are one 8-byte read each at a
+// constant offset from its base.
+constexpr int ROW_A = 2 * BO;  // floats per (coord, kq) row
+constexpr int ROW_B = 2 * BT;
+constexpr int A_FLOATS = 16 * 4 * ROW_A;
+constexpr int B_FLOATS = 16 * 4 * ROW_B;
+constexpr int A_PASSES = A_FLOATS / 4 / mfma::kThreads;  // float4 loads per thread per slab
+static_assert(A_PASSES == 8, "filter slab tiling");
+static_assert(BK * BT == mfma::kThreads, "one input patch per thread per slab");
+
+struct Args {
+  const float* x;    // [N][Cin][H][W]
+  const float* U;    // [G][16][nslab][4][Opad][2]
+  const float* bias;
+  float* y;          // [N][Cout][OH][OW]
+  int64_t x_bytes, u_bytes;
+  int Cin, H, W, Cout, OH, OW, ph, pw, C, O, Cpad, Opad, TH, TW, T, n_ob, nslab;
+  mfma::FastDiv f_thw, f_tw;
+};
+
+// U' for the padded (c, o) range, zero outside the real one: channel c of
+// coordinate t at [g][t][c / 8][(c % 8) / 2][o][c % 2].
+__global__ void filter_kernel(const float* __restrict__ w, float* __restrict__ U, int C, int O, int Cpad, int Opad,
+                              int G) {
+  const int64_t total = int64_t(G) * Cpad * Opad;
+  const int nslab = Cpad / BK;
+  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += int64_t(gridDim.x) * blockDim.x) {
+    const int c = int(idx % Cpad);
+    const int64_t go = idx / Cpad;
+    const int o = int(go % Opad), g = int(go / Opad);
+    float u[16];
+    if (o < O && c < C) {
+      const float* k = w + ((int64_t(g) * O + o) * C + c) * 9;
+      float z[4][3];
+      for (int j = 0; j < 3; ++j) {
+        z[0][j] = k[j];
+        z[1][j] = 0.5f * (k[j] + k[3 + j] + k[6 + j]);
+        z[2][j] = 0.5f * (k[j] - k[3 + j] + k[6 + j]);
+        z[3][j] = k[6 + j];
+      }
+      for (int r = 0; r < 4; ++r) {
+        u[r * 4 + 0] = z[r][0];
+        u[r * 4 + 1] = 0.5f * (z[r][0] + z[r][1] + z[r][2]);
+        u[r * 4 + 2] = 0.5f * (z[r][0] - z[r][1] + z[r][2]);
+        u[r * 4 + 3] = z[r][2];
+      }
+    } else {
+      for (int t = 0; t < 16; ++t) u[t] = 0.f;
+    }
+    const int slab = c / BK, kq = (c % BK) >> 1, j = c & 1;
+    for (int t = 0; t < 16; ++t)
+      U[(((int64_t(g) * 16 + t) * nslab + slab) * 4 + kq) * int64_t(Opad) * 2 + 2 * o + j] = u[t];
+  }
+}
+
+template <bool RAGGED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void wino_fused_kernel(Args p) {
+  __shared__ __attribute__((aligned(16))) float smem[A_FLOATS + B_FLOATS];
+  float* As = smem;
+  float* Bs = smem + A_FLOATS;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y;
+  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
+  const int ob = b % p.n_ob, tb = b / p.n_ob;
+  const int o0 = ob * BO, t0 = tb * BT;
+
+  // Filter loads: pass q copies row r = tid / 32 + 8 q (coordinate r / 4,
+  // k pair r % 4) of the slab, floats 4 * (tid % 32) .. + 3 of its 128.
+  const i32x4 ru = mfma::buffer_rsrc(p.U, p.u_bytes);
+  const int a_row = tid >> 5, a_f4 = tid & 31;
+  const uint32_t a_off = uint32_t(
+      ((((int64_t(g) * 16 + (a_row >> 2)) * p.nslab) * 4 + (a_row & 3)) * int64_t(p.Opad) * 2 + 2 * o0 + 4 * a_f4) *
+      4);
+  const uint32_t a_sstep = uint32_t(4) * p.Opad * 2 * 4;           // one slab
+  const uint32_t a_qstep = uint32_t(2) * p.nslab * a_sstep;        // two coordinates
+
+  // Input patch: channel b_c of the slab, tile t0 + b_t; four row offsets (or
+  // kOffNone off the image) and a column mask, the slab's channel offset in
+  // the scalar offset.
+  const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
+  const int b_c = tid >> 5, b_t = tid & 31;
+  uint32_t row_off[4];
+  uint32_t col_ok = 0;
+  {
+    const int t = t0 + b_t;
+    const bool tok = t < p.T;
+    const uint32_t tt = tok ? uint32_t(t) : 0u;
+    const uint32_t img = mfma::fdiv(tt, p.f_thw);
+    const uint32_t pos = tt - img * uint32_t(p.TH * p.TW);
+    const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
+    const int y0 = int(2 * ty) - p.ph, x0 = int(2 * tx) - p.pw;
+    const int64_t plane = (int64_t(img) * p.Cin + int64_t(g) * p.C + b_c) * p.H;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int iy = y0 + r;
+      row_off[r] = (tok && unsigned(iy) < unsigned(p.H)) ? uint32_t(((plane + iy) * p.W + x0) * 4) : kOffNone;
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) col_ok |= (unsigned(x0 + cc) < unsigned(p.W) ? 1u : 0u) << cc;
+  }
+  const uint32_t x_sstep = uint32_t(BK) * p.H * p.W * 4;
+
+  // Register staging of the next slab: filter (from L2) and input patches.
+  f32x4 av[A_PASSES];
+  float d[16];
+  auto load = [&](int slab) {
+    const uint32_t sa = uint32_t(slab) * a_sstep, sx = uint32_t(slab) * x_sstep;
+#pragma unroll
+    for (int q = 0; q < A_PASSES; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
+    // x0 may be -1 (left padding): row_off + 4 * cc is then computed modulo
+    // 2^32 and only used when column cc is inside the image.
+    const uint32_t cmask = (!RAGGED || slab * BK + b_c < p.C) ? col_ok : 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        d[r * 4 + cc] = mfma::bload(rx, ((cmask >> cc) & 1u) ? row_off[r] + 4u * cc : kOffNone, sx);
+  };
+  float* const a_st = As + a_row * ROW_A + 4 * a_f4;
+  float* const b_st = Bs + (b_c >> 1) * ROW_B + 2 * b_t + (b_c & 1);
+  auto store = [&]() {
+#pragma unroll
+    for (int q = 0; q < A_PASSES; ++q) *reinterpret_cast<f32x4*>(a_st + q * 8 * ROW_A) = av[q];
+    // V = B^T d B
+    float z[16];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      z[0 * 4 + cc] = d[0 * 4 + cc] - d[2 * 4 + cc];
+      z[1 * 4 + cc] = d[1 * 4 + cc] + d[2 * 4 + cc];
+      z[2 * 4 + cc] = d[2 * 4 + cc] - d[1 * 4 + cc];
+      z[3 * 4 + cc] = d[1 * 4 + cc] - d[3 * 4 + cc];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      b_st[(r * 4 + 0) * 4 * ROW_B] = z[r * 4 + 0] - z[r * 4 + 2];
+      b_st[(r * 4 + 1) * 4 * ROW_B] = z[r * 4 + 1] + z[r * 4 + 2];
+      b_st[(r * 4 + 2) * 4 * ROW_B] = z[r * 4 + 2] - z[r * 4 + 1];
+      b_st[(r * 4 + 3) * 4 * ROW_B] = z[r * 4 + 1] - z[r * 4 + 3];
+    }
+  };
+
+  // Wave (wo, wt) owns output channels wo*32 .. +31 (two 16-row blocks) and
+  // tiles wt*16 .. +15 of the workgroup tile, for all 16 coordinates.
+  const int wo = wave >> 1, wt = wave & 1;
+  const int kq = lane >> 4, li = lane & 15;
+  f32x4 acc[16][2];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f32x2* const a_frag = reinterpret_cast<const f32x2*>(As + kq * ROW_A + 2 * (wo * 32 + li));
+  const f32x2* const b_frag = reinterpret_cast<const f32x2*>(Bs + kq * ROW_B + 2 * (wt * 16 + li));
+
+  auto mma = [&]() {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const f32x2 fb = b_frag[t * 2 * ROW_B];        // 4 rows of ROW_B floats per coordinate
+      const f32x2 fa0 = a_frag[t * 2 * ROW_A];
+      const f32x2 fa1 = a_frag[t * 2 * ROW_A + 16];  // channels + 16
+      acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0[0], fb[0], acc[t][0], 0, 0, 0);
+      acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1[0], fb[0], acc[t][1], 0, 0, 0);
+      acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0[1], fb[1], acc[t][0], 0, 0, 0);
+      acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1[1], fb[1], acc[t][1], 0, 0, 0);
+    }
+    // The fragment reads (merged in pairs: three per two coordinates) run two
+    // coordinate pairs ahead of the products that use them.
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int t = 0; t < 6; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+  };
+
+  const int nslab = p.nslab;
+  load(0);
+  for (int s = 0; s < nslab; ++s) {
+    store();
+    __syncthreads();
+    load(min(s + 1, nslab - 1));  // the last slab re-reads itself: no branch around the loads
+    // The next slab's global loads are issued before any product.
+    __builtin_amdgcn_sched_barrier(0);
+    mma();
+    __syncthreads();
+  }
+
+  // Output transform.  16x16x4 layout: lane l, register v holds row
+  // 4 * (l / 16) + v (output channel) and column l % 16 (tile).
+  const int t = t0 + wt * 16 + li;
+  if (t >= p.T) return;
+  const uint32_t img = mfma::fdiv(uint32_t(t), p.f_thw);
+  const uint32_t pos = uint32_t(t) - img * uint32_t(p.TH * p.TW);
+  const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
+  const int oy = int(2 * ty), ox = int(2 * tx);
+  const bool right = ox + 1 < p.OW, below = oy + 1 < p.OH;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
+    if (o >= p.O) continue;
+    float m[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) m[q] = acc[q][i][v];
+    float r0[4], r1[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      r0[c] = m[c] + m[4 + c] + m[8 + c];
+      r1[c] = m[4 + c] - m[8 + c] - m[12 + c];
+    }
+    const int oc = g * p.O + o;
+    const float bb = p.bias ? p.bias[oc] : 0.f;
+    float* yo = p.y + ((int64_t(img) * p.Cout + oc) * p.OH + oy) * p.OW + ox;
+    yo[0] = r0[0] + r0[1] + r0[2] + bb;
+    if (right) yo[1] = r0[1] - r0[2] - r0[3] + bb;
+    if (below) {
+      yo[p.OW] = r1[0] + r1[1] + r1[2] + bb;
+      if (right) yo[p.OW + 1] = r1[1] - r1[2] - r1[3] + bb;
+    }
+  }
+}
+
+// The fused kernel keeps one slab of loads in flight per workgroup and two
+// workgroups fit on a CU, so it needs most CUs doubly occupied to hide HBM
+// latency: measured on MI355X it wins from 1.5 workgroups per CU up (392 and
+// more at 256 CUs) and loses below (256: 155 vs 111 us, 128: 79 vs 48 us).
+bool prefer_fused(int64_t workgroups) { return 2 * workgroups >= 3 * int64_t(cu_count()); }
+
+}  // namespace fused
+
+int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+                     hipStream_t s);
+
 }  // namespace
 
-int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+namespace {
+int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
                      hipStream_t s) {
   WinoArgs p{};
   p.x = x;
@@ -176,6 +438,66 @@ int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, co
   gd.bias_kind = MX_BIAS_NONE;
   MX_TRY(mx_gemm_f32(&gd, p.U, p.V, nullptr, p.M, s));
   hipLaunchKernelGGL(wino_output_kernel, dim3(blocks_for(int64_t(p.Cout) * T)), dim3(256), 0, s, p);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+}  // namespace
+
+int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+                     hipStream_t s) {
+  fused::Args p{};
+  p.bias = bias;
+  p.Cin = int(d.cin);
+  p.H = int(d.h);
+  p.W = int(d.w);
+  p.Cout = int(d.cout);
+  p.OH = int(d.oh);
+  p.OW = int(d.ow);
+  p.ph = int(d.ph);
+  p.pw = int(d.pw);
+  const int G = int(d.groups);
+  p.C = p.Cin / G;
+  p.O = p.Cout / G;
+  p.Cpad = (p.C + fused::BK - 1) / fused::BK * fused::BK;
+  p.Opad = (p.O + fused::BO - 1) / fused::BO * fused::BO;
+  p.TH = (p.OH + 1) / 2;
+  p.TW = (p.OW + 1) / 2;
+  p.n_ob = p.Opad / fused::BO;
+  p.nslab = p.Cpad / fused::BK;
+  p.f_tw = mfma::fast_div(uint32_t(p.TW));
+  p.f_thw = mfma::fast_div(uint32_t(p.TH * p.TW));
+  const int64_t u_bytes = int64_t(G) * 16 * p.Cpad * p.Opad * 4;
+  MX_REQUIRE(u_bytes < mfma::kBufMaxBytes, MX_ERR_UNSUPPORTED, "winograd: the transformed filter exceeds 2 GiB");
+  p.u_bytes = u_bytes;
+  // The caller splits batches so the input stays one buffer resource with
+  // 32-bit offsets (images_per_launch).
+  const int64_t x_bytes = d.n * int64_t(p.Cin) * p.H * p.W * 4;
+  const int64_t T = d.n * int64_t(p.TH) * p.TW;
+  MX_REQUIRE(x_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
+             "winograd: the input exceeds the 2 GiB operand bound");
+  if (T == 0) return MX_OK;
+  const int64_t blocks = (T + fused::BT - 1) / fused::BT * p.n_ob;
+  MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "winograd: grid too large");
+  // MX_WINOGRAD_FUSED=1 / 0 forces the fused / unfused kernels (tests, tuning).
+  bool fused_path = fused::prefer_fused(blocks * G);
+  if (const char* e = std::getenv("MX_WINOGRAD_FUSED"))
+    if (e[0] == '0' || e[0] == '1') fused_path = e[0] == '1';
+  if (!fused_path) return winograd_unfused(d, x, w, bias, y, s);
+  Scratch U;
+  MX_TRY(U.alloc(size_t(u_bytes), s));
+  p.U = U.as<float>();
+  hipLaunchKernelGGL(fused::filter_kernel, dim3(blocks_for(int64_t(G) * p.Cpad * p.Opad)), dim3(256), 0, s, w,
+                     U.as<float>(), p.C, p.O, p.Cpad, p.Opad, G);
+  MX_HIP(hipGetLastError());
+  p.x = x;
+  p.y = y;
+  p.x_bytes = x_bytes;
+  p.T = int(T);
+  const dim3 grid{unsigned(blocks), unsigned(G), 1u};
+  if (p.C % fused::BK)
+    hipLaunchKernelGGL(fused::wino_fused_kernel<true>, grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(fused::wino_fused_kernel<false>, grid, dim3(256), 0, s, p);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }

@@ -253,9 +253,26 @@ def test_conv_batch_chunks(mx, case, monkeypatch):
         close(got, ref, mag=mag, what=name)
 
 
-@pytest.mark.parametrize("case", [CONV_CASES[0], ((2, 16, 9, 11), 24, (3, 3), (1, 1), (1, 1), (1, 1), 1),
-                                  ((1, 32, 8, 8), 32, (3, 3), (1, 1), (0, 0), (1, 1), 4)])
-def test_conv_winograd_forward(mx, case):
+# Winograd geometries: input channels that are not a multiple of the 8-channel
+# slab (3, 12), output channels that are not a multiple of the 64-channel
+# block (24, 70) or span several (130), odd output sizes (half tiles), tile
+# counts off the 32-tile block, padding 0 and 2, groups.
+WINO_CASES = [
+    CONV_CASES[0],
+    ((2, 16, 9, 11), 24, (3, 3), (1, 1), (1, 1), (1, 1), 1),
+    ((1, 32, 8, 8), 32, (3, 3), (1, 1), (0, 0), (1, 1), 4),
+    ((2, 3, 10, 10), 130, (3, 3), (1, 1), (1, 1), (1, 1), 1),
+    ((3, 12, 7, 9), 70, (3, 3), (1, 1), (1, 1), (1, 1), 1),
+    ((2, 64, 14, 14), 64, (3, 3), (1, 1), (1, 1), (1, 1), 1),
+    ((1, 16, 6, 6), 8, (3, 3), (1, 1), (2, 2), (1, 1), 1),
+    ((2, 24, 5, 4), 48, (3, 3), (1, 1), (1, 1), (1, 1), 3),
+]
+
+
+@pytest.mark.parametrize("fused", ["1", "0"], ids=["fused", "unfused"])
+@pytest.mark.parametrize("case", WINO_CASES, ids=[f"w{i}" for i in range(len(WINO_CASES))])
+def test_conv_winograd_forward(mx, monkeypatch, case, fused):
+    monkeypatch.setenv("MX_WINOGRAD_FUSED", fused)
     xs, cout, kernel, stride, padding, dilation, groups = case
     x, w, b = conv_inputs(xs, cout, kernel, groups, seed=3)
     d = mx.conv_desc(xs, w.shape, stride, padding, dilation, groups)
@@ -264,6 +281,21 @@ def test_conv_winograd_forward(mx, case):
     y = torch.empty(yref.shape, device="cuda")
     mx.conv2d_forward(d, dev(x), dev(w), dev(b), y, mx.ALGO_WINOGRAD, stream())
     close(y, yref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd y")
+
+
+def test_conv_winograd_batch_chunks(mx, monkeypatch):
+    """A batch past the operand bound runs as several launches (bound lowered
+    so three images need three launches)."""
+    xs, cout = (3, 16, 12, 10), 40
+    x, w, b = conv_inputs(xs, cout, (3, 3), 1, seed=8)
+    d = mx.conv_desc(xs, w.shape, (1, 1), (1, 1), (1, 1), 1)
+    monkeypatch.setenv("MX_CONV_BUFFER_LIMIT", str(4 * max(16 * 12 * 10, cout * d.oh * d.ow) + 5))
+    monkeypatch.setenv("MX_WINOGRAD_FUSED", "1")
+    dy = torch.zeros((xs[0], cout, d.oh, d.ow))
+    yref, mag = conv_refs(x, w, b, dy, (1, 1), (1, 1), (1, 1), 1)["y"]
+    y = torch.empty(yref.shape, device="cuda")
+    mx.conv2d_forward(d, dev(x), dev(w), dev(b), y, mx.ALGO_WINOGRAD, stream())
+    close(y, yref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd chunked y")
 
 
 def test_conv_closed_form_1x1(mx):
