@@ -650,11 +650,14 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
   Scratch wt, ws;
   if (packed) MX_TRY(wt.alloc(size_t(p.Cout) * p.Cin_g * p.KK * 4, s));
   if (gp.splits > 1) MX_TRY(ws.alloc(size_t(gp.splits) * size_t(out_elems) * 4, s));
+  // Positions no tap reaches (a phase with K = 0) are zero: one contiguous
+  // fill of dx, then the phase GEMMs overwrite the reached positions (such
+  // plans never split K, so the GEMMs write dx directly).
+  bool any_zero = false;
+  for (const ConvArgs& q : phases) any_zero |= q.K == 0;
+  if (any_zero) MX_TRY(conv::conv_dx_zero(dx, out_elems, s));
   for (ConvArgs& q : phases) {
-    if (q.K == 0) {
-      MX_TRY(conv::conv_dx_zero_phase(q, s));
-      continue;
-    }
+    if (q.K == 0) continue;
     q.wt = packed ? wt.as<float>() : w;
     q.f_kblk = conv::fast_div(uint32_t(q.nth * q.ntw * conv::kChanBlock));
     q.f_tapw = conv::fast_div(uint32_t(q.ntw));

@@ -575,7 +575,7 @@ int conv_dx_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t 
 int conv_dw_launch(const ConvArgs& p, int tile, int amode, int bmode, hipStream_t s);
 int conv_dx_pack_weights(const ConvArgs& p, float* wt, hipStream_t s);
 int conv_fwd_pack_weights(const ConvArgs& p, float* wt, hipStream_t s);
-int conv_dx_zero_phase(const ConvArgs& p, hipStream_t s);
+int conv_dx_zero(float* dx, int64_t n, hipStream_t s);
 int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s);
 // out[i] = sum over splits of ws[split][i] (+ bias[(i / hw) % cout] when bias).
 int conv_sum_splits(const float* ws, int splits, int64_t n, float* out, const float* bias, int hw, int cout,

@@ -81,36 +81,74 @@ MX_TILE_KERNEL(C) void conv_dw_kernel(ConvArgs p) {
   }
 }
 
-// dw[i] = sum over splits (in order) of ws[split][i]; same for db.
-__global__ void conv_dw_finalize_kernel(const float* __restrict__ ws, const float* __restrict__ ws_db,
-                                        float* __restrict__ dw, float* __restrict__ db, int64_t n_dw, int n_db,
-                                        int splits) {
-  const int64_t total = n_dw + n_db;
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    float s = 0.f;
-    if (idx < n_dw) {
-#pragma unroll 8
-      for (int sp = 0; sp < splits; ++sp) s += ws[sp * n_dw + idx];
-      dw[idx] = s;
-    } else {
-      const int64_t j = idx - n_dw;
-#pragma unroll 8
-      for (int sp = 0; sp < splits; ++sp) s += ws_db[sp * int64_t(n_db) + j];
-      db[j] = s;
-    }
+// dw[i] = sum over the K splits of ws[split][i]; same for db (elements past
+// n_dw).  A workgroup takes 64 elements; wave q sums splits q, q + 4, q + 8,
+// ... in order (64 consecutive floats per load), and the four partials are
+// added in wave order, so the result is the same on every run and many
+// splits of a small dW keep four times more loads in flight than one
+// thread per element would.
+__global__ __launch_bounds__(256) void conv_dw_finalize_kernel(const float* __restrict__ ws,
+                                                               const float* __restrict__ ws_db, float* __restrict__ dw,
+                                                               float* __restrict__ db, int64_t n_dw, int n_db,
+                                                               int splits) {
+  __shared__ float part[4][64];
+  const int e = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int64_t idx = int64_t(blockIdx.x) * 64 + e;
+  float s = 0.f;
+  if (idx < n_dw) {
+    const float* src = ws + idx;
+#pragma unroll 4
+    for (int sp = q; sp < splits; sp += 4) s += src[sp * n_dw];
+  } else if (idx < n_dw + n_db) {
+    const float* src = ws_db + (idx - n_dw);
+#pragma unroll 4
+    for (int sp = q; sp < splits; sp += 4) s += src[sp * int64_t(n_db)];
+  }
+  part[q][e] = s;
+  __syncthreads();
+  if (q == 0) {
+    const float v = ((part[0][e] + part[1][e]) + part[2][e]) + part[3][e];
+    if (idx < n_dw) dw[idx] = v;
+    else if (idx < n_dw + n_db) db[idx - n_dw] = v;
   }
 }
 
+// out[i] = sum over splits (in order) of ws[split][i] (+ bias of i's channel).
+// VEC: 16-byte vectors; the host guarantees n % 4 == 0, hw % 4 == 0 (one
+// channel per vector) and aligned buffers.  Indices are 32-bit: a launch's
+// output is one buffer-addressable tensor (< 2^31 bytes).
+template <bool VEC>
 __global__ void conv_sum_splits_kernel(const float* __restrict__ ws, int splits, int64_t n, float* __restrict__ out,
                                        const float* __restrict__ bias, int hw, int cout) {
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < n;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    float s = 0.f;
+  const uint32_t n_vec = uint32_t(VEC ? n / 4 : n);
+  for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < n_vec; idx += gridDim.x * blockDim.x) {
+    if constexpr (VEC) {
+      const float4* src = reinterpret_cast<const float4*>(ws) + idx;
+      float4 s = *src;
+#pragma unroll 4
+      for (int sp = 1; sp < splits; ++sp) {
+        src += n_vec;
+        const float4 v = *src;
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+      }
+      if (bias) {
+        const float b = bias[(4 * idx / uint32_t(hw)) % uint32_t(cout)];
+        s.x += b;
+        s.y += b;
+        s.z += b;
+        s.w += b;
+      }
+      reinterpret_cast<float4*>(out)[idx] = s;
+    } else {
+      float s = 0.f;
 #pragma unroll 8
-    for (int sp = 0; sp < splits; ++sp) s += ws[sp * n + idx];
-    if (bias) s += bias[(idx / hw) % cout];
-    out[idx] = s;
+      for (int sp = 0; sp < splits; ++sp) s += ws[sp * n + idx];
+      if (bias) s += bias[(idx / uint32_t(hw)) % uint32_t(cout)];
+      out[idx] = s;
+    }
   }
 }
 
@@ -159,10 +197,19 @@ int conv_dw_launch(const ConvArgs& p, int tile, int amode, int bmode, hipStream_
   }
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 int conv_sum_splits(const float* ws, int splits, int64_t n, float* out, const float* bias, int hw, int cout,
                     hipStream_t s) {
-  const int blocks = int(std::min<int64_t>((n + 255) / 256, 1 << 20));
-  hipLaunchKernelGGL(conv_sum_splits_kernel, dim3(blocks), dim3(256), 0, s, ws, splits, n, out, bias, hw, cout);
+  const bool vec = n % 4 == 0 && (!bias || hw % 4 == 0) && aligned16(ws) && aligned16(out);
+  const int64_t items = vec ? n / 4 : n;
+  const int blocks = int(std::min<int64_t>((items + 255) / 256, 1 << 20));
+  if (vec)
+    hipLaunchKernelGGL(conv_sum_splits_kernel<true>, dim3(blocks), dim3(256), 0, s, ws, splits, n, out, bias, hw,
+                       cout);
+  else
+    hipLaunchKernelGGL(conv_sum_splits_kernel<false>, dim3(blocks), dim3(256), 0, s, ws, splits, n, out, bias, hw,
+                       cout);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }
@@ -170,10 +217,10 @@ int conv_sum_splits(const float* ws, int splits, int64_t n, float* out, const fl
 int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s) {
   const int64_t n_dw = int64_t(p.G) * p.Cout_g * p.Ncols;
   const int n_db = db ? p.Cout : 0;
-  const int64_t total = n_dw + n_db;
-  const int blocks = int(std::min<int64_t>((total + 255) / 256, 1 << 20));
-  hipLaunchKernelGGL(conv_dw_finalize_kernel, dim3(blocks), dim3(256), 0, s, p.ws, p.ws_db, dw, db, n_dw, n_db,
-                     p.splits);
+  const int64_t blocks = (n_dw + n_db + 63) / 64;
+  MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "conv2d dweight: finalize grid too large");
+  hipLaunchKernelGGL(conv_dw_finalize_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, p.ws, p.ws_db, dw, db, n_dw,
+                     n_db, p.splits);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }

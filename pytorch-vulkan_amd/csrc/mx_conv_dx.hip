@@ -21,43 +21,45 @@ namespace {
 
 // Wt_p[g][k][ci] = w[g*Cout_g + co][ci][kh0 + th*stph][kw0 + tw*stpw] with k
 // the gathered K order over (co, th, tw): the A operand of the phase GEMM,
-// ci contiguous.
+// ci contiguous.  32-bit indices: the packed weights are below 2^31 bytes.
 __global__ void conv_dx_pack_kernel(ConvArgs p, float* wt) {
-  const int nt = p.nth * p.ntw;
-  const int64_t total = int64_t(p.G) * p.K * p.Cin_g;
+  const uint32_t nt = p.nth * p.ntw;
+  const uint32_t total = uint32_t(p.G) * p.K * p.Cin_g;
   const bool blocked = blocked_channels(p.Cout_g);
-  const int kblk = nt * kChanBlock;
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    const int ci = int(idx % p.Cin_g);
-    const int64_t rest = idx / p.Cin_g;
-    const int k = int(rest % p.K);
-    const int g = int(rest / p.K);
-    int co, t;
+  const uint32_t kblk = nt * kChanBlock;
+  for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+    const uint32_t rest = idx / uint32_t(p.Cin_g);
+    const uint32_t ci = idx - rest * uint32_t(p.Cin_g);
+    const uint32_t g = rest / uint32_t(p.K);
+    const uint32_t k = rest - g * uint32_t(p.K);
+    uint32_t co, t;
     if (blocked) {
-      const int cb = k / kblk, rem = k - (k / kblk) * kblk;
+      const uint32_t cb = k / kblk, rem = k - cb * kblk;
       t = rem / kChanBlock;
       co = cb * kChanBlock + rem - t * kChanBlock;
     } else {
       co = k / nt;
       t = k - co * nt;
     }
-    const int th = t / p.ntw, tw = t - (t / p.ntw) * p.ntw;
-    const int kh = p.kh0 + th * p.stph, kw = p.kw0 + tw * p.stpw;
+    const uint32_t th = t / uint32_t(p.ntw), tw = t - th * uint32_t(p.ntw);
+    const int kh = p.kh0 + int(th) * p.stph, kw = p.kw0 + int(tw) * p.stpw;
     wt[idx] = p.w[((int64_t(g * p.Cout_g + co) * p.Cin_g + ci) * p.KH + kh) * p.KW + kw];
   }
 }
 
-// dx = 0 at the input positions of a phase that no tap reaches.
-__global__ void conv_dx_zero_kernel(ConvArgs p) {
-  const int64_t total = int64_t(p.N) * p.Cin * p.HpWp;
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    const int q = int(idx % p.HpWp);
-    const int64_t plane = idx / p.HpWp;  // img * Cin + c
-    const int i = q / p.Wp, j = q - (q / p.Wp) * p.Wp;
-    p.out[plane * p.HW + int64_t(p.pa + p.sh * i) * p.W + p.pb + p.sw * j] = 0.f;
+// dx = 0 everywhere (16-byte stores where the tensor allows): run before the
+// phase GEMMs of a convolution whose stride leaves some input positions
+// untouched by every tap; the GEMMs then overwrite the reached positions.
+__global__ void conv_dx_zero_kernel(float* __restrict__ dx, int64_t n) {
+  const int64_t n4 = n / 4;
+  const bool vec = (reinterpret_cast<uintptr_t>(dx) & 15) == 0;
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (vec) {
+    for (; i < n4; i += stride) reinterpret_cast<float4*>(dx)[i] = float4{0.f, 0.f, 0.f, 0.f};
+    i = 4 * n4 + (int64_t(blockIdx.x) * blockDim.x + threadIdx.x);
   }
+  for (; i < n; i += stride) dx[i] = 0.f;
 }
 
 template <class C, Mode MA, class LB>
@@ -131,8 +133,8 @@ int conv_dx_pack_weights(const ConvArgs& p, float* wt, hipStream_t s) {
   return MX_OK;
 }
 
-int conv_dx_zero_phase(const ConvArgs& p, hipStream_t s) {
-  hipLaunchKernelGGL(conv_dx_zero_kernel, dim3(grid_for(int64_t(p.N) * p.Cin * p.HpWp)), dim3(256), 0, s, p);
+int conv_dx_zero(float* dx, int64_t n, hipStream_t s) {
+  hipLaunchKernelGGL(conv_dx_zero_kernel, dim3(grid_for((n + 3) / 4)), dim3(256), 0, s, dx, n);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }

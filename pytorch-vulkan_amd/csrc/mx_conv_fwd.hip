@@ -57,18 +57,18 @@ MX_TILE_KERNEL(C) void conv_fwd_kernel(ConvArgs p) {
 }
 
 // Wp[g][co][k] = w[g*Cout_g + co][ci][kh][kw] with k the blocked gathered
-// order (channel block, kh, kw, channel in block).
+// order (channel block, kh, kw, channel in block).  32-bit indices: the
+// weights are below 2^31 bytes.
 __global__ void conv_fwd_pack_kernel(ConvArgs p, float* wp) {
-  const int64_t total = int64_t(p.Cout) * p.Cin_g * p.KK;
-  const int kblk = p.KK * kChanBlock;
-  for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-       idx += int64_t(gridDim.x) * blockDim.x) {
-    const int k = int(idx % p.K);
-    const int64_t oc = idx / p.K;
-    const int cb = k / kblk, rem = k - (k / kblk) * kblk;
-    const int t = rem / kChanBlock;  // kh * KW + kw
-    const int ci = cb * kChanBlock + rem - t * kChanBlock;
-    wp[idx] = p.w[(oc * p.Cin_g + ci) * p.KK + t];
+  const uint32_t total = uint32_t(p.Cout) * p.Cin_g * p.KK;
+  const uint32_t kblk = p.KK * kChanBlock;
+  for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+    const uint32_t oc = idx / uint32_t(p.K);
+    const uint32_t k = idx - oc * uint32_t(p.K);
+    const uint32_t cb = k / kblk, rem = k - cb * kblk;
+    const uint32_t t = rem / kChanBlock;  // kh * KW + kw
+    const uint32_t ci = cb * kChanBlock + rem - t * kChanBlock;
+    wp[idx] = p.w[(uint32_t(oc) * p.Cin_g + ci) * p.KK + t];
   }
 }
 

@@ -25,6 +25,13 @@ __global__ void fill_kernel(T* dst, int64_t n, T value) {
     dst[i] = value;
 }
 
+// 16-byte stores of a repeated 16-byte pattern (the host checks alignment
+// and that the byte count is a multiple of 16).
+__global__ void fill16_kernel(uint4* dst, int64_t n16, uint4 value) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += int64_t(gridDim.x) * blockDim.x)
+    dst[i] = value;
+}
+
 struct StridedDesc {
   int ndim;
   int64_t sizes[8];
@@ -131,6 +138,19 @@ int mx_fill(void* dst, int64_t count, int elem_size, uint64_t pattern, void* str
   if (count == 0) return MX_OK;
   MX_REQUIRE(dst, MX_ERR_INVALID, "mx_fill: null destination");
   hipStream_t s = resolve_stream(stream);
+  const int64_t bytes = count * elem_size;
+  if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0 && bytes % 16 == 0 &&
+      (elem_size == 1 || elem_size == 2 || elem_size == 4 || elem_size == 8)) {
+    uint64_t rep = pattern;  // the element pattern repeated over 8 bytes
+    if (elem_size == 1) rep = (pattern & 0xFF) * 0x0101010101010101ull;
+    if (elem_size == 2) rep = (pattern & 0xFFFF) * 0x0001000100010001ull;
+    if (elem_size == 4) rep = (pattern & 0xFFFFFFFFull) * 0x0000000100000001ull;
+    const uint4 v{uint32_t(rep), uint32_t(rep >> 32), uint32_t(rep), uint32_t(rep >> 32)};
+    hipLaunchKernelGGL(fill16_kernel, dim3(grid_for(bytes / 16)), dim3(256), 0, s, static_cast<uint4*>(dst),
+                       bytes / 16, v);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
   const dim3 grid(grid_for(count)), block(256);
   switch (elem_size) {
     case 1: hipLaunchKernelGGL(fill_kernel<uint8_t>, grid, block, 0, s, static_cast<uint8_t*>(dst), count, uint8_t(pattern)); break;
