@@ -9,8 +9,10 @@
 Prints ONE JSON line.  The headline (`value`) is BASELINE.json's Conv2D
 fwd+bwd FP32 TFLOP/s on its largest single-GPU Conv2D configuration, C3: the
 53 convolutions of ResNet-50 v1.5 at batch 64, 224x224, each run forward +
-dInput + dWeight (the stem needs no dInput), 3x3 stride-1 forwards routed to
-Winograd F(2x2,3x3) as the configuration states.  A "step" is one pass of
+dInput + dWeight (the stem needs no dInput), 3x3 stride-1 layers routed to
+Winograd F(2x2,3x3) as the configuration states: their forwards, and their
+input gradients, which are 3x3 stride-1 convolutions of dy with the flipped
+filter (dWeight stays on the implicit GEMM).  A "step" is one pass of
 every layer; inputs are resident in HBM before timing.  `components` holds
 C1 (single conv layer fwd+dX+dW+dB), C2 (Linear addmm fwd+bwd, 8192x4096x4096),
 C5 (multi-tensor AdamW, 250 tensors, GB/s), C4 (the diffusion U-Net training
@@ -126,8 +128,13 @@ def build_c3(torch, mx, L, batch, winograd=True):
         st = L.stream
         calls.append((fname, flops, 0, lambda d=d, x=x, w=w, y=y, a=fwd_algo: mx.conv2d_forward(d, x, w, None, y, a, st)))
         if dx is not None:
-            calls.append((mx.conv2d_kernel_name(d, mx.MX_CONV_DINPUT, mx.ALGO_IMPLICIT_GEMM), flops, 0,
-                          lambda d=d, dy=dy, w=w, dx=dx: mx.conv2d_backward_input(d, dy, w, dx, mx.ALGO_IMPLICIT_GEMM, st)))
+            # The input gradient of a 3x3 stride-1 layer is itself a 3x3
+            # stride-1 convolution (of dy with the flipped filter): Winograd too.
+            dx_algo = fwd_algo
+            dname = ("winograd_dinput" if dx_algo == mx.ALGO_WINOGRAD
+                     else mx.conv2d_kernel_name(d, mx.MX_CONV_DINPUT, dx_algo))
+            calls.append((dname, flops, 0,
+                          lambda d=d, dy=dy, w=w, dx=dx, a=dx_algo: mx.conv2d_backward_input(d, dy, w, dx, a, st)))
             total += flops
         calls.append((mx.conv2d_kernel_name(d, mx.MX_CONV_DWEIGHT, mx.ALGO_IMPLICIT_GEMM), flops, 0,
                       lambda d=d, x=x, dy=dy, dw=dw: mx.conv2d_backward_weight(d, x, dy, dw, None, mx.ALGO_IMPLICIT_GEMM, st)))
@@ -460,7 +467,9 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir):
     return out
 
 
-WINOGRAD_KERNELS = ("wino_filter_kernel", "wino_input_kernel", "wino_output_kernel", "gemm_kernel")
+WINOGRAD_KERNELS = ("filter_kernel", "wino_fused_kernel",   # fused path
+                    "wino_filter_kernel", "wino_input_kernel", "wino_output_kernel", "gemm_kernel")
+WINOGRAD_CALL_START = ("filter_kernel", "wino_filter_kernel")  # first dispatch of every Winograd call
 BEFORE_HELPERS = ("conv_fwd_pack_kernel", "conv_dx_pack_kernel")       # run before their tile kernel
 AFTER_HELPERS = ("conv_dw_finalize_kernel", "conv_sum_splits_kernel")   # run after it
 
@@ -518,8 +527,11 @@ def trace_summary(trace_csv, bench_log):
     `avg_us`.  An ABI call can issue several dispatches (weight packing, one
     GEMM per dInput stride phase, zero phases, the split-K sum); helper
     dispatches are charged to the call's tile kernel (packing to the next one,
-    split sums and zero phases to the previous one), Winograd's four kernels to
-    "winograd_forward", and the class total is divided by the number of calls
+    split sums and zero phases to the previous one), Winograd's kernels to
+    "winograd_forward" or, when the run also routed input gradients there,
+    alternately to "winograd_forward" and "winograd_dinput" (C3 issues a
+    layer's forward call, then its dInput call; each call starts with a
+    filter transform), and the class total is divided by the number of calls
     the run made (warm-up + untimed + event-timed steps)."""
     import csv
     res = [json.loads(l) for l in open(bench_log) if l.startswith("{")][-1]
@@ -532,9 +544,12 @@ def trace_summary(trace_csv, bench_log):
            for r in rows]
     owner = [None] * len(seq)
     last_tile = None
+    wino_dx = "winograd_dinput" in res["kernels"]
+    wino_calls = 0
     for i, (label, _) in enumerate(seq):
         if label in WINOGRAD_KERNELS:
-            owner[i] = "winograd_forward"
+            wino_calls += label in WINOGRAD_CALL_START
+            owner[i] = "winograd_dinput" if (wino_dx and wino_calls % 2 == 0) else "winograd_forward"
         elif label in AFTER_HELPERS or label == "conv_dx_zero_kernel":
             owner[i] = last_tile
         elif label not in BEFORE_HELPERS:
@@ -544,7 +559,7 @@ def trace_summary(trace_csv, bench_log):
         label = seq[i][0]
         if label in BEFORE_HELPERS or (label == "conv_dx_zero_kernel" and owner[i] is None):
             owner[i] = nxt
-        elif owner[i] is not None and owner[i] != "winograd_forward":
+        elif owner[i] is not None and not owner[i].startswith("winograd"):
             nxt = owner[i]
     agg = defaultdict(float)
     for (label, us), own in zip(seq, owner):
@@ -589,7 +604,7 @@ def main(argv=None):
                     help="markdown tables (per launch class, per kernel) from a rocprofv3 --stats CSV")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-components", action="store_true")
-    ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 forwards to implicit GEMM")
+    ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 forwards and input gradients to implicit GEMM")
     args = ap.parse_args(argv)
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
@@ -625,7 +640,7 @@ def main(argv=None):
     if args.workload == "c3":
         calls, flops_step = build_c3(torch, mx, L, 64, winograd=not args.no_winograd)
         config = {"workload": "C3: ResNet-50 v1.5 conv stack (53 convs) fwd+dInput+dWeight, batch 64, 224x224, "
-                              + ("3x3/s1 forward via Winograd F(2x2,3x3)" if not args.no_winograd
+                              + ("3x3/s1 forward and dInput via Winograd F(2x2,3x3)" if not args.no_winograd
                                  else "all phases implicit-GEMM MFMA"),
                   "global_batch": 64, "image": 224, "layers": 53, "gflop_per_step": round(flops_step / 1e9, 2)}
     else:

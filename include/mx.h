@@ -165,8 +165,11 @@ enum mx_conv_phase { MX_CONV_FORWARD = 0, MX_CONV_DINPUT = 1, MX_CONV_DWEIGHT = 
 
 /* Algorithms (candidate menu of csrc/ops/convolution.cpp:161-187):
  * AUTO lets the planner choose; DIRECT is one-output-per-thread; IMPLICIT_GEMM
- * is the MFMA tile path; WINOGRAD is F(2x2,3x3) forward; REDUCE is the
- * no-scratch dWeight / dBias reduction. */
+ * is the MFMA tile path; WINOGRAD is F(2x2,3x3) for the forward and, when
+ * requested explicitly, the input gradient of a 3x3 stride-1 dilation-1 layer
+ * with padding <= 2 (an addition: the reference's Winograd is forward only;
+ * AUTO never picks it for dInput); REDUCE is the no-scratch dWeight / dBias
+ * reduction. */
 enum mx_conv_algo {
   MX_CONV_ALGO_AUTO = 0,
   MX_CONV_ALGO_DIRECT = 1,
@@ -192,7 +195,10 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
                       const float* bias, float* y, int algo, void* stream);
 
 /* dx = conv_transpose(dy, w): dispatch(Input) (csrc/ops/convolution.cpp:684-687,
- * conv2d_backward_input_tiled_body.glsl). */
+ * conv2d_backward_input_tiled_body.glsl).  With MX_CONV_ALGO_WINOGRAD (3x3,
+ * stride 1, dilation 1, padding <= 2) dx is computed as the F(2x2,3x3)
+ * convolution of dy with the spatially flipped, channel-swapped filter at
+ * padding 2 - p. */
 int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const float* w,
                              float* dx, int algo, void* stream);
 

@@ -297,8 +297,17 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
         *algo = MX_CONV_ALGO_DIRECT;
       return MX_OK;
     case MX_CONV_DINPUT:
-      MX_REQUIRE(requested != MX_CONV_ALGO_WINOGRAD && requested != MX_CONV_ALGO_REDUCE, MX_ERR_UNSUPPORTED,
-                 "dinput supports direct and implicit_gemm only");
+      // Winograd input gradients are a choice of this build (the reference's
+      // Winograd is forward only); AUTO keeps the reference's candidates.
+      if (requested == MX_CONV_ALGO_WINOGRAD) {
+        MX_REQUIRE(winograd_applicable(d) && d.ph <= 2 && d.pw <= 2, MX_ERR_UNSUPPORTED,
+                   "Forced convolution dinput candidate winograd_f2 needs a 3x3 stride-1 dilation-1 layer with "
+                   "padding <= 2");
+        *algo = MX_CONV_ALGO_WINOGRAD;
+        return MX_OK;
+      }
+      MX_REQUIRE(requested != MX_CONV_ALGO_REDUCE, MX_ERR_UNSUPPORTED,
+                 "dinput supports direct, implicit_gemm and winograd only");
       if (requested != MX_CONV_ALGO_AUTO) {
         *algo = requested;
         return MX_OK;
@@ -532,6 +541,7 @@ GemmPlan plan_dx(const ConvArgs& p, std::vector<ConvArgs>* phases) {
 // Winograd forward lives in mx_winograd.hip.
 int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
                      hipStream_t s);
+int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, hipStream_t s);
 
 }  // namespace mx
 
@@ -619,18 +629,19 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
   int chosen = 0;
   MX_TRY(select_algo(d, MX_CONV_DINPUT, algo, &chosen));
   hipStream_t s = resolve_stream(stream);
-  if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM) {
+  if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM || chosen == MX_CONV_ALGO_WINOGRAD) {
     const int64_t nc = images_per_launch(d);
     MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d dinput: one image or the weights exceed the 2 GiB operand bound");
     if (nc < d.n) {
       for (int64_t n0 = 0; n0 < d.n; n0 += nc) {
         const mx_conv2d_desc c = batch_slice(d, std::min(nc, d.n - n0));
         MX_TRY(mx_conv2d_backward_input(&c, dy + n0 * d.cout * d.oh * d.ow, w, dx + n0 * d.cin * d.h * d.w,
-                                        MX_CONV_ALGO_IMPLICIT_GEMM, stream));
+                                        chosen, stream));
       }
       return MX_OK;
     }
   }
+  if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_backward_input(d, dy, w, dx, s);
   ConvArgs p = make_args(d);
   p.dy = dy;
   p.w = w;

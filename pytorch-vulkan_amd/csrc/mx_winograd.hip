@@ -1,4 +1,12 @@
-// Winograd F(2x2, 3x3) forward convolution (3x3, stride 1, dilation 1).
+// Winograd F(2x2, 3x3) convolution (3x3, stride 1, dilation 1): the forward
+// pass, and the input gradient of such a layer, which is itself a 3x3 stride-1
+// convolution of dy with the filter flipped in both spatial axes and its
+// channel axes swapped per group, at padding 2 - p:
+//   dx[n, g*C + c, i, j] = sum_{o, r, s} dy[n, g*O + o, i + r - (2 - p), ...]
+//                                        * w[g*O + o, c, 2 - r, 2 - s]
+// (C, O the layer's input and output channels per group).  The filter
+// transforms read w in that order (`flip`); everything after them is the
+// forward kernel unchanged.
 //
 // Transform matrices follow the reference shaders
 // (conv2d_winograd_weights.comp:17-28, conv2d_winograd_input.comp:24-37,
@@ -43,6 +51,7 @@ struct WinoArgs {
   float* V;
   float* M;
   int N, Cin, H, W, Cout, OH, OW, ph, pw, G, Cin_g, Cout_g, TH, TW, T;
+  int flip;  // filter is the flipped, channel-swapped layer filter (input gradient)
 };
 
 __global__ void wino_filter_kernel(WinoArgs p) {
@@ -52,8 +61,16 @@ __global__ void wino_filter_kernel(WinoArgs p) {
     const int oc = int(idx / p.Cin_g), ci = int(idx % p.Cin_g);
     const int g = oc / p.Cout_g, co = oc % p.Cout_g;
     float k[3][3];
-    for (int r = 0; r < 3; ++r)
-      for (int c = 0; c < 3; ++c) k[r][c] = p.w[idx * 9 + r * 3 + c];
+    if (p.flip) {
+      // Layer filter [G*Cin_g][Cout_g][3][3]: element (oc, ci) is layer
+      // output channel g*Cin_g + ci, layer input channel co, flipped taps.
+      const float* src = p.w + ((int64_t(g) * p.Cin_g + ci) * p.Cout_g + co) * 9;
+      for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) k[r][c] = src[8 - (r * 3 + c)];
+    } else {
+      for (int r = 0; r < 3; ++r)
+        for (int c = 0; c < 3; ++c) k[r][c] = p.w[idx * 9 + r * 3 + c];
+    }
     float z[4][3];
     for (int c = 0; c < 3; ++c) {
       z[0][c] = k[0][c];
@@ -170,8 +187,11 @@ struct Args {
 
 // U' for the padded (c, o) range, zero outside the real one: channel c of
 // coordinate t at [g][t][c / 8][(c % 8) / 2][o][c % 2].
+// With `flip`, w is the layer filter [G*C][O][3][3] of an input gradient:
+// element (o, c) reads layer output channel g*C + c, input channel o, taps
+// reversed.
 __global__ void filter_kernel(const float* __restrict__ w, float* __restrict__ U, int C, int O, int Cpad, int Opad,
-                              int G) {
+                              int G, bool flip) {
   const int64_t total = int64_t(G) * Cpad * Opad;
   const int nslab = Cpad / BK;
   for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
@@ -181,7 +201,14 @@ __global__ void filter_kernel(const float* __restrict__ w, float* __restrict__ U
     const int o = int(go % Opad), g = int(go / Opad);
     float u[16];
     if (o < O && c < C) {
-      const float* k = w + ((int64_t(g) * O + o) * C + c) * 9;
+      float k[9];
+      if (flip) {
+        const float* src = w + ((int64_t(g) * C + c) * O + o) * 9;
+        for (int j = 0; j < 9; ++j) k[j] = src[8 - j];
+      } else {
+        const float* src = w + ((int64_t(g) * O + o) * C + c) * 9;
+        for (int j = 0; j < 9; ++j) k[j] = src[j];
+      }
       float z[4][3];
       for (int j = 0; j < 3; ++j) {
         z[0][j] = k[j];
@@ -379,14 +406,15 @@ bool prefer_fused(int64_t workgroups) { return 2 * workgroups >= 3 * int64_t(cu_
 }  // namespace fused
 
 int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
-                     hipStream_t s);
+                     bool flip, hipStream_t s);
 
 }  // namespace
 
 namespace {
 int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
-                     hipStream_t s) {
+                     bool flip, hipStream_t s) {
   WinoArgs p{};
+  p.flip = flip ? 1 : 0;
   p.x = x;
   p.w = w;
   p.bias = bias;
@@ -443,8 +471,11 @@ int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, co
 }
 }  // namespace
 
-int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
-                     hipStream_t s) {
+namespace {
+// The convolution d of x with filter w (read flipped and channel-swapped when
+// `flip`), Winograd F(2x2,3x3), plus bias.
+int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y, bool flip,
+                 hipStream_t s) {
   fused::Args p{};
   p.bias = bias;
   p.Cin = int(d.cin);
@@ -482,12 +513,12 @@ int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, co
   bool fused_path = fused::prefer_fused(blocks * G);
   if (const char* e = std::getenv("MX_WINOGRAD_FUSED"))
     if (e[0] == '0' || e[0] == '1') fused_path = e[0] == '1';
-  if (!fused_path) return winograd_unfused(d, x, w, bias, y, s);
+  if (!fused_path) return winograd_unfused(d, x, w, bias, y, flip, s);
   Scratch U;
   MX_TRY(U.alloc(size_t(u_bytes), s));
   p.U = U.as<float>();
   hipLaunchKernelGGL(fused::filter_kernel, dim3(blocks_for(int64_t(G) * p.Cpad * p.Opad)), dim3(256), 0, s, w,
-                     U.as<float>(), p.C, p.O, p.Cpad, p.Opad, G);
+                     U.as<float>(), p.C, p.O, p.Cpad, p.Opad, G, flip);
   MX_HIP(hipGetLastError());
   p.x = x;
   p.y = y;
@@ -500,6 +531,28 @@ int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, co
     hipLaunchKernelGGL(fused::wino_fused_kernel<false>, grid, dim3(256), 0, s, p);
   MX_HIP(hipGetLastError());
   return MX_OK;
+}
+}  // namespace
+
+int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+                     hipStream_t s) {
+  return winograd_run(d, x, w, bias, y, false, s);
+}
+
+// dx of the 3x3 stride-1 layer d: the forward convolution of dy
+// [N][Cout][OH][OW] with the flipped filter at padding 2 - p, whose output is
+// [N][Cin][H][W] since H = OH + 2 (2 - p) - 2.  Needs p <= 2.
+int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, hipStream_t s) {
+  mx_conv2d_desc t = d;
+  t.cin = d.cout;
+  t.h = d.oh;
+  t.w = d.ow;
+  t.cout = d.cin;
+  t.ph = 2 - d.ph;
+  t.pw = 2 - d.pw;
+  t.oh = d.h;
+  t.ow = d.w;
+  return winograd_run(t, dy, w, nullptr, dx, true, s);
 }
 
 }  // namespace mx

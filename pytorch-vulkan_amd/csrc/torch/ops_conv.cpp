@@ -44,13 +44,23 @@ int forward_algo() {
   TORCH_CHECK(false, "TORCH_VULKAN_CONV_ALGO has an invalid algorithm (forward: auto/direct/tiled/depthwise/winograd)");
 }
 
-// Backward algorithm from TORCH_VULKAN_CONV_BACKWARD_ALGO (auto/direct/optimized).
-int backward_algo(int phase) {
+// Backward algorithm from TORCH_VULKAN_CONV_BACKWARD_ALGO (auto/direct/optimized,
+// plus this build's winograd: F(2x2,3x3) input gradients for the layers it
+// applies to, the optimized kernels everywhere else).
+int backward_algo(const mx_conv2d_desc& d, int phase) {
   const std::string a = env_or("TORCH_VULKAN_CONV_BACKWARD_ALGO", "auto");
   if (a == "auto") return MX_CONV_ALGO_AUTO;
   if (a == "direct") return MX_CONV_ALGO_DIRECT;
-  if (a == "optimized") return phase == MX_CONV_DBIAS ? MX_CONV_ALGO_REDUCE : MX_CONV_ALGO_IMPLICIT_GEMM;
-  TORCH_CHECK(false, "TORCH_VULKAN_CONV_BACKWARD_ALGO has an invalid algorithm (backward: auto/direct/optimized)");
+  const int optimized = phase == MX_CONV_DBIAS ? MX_CONV_ALGO_REDUCE : MX_CONV_ALGO_IMPLICIT_GEMM;
+  if (a == "optimized") return optimized;
+  if (a == "winograd") {
+    int algo = 0;
+    if (phase == MX_CONV_DINPUT && mx_conv2d_select(&d, phase, MX_CONV_ALGO_WINOGRAD, &algo) == MX_OK)
+      return MX_CONV_ALGO_WINOGRAD;
+    return optimized;
+  }
+  TORCH_CHECK(false,
+              "TORCH_VULKAN_CONV_BACKWARD_ALGO has an invalid algorithm (backward: auto/direct/optimized/winograd)");
 }
 
 mx_conv2d_desc make_desc(const at::Tensor& input, const at::Tensor& weight, at::IntArrayRef stride,
@@ -153,7 +163,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   if (output_mask[0]) {
     dx = at::empty(input.sizes(), opts);
     const at::Tensor w = packed(weight);
-    const int algo = choose(d, MX_CONV_DINPUT, backward_algo(MX_CONV_DINPUT));
+    const int algo = choose(d, MX_CONV_DINPUT, backward_algo(d, MX_CONV_DINPUT));
     TVK_MX(mx_conv2d_backward_input(&d, dy.data_ptr<float>(), w.data_ptr<float>(), dx.data_ptr<float>(), algo,
                                     current_stream()));
     counters().kernel_launches++;
@@ -162,7 +172,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   if (output_mask[1]) {
     dw = at::empty(weight.sizes(), weight.options().memory_format(at::MemoryFormat::Contiguous));
     const at::Tensor x = packed(input);
-    const int algo = choose(d, MX_CONV_DWEIGHT, backward_algo(MX_CONV_DWEIGHT));
+    const int algo = choose(d, MX_CONV_DWEIGHT, backward_algo(d, MX_CONV_DWEIGHT));
     // dBias rides on the dWeight launch when both are requested.
     float* dbp = nullptr;
     if (output_mask[2]) {
@@ -173,7 +183,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
                                      current_stream()));
     counters().kernel_launches++;
   } else if (output_mask[2]) {
-    choose(d, MX_CONV_DBIAS, backward_algo(MX_CONV_DBIAS));
+    choose(d, MX_CONV_DBIAS, backward_algo(d, MX_CONV_DBIAS));
     TVK_MX(mx_conv2d_backward_bias(&d, dy.data_ptr<float>(), db.data_ptr<float>(), current_stream()));
     counters().kernel_launches++;
   }

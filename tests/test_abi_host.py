@@ -79,6 +79,15 @@ def test_forced_inapplicable_algorithm_raises(mx):
         mx.conv2d_select(strided, mx.MX_CONV_FORWARD, mx.ALGO_WINOGRAD)
     with pytest.raises(mx.MXError):
         mx.conv2d_select(strided, mx.MX_CONV_DINPUT, mx.ALGO_WINOGRAD)
+    # Winograd input gradients: 3x3 stride 1 with padding <= 2, only on request.
+    same = mx.conv_desc((1, 8, 9, 9), (8, 8, 3, 3), (1, 1), (1, 1))
+    assert mx.conv2d_select(same, mx.MX_CONV_DINPUT, mx.ALGO_WINOGRAD) == mx.ALGO_WINOGRAD
+    assert mx.conv2d_select(same, mx.MX_CONV_DINPUT) == mx.ALGO_IMPLICIT_GEMM
+    wide = mx.conv_desc((1, 8, 9, 9), (8, 8, 3, 3), (1, 1), (3, 3))
+    with pytest.raises(mx.MXError, match="winograd"):
+        mx.conv2d_select(wide, mx.MX_CONV_DINPUT, mx.ALGO_WINOGRAD)
+    with pytest.raises(mx.MXError):
+        mx.conv2d_select(same, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD)
     with pytest.raises(mx.MXError):
         mx.conv2d_select(strided, mx.MX_CONV_FORWARD, mx.ALGO_REDUCE)
 

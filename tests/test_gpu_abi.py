@@ -298,6 +298,39 @@ def test_conv_winograd_batch_chunks(mx, monkeypatch):
     close(y, yref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd chunked y")
 
 
+@pytest.mark.parametrize("fused", ["1", "0"], ids=["fused", "unfused"])
+@pytest.mark.parametrize("case", WINO_CASES, ids=[f"w{i}" for i in range(len(WINO_CASES))])
+def test_conv_winograd_dinput(mx, monkeypatch, case, fused):
+    """Input gradient of a 3x3 stride-1 layer through Winograd (dy convolved
+    with the flipped, channel-swapped filter at padding 2 - p) against float64
+    CPU torch at the Winograd tolerance; dx starts as NaN so every element
+    must be written."""
+    monkeypatch.setenv("MX_WINOGRAD_FUSED", fused)
+    xs, cout, kernel, stride, padding, dilation, groups = case
+    x, w, b = conv_inputs(xs, cout, kernel, groups, seed=11)
+    d = mx.conv_desc(xs, w.shape, stride, padding, dilation, groups)
+    dy = torch.randn((xs[0], cout, d.oh, d.ow), generator=torch.Generator().manual_seed(12))
+    ref, mag = conv_refs(x, w, b, dy, stride, padding, dilation, groups)["dx"]
+    dx = torch.full(ref.shape, float("nan"), device="cuda")
+    mx.conv2d_backward_input(d, dev(dy), dev(w), dx, mx.ALGO_WINOGRAD, stream())
+    close(dx, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd dx")
+
+
+def test_conv_winograd_dinput_batch_chunks(mx, monkeypatch):
+    """Winograd input gradient of a batch past the operand bound (lowered so
+    three images take three launches)."""
+    xs, cout = (3, 40, 12, 10), 16
+    x, w, b = conv_inputs(xs, cout, (3, 3), 1, seed=13)
+    d = mx.conv_desc(xs, w.shape, (1, 1), (1, 1), (1, 1), 1)
+    monkeypatch.setenv("MX_CONV_BUFFER_LIMIT", str(4 * max(40 * 12 * 10, cout * d.oh * d.ow) + 5))
+    monkeypatch.setenv("MX_WINOGRAD_FUSED", "1")
+    dy = torch.randn((xs[0], cout, d.oh, d.ow), generator=torch.Generator().manual_seed(14))
+    ref, mag = conv_refs(x, w, b, dy, (1, 1), (1, 1), (1, 1), 1)["dx"]
+    dx = torch.full(ref.shape, float("nan"), device="cuda")
+    mx.conv2d_backward_input(d, dev(dy), dev(w), dx, mx.ALGO_WINOGRAD, stream())
+    close(dx, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd chunked dx")
+
+
 def test_conv_closed_form_1x1(mx):
     # w = 2, b = 1 -> y = 2x + 1; dx = 0.5 * w-sum per input channel for dy = 0.25.
     x = torch.randn(2, 1, 5, 7)

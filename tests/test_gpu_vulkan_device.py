@@ -131,6 +131,26 @@ def test_forced_winograd(vk, monkeypatch):
         F.conv2d(x.to("vulkan"), w.to("vulkan"), None, 2, 1)  # stride 2 is not Winograd-eligible
 
 
+def test_backward_winograd_knob(vk, monkeypatch):
+    """TORCH_VULKAN_CONV_BACKWARD_ALGO=winograd: Winograd input gradients for
+    3x3 stride-1 layers, the implicit GEMM for the rest (stride 2 here)."""
+    monkeypatch.setenv("TORCH_VULKAN_CONV_BACKWARD_ALGO", "winograd")
+    vk.clear_conv_dispatch_cache()
+    g = torch.Generator().manual_seed(15)
+    x, w = torch.randn(2, 16, 12, 12, generator=g), torch.randn(24, 16, 3, 3, generator=g) / 12
+    for stride, algo in ((1, "winograd_f2"), (2, "implicit_gemm")):
+        args = ((stride, stride), (1, 1), (1, 1), 1)
+        y_shape = (2, 24, 12 // stride, 12 // stride)
+        dy = torch.randn(y_shape, generator=g)
+        refs = conv_refs(x, w, None, dy, *args)
+        xv, wv = x.to("vulkan").requires_grad_(), w.to("vulkan").requires_grad_()
+        yv = F.conv2d(xv, wv, None, stride, 1)
+        gx, gw = torch.autograd.grad(yv, (xv, wv), dy.to("vulkan"))
+        assert_close_mag(gx, *refs["dx"], rtol=1e-3, atol=1e-4, what=f"dx stride {stride}")
+        assert_close_mag(gw, *refs["dw"], what=f"dw stride {stride}")
+        assert vk.conv_dispatch_stats().get(f"selected_dinput_{algo}", 0) >= 1, vk.conv_dispatch_stats()
+
+
 def test_conv_views_and_output_mask(no_fallback):
     torch.manual_seed(9)
     base = torch.randn(2, 4, 10, 20)

@@ -51,6 +51,35 @@ def test_oracle_winograd_equals_direct(name):
     np.testing.assert_allclose(yw, g["y64"], rtol=1e-9, atol=1e-9 * (1 + mag.max()))
 
 
+def flipped_filter(w, groups):
+    """Filter of a 3x3 layer's input gradient seen as a convolution:
+    [G*C][O][3][3] from the layer's [G*O][C][3][3], taps reversed."""
+    go, c, kh, kw = w.shape
+    o = go // groups
+    wt = w.reshape(groups, o, c, kh, kw).transpose(0, 2, 1, 3, 4)[..., ::-1, ::-1]
+    return np.ascontiguousarray(wt.reshape(groups * c, o, kh, kw))
+
+
+@pytest.mark.parametrize("name", [c for c in CASES if c.startswith("winograd")])
+def test_oracle_winograd_dinput_identity(name):
+    """dx of a 3x3 stride-1 layer equals the Winograd convolution of dy with
+    the flipped, channel-swapped filter at padding 2 - p (the identity behind
+    the device's Winograd input gradient), against CPU torch float64's dx;
+    the same call with the taps left unflipped must not match."""
+    g, (stride, padding, dilation, groups) = case(name)
+    assert stride == (1, 1) and dilation == (1, 1) and max(padding) <= 2
+    pad_t = (2 - padding[0], 2 - padding[1])
+    dx, mag = oracle.conv2d_forward(g["dy"], flipped_filter(g["w"], groups), None, (1, 1), pad_t, (1, 1), groups,
+                                    winograd=True)
+    assert dx.shape == g["dx64"].shape
+    np.testing.assert_allclose(dx, g["dx64"], rtol=1e-9, atol=1e-9 * (1 + mag.max()))
+    go, c = g["w"].shape[:2]
+    unflipped = np.ascontiguousarray(
+        g["w"].reshape(groups, go // groups, c, 3, 3).transpose(0, 2, 1, 3, 4).reshape(groups * c, go // groups, 3, 3))
+    bad, _ = oracle.conv2d_forward(g["dy"], unflipped, None, (1, 1), pad_t, (1, 1), groups, winograd=True)
+    assert not np.allclose(bad, g["dx64"], rtol=1e-3, atol=1e-3)
+
+
 def test_winograd_rejects_ineligible():
     x = np.zeros((1, 2, 8, 8), np.float32)
     with pytest.raises(oracle.ConvError):
