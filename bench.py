@@ -136,8 +136,12 @@ def build_c3(torch, mx, L, batch, winograd=True):
             calls.append((dname, flops, 0,
                           lambda d=d, dy=dy, w=w, dx=dx, a=dx_algo: mx.conv2d_backward_input(d, dy, w, dx, a, st)))
             total += flops
-        calls.append((mx.conv2d_kernel_name(d, mx.MX_CONV_DWEIGHT, mx.ALGO_IMPLICIT_GEMM), flops, 0,
-                      lambda d=d, x=x, dy=dy, dw=dw: mx.conv2d_backward_weight(d, x, dy, dw, None, mx.ALGO_IMPLICIT_GEMM, st)))
+        # ... and so is its weight gradient, through the adjoint of the transform.
+        dw_algo = fwd_algo
+        wname = ("winograd_dweight" if dw_algo == mx.ALGO_WINOGRAD
+                 else mx.conv2d_kernel_name(d, mx.MX_CONV_DWEIGHT, dw_algo))
+        calls.append((wname, flops, 0,
+                      lambda d=d, x=x, dy=dy, dw=dw, a=dw_algo: mx.conv2d_backward_weight(d, x, dy, dw, None, a, st)))
         total += 2 * flops
     return calls, total
 

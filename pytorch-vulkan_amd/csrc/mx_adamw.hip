@@ -295,7 +295,9 @@ extern "C" int mx_adamw_step(const mx_adamw_tensor* tensors, int64_t count, cons
       hp.total_chunks = chunks;
       Scratch dtab;
       MX_TRY(upload(tab.data(), tab.size() * sizeof(AdamEntry), s, dtab));
-      const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(chunks, int64_t(cu_count()) * 16));
+      // 32 workgroups per CU: measured best for the 4-read / 3-write stream mix
+      // (5.64 TB/s vs 5.59 at 16 and 5.56 at 4, one 125M-element tensor).
+      const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(chunks, int64_t(cu_count()) * 32));
       if (ams)
         hipLaunchKernelGGL(adamw_kernel<true>, dim3(unsigned(grid)), dim3(256), 0, s, dtab.as<AdamEntry>(), hp);
       else

@@ -318,7 +318,14 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
                   : MX_CONV_ALGO_DIRECT;
       return MX_OK;
     case MX_CONV_DWEIGHT:
-      MX_REQUIRE(requested != MX_CONV_ALGO_WINOGRAD, MX_ERR_UNSUPPORTED, "winograd is forward only");
+      // Winograd weight gradients (the adjoint of the forward transform) are,
+      // like Winograd input gradients, a choice of this build made on request.
+      if (requested == MX_CONV_ALGO_WINOGRAD) {
+        MX_REQUIRE(winograd_applicable(d), MX_ERR_UNSUPPORTED,
+                   "Forced convolution dweight candidate winograd_f2 needs a 3x3 stride-1 dilation-1 layer");
+        *algo = MX_CONV_ALGO_WINOGRAD;
+        return MX_OK;
+      }
       if (requested != MX_CONV_ALGO_AUTO) {
         *algo = requested;
         return MX_OK;
@@ -542,6 +549,7 @@ GemmPlan plan_dx(const ConvArgs& p, std::vector<ConvArgs>* phases) {
 int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
                      hipStream_t s);
 int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, hipStream_t s);
+int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, hipStream_t s);
 
 }  // namespace mx
 
@@ -722,7 +730,7 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
   p.x = x;
   p.dy = dy;
   p.out = dw;
-  if (chosen != MX_CONV_ALGO_IMPLICIT_GEMM) {
+  if (chosen == MX_CONV_ALGO_DIRECT || chosen == MX_CONV_ALGO_REDUCE) {
     if (chosen == MX_CONV_ALGO_DIRECT)
       hipLaunchKernelGGL(conv_dw_direct_kernel, dim3(linear_blocks(d.cout * (d.cin / d.groups) * d.kh * d.kw)),
                          dim3(256), 0, s, p);
@@ -750,15 +758,19 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
         const float* xc = x + n0 * d.cin * d.h * d.w;
         const float* dyc = dy + n0 * d.cout * d.oh * d.ow;
         if (n0 == 0) {
-          MX_TRY(mx_conv2d_backward_weight(&c, xc, dyc, dw, db, MX_CONV_ALGO_IMPLICIT_GEMM, stream));
+          MX_TRY(mx_conv2d_backward_weight(&c, xc, dyc, dw, db, chosen, stream));
         } else {
-          MX_TRY(mx_conv2d_backward_weight(&c, xc, dyc, tw, tb, MX_CONV_ALGO_IMPLICIT_GEMM, stream));
+          MX_TRY(mx_conv2d_backward_weight(&c, xc, dyc, tw, tb, chosen, stream));
           MX_TRY(mx_add_f32(dw, dw, tw, 1.f, nw, stream));
           if (db) MX_TRY(mx_add_f32(db, db, tb, 1.f, d.cout, stream));
         }
       }
       return MX_OK;
     }
+  }
+  if (chosen == MX_CONV_ALGO_WINOGRAD) {
+    MX_TRY(winograd_backward_weight(d, x, dy, dw, s));
+    return db ? mx_conv2d_backward_bias(desc, dy, db, stream) : MX_OK;
   }
   p.db = db;
   p.M = p.Cout_g;
@@ -794,7 +806,7 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
   if (phase == MX_CONV_DBIAS) {
     name = chosen == MX_CONV_ALGO_DIRECT ? "conv_db_direct_kernel" : "conv_db_reduce_kernel";
   } else if (chosen == MX_CONV_ALGO_WINOGRAD) {
-    name = "wino_filter_kernel";
+    name = phase == MX_CONV_DWEIGHT ? "wino_dw_kernel" : "wino_filter_kernel";
   } else if (chosen == MX_CONV_ALGO_DIRECT) {
     name = phase == MX_CONV_FORWARD ? "conv_fwd_direct_kernel"
            : phase == MX_CONV_DINPUT ? "conv_dx_direct_kernel" : "conv_dw_direct_kernel";

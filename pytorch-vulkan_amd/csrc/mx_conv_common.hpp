@@ -580,6 +580,10 @@ int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s);
 // out[i] = sum over splits of ws[split][i] (+ bias[(i / hw) % cout] when bias).
 int conv_sum_splits(const float* ws, int splits, int64_t n, float* out, const float* bias, int hw, int cout,
                     hipStream_t s);
+// out[i] = sum of ws[split][i] over the splits in a fixed order (the dWeight
+// finalize: 64 elements per workgroup, four interleaved phases of splits),
+// for few elements over many splits.
+int sum_partials(const float* ws, int splits, int64_t n, float* out, hipStream_t s);
 
 }  // namespace conv
 }  // namespace mx

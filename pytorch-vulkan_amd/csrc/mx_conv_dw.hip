@@ -225,5 +225,14 @@ int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s) {
   return MX_OK;
 }
 
+int sum_partials(const float* ws, int splits, int64_t n, float* out, hipStream_t s) {
+  const int64_t blocks = (n + 63) / 64;
+  MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "conv2d dweight: finalize grid too large");
+  hipLaunchKernelGGL(conv_dw_finalize_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, ws, nullptr, out, nullptr, n,
+                     0, splits);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
 }  // namespace conv
 }  // namespace mx

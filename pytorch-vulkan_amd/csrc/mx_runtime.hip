@@ -562,16 +562,42 @@ struct RingSlot {
   hipEvent_t ev;
 };
 std::mutex g_ring_mu;
-char* g_ring = nullptr;
+char* g_ring = nullptr;      // host address of the page-locked ring
+char* g_ring_dev = nullptr;  // the same memory as the device addresses it
 size_t g_ring_head = 0;
 std::vector<RingSlot> g_ring_slots;  // FIFO of in-flight regions
+
+// Device-side copy of a staged table out of the page-locked ring.  A kernel on
+// the caller's stream starts a few microseconds after the previous one; a
+// DMA-engine copy (hipMemcpyAsync) costs its ~6 us transfer plus a ~30 us
+// hand-over between the copy engine and the compute queue before the kernel
+// that reads the table can start.
+__global__ __launch_bounds__(256) void ring_copy_kernel(const char* __restrict__ src, char* __restrict__ dst,
+                                                        size_t bytes) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const size_t n16 = bytes / 16;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += size_t(gridDim.x) * blockDim.x)
+    reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(src)[i];
+  if (blockIdx.x == 0 && threadIdx.x < bytes % 16) dst[n16 * 16 + threadIdx.x] = src[n16 * 16 + threadIdx.x];
+}
 }  // namespace
 
 int upload(const void* host, size_t bytes, hipStream_t s, Scratch& holder) {
   MX_REQUIRE(bytes <= kRingBytes / 2, MX_ERR_INVALID, "upload: table of ", bytes, " bytes too large");
   MX_TRY(holder.alloc(bytes, s));
   std::lock_guard<std::mutex> lock(g_ring_mu);
-  if (!g_ring) MX_HIP(hipHostMalloc(reinterpret_cast<void**>(&g_ring), kRingBytes, hipHostMallocDefault));
+  if (!g_ring) {
+    char* ring = nullptr;
+    MX_HIP(hipHostMalloc(reinterpret_cast<void**>(&ring), kRingBytes, hipHostMallocMapped | hipHostMallocPortable));
+    void* dev = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&dev, ring, 0);
+    if (e != hipSuccess) {
+      (void)hipHostFree(ring);
+      return set_error(MX_ERR_HIP, cat("hipHostGetDevicePointer (upload ring): ", hipGetErrorString(e)));
+    }
+    g_ring = ring;
+    g_ring_dev = static_cast<char*>(dev);
+  }
   const size_t sz = (bytes + 255) / 256 * 256;
   size_t off = g_ring_head;
   if (off + sz > kRingBytes) off = 0;
@@ -592,7 +618,12 @@ int upload(const void* host, size_t bytes, hipStream_t s, Scratch& holder) {
     }
   }
   std::memcpy(g_ring + off, host, bytes);
-  MX_HIP(hipMemcpyAsync(holder.ptr, g_ring + off, bytes, hipMemcpyHostToDevice, s));
+  // Ring offsets are 256-byte aligned and device blocks 512-byte aligned, so
+  // both ends of the copy are 16-byte aligned.
+  const unsigned blocks = unsigned(std::min<size_t>((bytes / 16 + 255) / 256, 64));
+  hipLaunchKernelGGL(ring_copy_kernel, dim3(std::max(blocks, 1u)), dim3(256), 0, s, g_ring_dev + off,
+                     static_cast<char*>(holder.ptr), bytes);
+  MX_HIP(hipGetLastError());
   hipEvent_t ev;
   MX_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   MX_HIP(hipEventRecord(ev, s));

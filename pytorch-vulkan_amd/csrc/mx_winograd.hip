@@ -40,6 +40,9 @@
 #include "mx_internal.hpp"
 
 namespace mx {
+namespace conv {
+int sum_partials(const float* ws, int splits, int64_t n, float* out, hipStream_t s);
+}
 namespace {
 
 struct WinoArgs {
@@ -405,6 +408,244 @@ bool prefer_fused(int64_t workgroups) { return 2 * workgroups >= 3 * int64_t(cu_
 
 }  // namespace fused
 
+// ------------------------------------------------------------ fused dWeight
+// Weight gradient of a 3x3 stride-1 layer as the adjoint of the forward
+// transform: with M_t = U_t V_t and Y = A^T M A, U = G w G^T,
+//   dM = A dY A^T   (4x4 per 2x2 output tile of dy),
+//   dU_t[o][c] = sum over tiles k of dM_t[o][k] V_t[c][k],
+//   dw = G^T dU G   (3x3 from 4x4).
+// V is the forward's input transform of the same 4x4 patches.  One workgroup
+// computes 64 output x 32 input channels of dU for all 16 coordinates over
+// one range of tiles (the GEMM's K); slabs of 8 tiles are transformed on the
+// way into LDS (dM from two 2x2 dy tiles per thread, V from one x patch per
+// thread) in the layout of the forward kernel, so the products are the same
+// v_mfma_f32_16x16x4f32 schedule.  The epilogue applies G^T dU G in
+// registers and writes the tile range's 3x3 partial, summed over ranges in a
+// fixed order by a second launch.
+namespace fused_dw {
+using fused::A_FLOATS;
+using fused::B_FLOATS;
+using fused::BK;  // tiles per slab
+using fused::BO;  // output channels per workgroup
+using fused::f32x2;
+using fused::ROW_A;
+using fused::ROW_B;
+using mfma::f32x4;
+using mfma::i32x4;
+using mfma::kOffNone;
+constexpr int BC = fused::BT;  // input channels per workgroup (the forward's tile columns)
+static_assert(BK * BC == mfma::kThreads, "one x patch per thread per slab");
+static_assert(BK * BO == 2 * mfma::kThreads, "two dy tiles per thread per slab");
+
+struct Args {
+  const float* x;   // [N][Cin][H][W]
+  const float* dy;  // [N][Cout][OH][OW]
+  float* out;       // [range][G][O][C][3][3]
+  int64_t x_bytes, dy_bytes;
+  int Cin, H, W, Cout, OH, OW, ph, pw, C, O, TH, TW, T, n_ob, n_cb, kps;
+  mfma::FastDiv f_thw, f_tw;
+};
+
+// Tile t -> image and the top-left output coordinate (2 ty, 2 tx).
+__device__ __forceinline__ void tile_origin(uint32_t t, const Args& p, uint32_t& img, int& oy, int& ox) {
+  img = mfma::fdiv(t, p.f_thw);
+  const uint32_t pos = t - img * uint32_t(p.TH * p.TW);
+  const uint32_t ty = mfma::fdiv(pos, p.f_tw);
+  oy = int(2 * ty);
+  ox = int(2 * (pos - ty * uint32_t(p.TW)));
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void wino_dw_kernel(Args p) {
+  __shared__ __attribute__((aligned(16))) float smem[A_FLOATS + B_FLOATS];
+  float* As = smem;
+  float* Bs = smem + A_FLOATS;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y;
+  // Blocks of one tile range are consecutive, so they share an XCD and read
+  // the same x and dy tiles through its L2.
+  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
+  const int nblk = p.n_ob * p.n_cb;
+  const int range = b / nblk, ob = (b % nblk) % p.n_ob, cb = (b % nblk) / p.n_ob;
+  const int o0 = ob * BO, c0 = cb * BC;
+  const int k_begin = range * p.kps;
+  const int k_end = min(p.T, k_begin + p.kps);
+  const int nslab = (k_end - k_begin + BK - 1) / BK;
+
+  // dy: the thread owns output channel a_o of the block and slab tiles
+  // 2 a_kq and 2 a_kq + 1 (the k pair one MFMA lane multiplies).
+  const i32x4 rdy = mfma::buffer_rsrc(p.dy, p.dy_bytes);
+  const int a_o = tid >> 2, a_kq = tid & 3;
+  const bool o_ok = o0 + a_o < p.O;
+  const uint32_t dy_chan = uint32_t(g * p.O + o0 + a_o);
+  // x: the thread owns input channel b_c of the block and slab tile b_t.
+  const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
+  const int b_c = tid >> 3, b_t = tid & 7;
+  const bool c_ok = c0 + b_c < p.C;
+  const uint32_t x_chan = uint32_t(g * p.C + c0 + b_c);
+
+  float gy[2][4];  // two 2x2 dy tiles
+  float d[16];     // one 4x4 x patch
+  auto load = [&](int slab) {
+    const int kb = k_begin + slab * BK;
+    {
+      const int t = kb + b_t;
+      const bool tok = c_ok && t < k_end;
+      uint32_t img;
+      int oy, ox;
+      tile_origin(tok ? uint32_t(t) : 0u, p, img, oy, ox);
+      const int y0 = oy - p.ph, x0 = ox - p.pw;
+      const uint32_t plane = (img * uint32_t(p.Cin) + x_chan) * uint32_t(p.H);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int iy = y0 + r;
+        const bool rok = tok && unsigned(iy) < unsigned(p.H);
+        // x0 may be negative (left padding): the offset wraps modulo 2^32 and
+        // is only used for columns inside the image.
+        const uint32_t row = (plane + uint32_t(iy)) * uint32_t(p.W) * 4u + uint32_t(x0) * 4u;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const bool ok = rok && unsigned(x0 + cc) < unsigned(p.W);
+          d[r * 4 + cc] = mfma::bload(rx, ok ? row + 4u * cc : kOffNone, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int t = kb + 2 * a_kq + j;
+      const bool tok = o_ok && t < k_end;
+      uint32_t img;
+      int oy, ox;
+      tile_origin(tok ? uint32_t(t) : 0u, p, img, oy, ox);
+      const uint32_t plane = (img * uint32_t(p.Cout) + dy_chan) * uint32_t(p.OH);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const bool rok = tok && oy + r < p.OH;
+        const uint32_t row = ((plane + uint32_t(oy + r)) * uint32_t(p.OW) + uint32_t(ox)) * 4u;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const bool ok = rok && ox + cc < p.OW;
+          gy[j][r * 2 + cc] = mfma::bload(rdy, ok ? row + 4u * cc : kOffNone, 0);
+        }
+      }
+    }
+  };
+  float* const a_st = As + a_kq * ROW_A + 2 * a_o;                       // [coord][kq][o][2]
+  float* const b_st = Bs + (b_t >> 1) * ROW_B + 2 * b_c + (b_t & 1);    // [coord][kq][c][2]
+  auto store = [&]() {
+    // dM = A g A^T, A = [[1,0],[1,1],[1,-1],[0,-1]], for both tiles.
+    float m[2][16];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float z[4][2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        z[0][c] = gy[j][c];
+        z[1][c] = gy[j][c] + gy[j][2 + c];
+        z[2][c] = gy[j][c] - gy[j][2 + c];
+        z[3][c] = -gy[j][2 + c];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        m[j][r * 4 + 0] = z[r][0];
+        m[j][r * 4 + 1] = z[r][0] + z[r][1];
+        m[j][r * 4 + 2] = z[r][0] - z[r][1];
+        m[j][r * 4 + 3] = -z[r][1];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) *reinterpret_cast<f32x2*>(a_st + q * 4 * ROW_A) = f32x2{m[0][q], m[1][q]};
+    // V = B^T d B
+    float z[16];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      z[0 * 4 + cc] = d[0 * 4 + cc] - d[2 * 4 + cc];
+      z[1 * 4 + cc] = d[1 * 4 + cc] + d[2 * 4 + cc];
+      z[2 * 4 + cc] = d[2 * 4 + cc] - d[1 * 4 + cc];
+      z[3 * 4 + cc] = d[1 * 4 + cc] - d[3 * 4 + cc];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      b_st[(r * 4 + 0) * 4 * ROW_B] = z[r * 4 + 0] - z[r * 4 + 2];
+      b_st[(r * 4 + 1) * 4 * ROW_B] = z[r * 4 + 1] + z[r * 4 + 2];
+      b_st[(r * 4 + 2) * 4 * ROW_B] = z[r * 4 + 2] - z[r * 4 + 1];
+      b_st[(r * 4 + 3) * 4 * ROW_B] = z[r * 4 + 1] - z[r * 4 + 3];
+    }
+  };
+
+  // Wave (wo, wc) owns output channels wo*32 .. +31 (two 16-row blocks) and
+  // input channels wc*16 .. +15 of the block, for all 16 coordinates.
+  const int wo = wave >> 1, wc = wave & 1;
+  const int kq = lane >> 4, li = lane & 15;
+  f32x4 acc[16][2];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f32x2* const a_frag = reinterpret_cast<const f32x2*>(As + kq * ROW_A + 2 * (wo * 32 + li));
+  const f32x2* const b_frag = reinterpret_cast<const f32x2*>(Bs + kq * ROW_B + 2 * (wc * 16 + li));
+  auto mma = [&]() {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const f32x2 fb = b_frag[t * 2 * ROW_B];
+      const f32x2 fa0 = a_frag[t * 2 * ROW_A];
+      const f32x2 fa1 = a_frag[t * 2 * ROW_A + 16];  // output channels + 16
+      acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0[0], fb[0], acc[t][0], 0, 0, 0);
+      acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1[0], fb[0], acc[t][1], 0, 0, 0);
+      acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0[1], fb[1], acc[t][0], 0, 0, 0);
+      acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1[1], fb[1], acc[t][1], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int t = 0; t < 6; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+  };
+
+  load(0);
+  for (int sl = 0; sl < nslab; ++sl) {
+    store();
+    __syncthreads();
+    load(min(sl + 1, nslab - 1));  // the last slab re-reads itself: no branch around the loads
+    __builtin_amdgcn_sched_barrier(0);
+    mma();
+    __syncthreads();
+  }
+
+  // dw = G^T dU G, G = [[1,0,0],[1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]].
+  // 16x16x4 layout: lane l, register v holds row 4 (l / 16) + v (output
+  // channel) and column l % 16 (input channel).
+  const int c = c0 + wc * 16 + li;
+  if (c >= p.C) return;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
+      if (o >= p.O) continue;
+      float u[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) u[q] = acc[q][i][v];
+      float z[3][4];
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const float s12 = 0.5f * (u[4 + cc] + u[8 + cc]);
+        z[0][cc] = u[cc] + s12;
+        z[1][cc] = 0.5f * (u[4 + cc] - u[8 + cc]);
+        z[2][cc] = s12 + u[12 + cc];
+      }
+      float* dst = p.out + ((int64_t(range) * gridDim.y + g) * p.O + o) * int64_t(p.C) * 9 + int64_t(c) * 9;
+#pragma unroll
+      for (int r = 0; r < 3; ++r) {
+        const float s12 = 0.5f * (z[r][1] + z[r][2]);
+        dst[r * 3 + 0] = z[r][0] + s12;
+        dst[r * 3 + 1] = 0.5f * (z[r][1] - z[r][2]);
+        dst[r * 3 + 2] = s12 + z[r][3];
+      }
+    }
+}
+
+}  // namespace fused_dw
+
 int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
                      bool flip, hipStream_t s);
 
@@ -537,6 +778,63 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
 int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
                      hipStream_t s) {
   return winograd_run(d, x, w, bias, y, false, s);
+}
+
+// dw of the 3x3 stride-1 layer d (any padding): the fused adjoint kernel
+// over K ranges of tiles sized so the launch fills every CU twice, then a
+// fixed-order sum of the ranges' partials.
+int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, hipStream_t s) {
+  fused_dw::Args p{};
+  p.Cin = int(d.cin);
+  p.H = int(d.h);
+  p.W = int(d.w);
+  p.Cout = int(d.cout);
+  p.OH = int(d.oh);
+  p.OW = int(d.ow);
+  p.ph = int(d.ph);
+  p.pw = int(d.pw);
+  const int G = int(d.groups);
+  p.C = p.Cin / G;
+  p.O = p.Cout / G;
+  p.TH = (p.OH + 1) / 2;
+  p.TW = (p.OW + 1) / 2;
+  p.n_ob = (p.O + fused_dw::BO - 1) / fused_dw::BO;
+  p.n_cb = (p.C + fused_dw::BC - 1) / fused_dw::BC;
+  p.f_tw = mfma::fast_div(uint32_t(p.TW));
+  p.f_thw = mfma::fast_div(uint32_t(p.TH * p.TW));
+  // The caller splits batches so both operands stay buffer-addressable.
+  const int64_t x_bytes = d.n * int64_t(p.Cin) * p.H * p.W * 4;
+  const int64_t dy_bytes = d.n * int64_t(p.Cout) * p.OH * p.OW * 4;
+  const int64_t T = d.n * int64_t(p.TH) * p.TW;
+  MX_REQUIRE(x_bytes < mfma::kBufMaxBytes && dy_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
+             "winograd dweight: an operand exceeds the 2 GiB bound");
+  const int64_t n_dw = int64_t(p.Cout) * p.C * 9;
+  const int64_t blocks = int64_t(p.n_ob) * p.n_cb * G;
+  // Ranges: two resident workgroups per CU in one wave of the launch, at
+  // least four slabs each.
+  const int64_t want = std::max<int64_t>(1, (2 * int64_t(cu_count()) + blocks - 1) / blocks);
+  int64_t kps = (T + want - 1) / want;
+  kps = std::max<int64_t>(kps, 4 * fused_dw::BK);
+  kps = (kps + fused_dw::BK - 1) / fused_dw::BK * fused_dw::BK;
+  const int64_t ranges = (T + kps - 1) / kps;
+  MX_REQUIRE(blocks * ranges <= INT32_MAX && G <= 65535, MX_ERR_UNSUPPORTED, "winograd dweight: grid too large");
+  p.kps = int(kps);
+  p.T = int(T);
+  p.x = x;
+  p.dy = dy;
+  p.x_bytes = x_bytes;
+  p.dy_bytes = dy_bytes;
+  Scratch ws;
+  if (ranges > 1) {
+    MX_TRY(ws.alloc(size_t(ranges) * size_t(n_dw) * 4, s));
+    p.out = ws.as<float>();
+  } else {
+    p.out = dw;
+  }
+  hipLaunchKernelGGL(fused_dw::wino_dw_kernel, dim3(unsigned(blocks / G * ranges), unsigned(G)), dim3(256), 0, s, p);
+  MX_HIP(hipGetLastError());
+  if (ranges > 1) return conv::sum_partials(ws.as<float>(), int(ranges), n_dw, dw, s);
+  return MX_OK;
 }
 
 // dx of the 3x3 stride-1 layer d: the forward convolution of dy

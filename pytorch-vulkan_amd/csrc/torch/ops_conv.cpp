@@ -45,8 +45,8 @@ int forward_algo() {
 }
 
 // Backward algorithm from TORCH_VULKAN_CONV_BACKWARD_ALGO (auto/direct/optimized,
-// plus this build's winograd: F(2x2,3x3) input gradients for the layers it
-// applies to, the optimized kernels everywhere else).
+// plus this build's winograd: F(2x2,3x3) input and weight gradients for the
+// layers they apply to, the optimized kernels everywhere else).
 int backward_algo(const mx_conv2d_desc& d, int phase) {
   const std::string a = env_or("TORCH_VULKAN_CONV_BACKWARD_ALGO", "auto");
   if (a == "auto") return MX_CONV_ALGO_AUTO;
@@ -55,7 +55,7 @@ int backward_algo(const mx_conv2d_desc& d, int phase) {
   if (a == "optimized") return optimized;
   if (a == "winograd") {
     int algo = 0;
-    if (phase == MX_CONV_DINPUT && mx_conv2d_select(&d, phase, MX_CONV_ALGO_WINOGRAD, &algo) == MX_OK)
+    if (phase != MX_CONV_DBIAS && mx_conv2d_select(&d, phase, MX_CONV_ALGO_WINOGRAD, &algo) == MX_OK)
       return MX_CONV_ALGO_WINOGRAD;
     return optimized;
   }

@@ -86,8 +86,12 @@ def test_forced_inapplicable_algorithm_raises(mx):
     wide = mx.conv_desc((1, 8, 9, 9), (8, 8, 3, 3), (1, 1), (3, 3))
     with pytest.raises(mx.MXError, match="winograd"):
         mx.conv2d_select(wide, mx.MX_CONV_DINPUT, mx.ALGO_WINOGRAD)
-    with pytest.raises(mx.MXError):
-        mx.conv2d_select(same, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD)
+    assert mx.conv2d_select(same, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD) == mx.ALGO_WINOGRAD
+    assert mx.conv2d_select(wide, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD) == mx.ALGO_WINOGRAD
+    assert mx.conv2d_select(same, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    with pytest.raises(mx.MXError, match="winograd"):
+        mx.conv2d_select(strided, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD)
+    assert mx.conv2d_kernel_name(same, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD) == "wino_dw_kernel"
     with pytest.raises(mx.MXError):
         mx.conv2d_select(strided, mx.MX_CONV_FORWARD, mx.ALGO_REDUCE)
 

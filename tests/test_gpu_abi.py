@@ -316,6 +316,52 @@ def test_conv_winograd_dinput(mx, monkeypatch, case, fused):
     close(dx, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd dx")
 
 
+@pytest.mark.parametrize("case", WINO_CASES, ids=[f"w{i}" for i in range(len(WINO_CASES))])
+def test_conv_winograd_dweight(mx, case):
+    """Weight gradient (and the bias gradient beside it) of a 3x3 stride-1
+    layer through the Winograd adjoint against float64 CPU torch at the
+    Winograd tolerance; outputs start as NaN so every element must be written."""
+    xs, cout, kernel, stride, padding, dilation, groups = case
+    x, w, b = conv_inputs(xs, cout, kernel, groups, seed=21)
+    d = mx.conv_desc(xs, w.shape, stride, padding, dilation, groups)
+    dy = torch.randn((xs[0], cout, d.oh, d.ow), generator=torch.Generator().manual_seed(22))
+    refs = conv_refs(x, w, b, dy, stride, padding, dilation, groups)
+    dw = torch.full(w.shape, float("nan"), device="cuda")
+    db = torch.full(b.shape, float("nan"), device="cuda")
+    mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, db, mx.ALGO_WINOGRAD, stream())
+    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, atol=1e-4, mag=refs["dw"][1], what="winograd dw")
+    close(db, refs["db"][0], mag=refs["db"][1], what="db beside winograd dw")
+
+
+def test_conv_winograd_dweight_large_k(mx):
+    """C1's layer (8x64x56x56, K = 6272 tiles over many ranges summed by the
+    finalize) through the Winograd adjoint."""
+    xs, cout = (8, 64, 56, 56), 64
+    x, w, b = conv_inputs(xs, cout, (3, 3), 1, seed=23)
+    d = mx.conv_desc(xs, w.shape, (1, 1), (1, 1), (1, 1), 1)
+    dy = torch.randn((8, cout, 56, 56), generator=torch.Generator().manual_seed(24))
+    ref, mag = conv_refs(x, w, None, dy, (1, 1), (1, 1), (1, 1), 1)["dw"]
+    dw = torch.full(w.shape, float("nan"), device="cuda")
+    mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, None, mx.ALGO_WINOGRAD, stream())
+    close(dw, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd dw (C1)")
+
+
+def test_conv_winograd_dweight_batch_chunks(mx, monkeypatch):
+    """Winograd weight gradient of a batch past the operand bound: the
+    per-slice gradients are summed in slice order."""
+    xs, cout = (3, 40, 12, 10), 24
+    x, w, b = conv_inputs(xs, cout, (3, 3), 1, seed=25)
+    d = mx.conv_desc(xs, w.shape, (1, 1), (1, 1), (1, 1), 1)
+    monkeypatch.setenv("MX_CONV_BUFFER_LIMIT", str(4 * max(40 * 12 * 10, cout * d.oh * d.ow) + 5))
+    dy = torch.randn((xs[0], cout, d.oh, d.ow), generator=torch.Generator().manual_seed(26))
+    refs = conv_refs(x, w, b, dy, (1, 1), (1, 1), (1, 1), 1)
+    dw = torch.full(w.shape, float("nan"), device="cuda")
+    db = torch.full(b.shape, float("nan"), device="cuda")
+    mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, db, mx.ALGO_WINOGRAD, stream())
+    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, atol=1e-4, mag=refs["dw"][1], what="winograd chunked dw")
+    close(db, refs["db"][0], mag=refs["db"][1], what="chunked db")
+
+
 def test_conv_winograd_dinput_batch_chunks(mx, monkeypatch):
     """Winograd input gradient of a batch past the operand bound (lowered so
     three images take three launches)."""

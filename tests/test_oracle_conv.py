@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle
+from oracle import winograd as wino
 from helpers import RTOL, ATOL, WINOGRAD_RTOL, assert_close_mag
 
 GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "conv.npz"))
@@ -51,15 +52,6 @@ def test_oracle_winograd_equals_direct(name):
     np.testing.assert_allclose(yw, g["y64"], rtol=1e-9, atol=1e-9 * (1 + mag.max()))
 
 
-def flipped_filter(w, groups):
-    """Filter of a 3x3 layer's input gradient seen as a convolution:
-    [G*C][O][3][3] from the layer's [G*O][C][3][3], taps reversed."""
-    go, c, kh, kw = w.shape
-    o = go // groups
-    wt = w.reshape(groups, o, c, kh, kw).transpose(0, 2, 1, 3, 4)[..., ::-1, ::-1]
-    return np.ascontiguousarray(wt.reshape(groups * c, o, kh, kw))
-
-
 @pytest.mark.parametrize("name", [c for c in CASES if c.startswith("winograd")])
 def test_oracle_winograd_dinput_identity(name):
     """dx of a 3x3 stride-1 layer equals the Winograd convolution of dy with
@@ -69,7 +61,7 @@ def test_oracle_winograd_dinput_identity(name):
     g, (stride, padding, dilation, groups) = case(name)
     assert stride == (1, 1) and dilation == (1, 1) and max(padding) <= 2
     pad_t = (2 - padding[0], 2 - padding[1])
-    dx, mag = oracle.conv2d_forward(g["dy"], flipped_filter(g["w"], groups), None, (1, 1), pad_t, (1, 1), groups,
+    dx, mag = oracle.conv2d_forward(g["dy"], wino.flipped_filter(g["w"], groups), None, (1, 1), pad_t, (1, 1), groups,
                                     winograd=True)
     assert dx.shape == g["dx64"].shape
     np.testing.assert_allclose(dx, g["dx64"], rtol=1e-9, atol=1e-9 * (1 + mag.max()))
@@ -78,6 +70,38 @@ def test_oracle_winograd_dinput_identity(name):
         g["w"].reshape(groups, go // groups, c, 3, 3).transpose(0, 2, 1, 3, 4).reshape(groups * c, go // groups, 3, 3))
     bad, _ = oracle.conv2d_forward(g["dy"], unflipped, None, (1, 1), pad_t, (1, 1), groups, winograd=True)
     assert not np.allclose(bad, g["dx64"], rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("name", [c for c in CASES if c.startswith("winograd")])
+def test_oracle_winograd_dweight_adjoint(name):
+    """dw of a 3x3 stride-1 layer as the adjoint of the Winograd forward
+    (G^T sum_tiles (A dY A^T) * (B^T d B) G) equals CPU torch float64's dw;
+    a sign flipped in A or an entry of G changed must not match."""
+    g, (stride, padding, dilation, groups) = case(name)
+    dw = wino.dweight_adjoint(g["x"], g["dy"], padding, groups)
+    mag = wino.dweight_adjoint(np.abs(g["x"]), np.abs(g["dy"]), padding, groups)
+    np.testing.assert_allclose(dw, g["dw64"], rtol=1e-9, atol=1e-9 * (1 + mag.max()))
+    bad_a = wino.AT.copy()
+    bad_a[1, 3] = 1.0
+    bad_g = wino.G.copy()
+    bad_g[2, 1] = 0.5
+    for kw in ({"at": bad_a}, {"g": bad_g}):
+        bad = wino.dweight_adjoint(g["x"], g["dy"], padding, groups, **kw)
+        assert not np.allclose(bad, g["dw64"], rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("hw,pad", [((5, 7), (0, 0)), ((6, 5), (1, 1)), ((4, 4), (2, 2)), ((7, 6), (0, 2))])
+def test_oracle_winograd_dweight_brute_force(hw, pad):
+    """Odd and even output sizes (half tiles at the edges) and paddings 0..2
+    against the direct restatement of conv2d_backward_weight.comp."""
+    rng = np.random.default_rng(sum(hw) + pad[0])
+    x = rng.standard_normal((2, 5, *hw)).astype(np.float32)
+    w = rng.standard_normal((3, 5, 3, 3)).astype(np.float32)
+    oh, ow = hw[0] + 2 * pad[0] - 2, hw[1] + 2 * pad[1] - 2
+    dy = rng.standard_normal((2, 3, oh, ow)).astype(np.float32)
+    ref, mag = oracle.conv2d_backward(x, w, dy, (1, 1), pad)["dw"]
+    got = wino.dweight_adjoint(x, dy, pad, 1)
+    np.testing.assert_allclose(got, ref, rtol=1e-9, atol=1e-9 * (1 + mag.max()))
 
 
 def test_winograd_rejects_ineligible():
