@@ -193,44 +193,61 @@ struct Args {
 // With `flip`, w is the layer filter [G*C][O][3][3] of an input gradient:
 // element (o, c) reads layer output channel g*C + c, input channel o, taps
 // reversed.
+// One thread per (g, channel pair c, c + 1, o), o fastest: the two channels
+// of a pair are adjacent in U', so each coordinate is one 8-byte store and a
+// wave writes 512 contiguous bytes.
+__device__ __forceinline__ void filter_transform(const float* __restrict__ w, int C, int O, int g, int o, int c,
+                                                 bool flip, float (&u)[16]) {
+  if (o >= O || c >= C) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) u[t] = 0.f;
+    return;
+  }
+  float k[9];
+  if (flip) {
+    const float* src = w + ((int64_t(g) * C + c) * O + o) * 9;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) k[j] = src[8 - j];
+  } else {
+    const float* src = w + ((int64_t(g) * O + o) * C + c) * 9;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) k[j] = src[j];
+  }
+  float z[4][3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    z[0][j] = k[j];
+    z[1][j] = 0.5f * (k[j] + k[3 + j] + k[6 + j]);
+    z[2][j] = 0.5f * (k[j] - k[3 + j] + k[6 + j]);
+    z[3][j] = k[6 + j];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    u[r * 4 + 0] = z[r][0];
+    u[r * 4 + 1] = 0.5f * (z[r][0] + z[r][1] + z[r][2]);
+    u[r * 4 + 2] = 0.5f * (z[r][0] - z[r][1] + z[r][2]);
+    u[r * 4 + 3] = z[r][2];
+  }
+}
+
 __global__ void filter_kernel(const float* __restrict__ w, float* __restrict__ U, int C, int O, int Cpad, int Opad,
                               int G, bool flip) {
-  const int64_t total = int64_t(G) * Cpad * Opad;
+  const int pairs = Cpad / 2;
+  const int64_t total = int64_t(G) * pairs * Opad;
   const int nslab = Cpad / BK;
   for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
        idx += int64_t(gridDim.x) * blockDim.x) {
-    const int c = int(idx % Cpad);
-    const int64_t go = idx / Cpad;
-    const int o = int(go % Opad), g = int(go / Opad);
-    float u[16];
-    if (o < O && c < C) {
-      float k[9];
-      if (flip) {
-        const float* src = w + ((int64_t(g) * C + c) * O + o) * 9;
-        for (int j = 0; j < 9; ++j) k[j] = src[8 - j];
-      } else {
-        const float* src = w + ((int64_t(g) * O + o) * C + c) * 9;
-        for (int j = 0; j < 9; ++j) k[j] = src[j];
-      }
-      float z[4][3];
-      for (int j = 0; j < 3; ++j) {
-        z[0][j] = k[j];
-        z[1][j] = 0.5f * (k[j] + k[3 + j] + k[6 + j]);
-        z[2][j] = 0.5f * (k[j] - k[3 + j] + k[6 + j]);
-        z[3][j] = k[6 + j];
-      }
-      for (int r = 0; r < 4; ++r) {
-        u[r * 4 + 0] = z[r][0];
-        u[r * 4 + 1] = 0.5f * (z[r][0] + z[r][1] + z[r][2]);
-        u[r * 4 + 2] = 0.5f * (z[r][0] - z[r][1] + z[r][2]);
-        u[r * 4 + 3] = z[r][2];
-      }
-    } else {
-      for (int t = 0; t < 16; ++t) u[t] = 0.f;
-    }
-    const int slab = c / BK, kq = (c % BK) >> 1, j = c & 1;
+    const int o = int(idx % Opad);
+    const int64_t rest = idx / Opad;
+    const int c = 2 * int(rest % pairs), g = int(rest / pairs);
+    float u0[16], u1[16];
+    filter_transform(w, C, O, g, o, c, flip, u0);
+    filter_transform(w, C, O, g, o, c + 1, flip, u1);
+    const int slab = c / BK, kq = (c % BK) >> 1;
+#pragma unroll
     for (int t = 0; t < 16; ++t)
-      U[(((int64_t(g) * 16 + t) * nslab + slab) * 4 + kq) * int64_t(Opad) * 2 + 2 * o + j] = u[t];
+      *reinterpret_cast<f32x2*>(U + (((int64_t(g) * 16 + t) * nslab + slab) * 4 + kq) * int64_t(Opad) * 2 + 2 * o) =
+          f32x2{u0[t], u1[t]};
   }
 }
 
@@ -758,7 +775,7 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   Scratch U;
   MX_TRY(U.alloc(size_t(u_bytes), s));
   p.U = U.as<float>();
-  hipLaunchKernelGGL(fused::filter_kernel, dim3(blocks_for(int64_t(G) * p.Cpad * p.Opad)), dim3(256), 0, s, w,
+  hipLaunchKernelGGL(fused::filter_kernel, dim3(blocks_for(int64_t(G) * (p.Cpad / 2) * p.Opad)), dim3(256), 0, s, w,
                      U.as<float>(), p.C, p.O, p.Cpad, p.Opad, G, flip);
   MX_HIP(hipGetLastError());
   p.x = x;
