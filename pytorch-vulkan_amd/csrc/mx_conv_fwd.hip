@@ -34,26 +34,39 @@ MX_TILE_KERNEL(C) void conv_fwd_kernel(ConvArgs p) {
   // the finalize).
   float* const out = p.splits == 1 ? p.out : p.ws + split * p.out_elems;
   const float* const bias = p.splits == 1 ? p.bias : nullptr;
-  // Output offset of each fragment column (img * Cout * OHOW + q), once.
-  int cbase[C::FN];
-  bool cok[C::FN];
+  // The output (one launch's, below 2^31 bytes) as a buffer resource: a
+  // store outside the tile's valid rows / columns goes to kOffNone and is
+  // dropped, so the epilogue has no branches.  Stores count in the same
+  // vector-memory counter as loads, so the bias values of a fragment row
+  // block are all loaded before its first store: a load between stores would
+  // make every later store wait for the earlier ones to complete.
+  const i32x4 ro = buffer_rsrc(out, p.out_elems * 4);
+  // Output byte offset of each fragment column (img * Cout * OHOW + q), once.
+  uint32_t cbase[C::FN];
 #pragma unroll
   for (int j = 0; j < C::FN; ++j) {
     const int pos = col0 + acc_col<C>(j);
-    cok[j] = pos < p.Ncols;
-    const int img = (cok[j] ? pos : 0) / p.OHOW;
-    cbase[j] = img * p.Cout * p.OHOW + (pos - img * p.OHOW);
+    const int img = (pos < p.Ncols ? pos : 0) / p.OHOW;
+    cbase[j] = pos < p.Ncols ? uint32_t(img * p.Cout * p.OHOW + (pos - img * p.OHOW)) * 4u : kOffNone;
   }
-  for_each_acc_row<C>([&](int r, int i, int v) {
-    const int co = row0 + r;
-    if (co >= p.M) return;
-    const int oc = g * p.Cout_g + co;
-    const float b = bias ? bias[oc] : 0.f;
-    float* dst = out + int64_t(oc) * p.OHOW;
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j)
-      if (cok[j]) dst[cbase[j]] = acc.v[i][j][v] + b;
-  });
+  for (int i = 0; i < C::FM; ++i) {
+    float b[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int co = row0 + acc_row<C>(i, v);
+      b[v] = (bias && co < p.M) ? bias[g * p.Cout_g + co] : 0.f;
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int co = row0 + acc_row<C>(i, v);
+      const bool rok = co < p.M;
+      const uint32_t roff = uint32_t((g * p.Cout_g + co) * p.OHOW) * 4u;
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j)
+        bstore(acc.v[i][j][v] + b[v], ro, (rok && cbase[j] != kOffNone) ? roff + cbase[j] : kOffNone, 0);
+    }
+  }
 }
 
 // Wp[g][co][k] = w[g*Cout_g + co][ci][kh][kw] with k the blocked gathered
