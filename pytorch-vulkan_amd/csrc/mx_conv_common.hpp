@@ -163,7 +163,11 @@ struct Im2colLoader {
       for (int e = 0; e < EPT; ++e) {
         const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
         const bool valid = ok && (kb + e) < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-        v[e] = bload(rs, valid ? xoff + uint32_t(ih * W + iw) * 4u : kOffNone, uint32_t(ci) * uint32_t(HW) * 4u);
+        // The channel walk is uniform, but the compiler loses track of that
+        // through the wrap-arounds; readfirstlane keeps the scalar offset in
+        // an SGPR (otherwise each load becomes a loop over distinct values).
+        v[e] = bload(rs, valid ? xoff + uint32_t(ih * W + iw) * 4u : kOffNone,
+                     uint32_t(wave_uniform(ci)) * uint32_t(HW) * 4u);
         if (++kw == KW) {
           kw = 0;
           if (++kh == KH) {
@@ -313,7 +317,9 @@ struct PhaseGatherLoader {
       for (int e = 0; e < EPT; ++e) {
         const int oh = ib - th * dsh, ow = jb - tw * dsw;
         const bool valid = ok && (kb + e) < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
-        v[e] = bload(rs, valid ? doff + uint32_t(oh * OW + ow) * 4u : kOffNone, uint32_t(co) * uint32_t(OHOW) * 4u);
+        // Uniform walk: readfirstlane keeps the scalar offset in an SGPR.
+        v[e] = bload(rs, valid ? doff + uint32_t(oh * OW + ow) * 4u : kOffNone,
+                     uint32_t(wave_uniform(co)) * uint32_t(OHOW) * 4u);
         if (++tw == ntw) {
           tw = 0;
           if (++th == nth) {

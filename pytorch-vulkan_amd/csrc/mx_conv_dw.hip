@@ -29,9 +29,16 @@ __device__ __forceinline__ float row_lane_sum(float v) {
 template <class C, class LA, class LB>
 MX_TILE_KERNEL(C) void conv_dw_kernel(ConvArgs p) {
   __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
-  const int g = blockIdx.z, split = blockIdx.y;
+  // The (tile, split) grid is remapped as one sequence, tiles fastest, so
+  // the tiles of a split -- which read the same dy and x range -- share an
+  // XCD's L2 even when a split has fewer tiles than there are XCDs (the
+  // 7x7 stem: 3 tiles over 147 columns).
+  const int g = blockIdx.z;
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int lin = xcd_remap(int(blockIdx.y) * int(gridDim.x) + int(blockIdx.x), int(gridDim.x * gridDim.y));
+  const int split = lin / ntiles;
   int tm, tn;
-  tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
+  tile_coords(lin - split * ntiles, p.tiles_m, p.tiles_n, tm, tn);
   const int row0 = tm * C::BM, col0 = tn * C::BN;
   const int k_begin = split * p.kps;
   const int k_end = min(p.K, k_begin + p.kps);
