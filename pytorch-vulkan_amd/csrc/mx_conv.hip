@@ -364,6 +364,12 @@ constexpr TileInfo kTileInfo[conv::NTILES] = {
     {256, 128, 2, 1.20, "256x128x16"}, {128, 256, 2, 1.22, "128x256x16"}, {128, 128, 2, 1.15, "128x128x16"},
     {64, 256, 2, 0.68, "64x256x16"},   {256, 64, 2, 0.76, "256x64x16"},   {64, 64, 4, 1.10, "64x64x32"}};
 
+// Kernel tag of a tile for a phase: forward and dInput compile the small tile
+// with 16-deep slabs (conv::TileSmallShallow).
+const char* tile_name(int tile, int phase) {
+  return (tile == conv::SMALL && phase != MX_CONV_DWEIGHT) ? "64x64x16" : kTileInfo[tile].name;
+}
+
 // Estimated time of one implicit GEMM (per group M x Ncols x K, G groups)
 // with tile `ti` and K split `splits` ways of kps each, plus the finalize pass
 // that sums the partial outputs.  A CU holding n tiles runs at
@@ -813,9 +819,9 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
   } else if (chosen == MX_CONV_ALGO_REDUCE) {
     name = "conv_dw_reduce_kernel";
   } else if (phase == MX_CONV_FORWARD) {
-    name = cat("conv_fwd_kernel<", kTileInfo[plan_fwd(p).tile].name, ">");
+    name = cat("conv_fwd_kernel<", tile_name(plan_fwd(p).tile, phase), ">");
   } else if (phase == MX_CONV_DINPUT) {
-    name = cat("conv_dx_kernel<", kTileInfo[plan_dx(p, nullptr).tile].name, ">");
+    name = cat("conv_dx_kernel<", tile_name(plan_dx(p, nullptr).tile, phase), ">");
   } else {
     p.M = p.Cout_g;
     p.Ncols = p.Cin_g * p.KK;

@@ -131,7 +131,7 @@ int conv_fwd_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t
     case WIDE: return launch_a<TileWide>(p, ma, bmode, s);
     case SQ: return launch_a<TileSq>(p, ma, bmode, s);
     case FLAT: return launch_a<TileFlat>(p, ma, bmode, s);
-    default: return launch_a<TileSmall>(p, ma, bmode, s);
+    default: return launch_a<TileSmallShallow>(p, ma, bmode, s);
   }
 }
 

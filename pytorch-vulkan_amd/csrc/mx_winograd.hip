@@ -829,7 +829,9 @@ int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const floa
   const int64_t blocks = int64_t(p.n_ob) * p.n_cb * G;
   // Ranges: two resident workgroups per CU in one wave of the launch, at
   // least four slabs each.
-  const int64_t want = std::max<int64_t>(1, (2 * int64_t(cu_count()) + blocks - 1) / blocks);
+  int64_t per_cu = 2;
+  if (const char* e = std::getenv("MX_WINO_DW_PER_CU")) per_cu = std::max(1, std::atoi(e));
+  const int64_t want = std::max<int64_t>(1, (per_cu * int64_t(cu_count()) + blocks - 1) / blocks);
   int64_t kps = (T + want - 1) / want;
   kps = std::max<int64_t>(kps, 4 * fused_dw::BK);
   kps = (kps + fused_dw::BK - 1) / fused_dw::BK * fused_dw::BK;
