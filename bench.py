@@ -551,7 +551,10 @@ def trace_summary(trace_csv, bench_log):
     wino_dx = "winograd_dinput" in res["kernels"]
     wino_calls = 0
     for i, (label, _) in enumerate(seq):
-        if label in WINOGRAD_KERNELS:
+        if label == "wino_dw_kernel":
+            # the Winograd weight gradient; its range sum follows as a helper
+            owner[i] = last_tile = "winograd_dweight"
+        elif label in WINOGRAD_KERNELS:
             wino_calls += label in WINOGRAD_CALL_START
             owner[i] = "winograd_dinput" if (wino_dx and wino_calls % 2 == 0) else "winograd_forward"
         elif label in AFTER_HELPERS or label == "conv_dx_zero_kernel":
