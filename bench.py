@@ -611,7 +611,7 @@ def main(argv=None):
                     help="markdown tables (per launch class, per kernel) from a rocprofv3 --stats CSV")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-components", action="store_true")
-    ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 forwards and input gradients to implicit GEMM")
+    ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 layers (all three phases) to implicit GEMM")
     args = ap.parse_args(argv)
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
@@ -647,7 +647,7 @@ def main(argv=None):
     if args.workload == "c3":
         calls, flops_step = build_c3(torch, mx, L, 64, winograd=not args.no_winograd)
         config = {"workload": "C3: ResNet-50 v1.5 conv stack (53 convs) fwd+dInput+dWeight, batch 64, 224x224, "
-                              + ("3x3/s1 forward and dInput via Winograd F(2x2,3x3)" if not args.no_winograd
+                              + ("3x3/s1 layers (forward, dInput, dWeight) via Winograd F(2x2,3x3)" if not args.no_winograd
                                  else "all phases implicit-GEMM MFMA"),
                   "global_batch": 64, "image": 224, "layers": 53, "gflop_per_step": round(flops_step / 1e9, 2)}
     else:
