@@ -233,6 +233,7 @@ ConvArgs make_args(const mx_conv2d_desc& d) {
   p.f_hw = conv::fast_div(uint32_t(p.HW));
   p.f_kblk = conv::fast_div(uint32_t(p.KK * conv::kChanBlock));
   p.f_tapw = conv::fast_div(uint32_t(p.KW));
+  p.f_kk = conv::fast_div(uint32_t(p.KK));
   return p;
 }
 
@@ -686,6 +687,7 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
     q.wt = packed ? wt.as<float>() : w;
     q.f_kblk = conv::fast_div(uint32_t(q.nth * q.ntw * conv::kChanBlock));
     q.f_tapw = conv::fast_div(uint32_t(q.ntw));
+    q.f_kk = conv::fast_div(uint32_t(q.nth * q.ntw));
     q.splits = gp.splits;
     q.kps = int((q.K + gp.splits - 1) / gp.splits + kSplitBK - 1) / kSplitBK * kSplitBK;
     q.ws = ws.as<float>();

@@ -63,6 +63,7 @@ struct ConvArgs {
   // tap) by taps * kChanBlock, tap -> (row, column) by the tap-grid width
   // (forward: KK * 16 and KW; dInput phase: nth * ntw * 16 and ntw).
   FastDiv f_kblk, f_tapw;
+  FastDiv f_kk;  // non-blocked gathers: taps per channel (forward KK, dInput phase nth * ntw)
   // dWeight: the B gather runs its columns in the channel-blocked order
   // (channel block, kh, kw, channel in block); the epilogue maps them back.
   int cols_blocked;
@@ -106,7 +107,7 @@ struct Im2colLoader {
   uint32_t xoff;  // bytes to (img, first channel of the group, 0, 0)
   int ih0, iw0, ks, k, kmax;
   bool ok;
-  FastDiv f_kblk, f_kw;
+  FastDiv f_kblk, f_kw, f_kk;
   int KK, KBLK, KH, KW, dh, dw, H, W, HW;
   __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
@@ -119,12 +120,13 @@ struct Im2colLoader {
     const int q = pp - img * p.OHOW;
     const int oh = q / p.OW;
     const int ow = q - oh * p.OW;
-    ih0 = oh * p.sh - p.ph;
+    ih0 = ok ? oh * p.sh - p.ph : INT_MIN / 2;  // fails every bounds test
     iw0 = ow * p.sw - p.pw;
     xoff = uint32_t((int64_t(img) * p.Cin + int64_t(g) * p.Cin_g) * p.HW * 4);
     rs = buffer_rsrc(p.x, int64_t(p.N) * p.Cin * p.HW * 4);
     f_kblk = p.f_kblk;
     f_kw = p.f_tapw;
+    f_kk = p.f_kk;
     KK = p.KK;
     KBLK = p.KK * kChanBlock;
     KH = p.KH;
@@ -148,33 +150,28 @@ struct Im2colLoader {
       const int kw = t - kh * KW;
       const int c = cb * kChanBlock + (rem - t * kChanBlock);
       const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
-      const bool valid = ok && kb < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
+      const bool valid = (kb < kmax) & (unsigned(ih) < unsigned(H)) & (unsigned(iw) < unsigned(W));
       const uint32_t voff = valid ? xoff + uint32_t(ih * W + iw) * 4u : kOffNone;
       const uint32_t s0 = uint32_t(c) * uint32_t(HW) * 4u;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) v[e] = bload(rs, voff, s0 + uint32_t(e * HW) * 4u);
     } else {
-      // (ci, kh, kw) with kw fastest; the walk is wave-uniform.
-      int ci = kb / KK;
-      const int rem = kb - ci * KK;
-      int kh = rem / KW;
-      int kw = rem - kh * KW;
+      // (ci, kh, kw) with kw fastest, decomposed per element by multiply-high
+      // divisions of the wave-uniform k on the scalar unit (readfirstlane
+      // keeps it there: a channel offset the compiler thinks divergent turns
+      // each load into a loop over distinct values).  Out-of-range positions
+      // carry ih0 far below zero, so one bounds test covers them and nothing
+      // branches.
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
+        const int ke = wave_uniform(kb + e);
+        const int ci = int(fdiv(uint32_t(ke), f_kk));
+        const int rem = ke - ci * KK;
+        const int kh = int(fdiv(uint32_t(rem), f_kw));
+        const int kw = rem - kh * KW;
         const int ih = ih0 + kh * dh, iw = iw0 + kw * dw;
-        const bool valid = ok && (kb + e) < kmax && unsigned(ih) < unsigned(H) && unsigned(iw) < unsigned(W);
-        // The channel walk is uniform, but the compiler loses track of that
-        // through the wrap-arounds; readfirstlane keeps the scalar offset in
-        // an SGPR (otherwise each load becomes a loop over distinct values).
-        v[e] = bload(rs, valid ? xoff + uint32_t(ih * W + iw) * 4u : kOffNone,
-                     uint32_t(wave_uniform(ci)) * uint32_t(HW) * 4u);
-        if (++kw == KW) {
-          kw = 0;
-          if (++kh == KH) {
-            kh = 0;
-            ++ci;
-          }
-        }
+        const bool valid = (ke < kmax) & (unsigned(ih) < unsigned(H)) & (unsigned(iw) < unsigned(W));
+        v[e] = bload(rs, valid ? xoff + uint32_t(ih * W + iw) * 4u : kOffNone, uint32_t(ci) * uint32_t(HW) * 4u);
       }
     }
     k += kstep;
@@ -260,7 +257,7 @@ struct PhaseGatherLoader {
   uint32_t doff;  // bytes to (img, first channel of the group, 0, 0)
   int ib, jb, ks, k, kmax;
   bool ok;
-  FastDiv f_kblk, f_tw;
+  FastDiv f_kblk, f_tw, f_nt;
   int NT, KBLK, nth, ntw, dsh, dsw, OH, OW, OHOW;
   __device__ __forceinline__ void init(const ConvArgs& p, int col0, int g, int k0, int kmax_) {
     const int tid = threadIdx.x;
@@ -273,12 +270,13 @@ struct PhaseGatherLoader {
     const int q = pp - img * p.HpWp;
     const int i = q / p.Wp;
     const int j = q - i * p.Wp;
-    ib = i + p.offh0;
+    ib = ok ? i + p.offh0 : INT_MIN / 2;  // fails every bounds test
     jb = j + p.offw0;
     doff = uint32_t((int64_t(img) * p.Cout + int64_t(g) * p.Cout_g) * p.OHOW * 4);
     rs = buffer_rsrc(p.dy, int64_t(p.N) * p.Cout * p.OHOW * 4);
     f_kblk = p.f_kblk;
     f_tw = p.f_tapw;
+    f_nt = p.f_kk;
     NT = p.nth * p.ntw;
     KBLK = NT * kChanBlock;
     nth = p.nth;
@@ -302,31 +300,25 @@ struct PhaseGatherLoader {
       const int tw = t - th * ntw;
       const int co = cb * kChanBlock + (rem - t * kChanBlock);
       const int oh = ib - th * dsh, ow = jb - tw * dsw;
-      const bool valid = ok && kb < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
+      const bool valid = (kb < kmax) & (unsigned(oh) < unsigned(OH)) & (unsigned(ow) < unsigned(OW));
       const uint32_t voff = valid ? doff + uint32_t(oh * OW + ow) * 4u : kOffNone;
       const uint32_t s0 = uint32_t(co) * uint32_t(OHOW) * 4u;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) v[e] = bload(rs, voff, s0 + uint32_t(e * OHOW) * 4u);
     } else {
-      // (co, th, tw) with tw fastest; the walk is wave-uniform.
-      int co = kb / NT;
-      const int rem = kb - co * NT;
-      int th = rem / ntw;
-      int tw = rem - th * ntw;
+      // (co, th, tw) with tw fastest, decomposed per element from the
+      // wave-uniform k on the scalar unit; out-of-range positions carry ib far
+      // below zero, so nothing branches.
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
+        const int ke = wave_uniform(kb + e);
+        const int co = int(fdiv(uint32_t(ke), f_nt));
+        const int rem = ke - co * NT;
+        const int th = int(fdiv(uint32_t(rem), f_tw));
+        const int tw = rem - th * ntw;
         const int oh = ib - th * dsh, ow = jb - tw * dsw;
-        const bool valid = ok && (kb + e) < kmax && unsigned(oh) < unsigned(OH) && unsigned(ow) < unsigned(OW);
-        // Uniform walk: readfirstlane keeps the scalar offset in an SGPR.
-        v[e] = bload(rs, valid ? doff + uint32_t(oh * OW + ow) * 4u : kOffNone,
-                     uint32_t(wave_uniform(co)) * uint32_t(OHOW) * 4u);
-        if (++tw == ntw) {
-          tw = 0;
-          if (++th == nth) {
-            th = 0;
-            ++co;
-          }
-        }
+        const bool valid = (ke < kmax) & (unsigned(oh) < unsigned(OH)) & (unsigned(ow) < unsigned(OW));
+        v[e] = bload(rs, valid ? doff + uint32_t(oh * OW + ow) * 4u : kOffNone, uint32_t(co) * uint32_t(OHOW) * 4u);
       }
     }
     k += kstep;
