@@ -171,16 +171,37 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamEntry* __restrict_
         if constexpr (AMS) __builtin_nontemporal_store(x4[u], reinterpret_cast<f32x4*>(e.vmax + i));
       }
     } else {
-      for (int u = 0; u < kVec; ++u)
-        for (int64_t i = base + u * 1024; i < min(base + u * 1024 + 4, e.numel); ++i) {
-          float p = e.p[i], m = e.m[i], v = e.v[i];
-          float x = AMS ? e.vmax[i] : 0.f;
-          update<AMS>(p, e.g[i], m, v, &x, c, hp, scale);
-          e.p[i] = p;
-          e.m[i] = m;
-          e.v[i] = v;
-          if constexpr (AMS) e.vmax[i] = x;
+      // A tensor's last (partial) chunk, or unaligned streams: element loads,
+      // a group of four elements per stream issued before its stores (a store
+      // between them would order every later load after it, one memory round
+      // trip per element); the groups run one after another to keep the
+      // register count of the vector path.
+#pragma unroll 1
+      for (int u = 0; u < kVec; ++u) {
+        float pp[4], gg[4], mm[4], vv[4], xx[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t i = base + u * 1024 + j;
+          const bool in = i < e.numel;
+          pp[j] = in ? e.p[i] : 0.f;
+          gg[j] = in ? e.g[i] : 0.f;
+          mm[j] = in ? e.m[i] : 0.f;
+          vv[j] = in ? e.v[i] : 0.f;
+          xx[j] = (AMS && in) ? e.vmax[i] : 0.f;
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) update<AMS>(pp[j], gg[j], mm[j], vv[j], &xx[j], c, hp, scale);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t i = base + u * 1024 + j;
+          if (i < e.numel) {
+            e.p[i] = pp[j];
+            e.m[i] = mm[j];
+            e.v[i] = vv[j];
+            if constexpr (AMS) e.vmax[i] = xx[j];
+          }
+        }
+      }
     }
   }
 }
