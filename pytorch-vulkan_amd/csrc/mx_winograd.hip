@@ -276,7 +276,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // kOffNone off the image) and a column mask, the slab's channel offset in
   // the scalar offset.
   const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
-  const int b_c = tid >> 5, b_t = tid & 31;
+  // Lanes 0-15 and 16-31 of a half-wave take the two channels of a pair for
+  // the same 16 tiles, so the half-wave's V stores cover 32 consecutive
+  // floats ([k pair][tile][2]) -- distinct banks.
+  const int b_t = (tid & 15) | ((tid >> 1) & 16);
+  const int b_c = ((tid >> 4) & 1) | ((tid >> 5) & 6);
   uint32_t row_off[4];
   uint32_t col_ok = 0;
   {
@@ -440,13 +444,17 @@ bool prefer_fused(int64_t workgroups) { return 2 * workgroups >= 3 * int64_t(cu_
 // registers and writes the tile range's 3x3 partial, summed over ranges in a
 // fixed order by a second launch.
 namespace fused_dw {
-using fused::A_FLOATS;
-using fused::B_FLOATS;
 using fused::BK;  // tiles per slab
 using fused::BO;  // output channels per workgroup
 using fused::f32x2;
-using fused::ROW_A;
-using fused::ROW_B;
+// The forward kernel's stage layout with each (coord, k pair) row padded by
+// 8 floats, so consecutive rows start 8 banks apart: the dM stores (four k
+// pairs per 16 lanes) and the V stores (four pairs x two halves per 32
+// lanes) then hit distinct banks (unpadded they were 4-way conflicts).
+constexpr int ROW_A = fused::ROW_A + 8;
+constexpr int ROW_B = fused::ROW_B + 8;
+constexpr int A_FLOATS = 16 * 4 * ROW_A;
+constexpr int B_FLOATS = 16 * 4 * ROW_B;
 using mfma::f32x4;
 using mfma::i32x4;
 using mfma::kOffNone;
