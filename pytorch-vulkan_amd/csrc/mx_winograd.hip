@@ -422,10 +422,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // The fused kernel keeps one slab of loads in flight per workgroup and two
-// workgroups fit on a CU, so it needs most CUs doubly occupied to hide HBM
-// latency: measured on MI355X it wins from 1.5 workgroups per CU up (392 and
-// more at 256 CUs) and loses below (256: 155 vs 111 us, 128: 79 vs 48 us).
-bool prefer_fused(int64_t workgroups) { return 2 * workgroups >= 3 * int64_t(cu_count()); }
+// workgroups fit on a CU, so with long channel walks it needs most CUs
+// doubly occupied to hide HBM latency: measured on MI355X it wins from 1.5
+// workgroups per CU up (392 and more at 256 CUs) and loses below with 512
+// channels (256 workgroups of 64 slabs: 149 vs 123 us).  Short walks win
+// at any count (64 channels, 196 workgroups of 8 slabs: 24 vs 41 us), since
+// the unfused passes' V and M round trips then dominate.
+bool prefer_fused(int64_t workgroups, int nslab) {
+  return 2 * workgroups >= 3 * int64_t(cu_count()) || nslab <= 16;
+}
 
 }  // namespace fused
 
@@ -776,7 +781,7 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   const int64_t blocks = (T + fused::BT - 1) / fused::BT * p.n_ob;
   MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "winograd: grid too large");
   // MX_WINOGRAD_FUSED=1 / 0 forces the fused / unfused kernels (tests, tuning).
-  bool fused_path = fused::prefer_fused(blocks * G);
+  bool fused_path = fused::prefer_fused(blocks * G, p.nslab);
   if (const char* e = std::getenv("MX_WINOGRAD_FUSED"))
     if (e[0] == '0' || e[0] == '1') fused_path = e[0] == '1';
   if (!fused_path) return winograd_unfused(d, x, w, bias, y, flip, s);
