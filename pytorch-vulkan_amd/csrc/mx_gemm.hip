@@ -60,20 +60,28 @@ MX_TILE_KERNEL(C) void gemm_kernel(GemmArgs p) {
     // Column bias (nn.Linear): one value per fragment column, loaded once.
     bcol[j] = (kind == MX_BIAS_COL && ccol[j] < p.N) ? beta * bias[int64_t(ccol[j]) * p.bias_sn] : 0.f;
   }
-  for_each_acc_row<C>([&](int r, int i, int v) {
-    const int row = row0 + r;
-    if (row >= p.M) return;
-    float* __restrict__ crow = cb + int64_t(row) * p.ldc;
-    if (kind == MX_BIAS_MATRIX) {
+  // Two separate walks: stores and loads share the vector-memory counter, so
+  // a bias load between stores makes every later store wait for the earlier
+  // ones; only the matrix-bias walk (baddbmm) reads memory between stores.
+  if (kind == MX_BIAS_MATRIX) {
+    for_each_acc_row<C>([&](int r, int i, int v) {
+      const int row = row0 + r;
+      if (row >= p.M) return;
+      float* __restrict__ crow = cb + int64_t(row) * p.ldc;
       const float* __restrict__ brow = bias + int64_t(row) * p.bias_sm;
 #pragma unroll
       for (int j = 0; j < C::FN; ++j)
         if (ccol[j] < p.N) crow[ccol[j]] = alpha * acc.v[i][j][v] + beta * brow[int64_t(ccol[j]) * p.bias_sn];
-    } else {
+    });
+    return;
+  }
+  for_each_acc_row<C>([&](int r, int i, int v) {
+    const int row = row0 + r;
+    if (row >= p.M) return;
+    float* __restrict__ crow = cb + int64_t(row) * p.ldc;
 #pragma unroll
-      for (int j = 0; j < C::FN; ++j)
-        if (ccol[j] < p.N) crow[ccol[j]] = alpha * acc.v[i][j][v] + bcol[j];
-    }
+    for (int j = 0; j < C::FN; ++j)
+      if (ccol[j] < p.N) crow[ccol[j]] = alpha * acc.v[i][j][v] + bcol[j];
   });
 }
 

@@ -183,7 +183,7 @@ struct Args {
   const float* U;    // [G][16][nslab][4][Opad][2]
   const float* bias;
   float* y;          // [N][Cout][OH][OW]
-  int64_t x_bytes, u_bytes;
+  int64_t x_bytes, u_bytes, y_bytes;
   int Cin, H, W, Cout, OH, OW, ph, pw, C, O, Cpad, Opad, TH, TW, T, n_ob, nslab;
   mfma::FastDiv f_thw, f_tw;
 };
@@ -394,12 +394,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
   const int oy = int(2 * ty), ox = int(2 * tx);
   const bool right = ox + 1 < p.OW, below = oy + 1 < p.OH;
+  // All bias values before the first store: stores and loads share the
+  // vector-memory counter, so a load between stores would make each later
+  // store wait for the earlier ones.
+  float bias_v[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
+      bias_v[i][v] = (p.bias && o < p.O) ? p.bias[g * p.O + o] : 0.f;
+    }
+  // y (below 2^31 bytes: the caller splits batches) as a buffer resource:
+  // positions outside the image or channels past O store to kOffNone and are
+  // dropped, so the 32 stores need no branches.
+  const i32x4 ry = mfma::buffer_rsrc(p.y, p.y_bytes);
+  const uint32_t row_step = uint32_t(p.OW) * 4u;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
-    if (o >= p.O) continue;
     float m[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) m[q] = acc[q][i][v];
@@ -409,15 +424,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       r0[c] = m[c] + m[4 + c] + m[8 + c];
       r1[c] = m[4 + c] - m[8 + c] - m[12 + c];
     }
-    const int oc = g * p.O + o;
-    const float bb = p.bias ? p.bias[oc] : 0.f;
-    float* yo = p.y + ((int64_t(img) * p.Cout + oc) * p.OH + oy) * p.OW + ox;
-    yo[0] = r0[0] + r0[1] + r0[2] + bb;
-    if (right) yo[1] = r0[1] - r0[2] - r0[3] + bb;
-    if (below) {
-      yo[p.OW] = r1[0] + r1[1] + r1[2] + bb;
-      if (right) yo[p.OW + 1] = r1[1] - r1[2] - r1[3] + bb;
-    }
+    const float bb = bias_v[i][v];
+    const bool ok = o < p.O;
+    const uint32_t off = uint32_t(((img * uint32_t(p.Cout) + uint32_t(g * p.O + o)) * uint32_t(p.OH) + uint32_t(oy)) *
+                                      uint32_t(p.OW) + uint32_t(ox)) * 4u;
+    mfma::bstore(r0[0] + r0[1] + r0[2] + bb, ry, ok ? off : kOffNone, 0);
+    mfma::bstore(r0[1] - r0[2] - r0[3] + bb, ry, (ok && right) ? off + 4u : kOffNone, 0);
+    mfma::bstore(r1[0] + r1[1] + r1[2] + bb, ry, (ok && below) ? off + row_step : kOffNone, 0);
+    mfma::bstore(r1[1] - r1[2] - r1[3] + bb, ry, (ok && below && right) ? off + row_step + 4u : kOffNone, 0);
   }
 }
 
@@ -774,9 +788,10 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   // The caller splits batches so the input stays one buffer resource with
   // 32-bit offsets (images_per_launch).
   const int64_t x_bytes = d.n * int64_t(p.Cin) * p.H * p.W * 4;
+  const int64_t y_bytes = d.n * int64_t(p.Cout) * p.OH * p.OW * 4;
   const int64_t T = d.n * int64_t(p.TH) * p.TW;
-  MX_REQUIRE(x_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
-             "winograd: the input exceeds the 2 GiB operand bound");
+  MX_REQUIRE(x_bytes < mfma::kBufMaxBytes && y_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
+             "winograd: an operand exceeds the 2 GiB bound");
   if (T == 0) return MX_OK;
   const int64_t blocks = (T + fused::BT - 1) / fused::BT * p.n_ob;
   MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "winograd: grid too large");
@@ -794,6 +809,7 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   p.x = x;
   p.y = y;
   p.x_bytes = x_bytes;
+  p.y_bytes = y_bytes;
   p.T = int(T);
   const dim3 grid{unsigned(blocks), unsigned(G), 1u};
   if (p.C % fused::BK)
