@@ -127,6 +127,20 @@ inline FastDiv fast_div(uint32_t d) {
 }
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) { return (__umulhi(n, f.m) + n) >> f.l; }
 
+// Row (within one pass) of the 16-byte chunk thread `tid` moves for a
+// row-major stage with TPR threads per row.  With four threads per row, LDS
+// serves a 16-byte store eight lanes at a time over 32 banks: rows r and r + 1
+// at a 20-float pitch overlap in four banks, rows r and r + 4 sit 16 banks
+// apart.  Swapping bits 0 and 2 of the row index pairs rows r and r + 4 in
+// each group of eight lanes; global coalescing is unchanged (four lanes still
+// read 64 contiguous bytes of one row).
+template <int TPR>
+__device__ __forceinline__ int kvec_row(int tid) {
+  const int j = tid / TPR;
+  if constexpr (TPR == 4) return (j & ~5) | ((j & 1) << 2) | ((j >> 2) & 1);
+  return j;
+}
+
 template <class C>
 __device__ __forceinline__ void acc_zero(Acc<C>& acc) {
 #pragma unroll
@@ -390,7 +404,7 @@ struct StridedLoader<ROWS, BK, Mode::KVEC> {
     kmax = kmax_;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-      const int row = row0 + tid / TPR + p * RPP;
+      const int row = row0 + kvec_row<TPR>(tid) + p * RPP;
       ok[p] = row < R;
       ptr[p] = base + (ok[p] ? int64_t(row) * s_row : 0) + 4 * kq;
     }
@@ -407,7 +421,7 @@ struct StridedLoader<ROWS, BK, Mode::KVEC> {
     constexpr int LDK = BK + 4;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p)
-      *reinterpret_cast<f32x4*>(lds + (tid / TPR + p * RPP) * LDK + 4 * kq) = v[p];
+      *reinterpret_cast<f32x4*>(lds + (kvec_row<TPR>(tid) + p * RPP) * LDK + 4 * kq) = v[p];
   }
 };
 
@@ -571,7 +585,7 @@ struct BufStridedLoader<ROWS, BK, Mode::KVEC> {
     rs = buffer_rsrc(base, bytes);
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
-      const int row = row0 + tid / TPR + p * RPP;
+      const int row = row0 + kvec_row<TPR>(tid) + p * RPP;
       off[p] = row < R ? uint32_t(row * s_row + 4 * kq) * 4u : kOffNone;
     }
     k = k0;
@@ -588,7 +602,7 @@ struct BufStridedLoader<ROWS, BK, Mode::KVEC> {
     constexpr int LDK = BK + 4;
 #pragma unroll
     for (int p = 0; p < PASSES; ++p)
-      *reinterpret_cast<f32x4*>(lds + (tid / TPR + p * RPP) * LDK + 4 * kq) = v[p];
+      *reinterpret_cast<f32x4*>(lds + (kvec_row<TPR>(tid) + p * RPP) * LDK + 4 * kq) = v[p];
   }
 };
 
