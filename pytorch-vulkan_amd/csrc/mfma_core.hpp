@@ -279,6 +279,11 @@ __device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la0, LB& lb0, int nk, 
   la0.store(As0);
   lb0.store(Bs0);
   __syncthreads();
+  // With 16-deep slabs an odd slab count runs one more slab, of zeros (the
+  // loaders mask k >= kmax): a loop with one exit keeps the accumulators in
+  // the same registers across iterations, where an exit between the two
+  // halves made the compiler copy them every iteration.  (The 32-deep
+  // weight-gradient tile keeps the exit: without it, it spills.)
   for (int t = 0; t < nk; t += 2) {
     // Slab t (stage 0); slab t + 1 waits in set 1.
     la0.load();
@@ -287,7 +292,9 @@ __device__ __forceinline__ void mainloop(Acc<C>& acc, LA& la0, LB& lb0, int nk, 
     la1.store(As1);
     lb1.store(Bs1);
     __syncthreads();
-    if (t + 1 >= nk) break;
+    if constexpr (C::BK >= 32) {
+      if (t + 1 >= nk) break;
+    }
     // Slab t + 1 (stage 1); slab t + 2 waits in set 0.
     la1.load();
     lb1.load();
