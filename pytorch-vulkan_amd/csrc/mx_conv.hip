@@ -496,12 +496,9 @@ AxisPhase axis_phase(int a, int in, int k, int s, int pad, int dil) {
   return ph;
 }
 
-// Forward plan.  With K % 4 != 0 the weights load as scalars, for which no
-// 256-row tile is built.
+// Forward plan.
 GemmPlan plan_fwd(const ConvArgs& p) {
-  const bool scalar_w = (int64_t(p.Cin_g) * p.KK) % 4 != 0;
-  return plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G,
-                   scalar_w ? kSinglePassTiles & ~(1u << conv::TALL) : kSinglePassTiles, 512,
+  return plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G, kSinglePassTiles, 512,
                    int64_t(p.N) * p.Cout * p.OHOW);
 }
 
@@ -614,7 +611,11 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
   p.Ncols = p.N * p.OHOW;
   p.K = p.Cin_g * p.KK;
   const bool fwd_packed = p.KK > 1 && conv::blocked_channels(p.Cin_g);
-  const Mode ma = (p.K % 4 == 0 && (fwd_packed || aligned16(w))) ? Mode::KVEC : Mode::KSCALAR;
+  // Weight rows are read 16 bytes per lane: a K that is not a multiple of
+  // four, or unaligned weights, get a copy with rows padded to a multiple of
+  // four floats.
+  const bool fwd_padded = !fwd_packed && (p.K % 4 != 0 || !aligned16(w));
+  const Mode ma = Mode::KVEC;
   const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
   const GemmPlan gp = plan_fwd(p);
   p.splits = gp.splits;
@@ -622,9 +623,15 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
   p.out_elems = int64_t(p.N) * p.Cout * p.OHOW;
   Scratch wp, ws;
   p.wt = w;
-  if (p.KK > 1 && conv::blocked_channels(p.Cin_g)) {  // pack to the blocked K order
+  p.ldw = p.K;
+  if (fwd_packed) {  // pack to the blocked K order
     MX_TRY(wp.alloc(size_t(p.Cout) * p.Cin_g * p.KK * 4, s));
     MX_TRY(conv::conv_fwd_pack_weights(p, wp.as<float>(), s));
+    p.wt = wp.as<float>();
+  } else if (fwd_padded) {
+    p.ldw = (p.K + 3) / 4 * 4;
+    MX_TRY(wp.alloc(size_t(p.Cout) * p.ldw * 4, s));
+    MX_TRY(conv::conv_fwd_pad_weights(p, wp.as<float>(), s));
     p.wt = wp.as<float>();
   }
   if (gp.splits == 1) return conv::conv_fwd_launch(p, gp.tile, ma, bmode, s);

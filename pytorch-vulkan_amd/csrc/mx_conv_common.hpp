@@ -49,6 +49,7 @@ struct ConvArgs {
   // Tap th is kernel row kh0 + th*stph (tw: kernel column kw0 + tw*stpw).
   int pa, pb, Hp, Wp, HpWp, nth, ntw, offh0, offw0, dsh, dsw, kh0, kw0, stph, stpw;
   const float* wt;  // weights packed to the gathered K order: forward [g][co][k], dInput [g][k][ci]
+  int ldw;          // forward: row pitch of wt in floats (K, or K rounded up to 4 in a padded copy)
   // Split-K partials (splits > 1): forward / dInput write their tile to
   // ws + split * out_elems at the output's own offsets; dWeight writes
   // [split][G*Cout_g][Cin_g*KK] and the dBias partials to ws_db [split][Cout].
@@ -579,6 +580,7 @@ int conv_dx_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t 
 int conv_dw_launch(const ConvArgs& p, int tile, int amode, int bmode, hipStream_t s);
 int conv_dx_pack_weights(const ConvArgs& p, float* wt, hipStream_t s);
 int conv_fwd_pack_weights(const ConvArgs& p, float* wt, hipStream_t s);
+int conv_fwd_pad_weights(const ConvArgs& p, float* wt, hipStream_t s);
 int conv_dx_zero(float* dx, int64_t n, hipStream_t s);
 int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s);
 // out[i] = sum over splits of ws[split][i] (+ bias[(i / hw) % cout] when bias).

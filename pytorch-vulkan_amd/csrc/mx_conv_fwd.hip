@@ -25,7 +25,7 @@ MX_TILE_KERNEL(C) void conv_fwd_kernel(ConvArgs p) {
   const int split = blockIdx.y;
   const int k0 = split * p.kps, k1 = min(p.K, k0 + p.kps);
   BufStridedLoader<C::BM, C::BK, MA> la;
-  la.init(p.wt + int64_t(g) * p.Cout_g * p.K, int64_t(p.Cout_g) * p.K * 4, p.K, 1, row0, p.M, k0, k1);
+  la.init(p.wt + int64_t(g) * p.Cout_g * p.ldw, int64_t(p.Cout_g) * p.ldw * 4, p.ldw, 1, row0, p.M, k0, k1);
   LB lb;
   lb.init(p, col0, g, k0, k1);
   Acc<C> acc;
@@ -85,6 +85,18 @@ __global__ void conv_fwd_pack_kernel(ConvArgs p, float* wp) {
   }
 }
 
+// wp[row][k] = w[row][k] for k < K, zero for K <= k < ldw: rows of a
+// multiple of four floats, so the weight operand is read 16 bytes per lane
+// whatever K is (the 7x7 stem has K = 147).
+__global__ void conv_fwd_pad_kernel(const float* __restrict__ w, float* __restrict__ wp, uint32_t rows, uint32_t K,
+                                    uint32_t ldw) {
+  const uint32_t total = rows * ldw;
+  for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+    const uint32_t r = idx / ldw, k = idx - r * ldw;
+    wp[idx] = k < K ? w[r * K + k] : 0.f;
+  }
+}
+
 template <class C, Mode MA>
 int launch_b(ConvArgs p, int bmode, hipStream_t s) {
   p.tiles_m = (p.M + C::BM - 1) / C::BM;
@@ -106,13 +118,12 @@ int launch_b(ConvArgs p, int bmode, hipStream_t s) {
   return MX_OK;
 }
 
+// The weight operand is always read 16 bytes per lane: the host pads rows
+// whose length is not a multiple of four (conv_fwd_pad_kernel).
 template <class C>
 int launch_a(const ConvArgs& p, Mode ma, int bmode, hipStream_t s) {
-  if (ma == Mode::KVEC) return launch_b<C, Mode::KVEC>(p, bmode, s);
-  // Scalar weights (K % 4 != 0) keep a pointer per row pass: not built for
-  // 256-row tiles, which the planner does not pick for them.
-  if constexpr (C::BM <= 128) return launch_b<C, Mode::KSCALAR>(p, bmode, s);
-  return set_error(MX_ERR_INVALID, "conv2d forward: 256-row tile with scalar weight loads");
+  if (ma != Mode::KVEC || p.ldw % 4 != 0) return set_error(MX_ERR_INVALID, "conv2d forward: weight rows not padded");
+  return launch_b<C, Mode::KVEC>(p, bmode, s);
 }
 
 }  // namespace
@@ -121,6 +132,14 @@ int conv_fwd_pack_weights(const ConvArgs& p, float* wp, hipStream_t s) {
   const int64_t total = int64_t(p.Cout) * p.Cin_g * p.KK;
   hipLaunchKernelGGL(conv_fwd_pack_kernel, dim3(int(std::min<int64_t>((total + 255) / 256, 1 << 20))), dim3(256), 0,
                      s, p, wp);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+int conv_fwd_pad_weights(const ConvArgs& p, float* wp, hipStream_t s) {
+  const int64_t total = int64_t(p.Cout) * p.ldw;
+  hipLaunchKernelGGL(conv_fwd_pad_kernel, dim3(int(std::min<int64_t>((total + 255) / 256, 1 << 20))), dim3(256), 0, s,
+                     p.w, wp, uint32_t(p.Cout), uint32_t(p.K), uint32_t(p.ldw));
   MX_HIP(hipGetLastError());
   return MX_OK;
 }
