@@ -6,9 +6,9 @@
 //   C[co, pos] = Wp[co, k] x im2col(x)[k, pos] + bias[co]
 // with k the gathered K order over (ci, kh, kw) (mx_conv_common.hpp); the
 // weights are packed to it when it differs from their own [co][ci][kh][kw].
-// A is read 16 bytes per lane when K % 4 == 0; B is the im2col gather, or for
-// an unpadded 1x1 stride-1 convolution the input itself read as rows of four
-// positions.
+// A is read 16 bytes per lane (rows padded to a multiple of four floats by
+// the host when K is not); B is the im2col gather, or for an unpadded 1x1
+// stride-1 convolution the input itself read as rows of four positions.
 #include "mx_conv_common.hpp"
 
 namespace mx {
