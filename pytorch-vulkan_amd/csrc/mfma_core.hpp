@@ -652,45 +652,6 @@ struct BufStridedLoader<ROWS, BK, Mode::RVEC> {
 };
 
 template <int ROWS, int BK>
-struct BufStridedLoader<ROWS, BK, Mode::KSCALAR> {
-  static constexpr bool KMAJOR = false;
-  int kstep = BK;
-  static constexpr int RPP = kThreads / BK;
-  static constexpr int PASSES = ROWS / RPP;
-  static_assert(PASSES >= 1 && ROWS % RPP == 0, "KSCALAR tiling");
-  float v[PASSES];
-  i32x4 rs;
-  uint32_t off[PASSES], sk4;
-  int k, kmax, kk;
-  __device__ __forceinline__ void init(const float* base, int64_t bytes, int s_row, int s_k, int row0, int R, int k0,
-                                       int kmax_) {
-    const int tid = threadIdx.x;
-    kk = tid % BK;
-    rs = buffer_rsrc(base, bytes);
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int row = row0 + tid / BK + p * RPP;
-      off[p] = row < R ? uint32_t(row * s_row + kk * s_k) * 4u : kOffNone;
-    }
-    sk4 = uint32_t(s_k) * 4u;
-    k = k0;
-    kmax = kmax_;
-  }
-  __device__ __forceinline__ void load() {
-    const bool kin = k + kk < kmax;
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) v[p] = bload(rs, kin ? off[p] : kOffNone, uint32_t(k) * sk4);
-    k += kstep;
-  }
-  __device__ __forceinline__ void store(float* lds) const {
-    const int tid = threadIdx.x;
-    constexpr int LDK = BK + 4;
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) lds[(tid / BK + p * RPP) * LDK + kk] = v[p];
-  }
-};
-
-template <int ROWS, int BK>
 struct BufStridedLoader<ROWS, BK, Mode::RSCALAR> {
   static constexpr bool KMAJOR = false;
   int kstep = BK;
