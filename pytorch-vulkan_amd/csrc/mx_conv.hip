@@ -686,11 +686,20 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
   // Positions no tap reaches (a phase with K = 0) are zero: one contiguous
   // fill of dx, then the phase GEMMs overwrite the reached positions (such
   // plans never split K, so the GEMMs write dx directly).
-  bool any_zero = false;
-  for (const ConvArgs& q : phases) any_zero |= q.K == 0;
-  if (any_zero) MX_TRY(conv::conv_dx_zero(dx, out_elems, s));
+  bool any_zero = false, only_00 = true;
+  for (const ConvArgs& q : phases) {
+    any_zero |= q.K == 0;
+    if (q.K != 0 && (q.pa != 0 || q.pb != 0)) only_00 = false;
+  }
+  // Stride 2 x 2 with phase (0, 0) the only one reached and W even: the
+  // GEMM writes the zeros of each 2x2 block itself (8-byte aligned stores).
+  const bool zfill = any_zero && only_00 && p.sh == 2 && p.sw == 2 && p.W % 2 == 0 &&
+                     (reinterpret_cast<uintptr_t>(dx) & 7) == 0 && gp.splits == 1 && gp.tile != conv::TALL &&
+                     gp.tile != conv::WIDE;
+  if (any_zero && !zfill) MX_TRY(conv::conv_dx_zero(dx, out_elems, s));
   for (ConvArgs& q : phases) {
     if (q.K == 0) continue;
+    q.zfill = zfill ? 1 : 0;
     q.wt = packed ? wt.as<float>() : w;
     q.f_kblk = conv::fast_div(uint32_t(q.nth * q.ntw * conv::kChanBlock));
     q.f_tapw = conv::fast_div(uint32_t(q.ntw));

@@ -50,6 +50,10 @@ struct ConvArgs {
   int pa, pb, Hp, Wp, HpWp, nth, ntw, offh0, offw0, dsh, dsw, kh0, kw0, stph, stpw;
   const float* wt;  // weights packed to the gathered K order: forward [g][co][k], dInput [g][k][ci]
   int ldw;          // forward: row pitch of wt in floats (K, or K rounded up to 4 in a padded copy)
+  // dInput, stride 2 x 2 with only phase (0, 0) reached (a 1x1 stride-2
+  // layer): each phase output also writes the three unreached positions of
+  // its 2x2 input block as zeros (8-byte stores), in place of a separate fill.
+  int zfill;
   // Split-K partials (splits > 1): forward / dInput write their tile to
   // ws + split * out_elems at the output's own offsets; dWeight writes
   // [split][G*Cout_g][Cin_g*KK] and the dBias partials to ws_db [split][Cout].

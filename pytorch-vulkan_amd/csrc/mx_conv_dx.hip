@@ -78,6 +78,37 @@ MX_TILE_KERNEL(C) void conv_dx_kernel(ConvArgs p) {
   Acc<C> acc;
   mainloop<C>(acc, la, lb, (k1 - k0 + C::BK - 1) / C::BK, smem);
   float* const out = p.splits == 1 ? p.out : p.ws + split * p.out_elems;
+  // (Not built for the 256-wide tiles, whose registers it would spill; the
+  // host does not request it for them.)
+  if constexpr (C::BM * C::BN <= 128 * 128) if (p.zfill) {
+    // Phase (0, 0) of stride 2 x 2, W even: position (i, j) owns input rows
+    // 2i, 2i + 1 (if < H) and columns 2j, 2j + 1; one 8-byte store per row.
+    int cb[C::FN];
+    bool ok[C::FN], row2[C::FN];
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      const int pos = col0 + acc_col<C>(j);
+      ok[j] = pos < p.Ncols;
+      const int pp = ok[j] ? pos : 0;
+      const int img = pp / p.HpWp;
+      const int q = pp - img * p.HpWp;
+      const int i = q / p.Wp;
+      cb[j] = img * p.Cin * p.HW + 2 * i * p.W + 2 * (q - i * p.Wp);
+      row2[j] = 2 * i + 1 < p.H;
+    }
+    for_each_acc_row<C>([&](int r, int i, int v) {
+      const int ci = row0 + r;
+      if (ci >= p.M) return;
+      float* dst = out + int64_t(g * p.Cin_g + ci) * p.HW;
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) {
+        if (!ok[j]) continue;
+        *reinterpret_cast<float2*>(dst + cb[j]) = float2{acc.v[i][j][v], 0.f};
+        if (row2[j]) *reinterpret_cast<float2*>(dst + cb[j] + p.W) = float2{0.f, 0.f};
+      }
+    });
+    return;
+  }
   // Output offset of each fragment column (img * Cin * HW + phase position), once.
   int cbase[C::FN];
   bool cok[C::FN];

@@ -149,6 +149,10 @@ CONV_CASES = [
     # dInput stride phases: zero phases, one-to-one phase, 1/2-tap phases,
     # stride 3 with dilation 2, stride 2 with dilation 2
     ((2, 64, 16, 16), 128, (1, 1), (2, 2), (0, 0), (1, 1), 1),
+    # 1x1 stride 2: the phase GEMM zero-fills its 2x2 blocks (odd H: the last
+    # block has one row); odd W keeps the separate fill
+    ((2, 32, 15, 12), 48, (1, 1), (2, 2), (0, 0), (1, 1), 1),
+    ((1, 16, 10, 9), 16, (1, 1), (2, 2), (0, 0), (1, 1), 1),
     ((2, 64, 16, 16), 64, (3, 3), (2, 2), (1, 1), (1, 1), 1),
     ((1, 8, 20, 20), 8, (5, 5), (3, 3), (2, 2), (2, 2), 1),
     ((1, 8, 15, 15), 8, (3, 3), (2, 2), (2, 2), (2, 2), 1),
