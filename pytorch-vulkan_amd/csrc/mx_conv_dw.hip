@@ -89,18 +89,37 @@ MX_TILE_KERNEL(C) void conv_dw_kernel(ConvArgs p) {
 }
 
 // dw[i] = sum over the K splits of ws[split][i]; same for db (elements past
-// n_dw).  A workgroup takes 64 elements; wave q sums splits q, q + 4, q + 8,
-// ... in order (64 consecutive floats per load), and the four partials are
-// added in wave order, so the result is the same on every run and many
-// splits of a small dW keep four times more loads in flight than one
-// thread per element would.
+// n_dw).  A workgroup takes 64 lanes' worth of elements; wave q sums splits
+// q, q + 4, q + 8, ... in order, and the four partials are added in wave
+// order, so the result is the same on every run and many splits of a small
+// dW keep four times more loads in flight than one thread per element would.
+// The first n4 = n_dw / 4 groups of four (n4 = 0 unless the host found ws
+// and dw 16-byte aligned) are summed as 16-byte vectors, 256 elements per
+// workgroup; workgroups past them take the rest (dw's tail, then db) one
+// element per lane.
 __global__ __launch_bounds__(256) void conv_dw_finalize_kernel(const float* __restrict__ ws,
                                                                const float* __restrict__ ws_db, float* __restrict__ dw,
                                                                float* __restrict__ db, int64_t n_dw, int n_db,
-                                                               int splits) {
-  __shared__ float part[4][64];
+                                                               int splits, int64_t n4) {
+  __shared__ f32x4 part[4][64];
   const int e = threadIdx.x & 63, q = threadIdx.x >> 6;
-  const int64_t idx = int64_t(blockIdx.x) * 64 + e;
+  const int64_t vblocks = (n4 + 63) / 64;
+  if (int64_t(blockIdx.x) < vblocks) {
+    const int64_t g4 = int64_t(blockIdx.x) * 64 + e;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if (g4 < n4) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(ws) + g4;
+      const int64_t stride4 = n_dw / 4;
+#pragma unroll 4
+      for (int sp = q; sp < splits; sp += 4) s += src[sp * stride4];
+    }
+    part[q][e] = s;
+    __syncthreads();
+    if (q == 0 && g4 < n4)
+      reinterpret_cast<f32x4*>(dw)[g4] = ((part[0][e] + part[1][e]) + part[2][e]) + part[3][e];
+    return;
+  }
+  const int64_t idx = 4 * n4 + (int64_t(blockIdx.x) - vblocks) * 64 + e;
   float s = 0.f;
   if (idx < n_dw) {
     const float* src = ws + idx;
@@ -111,10 +130,10 @@ __global__ __launch_bounds__(256) void conv_dw_finalize_kernel(const float* __re
 #pragma unroll 4
     for (int sp = q; sp < splits; sp += 4) s += src[sp * int64_t(n_db)];
   }
-  part[q][e] = s;
+  part[q][e][0] = s;
   __syncthreads();
   if (q == 0) {
-    const float v = ((part[0][e] + part[1][e]) + part[2][e]) + part[3][e];
+    const float v = ((part[0][e][0] + part[1][e][0]) + part[2][e][0]) + part[3][e][0];
     if (idx < n_dw) dw[idx] = v;
     else if (idx < n_dw + n_db) db[idx - n_dw] = v;
   }
@@ -221,24 +240,29 @@ int conv_sum_splits(const float* ws, int splits, int64_t n, float* out, const fl
   return MX_OK;
 }
 
-int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s) {
-  const int64_t n_dw = int64_t(p.G) * p.Cout_g * p.Ncols;
-  const int n_db = db ? p.Cout : 0;
-  const int64_t blocks = (n_dw + n_db + 63) / 64;
+namespace {
+// Finalize launch: vector groups when ws and out are 16-byte aligned and the
+// partial planes stay so (n % 4 == 0), scalar elements for the rest.
+int launch_finalize(const float* ws, const float* ws_db, float* out, float* db, int64_t n, int n_db, int splits,
+                    hipStream_t s) {
+  const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  const int64_t n4 = vec ? n / 4 : 0;
+  const int64_t blocks = (n4 + 63) / 64 + (n - 4 * n4 + n_db + 63) / 64;
   MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "conv2d dweight: finalize grid too large");
-  hipLaunchKernelGGL(conv_dw_finalize_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, p.ws, p.ws_db, dw, db, n_dw,
-                     n_db, p.splits);
+  hipLaunchKernelGGL(conv_dw_finalize_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, ws, ws_db, out, db, n, n_db,
+                     splits, n4);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }
+}  // namespace
+
+int conv_dw_finalize(const ConvArgs& p, float* dw, float* db, hipStream_t s) {
+  return launch_finalize(p.ws, p.ws_db, dw, db, int64_t(p.G) * p.Cout_g * p.Ncols, db ? p.Cout : 0, p.splits, s);
+}
 
 int sum_partials(const float* ws, int splits, int64_t n, float* out, hipStream_t s) {
-  const int64_t blocks = (n + 63) / 64;
-  MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "conv2d dweight: finalize grid too large");
-  hipLaunchKernelGGL(conv_dw_finalize_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, ws, nullptr, out, nullptr, n,
-                     0, splits);
-  MX_HIP(hipGetLastError());
-  return MX_OK;
+  return launch_finalize(ws, nullptr, out, nullptr, n, 0, splits, s);
 }
 
 }  // namespace conv
