@@ -697,10 +697,28 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
                      (reinterpret_cast<uintptr_t>(dx) & 7) == 0 && gp.splits == 1 && gp.tile != conv::TALL &&
                      gp.tile != conv::WIDE;
   if (any_zero && !zfill) MX_TRY(conv::conv_dx_zero(dx, out_elems, s));
+  // Pack every reached phase's weights up front, each at its own offset
+  // (the phases partition the taps, so they fit the weights' size), in
+  // launches of up to kMaxPackPhases phases.
+  if (packed) {
+    conv::DxPackSet set{};
+    uint32_t off = 0;
+    for (ConvArgs& q : phases) {
+      if (q.K == 0) continue;
+      set.ph[set.n++] = conv::DxPackPhase{q.K, q.nth, q.ntw, q.kh0, q.kw0, q.stph, q.stpw, off};
+      q.wt = wt.as<float>() + off;
+      off += uint32_t(p.G) * uint32_t(q.K) * uint32_t(p.Cin_g);
+      if (set.n == conv::kMaxPackPhases) {
+        MX_TRY(conv::conv_dx_pack_weights(p, set, wt.as<float>(), s));
+        set.n = 0;
+      }
+    }
+    if (set.n > 0) MX_TRY(conv::conv_dx_pack_weights(p, set, wt.as<float>(), s));
+  }
   for (ConvArgs& q : phases) {
     if (q.K == 0) continue;
     q.zfill = zfill ? 1 : 0;
-    q.wt = packed ? wt.as<float>() : w;
+    if (!packed) q.wt = w;
     q.f_kblk = conv::fast_div(uint32_t(q.nth * q.ntw * conv::kChanBlock));
     q.f_tapw = conv::fast_div(uint32_t(q.ntw));
     q.f_kk = conv::fast_div(uint32_t(q.nth * q.ntw));
@@ -708,7 +726,6 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
     q.kps = int((q.K + gp.splits - 1) / gp.splits + kSplitBK - 1) / kSplitBK * kSplitBK;
     q.ws = ws.as<float>();
     q.out_elems = out_elems;
-    if (packed) MX_TRY(conv::conv_dx_pack_weights(q, wt.as<float>(), s));
     const bool one_to_one = q.nth == 1 && q.ntw == 1 && q.offh0 == 0 && q.offw0 == 0 && q.Hp == p.OH &&
                             q.Wp == p.OW && p.OHOW % 4 == 0 && aligned16(dy);
     MX_TRY(conv::conv_dx_launch(q, gp.tile, vec_a ? Mode::RVEC : Mode::RSCALAR,

@@ -582,7 +582,17 @@ enum BMode : int { B_GATHER = 0, B_VEC = 1 };
 int conv_fwd_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t s);
 int conv_dx_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t s);
 int conv_dw_launch(const ConvArgs& p, int tile, int amode, int bmode, hipStream_t s);
-int conv_dx_pack_weights(const ConvArgs& p, float* wt, hipStream_t s);
+// Weight packing of several dInput stride phases in one launch.
+constexpr int kMaxPackPhases = 16;
+struct DxPackPhase {
+  int K, nth, ntw, kh0, kw0, stph, stpw;
+  uint32_t off;  // floats from the packed buffer's start
+};
+struct DxPackSet {
+  int n;
+  DxPackPhase ph[kMaxPackPhases];
+};
+int conv_dx_pack_weights(const ConvArgs& p, const DxPackSet& set, float* wt, hipStream_t s);
 int conv_fwd_pack_weights(const ConvArgs& p, float* wt, hipStream_t s);
 int conv_fwd_pad_weights(const ConvArgs& p, float* wt, hipStream_t s);
 int conv_dx_zero(float* dx, int64_t n, hipStream_t s);

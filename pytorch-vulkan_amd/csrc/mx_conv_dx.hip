@@ -20,18 +20,22 @@ namespace conv {
 namespace {
 
 // Wt_p[g][k][ci] = w[g*Cout_g + co][ci][kh0 + th*stph][kw0 + tw*stpw] with k
-// the gathered K order over (co, th, tw): the A operand of the phase GEMM,
-// ci contiguous.  32-bit indices: the packed weights are below 2^31 bytes.
-__global__ void conv_dx_pack_kernel(ConvArgs p, float* wt) {
-  const uint32_t nt = p.nth * p.ntw;
-  const uint32_t total = uint32_t(p.G) * p.K * p.Cin_g;
+// the gathered K order over (co, th, tw): the A operand of phase p's GEMM,
+// ci contiguous, at wt + set.ph[p].off.  One launch packs up to
+// kMaxPackPhases phases (blockIdx.y = phase).  32-bit indices: the packed
+// weights are below 2^31 bytes.
+__global__ void conv_dx_pack_kernel(ConvArgs p, DxPackSet set, float* wt) {
+  const DxPackPhase ph = set.ph[blockIdx.y];
+  const uint32_t nt = ph.nth * ph.ntw;
+  const uint32_t total = uint32_t(p.G) * ph.K * p.Cin_g;
   const bool blocked = blocked_channels(p.Cout_g);
   const uint32_t kblk = nt * kChanBlock;
+  float* const dst = wt + ph.off;
   for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
     const uint32_t rest = idx / uint32_t(p.Cin_g);
     const uint32_t ci = idx - rest * uint32_t(p.Cin_g);
-    const uint32_t g = rest / uint32_t(p.K);
-    const uint32_t k = rest - g * uint32_t(p.K);
+    const uint32_t g = rest / uint32_t(ph.K);
+    const uint32_t k = rest - g * uint32_t(ph.K);
     uint32_t co, t;
     if (blocked) {
       const uint32_t cb = k / kblk, rem = k - cb * kblk;
@@ -41,9 +45,9 @@ __global__ void conv_dx_pack_kernel(ConvArgs p, float* wt) {
       co = k / nt;
       t = k - co * nt;
     }
-    const uint32_t th = t / uint32_t(p.ntw), tw = t - th * uint32_t(p.ntw);
-    const int kh = p.kh0 + int(th) * p.stph, kw = p.kw0 + int(tw) * p.stpw;
-    wt[idx] = p.w[((int64_t(g * p.Cout_g + co) * p.Cin_g + ci) * p.KH + kh) * p.KW + kw];
+    const uint32_t th = t / uint32_t(ph.ntw), tw = t - th * uint32_t(ph.ntw);
+    const int kh = ph.kh0 + int(th) * ph.stph, kw = ph.kw0 + int(tw) * ph.stpw;
+    dst[idx] = p.w[((int64_t(g * p.Cout_g + co) * p.Cin_g + ci) * p.KH + kh) * p.KW + kw];
   }
 }
 
@@ -157,9 +161,10 @@ int grid_for(int64_t total) { return int(std::min<int64_t>((total + 255) / 256, 
 
 }  // namespace
 
-int conv_dx_pack_weights(const ConvArgs& p, float* wt, hipStream_t s) {
-  const int64_t total = int64_t(p.G) * p.Cout_g * p.nth * p.ntw * p.Cin_g;
-  hipLaunchKernelGGL(conv_dx_pack_kernel, dim3(grid_for(total)), dim3(256), 0, s, p, wt);
+int conv_dx_pack_weights(const ConvArgs& p, const DxPackSet& set, float* wt, hipStream_t s) {
+  int64_t most = 0;
+  for (int i = 0; i < set.n; ++i) most = std::max<int64_t>(most, int64_t(p.G) * set.ph[i].K * p.Cin_g);
+  hipLaunchKernelGGL(conv_dx_pack_kernel, dim3(grid_for(most), set.n), dim3(256), 0, s, p, set, wt);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }
