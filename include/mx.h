@@ -220,6 +220,30 @@ int mx_conv2d_backward_bias(const mx_conv2d_desc* desc, const float* dy, float* 
 int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t* span,
                            int64_t* workspace_bytes);
 
+/* Plan of one conv call with these arguments (no data is read; operands are
+ * taken to be contiguous and 256-byte aligned, as tensors from the device
+ * allocator are).  The reference's planner exposes the same facts through
+ * its dispatch counters and autotune plan cache (selected tile, split count,
+ * split span, workspace bytes: csrc/ops/convolution.cpp:204-247, :523-639;
+ * tests/test_conv_dispatch.py:255-297). */
+typedef struct mx_conv2d_plan_info {
+  int algo;                /* algorithm that runs (never AUTO) */
+  int tile;                /* implicit-GEMM tile (index of the tile menu), -1 for other algorithms */
+  int64_t splits;          /* K splits of the implicit GEMM (1: none) */
+  int64_t span;            /* K per split */
+  int64_t workspace_bytes; /* scratch counted against the workspace budget */
+  char variant[256];       /* kernel instantiations launched, space separated */
+} mx_conv2d_plan_info;
+
+/* `with_bias` != 0 plans a dWeight call that also writes dBias.
+ * Workspace budget: TORCH_VULKAN_CONV_WORKSPACE_MB (integer MiB in [0, 4096],
+ * default 64; csrc/ops/convolution.cpp:239-247) caps the split-K partials,
+ * the Winograd weight gradient's range partials and the unfused Winograd
+ * transforms of every conv call; plans shrink to fit, 0 means no such
+ * scratch at all, and a split forced through MX_CONV_PLAN that does not fit
+ * fails with MX_ERR_WORKSPACE. */
+int mx_conv2d_plan(const mx_conv2d_desc* desc, int phase, int algo, int with_bias, mx_conv2d_plan_info* info);
+
 /* Name of the main kernel a conv call with these arguments launches, e.g.
  * "conv_dw_kernel<64x64x32>": matches the kernel-trace names of a profiler and
  * keys per-kernel timing (the reference's gpu_timing_stats() per shader,
@@ -254,6 +278,12 @@ typedef struct mx_gemm_desc {
 int mx_gemm_f32(const mx_gemm_desc* desc, const float* a, const float* b, const float* bias,
                 float* c, void* stream);
 
+/* Kernel instantiation mx_gemm_f32 launches for these arguments (tile,
+ * operand loader modes, epilogue), e.g. "gemm_kernel<256x128x16,KVEC,RVEC>+bias_col";
+ * a and b are only inspected for alignment.  The counterpart of the
+ * reference's kernel choice in mm_impl (csrc/ops/mm.cpp:302-307). */
+int mx_gemm_variant(const mx_gemm_desc* desc, const float* a, const float* b, char* buf, size_t len);
+
 /* ------------------------------------------------------------------------ */
 /* Multi-tensor fused AdamW                                                   */
 /* ------------------------------------------------------------------------ */
@@ -263,7 +293,7 @@ int mx_gemm_f32(const mx_gemm_desc* desc, const float* a, const float* b, const 
  * already incremented, as aten::_fused_adamw_'s state_steps) is used. */
 typedef struct mx_adamw_tensor {
   float* param;
-  const float* grad;
+  float* grad;           /* read; written back unscaled when hparams.grad_scale is set */
   float* exp_avg;
   float* exp_avg_sq;
   float* max_exp_avg_sq; /* AMSGrad only, else NULL */
@@ -277,7 +307,8 @@ typedef struct mx_adamw_hparams {
   int amsgrad;
   int maximize;
   const float* lr_dev;      /* optional device scalar lr (_fused_adamw_.tensor_lr) */
-  const float* grad_scale;  /* optional device scalar: grads are divided by it */
+  const float* grad_scale;  /* optional device scalar: grads are divided by it and the unscaled
+                            * grads written back (torch's fused AdamW under GradScaler) */
   const float* found_inf;   /* optional device scalar: when != 0 the step is skipped */
 } mx_adamw_hparams;
 

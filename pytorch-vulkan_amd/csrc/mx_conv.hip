@@ -398,31 +398,40 @@ struct GemmPlan {
 };
 
 // Cheapest (tile, K split) over the allowed tiles (bit mask over conv::Tile)
-// and split counts up to max_splits.  MX_CONV_PLAN="tile,splits" (tile index
-// in conv::Tile order, splits from the candidate list) restricts the choice,
-// for tuning and diagnosis; a combination this shape cannot use is ignored.
-GemmPlan plan_gemm(int64_t M, int64_t Ncols, int64_t K, int64_t G, unsigned tiles, int64_t max_splits,
-                   int64_t out_elems) {
+// and split counts up to max_splits.  A split plan needs `ws_per_split` bytes
+// of partial outputs per split, all within the workspace budget `ws_limit`.
+// MX_CONV_PLAN="tile,splits" (tile index in conv::Tile order) forces the tile
+// when this phase and shape can use it, with the largest split count up to
+// `splits` that the shape and the budget allow (for tests, tuning and
+// diagnosis); a forced split for which the budget holds no split at all is an
+// error, as a forced algorithm beyond the budget is in
+// csrc/ops/convolution.cpp:472-473.
+int plan_gemm(int64_t M, int64_t Ncols, int64_t K, int64_t G, unsigned tiles, int64_t max_splits,
+              int64_t out_elems, int64_t ws_per_split, int64_t ws_limit, GemmPlan* out) {
   int force_tile = -1, force_splits = 0;
   if (const char* e = std::getenv("MX_CONV_PLAN")) {
-    if (std::sscanf(e, "%d,%d", &force_tile, &force_splits) != 2) force_tile = -1;
+    if (std::sscanf(e, "%d,%d", &force_tile, &force_splits) != 2 || force_tile < 0 || force_tile >= conv::NTILES ||
+        !(tiles & (1u << force_tile)) || force_splits < 1)
+      force_tile = -1;
   }
   GemmPlan best;
   double best_t = -1;
+  bool budget_stop = false;
   static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128, 192, 256, 384, 512};
-  for (int pass = force_tile >= 0 ? 0 : 1; pass < 2 && best_t < 0; ++pass)
   for (int t = 0; t < conv::NTILES; ++t) {
-    if (!(tiles & (1u << t))) continue;
-    if (pass == 0 && t != force_tile) continue;
+    if (!(tiles & (1u << t)) || (force_tile >= 0 && t != force_tile)) continue;
     for (int want : kSplits) {
-      if (want > max_splits) break;
-      if (pass == 0 && want != force_splits) continue;
+      if (want > max_splits || (force_tile >= 0 && want > force_splits)) break;
       int64_t kps = (K + want - 1) / want;
       kps = (kps + kSplitBK - 1) / kSplitBK * kSplitBK;
       const int64_t splits = (K + kps - 1) / kps;
       if (splits > 1 && kps < kMinSplitSpan) break;
+      if (splits > 1 && splits * ws_per_split > ws_limit) {
+        budget_stop = true;
+        break;
+      }
       const double cost = plan_cost(kTileInfo[t], M, Ncols, G, splits, kps, out_elems);
-      if (best_t < 0 || cost < best_t) {
+      if (force_tile >= 0 || best_t < 0 || cost < best_t) {  // forced: the largest split that fits
         best_t = cost;
         best.tile = t;
         best.splits = int(splits);
@@ -430,7 +439,11 @@ GemmPlan plan_gemm(int64_t M, int64_t Ncols, int64_t K, int64_t G, unsigned tile
       }
     }
   }
-  return best;
+  if (force_tile >= 0 && budget_stop && best.splits == 1)
+    return set_error(MX_ERR_WORKSPACE, cat("Forced convolution plan ", force_tile, ",", force_splits,
+                                           " exceeds the workspace budget (TORCH_VULKAN_CONV_WORKSPACE_MB)"));
+  *out = best;
+  return MX_OK;
 }
 
 constexpr unsigned kAllTiles = (1u << conv::NTILES) - 1;
@@ -438,36 +451,62 @@ constexpr unsigned kSinglePassTiles = kAllTiles & ~(1u << conv::NARROW);  // for
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
+// Stand-in operand address for plans made without data (the variant and
+// plan queries): device allocations are at least 256-byte aligned.
+const float* kAlignedNull = reinterpret_cast<const float*>(uintptr_t(256));
+float* const kAlignedOut = reinterpret_cast<float*>(uintptr_t(256));
+
 bool unpadded_1x1(const ConvArgs& p) {
   return p.KH == 1 && p.KW == 1 && p.sh == 1 && p.sw == 1 && p.ph == 0 && p.pw == 0;
 }
 
-struct DwPlan {
-  GemmPlan g;
-  int64_t ws_bytes = 0;
-  int64_t db_bytes = 0;
+// ----------------------------------------------------------------- forward
+struct FwdPlan {
+  ConvArgs p{};
+  GemmPlan gp;
+  bool packed = false;  // weights copied to the channel-blocked K order
+  bool padded = false;  // weights copied to rows padded to a multiple of four floats
+  int bmode = conv::B_GATHER;
+  int64_t w_bytes = 0, ws_bytes = 0;
 };
 
-// dWeight: K = N*OH*OW positions, split so every CU gets work; each split
-// writes one full-size partial dW that the finalize re-reads.
-// `x_gather`: the x operand is the column gather (any kernel but an unpadded
-// 1x1 stride-1 one with 4-aligned planes); `dy_gather`: dy is read as scalar
-// rows (OH*OW % 4 != 0).  Gathers over 256 columns (and a 256-wide tile with
-// both gathers) are not built.
-DwPlan plan_dw(const ConvArgs& p, bool with_db, bool x_gather, bool dy_gather) {
-  DwPlan pl;
-  const int64_t out = int64_t(p.G) * p.Cout_g * p.Ncols;
-  unsigned tiles = kAllTiles;
-  if (x_gather) tiles &= ~((1u << conv::WIDE) | (1u << conv::FLAT));
-  if (x_gather && dy_gather) tiles &= ~(1u << conv::TALL);
-  pl.g = plan_gemm(p.M, p.Ncols, p.K, p.G, tiles, 65535, out);
-  if (pl.g.splits > 1) {
-    pl.ws_bytes = int64_t(pl.g.splits) * out * 4;
-    pl.db_bytes = with_db ? int64_t(pl.g.splits) * p.Cout * 4 : 0;
-  }
-  return pl;
+int plan_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+                 int64_t ws_limit, FwdPlan* f) {
+  ConvArgs& p = f->p;
+  p = make_args(d);
+  p.x = x;
+  p.w = w;
+  p.wt = w;
+  p.bias = bias;
+  p.out = y;
+  p.M = p.Cout_g;
+  p.Ncols = p.N * p.OHOW;
+  p.K = p.Cin_g * p.KK;
+  f->packed = p.KK > 1 && conv::blocked_channels(p.Cin_g);
+  // Weight rows are read 16 bytes per lane: a K that is not a multiple of
+  // four, or unaligned weights, get a copy with rows padded to a multiple of
+  // four floats.
+  f->padded = !f->packed && (p.K % 4 != 0 || !aligned16(w));
+  f->bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
+  p.out_elems = int64_t(p.N) * p.Cout * p.OHOW;
+  MX_TRY(plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G, kSinglePassTiles, 512,
+                   p.out_elems, p.out_elems * 4, ws_limit, &f->gp));
+  p.splits = f->gp.splits;
+  p.kps = f->gp.kps;
+  p.ldw = f->padded ? (p.K + 3) / 4 * 4 : p.K;
+  f->w_bytes = f->packed ? int64_t(p.Cout) * p.Cin_g * p.KK * 4 : f->padded ? int64_t(p.Cout) * p.ldw * 4 : 0;
+  f->ws_bytes = f->gp.splits > 1 ? int64_t(f->gp.splits) * p.out_elems * 4 : 0;
+  return MX_OK;
 }
 
+std::string fwd_variant(const FwdPlan& f) {
+  const char* b = f.bmode == conv::B_VEC ? "PosQuad"
+                  : conv::blocked_channels(f.p.Cin_g) ? "Im2col<blocked>" : "Im2col";
+  return cat("conv_fwd_kernel<", tile_name(f.gp.tile, MX_CONV_FORWARD), ",KVEC,", b, ">",
+             f.gp.splits > 1 ? "+split" : "");
+}
+
+// ----------------------------------------------------------------- dInput
 // dInput stride phases.  Along one axis, phase a (input index = a mod s) is
 // reached by the taps k with (a + pad - k*dil) % s == 0: k = k0 + t*step with
 // step = s / gcd(s, dil); tap t reads output index i + off0 - t*(dil / gcd).
@@ -496,17 +535,26 @@ AxisPhase axis_phase(int a, int in, int k, int s, int pad, int dil) {
   return ph;
 }
 
-// Forward plan.
-GemmPlan plan_fwd(const ConvArgs& p) {
-  return plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G, kSinglePassTiles, 512,
-                   int64_t(p.N) * p.Cout * p.OHOW);
-}
+struct DxPlan {
+  ConvArgs p{};
+  std::vector<ConvArgs> phases;  // every phase with input positions (K == 0: no tap reaches it)
+  std::vector<int> bmodes;       // per phase: B_VEC for a one-to-one phase read 16 bytes per lane
+  GemmPlan gp;
+  bool packed = false, vec_a = false, any_zero = false, zfill = false;
+  int64_t out_elems = 0, w_bytes = 0, ws_bytes = 0;
+};
 
-// dInput stride phases of `p` (GEMM fields filled in) and one plan for all of
-// them, made on the phase with the most work.  Split-K only when every phase
-// has taps, so every partial output element is written by some phase.
-GemmPlan plan_dx(const ConvArgs& p, std::vector<ConvArgs>* phases) {
-  bool any_zero = false;
+// One GEMM per stride phase over exactly the taps that reach it, one
+// (tile, split) plan for all of them made on the phase with the most work.
+// Split-K only when every phase has taps, so every partial output element is
+// written by some phase.
+int plan_dinput(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, int64_t ws_limit, DxPlan* f) {
+  ConvArgs& p = f->p;
+  p = make_args(d);
+  p.dy = dy;
+  p.w = w;
+  p.wt = w;
+  p.out = dx;
   int64_t best_work = -1, bm = 0, bn = 0, bk = 0;
   for (int a = 0; a < p.sh; ++a) {
     const AxisPhase ah = axis_phase(a, p.H, p.KH, p.sh, p.ph, p.dh);
@@ -532,7 +580,7 @@ GemmPlan plan_dx(const ConvArgs& p, std::vector<ConvArgs>* phases) {
       q.M = p.Cin_g;
       q.Ncols = p.N * q.HpWp;
       q.K = p.Cout_g * q.nth * q.ntw;
-      if (q.K == 0) any_zero = true;
+      if (q.K == 0) f->any_zero = true;
       const int64_t work = int64_t(q.K) * q.Ncols;
       if (work > best_work) {
         best_work = work;
@@ -540,24 +588,209 @@ GemmPlan plan_dx(const ConvArgs& p, std::vector<ConvArgs>* phases) {
         bn = q.Ncols;
         bk = q.K;
       }
-      if (phases) phases->push_back(q);
+      f->phases.push_back(q);
     }
   }
-  return plan_gemm(bm, bn, std::max<int64_t>(bk, 1), p.G, kSinglePassTiles, any_zero ? 1 : 512,
-                   int64_t(p.N) * p.Cin * p.HW);
+  f->out_elems = int64_t(p.N) * p.Cin * p.HW;
+  MX_TRY(plan_gemm(bm, bn, std::max<int64_t>(bk, 1), p.G, kSinglePassTiles, f->any_zero ? 1 : 512, f->out_elems,
+                   f->out_elems * 4, ws_limit, &f->gp));
+  // A 1x1 kernel is already [g][co][ci]; larger kernels are packed per phase.
+  f->packed = p.KK > 1;
+  f->vec_a = p.Cin_g % 4 == 0 && (f->packed || aligned16(w));
+  bool only_00 = true;
+  for (const ConvArgs& q : f->phases)
+    if (q.K != 0 && (q.pa != 0 || q.pb != 0)) only_00 = false;
+  // Stride 2 x 2 with phase (0, 0) the only one reached and W even: the
+  // GEMM writes the zeros of each 2x2 block itself (8-byte aligned stores).
+  f->zfill = f->any_zero && only_00 && p.sh == 2 && p.sw == 2 && p.W % 2 == 0 &&
+             (reinterpret_cast<uintptr_t>(dx) & 7) == 0 && f->gp.splits == 1 && f->gp.tile != conv::TALL &&
+             f->gp.tile != conv::WIDE;
+  for (ConvArgs& q : f->phases) {
+    const bool one_to_one = q.nth == 1 && q.ntw == 1 && q.offh0 == 0 && q.offw0 == 0 && q.Hp == p.OH &&
+                            q.Wp == p.OW && p.OHOW % 4 == 0 && aligned16(dy);
+    f->bmodes.push_back(one_to_one ? conv::B_VEC : conv::B_GATHER);
+    if (q.K == 0) continue;
+    q.zfill = f->zfill ? 1 : 0;
+    q.f_kblk = conv::fast_div(uint32_t(q.nth * q.ntw * conv::kChanBlock));
+    q.f_tapw = conv::fast_div(uint32_t(q.ntw));
+    q.f_kk = conv::fast_div(uint32_t(q.nth * q.ntw));
+    q.splits = f->gp.splits;
+    q.kps = int((q.K + f->gp.splits - 1) / f->gp.splits + kSplitBK - 1) / kSplitBK * kSplitBK;
+    q.out_elems = f->out_elems;
+  }
+  f->w_bytes = f->packed ? int64_t(p.Cout) * p.Cin_g * p.KK * 4 : 0;
+  f->ws_bytes = f->gp.splits > 1 ? int64_t(f->gp.splits) * f->out_elems * 4 : 0;
+  return MX_OK;
+}
+
+std::string dx_variant(const DxPlan& f) {
+  std::vector<std::string> names;
+  for (size_t i = 0; i < f.phases.size(); ++i) {
+    const ConvArgs& q = f.phases[i];
+    if (q.K == 0) continue;
+    const char* b = f.bmodes[i] == conv::B_VEC ? "PosQuad"
+                    : conv::blocked_channels(q.Cout_g) ? "PhaseGather<blocked>" : "PhaseGather";
+    std::string n = cat("conv_dx_kernel<", tile_name(f.gp.tile, MX_CONV_DINPUT), ",", f.vec_a ? "RVEC" : "RSCALAR",
+                        ",", b, ">", f.gp.splits > 1 ? "+split" : "", f.zfill ? "+zfill" : "");
+    if (std::find(names.begin(), names.end(), n) == names.end()) names.push_back(n);
+  }
+  std::string out;
+  for (const std::string& n : names) out += (out.empty() ? "" : " ") + n;
+  return out.empty() ? "conv_dx_zero_kernel" : out;
+}
+
+// ----------------------------------------------------------------- dWeight
+struct DwPlan {
+  ConvArgs p{};
+  GemmPlan gp;
+  int amode = conv::B_GATHER, bmode = conv::B_GATHER;
+  bool with_db = false;
+  int64_t ws_bytes = 0, db_bytes = 0;
+};
+
+// dWeight: K = N*OH*OW positions, split so every CU gets work; each split
+// writes one full-size partial dW (and a dBias partial) that the finalize
+// re-reads.  The x operand is the column gather unless the kernel is an
+// unpadded 1x1 stride-1 one with 4-aligned planes; dy is read as scalar rows
+// when OH*OW % 4 != 0.  Gathers over 256 columns (and a 256-wide tile with
+// both gathers) are not built.
+int plan_dweight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, float* db, int64_t ws_limit,
+                 DwPlan* f) {
+  ConvArgs& p = f->p;
+  p = make_args(d);
+  p.x = x;
+  p.dy = dy;
+  p.out = dw;
+  p.db = db;
+  const bool with_db = db != nullptr;
+  p.M = p.Cout_g;
+  p.Ncols = p.Cin_g * p.KK;
+  p.K = p.N * p.OHOW;
+  f->with_db = with_db;
+  f->amode = (p.OHOW % 4 == 0 && aligned16(dy)) ? conv::B_VEC : conv::B_GATHER;
+  f->bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
+  p.cols_blocked = f->bmode == conv::B_GATHER && conv::blocked_channels(p.Cin_g) ? 1 : 0;
+  const int64_t out = int64_t(p.G) * p.Cout_g * p.Ncols;
+  unsigned tiles = kAllTiles;
+  if (f->bmode == conv::B_GATHER) tiles &= ~((1u << conv::WIDE) | (1u << conv::FLAT));
+  if (f->bmode == conv::B_GATHER && f->amode == conv::B_GATHER) tiles &= ~(1u << conv::TALL);
+  const int64_t per_split = out * 4 + (with_db ? int64_t(p.Cout) * 4 : 0);
+  MX_TRY(plan_gemm(p.M, p.Ncols, p.K, p.G, tiles, 65535, out, per_split, ws_limit, &f->gp));
+  p.splits = f->gp.splits;
+  p.kps = f->gp.kps;
+  if (f->gp.splits > 1) {
+    f->ws_bytes = int64_t(f->gp.splits) * out * 4;
+    f->db_bytes = with_db ? int64_t(f->gp.splits) * p.Cout * 4 : 0;
+  }
+  return MX_OK;
+}
+
+std::string dw_variant(const DwPlan& f) {
+  const char* a = f.amode == conv::B_VEC ? "PosK" : "DyRows";
+  const char* b = f.bmode == conv::B_VEC ? "PosK" : f.p.cols_blocked ? "XCols<blocked>" : "XCols";
+  return cat("conv_dw_kernel<", kTileInfo[f.gp.tile].name, ",", a, ",", b, ">", f.gp.splits > 1 ? "+split" : "",
+             f.with_db ? "+db" : "");
 }
 
 }  // namespace
 
-// Winograd forward lives in mx_winograd.hip.
+// Winograd lives in mx_winograd.hip.
 int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
-                     hipStream_t s);
-int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, hipStream_t s);
-int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, hipStream_t s);
+                     int64_t ws_limit, hipStream_t s);
+int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, int64_t ws_limit,
+                            hipStream_t s);
+int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, int64_t ws_limit,
+                             hipStream_t s);
+int winograd_describe(const mx_conv2d_desc& d, int phase, int64_t ws_limit, std::string* variant, int64_t* ws_bytes);
+
+namespace conv {
+// Scratch budget of one convolution call (split-K partials, the Winograd
+// weight gradient's range partials, the unfused Winograd transforms):
+// TORCH_VULKAN_CONV_WORKSPACE_MB, an integer number of MiB in [0, 4096],
+// 64 when unset (csrc/ops/convolution.cpp:239-247).  Weight-sized copies
+// (packed or transformed filters) are not counted.
+int workspace_limit(int64_t* bytes) {
+  const char* v = std::getenv("TORCH_VULKAN_CONV_WORKSPACE_MB");
+  if (!v || !*v) {
+    *bytes = int64_t(64) << 20;
+    return MX_OK;
+  }
+  char* end = nullptr;
+  const unsigned long long mb = std::strtoull(v, &end, 10);
+  MX_REQUIRE(*v != '-' && end != v && *end == '\0' && mb <= 4096, MX_ERR_INVALID,
+             "TORCH_VULKAN_CONV_WORKSPACE_MB must be an integer in [0,4096]");
+  *bytes = int64_t(mb) << 20;
+  return MX_OK;
+}
+}  // namespace conv
 
 }  // namespace mx
 
 using namespace mx;
+
+namespace {
+
+// Plan of one call of `phase` (no data touched): the algorithm that runs, the
+// implicit GEMM's tile and K split, the scratch counted against the workspace
+// budget and the kernel instantiations launched.
+int describe(const mx_conv2d_desc* desc, int phase, int algo, int with_bias, mx_conv2d_plan_info* info) {
+  mx_conv2d_desc d = *desc;
+  MX_TRY(checked_desc(&d));
+  int chosen = 0;
+  MX_TRY(select_algo(d, phase, algo, &chosen));
+  int64_t limit = 0;
+  MX_TRY(conv::workspace_limit(&limit));
+  mx_conv2d_plan_info r{};
+  r.algo = chosen;
+  r.tile = -1;
+  r.splits = 1;
+  std::string name;
+  if (phase == MX_CONV_DBIAS) {
+    name = chosen == MX_CONV_ALGO_DIRECT ? "conv_db_direct_kernel" : "conv_db_reduce_kernel";
+  } else if (chosen == MX_CONV_ALGO_WINOGRAD) {
+    MX_TRY(winograd_describe(d, phase, limit, &name, &r.workspace_bytes));
+    if (phase == MX_CONV_DWEIGHT && with_bias) name += " conv_db_reduce_kernel";
+  } else if (chosen == MX_CONV_ALGO_DIRECT) {
+    name = phase == MX_CONV_FORWARD  ? "conv_fwd_direct_kernel"
+           : phase == MX_CONV_DINPUT ? "conv_dx_direct_kernel"
+                                     : "conv_dw_direct_kernel";
+    if (phase == MX_CONV_DWEIGHT && with_bias) name += " conv_db_reduce_kernel";
+  } else if (chosen == MX_CONV_ALGO_REDUCE) {
+    name = "conv_dw_reduce_kernel";
+    if (with_bias) name += " conv_db_reduce_kernel";
+  } else if (phase == MX_CONV_FORWARD) {
+    FwdPlan f;
+    MX_TRY(plan_forward(d, kAlignedNull, kAlignedNull, nullptr, kAlignedOut, limit, &f));
+    name = fwd_variant(f);
+    r.tile = f.gp.tile;
+    r.splits = f.gp.splits;
+    r.span = f.gp.kps;
+    r.workspace_bytes = f.ws_bytes;
+  } else if (phase == MX_CONV_DINPUT) {
+    DxPlan f;
+    MX_TRY(plan_dinput(d, kAlignedNull, kAlignedNull, kAlignedOut, limit, &f));
+    name = dx_variant(f);
+    r.tile = f.gp.tile;
+    r.splits = f.gp.splits;
+    r.span = f.gp.kps;
+    r.workspace_bytes = f.ws_bytes;
+  } else {
+    DwPlan f;
+    MX_TRY(plan_dweight(d, kAlignedNull, kAlignedNull, kAlignedOut, with_bias ? kAlignedOut : nullptr, limit, &f));
+    name = dw_variant(f);
+    r.tile = f.gp.tile;
+    r.splits = f.gp.splits;
+    r.span = f.gp.kps;
+    r.workspace_bytes = f.ws_bytes + f.db_bytes;
+  }
+  if (images_per_launch(d) < d.n && (chosen == MX_CONV_ALGO_IMPLICIT_GEMM || chosen == MX_CONV_ALGO_WINOGRAD))
+    name += "+batch_chunks";
+  std::strncpy(r.variant, name.c_str(), sizeof r.variant - 1);
+  *info = r;
+  return MX_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -583,6 +816,8 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
   MX_REQUIRE(x && w && y, MX_ERR_INVALID, "conv2d forward: null tensor");
   int chosen = 0;
   MX_TRY(select_algo(d, MX_CONV_FORWARD, algo, &chosen));
+  int64_t limit = 0;
+  MX_TRY(conv::workspace_limit(&limit));
   hipStream_t s = resolve_stream(stream);
   if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM || chosen == MX_CONV_ALGO_WINOGRAD) {
     const int64_t nc = images_per_launch(d);
@@ -596,49 +831,35 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
       return MX_OK;
     }
   }
-  if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_forward(d, x, w, bias, y, s);
-  ConvArgs p = make_args(d);
-  p.x = x;
-  p.w = w;
-  p.bias = bias;
-  p.out = y;
+  if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_forward(d, x, w, bias, y, limit, s);
   if (chosen == MX_CONV_ALGO_DIRECT) {
+    ConvArgs p = make_args(d);
+    p.x = x;
+    p.w = w;
+    p.bias = bias;
+    p.out = y;
     hipLaunchKernelGGL(conv_fwd_direct_kernel, dim3(linear_blocks(d.n * d.cout * d.oh * d.ow)), dim3(256), 0, s, p);
     MX_HIP(hipGetLastError());
     return MX_OK;
   }
-  p.M = p.Cout_g;
-  p.Ncols = p.N * p.OHOW;
-  p.K = p.Cin_g * p.KK;
-  const bool fwd_packed = p.KK > 1 && conv::blocked_channels(p.Cin_g);
-  // Weight rows are read 16 bytes per lane: a K that is not a multiple of
-  // four, or unaligned weights, get a copy with rows padded to a multiple of
-  // four floats.
-  const bool fwd_padded = !fwd_packed && (p.K % 4 != 0 || !aligned16(w));
-  const Mode ma = Mode::KVEC;
-  const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
-  const GemmPlan gp = plan_fwd(p);
-  p.splits = gp.splits;
-  p.kps = gp.kps;
-  p.out_elems = int64_t(p.N) * p.Cout * p.OHOW;
+  FwdPlan f;
+  MX_TRY(plan_forward(d, x, w, bias, y, limit, &f));
+  ConvArgs& p = f.p;
   Scratch wp, ws;
-  p.wt = w;
-  p.ldw = p.K;
-  if (fwd_packed) {  // pack to the blocked K order
-    MX_TRY(wp.alloc(size_t(p.Cout) * p.Cin_g * p.KK * 4, s));
+  if (f.packed) {  // pack to the blocked K order
+    MX_TRY(wp.alloc(size_t(f.w_bytes), s));
     MX_TRY(conv::conv_fwd_pack_weights(p, wp.as<float>(), s));
     p.wt = wp.as<float>();
-  } else if (fwd_padded) {
-    p.ldw = (p.K + 3) / 4 * 4;
-    MX_TRY(wp.alloc(size_t(p.Cout) * p.ldw * 4, s));
+  } else if (f.padded) {
+    MX_TRY(wp.alloc(size_t(f.w_bytes), s));
     MX_TRY(conv::conv_fwd_pad_weights(p, wp.as<float>(), s));
     p.wt = wp.as<float>();
   }
-  if (gp.splits == 1) return conv::conv_fwd_launch(p, gp.tile, ma, bmode, s);
-  MX_TRY(ws.alloc(size_t(gp.splits) * size_t(p.out_elems) * 4, s));
+  if (f.gp.splits == 1) return conv::conv_fwd_launch(p, f.gp.tile, Mode::KVEC, f.bmode, s);
+  MX_TRY(ws.alloc(size_t(f.ws_bytes), s));
   p.ws = ws.as<float>();
-  MX_TRY(conv::conv_fwd_launch(p, gp.tile, ma, bmode, s));
-  return conv::conv_sum_splits(p.ws, gp.splits, p.out_elems, y, bias, p.OHOW, p.Cout, s);
+  MX_TRY(conv::conv_fwd_launch(p, f.gp.tile, Mode::KVEC, f.bmode, s));
+  return conv::conv_sum_splits(p.ws, f.gp.splits, p.out_elems, y, bias, p.OHOW, p.Cout, s);
   MX_ABI_END
 }
 
@@ -650,6 +871,8 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
   MX_REQUIRE(dy && w && dx, MX_ERR_INVALID, "conv2d dinput: null tensor");
   int chosen = 0;
   MX_TRY(select_algo(d, MX_CONV_DINPUT, algo, &chosen));
+  int64_t limit = 0;
+  MX_TRY(conv::workspace_limit(&limit));
   hipStream_t s = resolve_stream(stream);
   if (chosen == MX_CONV_ALGO_IMPLICIT_GEMM || chosen == MX_CONV_ALGO_WINOGRAD) {
     const int64_t nc = images_per_launch(d);
@@ -663,47 +886,34 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
       return MX_OK;
     }
   }
-  if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_backward_input(d, dy, w, dx, s);
-  ConvArgs p = make_args(d);
-  p.dy = dy;
-  p.w = w;
-  p.out = dx;
+  if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_backward_input(d, dy, w, dx, limit, s);
   if (chosen == MX_CONV_ALGO_DIRECT) {
+    ConvArgs p = make_args(d);
+    p.dy = dy;
+    p.w = w;
+    p.out = dx;
     hipLaunchKernelGGL(conv_dx_direct_kernel, dim3(linear_blocks(d.n * d.cin * d.h * d.w)), dim3(256), 0, s, p);
     MX_HIP(hipGetLastError());
     return MX_OK;
   }
-  // One GEMM per stride phase over exactly the taps that reach it.
-  std::vector<ConvArgs> phases;
-  const GemmPlan gp = plan_dx(p, &phases);
-  // A 1x1 kernel is already [g][co][ci]; larger kernels are packed per phase.
-  const bool packed = p.KK > 1;
-  const bool vec_a = p.Cin_g % 4 == 0 && (packed || aligned16(w));
-  const int64_t out_elems = int64_t(p.N) * p.Cin * p.HW;
+  DxPlan f;
+  MX_TRY(plan_dinput(d, dy, w, dx, limit, &f));
+  const ConvArgs& p = f.p;  // data pointers set; every phase is a copy of it
   Scratch wt, ws;
-  if (packed) MX_TRY(wt.alloc(size_t(p.Cout) * p.Cin_g * p.KK * 4, s));
-  if (gp.splits > 1) MX_TRY(ws.alloc(size_t(gp.splits) * size_t(out_elems) * 4, s));
+  if (f.packed) MX_TRY(wt.alloc(size_t(f.w_bytes), s));
+  if (f.ws_bytes) MX_TRY(ws.alloc(size_t(f.ws_bytes), s));
   // Positions no tap reaches (a phase with K = 0) are zero: one contiguous
   // fill of dx, then the phase GEMMs overwrite the reached positions (such
-  // plans never split K, so the GEMMs write dx directly).
-  bool any_zero = false, only_00 = true;
-  for (const ConvArgs& q : phases) {
-    any_zero |= q.K == 0;
-    if (q.K != 0 && (q.pa != 0 || q.pb != 0)) only_00 = false;
-  }
-  // Stride 2 x 2 with phase (0, 0) the only one reached and W even: the
-  // GEMM writes the zeros of each 2x2 block itself (8-byte aligned stores).
-  const bool zfill = any_zero && only_00 && p.sh == 2 && p.sw == 2 && p.W % 2 == 0 &&
-                     (reinterpret_cast<uintptr_t>(dx) & 7) == 0 && gp.splits == 1 && gp.tile != conv::TALL &&
-                     gp.tile != conv::WIDE;
-  if (any_zero && !zfill) MX_TRY(conv::conv_dx_zero(dx, out_elems, s));
+  // plans never split K, so the GEMMs write dx directly) -- unless the GEMM
+  // writes those zeros itself (zfill).
+  if (f.any_zero && !f.zfill) MX_TRY(conv::conv_dx_zero(dx, f.out_elems, s));
   // Pack every reached phase's weights up front, each at its own offset
   // (the phases partition the taps, so they fit the weights' size), in
   // launches of up to kMaxPackPhases phases.
-  if (packed) {
+  if (f.packed) {
     conv::DxPackSet set{};
     uint32_t off = 0;
-    for (ConvArgs& q : phases) {
+    for (ConvArgs& q : f.phases) {
       if (q.K == 0) continue;
       set.ph[set.n++] = conv::DxPackPhase{q.K, q.nth, q.ntw, q.kh0, q.kw0, q.stph, q.stpw, off};
       q.wt = wt.as<float>() + off;
@@ -715,23 +925,13 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
     }
     if (set.n > 0) MX_TRY(conv::conv_dx_pack_weights(p, set, wt.as<float>(), s));
   }
-  for (ConvArgs& q : phases) {
+  for (size_t i = 0; i < f.phases.size(); ++i) {
+    ConvArgs& q = f.phases[i];
     if (q.K == 0) continue;
-    q.zfill = zfill ? 1 : 0;
-    if (!packed) q.wt = w;
-    q.f_kblk = conv::fast_div(uint32_t(q.nth * q.ntw * conv::kChanBlock));
-    q.f_tapw = conv::fast_div(uint32_t(q.ntw));
-    q.f_kk = conv::fast_div(uint32_t(q.nth * q.ntw));
-    q.splits = gp.splits;
-    q.kps = int((q.K + gp.splits - 1) / gp.splits + kSplitBK - 1) / kSplitBK * kSplitBK;
     q.ws = ws.as<float>();
-    q.out_elems = out_elems;
-    const bool one_to_one = q.nth == 1 && q.ntw == 1 && q.offh0 == 0 && q.offw0 == 0 && q.Hp == p.OH &&
-                            q.Wp == p.OW && p.OHOW % 4 == 0 && aligned16(dy);
-    MX_TRY(conv::conv_dx_launch(q, gp.tile, vec_a ? Mode::RVEC : Mode::RSCALAR,
-                                one_to_one ? conv::B_VEC : conv::B_GATHER, s));
+    MX_TRY(conv::conv_dx_launch(q, f.gp.tile, f.vec_a ? Mode::RVEC : Mode::RSCALAR, f.bmodes[i], s));
   }
-  if (gp.splits > 1) return conv::conv_sum_splits(ws.as<float>(), gp.splits, out_elems, dx, nullptr, 1, 1, s);
+  if (f.gp.splits > 1) return conv::conv_sum_splits(ws.as<float>(), f.gp.splits, f.out_elems, dx, nullptr, 1, 1, s);
   return MX_OK;
   MX_ABI_END
 }
@@ -766,12 +966,14 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
   if (!dw) return mx_conv2d_backward_bias(desc, dy, db, stream);
   int chosen = 0;
   MX_TRY(select_algo(d, MX_CONV_DWEIGHT, algo, &chosen));
+  int64_t limit = 0;
+  MX_TRY(conv::workspace_limit(&limit));
   hipStream_t s = resolve_stream(stream);
-  ConvArgs p = make_args(d);
-  p.x = x;
-  p.dy = dy;
-  p.out = dw;
   if (chosen == MX_CONV_ALGO_DIRECT || chosen == MX_CONV_ALGO_REDUCE) {
+    ConvArgs p = make_args(d);
+    p.x = x;
+    p.dy = dy;
+    p.out = dw;
     if (chosen == MX_CONV_ALGO_DIRECT)
       hipLaunchKernelGGL(conv_dw_direct_kernel, dim3(linear_blocks(d.cout * (d.cin / d.groups) * d.kh * d.kw)),
                          dim3(256), 0, s, p);
@@ -810,58 +1012,45 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
     }
   }
   if (chosen == MX_CONV_ALGO_WINOGRAD) {
-    MX_TRY(winograd_backward_weight(d, x, dy, dw, s));
+    MX_TRY(winograd_backward_weight(d, x, dy, dw, limit, s));
     return db ? mx_conv2d_backward_bias(desc, dy, db, stream) : MX_OK;
   }
-  p.db = db;
-  p.M = p.Cout_g;
-  p.Ncols = p.Cin_g * p.KK;
-  p.K = p.N * p.OHOW;
-  const int amode = (p.OHOW % 4 == 0 && aligned16(dy)) ? conv::B_VEC : conv::B_GATHER;
-  const int bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
-  p.cols_blocked = bmode == conv::B_GATHER && conv::blocked_channels(p.Cin_g) ? 1 : 0;
-  const DwPlan pl = plan_dw(p, db != nullptr, bmode == conv::B_GATHER, amode == conv::B_GATHER);
-  p.splits = pl.g.splits;
-  p.kps = pl.g.kps;
-  if (pl.g.splits == 1) return conv::conv_dw_launch(p, pl.g.tile, amode, bmode, s);
+  DwPlan f;
+  MX_TRY(plan_dweight(d, x, dy, dw, db, limit, &f));
+  ConvArgs& p = f.p;
+  if (f.gp.splits == 1) return conv::conv_dw_launch(p, f.gp.tile, f.amode, f.bmode, s);
   Scratch ws, wsdb;
-  MX_TRY(ws.alloc(size_t(pl.ws_bytes), s));
+  MX_TRY(ws.alloc(size_t(f.ws_bytes), s));
   p.ws = ws.as<float>();
   if (db) {
-    MX_TRY(wsdb.alloc(size_t(pl.db_bytes), s));
+    MX_TRY(wsdb.alloc(size_t(f.db_bytes), s));
     p.ws_db = wsdb.as<float>();
   }
-  MX_TRY(conv::conv_dw_launch(p, pl.g.tile, amode, bmode, s));
+  MX_TRY(conv::conv_dw_launch(p, f.gp.tile, f.amode, f.bmode, s));
   return conv::conv_dw_finalize(p, dw, db, s);
   MX_ABI_END
 }
 
 int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char* buf, size_t len) {
   MX_ABI_BEGIN
-  mx_conv2d_desc d = *desc;
-  MX_TRY(checked_desc(&d));
-  int chosen = 0;
-  MX_TRY(select_algo(d, phase, algo, &chosen));
-  ConvArgs p = make_args(d);
+  MX_REQUIRE(buf || !len, MX_ERR_INVALID, "mx_conv2d_kernel_name: null buffer");
+  mx_conv2d_plan_info info{};
+  MX_TRY(describe(desc, phase, algo, 1, &info));
   std::string name;
   if (phase == MX_CONV_DBIAS) {
-    name = chosen == MX_CONV_ALGO_DIRECT ? "conv_db_direct_kernel" : "conv_db_reduce_kernel";
-  } else if (chosen == MX_CONV_ALGO_WINOGRAD) {
+    name = info.variant;
+  } else if (info.algo == MX_CONV_ALGO_WINOGRAD) {
     name = phase == MX_CONV_DWEIGHT ? "wino_dw_kernel" : "wino_filter_kernel";
-  } else if (chosen == MX_CONV_ALGO_DIRECT) {
-    name = phase == MX_CONV_FORWARD ? "conv_fwd_direct_kernel"
-           : phase == MX_CONV_DINPUT ? "conv_dx_direct_kernel" : "conv_dw_direct_kernel";
-  } else if (chosen == MX_CONV_ALGO_REDUCE) {
+  } else if (info.algo == MX_CONV_ALGO_DIRECT) {
+    name = phase == MX_CONV_FORWARD  ? "conv_fwd_direct_kernel"
+           : phase == MX_CONV_DINPUT ? "conv_dx_direct_kernel"
+                                     : "conv_dw_direct_kernel";
+  } else if (info.algo == MX_CONV_ALGO_REDUCE) {
     name = "conv_dw_reduce_kernel";
-  } else if (phase == MX_CONV_FORWARD) {
-    name = cat("conv_fwd_kernel<", tile_name(plan_fwd(p).tile, phase), ">");
-  } else if (phase == MX_CONV_DINPUT) {
-    name = cat("conv_dx_kernel<", tile_name(plan_dx(p, nullptr).tile, phase), ">");
   } else {
-    p.M = p.Cout_g;
-    p.Ncols = p.Cin_g * p.KK;
-    p.K = p.N * p.OHOW;
-    name = cat("conv_dw_kernel<", kTileInfo[plan_dw(p, true, !(unpadded_1x1(p) && p.HW % 4 == 0), p.OHOW % 4 != 0).g.tile].name, ">");
+    const char* kind = phase == MX_CONV_FORWARD ? "conv_fwd_kernel" : phase == MX_CONV_DINPUT ? "conv_dx_kernel"
+                                                                                                : "conv_dw_kernel";
+    name = cat(kind, "<", tile_name(info.tile, phase), ">");
   }
   if (len) {
     std::strncpy(buf, name.c_str(), len - 1);
@@ -871,18 +1060,24 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
   MX_ABI_END
 }
 
+int mx_conv2d_plan(const mx_conv2d_desc* desc, int phase, int algo, int with_bias, mx_conv2d_plan_info* info) {
+  MX_ABI_BEGIN
+  MX_REQUIRE(desc && info, MX_ERR_INVALID, "mx_conv2d_plan: null argument");
+  return describe(desc, phase, algo, with_bias, info);
+  MX_ABI_END
+}
+
 int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t* span, int64_t* workspace_bytes) {
   MX_ABI_BEGIN
   mx_conv2d_desc d = *desc;
   MX_TRY(checked_desc(&d));
-  ConvArgs p = make_args(d);
-  p.M = p.Cout_g;
-  p.Ncols = p.Cin_g * p.KK;
-  p.K = p.N * p.OHOW;
-  const DwPlan pl = plan_dw(p, true, !(unpadded_1x1(p) && p.HW % 4 == 0), p.OHOW % 4 != 0);
-  if (splits) *splits = pl.g.splits;
-  if (span) *span = pl.g.kps;
-  if (workspace_bytes) *workspace_bytes = pl.ws_bytes + pl.db_bytes;
+  int64_t limit = 0;
+  MX_TRY(conv::workspace_limit(&limit));
+  DwPlan f;
+  MX_TRY(plan_dweight(d, kAlignedNull, kAlignedNull, kAlignedOut, kAlignedOut, limit, &f));
+  if (splits) *splits = f.gp.splits;
+  if (span) *span = f.gp.kps;
+  if (workspace_bytes) *workspace_bytes = f.ws_bytes + f.db_bytes;
   return MX_OK;
   MX_ABI_END
 }

@@ -11,6 +11,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
+#include <string>
 
 #include "mfma_core.hpp"
 #include "mx_internal.hpp"
@@ -207,9 +209,29 @@ int pick_gemm_tile(int64_t m, int64_t n, int64_t batch, bool vec) {
 
 using namespace mx;
 
-extern "C" int mx_gemm_f32(const mx_gemm_desc* d, const float* a, const float* b, const float* bias,
-                           float* c, void* stream) {
-  MX_ABI_BEGIN
+namespace mx {
+namespace {
+
+const char* mode_name(Mode m) {
+  switch (m) {
+    case Mode::KVEC: return "KVEC";
+    case Mode::RVEC: return "RVEC";
+    case Mode::KSCALAR: return "KSCALAR";
+    default: return "RSCALAR";
+  }
+}
+
+// Validated arguments, operand modes and tile of one mx_gemm_f32 call (the
+// pointers only decide alignment; nothing is read).  Returns MX_OK with
+// *empty set when the call writes nothing.
+struct GemmPlan {
+  GemmArgs p{};
+  Mode ma = Mode::KVEC, mb = Mode::KVEC;
+  int tile = 2;
+  bool empty = false;
+};
+
+int plan_gemm(const mx_gemm_desc* d, const float* a, const float* b, const float* bias, float* c, GemmPlan* g) {
   MX_REQUIRE(d, MX_ERR_INVALID, "mx_gemm_f32: null descriptor");
   MX_REQUIRE(d->batch >= 0 && d->m >= 0 && d->n >= 0 && d->k >= 0, MX_ERR_INVALID,
              "mx_gemm_f32: negative dimension");
@@ -217,15 +239,13 @@ extern "C" int mx_gemm_f32(const mx_gemm_desc* d, const float* a, const float* b
              MX_ERR_INVALID, "mx_gemm_f32: dimension exceeds int32");
   MX_REQUIRE(d->bias_kind >= MX_BIAS_NONE && d->bias_kind <= MX_BIAS_MATRIX, MX_ERR_INVALID,
              "mx_gemm_f32: bad bias kind");
-  if (d->batch == 0 || d->m == 0 || d->n == 0) return MX_OK;
-  MX_REQUIRE(c, MX_ERR_INVALID, "mx_gemm_f32: null output");
-  MX_REQUIRE(d->bias_kind == MX_BIAS_NONE || bias, MX_ERR_INVALID, "mx_gemm_f32: null bias");
-  hipStream_t s = resolve_stream(stream);
-  GemmArgs p{};
+  g->empty = d->batch == 0 || d->m == 0 || d->n == 0;
+  if (g->empty) return MX_OK;
+  GemmArgs& p = g->p;
   p.a = a ? a + d->a_offset : nullptr;
   p.b = b ? b + d->b_offset : nullptr;
   p.bias = bias ? bias + d->bias_offset : nullptr;
-  p.c = c + d->c_offset;
+  p.c = c ? c + d->c_offset : nullptr;
   p.a_sb = d->a_stride_b;
   p.a_sm = d->a_stride_m;
   p.a_sk = d->a_stride_k;
@@ -244,6 +264,29 @@ extern "C" int mx_gemm_f32(const mx_gemm_desc* d, const float* a, const float* b
   p.alpha = d->alpha;
   p.beta = d->beta;
   p.bias_kind = d->bias_kind;
+  if (d->k == 0) return MX_OK;
+  MX_REQUIRE(((d->m + 63) / 64) * ((d->n + 63) / 64) <= INT32_MAX, MX_ERR_INVALID, "mx_gemm_f32: too many tiles");
+  g->ma = pick_mode(p.a, p.a_sm, p.a_sk, p.a_sb, p.batch, p.M, p.K);
+  g->mb = pick_mode(p.b, p.b_sn, p.b_sk, p.b_sb, p.batch, p.N, p.K);
+  g->tile = pick_gemm_tile(d->m, d->n, d->batch, is_vec(g->ma) && is_vec(g->mb));
+  return MX_OK;
+}
+
+constexpr const char* kTileNames[] = {"256x128x16", "128x256x16", "128x128x16", "64x64x16"};
+
+}  // namespace
+}  // namespace mx
+
+extern "C" int mx_gemm_f32(const mx_gemm_desc* d, const float* a, const float* b, const float* bias,
+                           float* c, void* stream) {
+  MX_ABI_BEGIN
+  GemmPlan g;
+  MX_TRY(plan_gemm(d, a, b, bias, c, &g));
+  if (g.empty) return MX_OK;
+  MX_REQUIRE(c, MX_ERR_INVALID, "mx_gemm_f32: null output");
+  MX_REQUIRE(d->bias_kind == MX_BIAS_NONE || bias, MX_ERR_INVALID, "mx_gemm_f32: null bias");
+  hipStream_t s = resolve_stream(stream);
+  GemmArgs& p = g.p;
   if (d->k == 0) {
     const int64_t total = d->batch * d->m * d->n;
     const int blocks = int(std::min<int64_t>((total + 255) / 256, 65535));
@@ -252,14 +295,35 @@ extern "C" int mx_gemm_f32(const mx_gemm_desc* d, const float* a, const float* b
     return MX_OK;
   }
   MX_REQUIRE(a && b, MX_ERR_INVALID, "mx_gemm_f32: null operand");
-  const Mode ma = pick_mode(p.a, p.a_sm, p.a_sk, p.a_sb, p.batch, p.M, p.K);
-  const Mode mb = pick_mode(p.b, p.b_sn, p.b_sk, p.b_sb, p.batch, p.N, p.K);
-  MX_REQUIRE(((d->m + 63) / 64) * ((d->n + 63) / 64) <= INT32_MAX, MX_ERR_INVALID, "mx_gemm_f32: too many tiles");
-  switch (pick_gemm_tile(d->m, d->n, d->batch, is_vec(ma) && is_vec(mb))) {
-    case 0: return launch1_vec<TileTall>(p, ma, mb, s);
-    case 1: return launch1_vec<TileWide>(p, ma, mb, s);
-    case 2: return launch1<TileSq>(p, ma, mb, s);
-    default: return launch1<TileSmall>(p, ma, mb, s);
+  switch (g.tile) {
+    case 0: return launch1_vec<TileTall>(p, g.ma, g.mb, s);
+    case 1: return launch1_vec<TileWide>(p, g.ma, g.mb, s);
+    case 2: return launch1<TileSq>(p, g.ma, g.mb, s);
+    default: return launch1<TileSmall>(p, g.ma, g.mb, s);
   }
+  MX_ABI_END
+}
+
+extern "C" int mx_gemm_variant(const mx_gemm_desc* d, const float* a, const float* b, char* buf, size_t len) {
+  MX_ABI_BEGIN
+  MX_REQUIRE(buf || !len, MX_ERR_INVALID, "mx_gemm_variant: null buffer");
+  GemmPlan g;
+  MX_TRY(plan_gemm(d, a, b, nullptr, nullptr, &g));
+  std::string name;
+  if (g.empty) {
+    name = "none";
+  } else if (d->k == 0) {
+    name = "gemm_k0_kernel";
+  } else {
+    const int kind = (d->bias_kind == MX_BIAS_NONE || d->beta == 0.f) ? MX_BIAS_NONE : d->bias_kind;
+    name = cat("gemm_kernel<", kTileNames[g.tile], ",", mode_name(g.ma), ",", mode_name(g.mb), ">",
+               kind == MX_BIAS_COL ? "+bias_col" : kind == MX_BIAS_MATRIX ? "+bias_matrix" : "",
+               d->batch > 65535 ? "+batch_chunks" : "");
+  }
+  if (len) {
+    std::strncpy(buf, name.c_str(), len - 1);
+    buf[len - 1] = 0;
+  }
+  return MX_OK;
   MX_ABI_END
 }

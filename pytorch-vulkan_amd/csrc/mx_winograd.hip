@@ -35,6 +35,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <string>
 
 #include "mfma_core.hpp"
 #include "mx_internal.hpp"
@@ -691,20 +692,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }  // namespace fused_dw
 
 int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
-                     bool flip, hipStream_t s);
+                     bool flip, int64_t chunk, hipStream_t s);
 
 }  // namespace
 
 namespace {
+// The batched GEMM of the unfused passes: M_t = U_t V_t for the 16*G
+// coordinates, U [16*G][Cout_g][Cin_g], V [16*G][Cin_g][T], M [16*G][Cout_g][T].
+mx_gemm_desc unfused_gemm_desc(int G, int Cout_g, int Cin_g, int64_t T) {
+  mx_gemm_desc gd{};
+  gd.batch = 16 * int64_t(G);
+  gd.m = Cout_g;
+  gd.n = T;
+  gd.k = Cin_g;
+  gd.a_stride_b = int64_t(Cout_g) * Cin_g;
+  gd.a_stride_m = Cin_g;
+  gd.a_stride_k = 1;
+  gd.b_stride_b = int64_t(Cin_g) * T;
+  gd.b_stride_k = T;
+  gd.b_stride_n = 1;
+  gd.c_stride_b = int64_t(Cout_g) * T;
+  gd.ldc = T;
+  gd.alpha = 1.f;
+  gd.beta = 0.f;
+  gd.bias_kind = MX_BIAS_NONE;
+  return gd;
+}
+
 int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
-                     bool flip, hipStream_t s) {
+                     bool flip, int64_t chunk, hipStream_t s) {
   WinoArgs p{};
   p.flip = flip ? 1 : 0;
-  p.x = x;
   p.w = w;
   p.bias = bias;
-  p.y = y;
-  p.N = int(d.n);
   p.Cin = int(d.cin);
   p.H = int(d.h);
   p.W = int(d.w);
@@ -718,10 +738,9 @@ int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, co
   p.Cout_g = p.Cout / p.G;
   p.TH = (p.OH + 1) / 2;
   p.TW = (p.OW + 1) / 2;
-  const int64_t T = int64_t(p.N) * p.TH * p.TW;
+  const int64_t T = chunk * p.TH * p.TW;  // tiles of one chunk of images
   MX_REQUIRE(T <= INT32_MAX && 16 * int64_t(p.Cin) * T <= INT32_MAX && 16 * int64_t(p.Cout) * T <= INT32_MAX,
              MX_ERR_UNSUPPORTED, "winograd: transformed tensors exceed int32 indexing");
-  p.T = int(T);
   Scratch U, V, M;
   MX_TRY(U.alloc(size_t(16) * p.Cout * p.Cin_g * 4, s));
   MX_TRY(V.alloc(size_t(16) * p.Cin * T * 4, s));
@@ -731,38 +750,41 @@ int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, co
   p.M = M.as<float>();
   hipLaunchKernelGGL(wino_filter_kernel, dim3(blocks_for(int64_t(p.Cout) * p.Cin_g)), dim3(256), 0, s, p);
   MX_HIP(hipGetLastError());
-  hipLaunchKernelGGL(wino_input_kernel, dim3(blocks_for(int64_t(p.Cin) * T)), dim3(256), 0, s, p);
-  MX_HIP(hipGetLastError());
-  mx_gemm_desc gd{};
-  gd.batch = 16 * int64_t(p.G);
-  gd.m = p.Cout_g;
-  gd.n = T;
-  gd.k = p.Cin_g;
-  gd.a_stride_b = int64_t(p.Cout_g) * p.Cin_g;
-  gd.a_stride_m = p.Cin_g;
-  gd.a_stride_k = 1;
-  gd.b_stride_b = int64_t(p.Cin_g) * T;
-  gd.b_stride_k = T;
-  gd.b_stride_n = 1;
-  gd.c_stride_b = int64_t(p.Cout_g) * T;
-  gd.ldc = T;
-  gd.alpha = 1.f;
-  gd.beta = 0.f;
-  gd.bias_kind = MX_BIAS_NONE;
-  MX_TRY(mx_gemm_f32(&gd, p.U, p.V, nullptr, p.M, s));
-  hipLaunchKernelGGL(wino_output_kernel, dim3(blocks_for(int64_t(p.Cout) * T)), dim3(256), 0, s, p);
-  MX_HIP(hipGetLastError());
+  // Images in chunks that reuse V and M (the workspace budget sets the chunk).
+  for (int64_t n0 = 0; n0 < d.n; n0 += chunk) {
+    p.N = int(std::min(chunk, d.n - n0));
+    p.T = p.N * p.TH * p.TW;
+    p.x = x + n0 * p.Cin * p.H * p.W;
+    p.y = y + n0 * p.Cout * p.OH * p.OW;
+    hipLaunchKernelGGL(wino_input_kernel, dim3(blocks_for(int64_t(p.Cin) * p.T)), dim3(256), 0, s, p);
+    MX_HIP(hipGetLastError());
+    const mx_gemm_desc gd = unfused_gemm_desc(p.G, p.Cout_g, p.Cin_g, p.T);
+    MX_TRY(mx_gemm_f32(&gd, p.U, p.V, nullptr, p.M, s));
+    hipLaunchKernelGGL(wino_output_kernel, dim3(blocks_for(int64_t(p.Cout) * p.T)), dim3(256), 0, s, p);
+    MX_HIP(hipGetLastError());
+  }
   return MX_OK;
 }
 }  // namespace
 
 namespace {
-// The convolution d of x with filter w (read flipped and channel-swapped when
-// `flip`), Winograd F(2x2,3x3), plus bias.
-int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y, bool flip,
-                 hipStream_t s) {
+// Launch plan of a Winograd convolution: the fused kernel's arguments (all
+// but the data pointers), its grid, and whether the fused or the unfused
+// passes run.  The unfused passes need U, V and M in scratch; V and M cover
+// as many images at a time as the workspace budget holds (`chunk`), and when
+// not even one image fits the fused kernel runs instead (it needs only the
+// transformed filter, which like a packed weight copy is not counted).
+struct RunPlan {
   fused::Args p{};
-  p.bias = bias;
+  int G = 1;
+  int64_t blocks = 0;
+  bool fused = true;
+  int64_t chunk = 0;          // images per unfused pass
+  int64_t unfused_bytes = 0;  // U, V and M of one pass
+};
+
+int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
+  fused::Args& p = r->p;
   p.Cin = int(d.cin);
   p.H = int(d.h);
   p.W = int(d.w);
@@ -771,9 +793,9 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   p.OW = int(d.ow);
   p.ph = int(d.ph);
   p.pw = int(d.pw);
-  const int G = int(d.groups);
-  p.C = p.Cin / G;
-  p.O = p.Cout / G;
+  r->G = int(d.groups);
+  p.C = p.Cin / r->G;
+  p.O = p.Cout / r->G;
   p.Cpad = (p.C + fused::BK - 1) / fused::BK * fused::BK;
   p.Opad = (p.O + fused::BO - 1) / fused::BO * fused::BO;
   p.TH = (p.OH + 1) / 2;
@@ -782,36 +804,54 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   p.nslab = p.Cpad / fused::BK;
   p.f_tw = mfma::fast_div(uint32_t(p.TW));
   p.f_thw = mfma::fast_div(uint32_t(p.TH * p.TW));
-  const int64_t u_bytes = int64_t(G) * 16 * p.Cpad * p.Opad * 4;
+  const int64_t u_bytes = int64_t(r->G) * 16 * p.Cpad * p.Opad * 4;
   MX_REQUIRE(u_bytes < mfma::kBufMaxBytes, MX_ERR_UNSUPPORTED, "winograd: the transformed filter exceeds 2 GiB");
   p.u_bytes = u_bytes;
   // The caller splits batches so the input stays one buffer resource with
   // 32-bit offsets (images_per_launch).
-  const int64_t x_bytes = d.n * int64_t(p.Cin) * p.H * p.W * 4;
-  const int64_t y_bytes = d.n * int64_t(p.Cout) * p.OH * p.OW * 4;
+  p.x_bytes = d.n * int64_t(p.Cin) * p.H * p.W * 4;
+  p.y_bytes = d.n * int64_t(p.Cout) * p.OH * p.OW * 4;
   const int64_t T = d.n * int64_t(p.TH) * p.TW;
-  MX_REQUIRE(x_bytes < mfma::kBufMaxBytes && y_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
+  MX_REQUIRE(p.x_bytes < mfma::kBufMaxBytes && p.y_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
              "winograd: an operand exceeds the 2 GiB bound");
-  if (T == 0) return MX_OK;
-  const int64_t blocks = (T + fused::BT - 1) / fused::BT * p.n_ob;
-  MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "winograd: grid too large");
+  p.T = int(T);
+  r->blocks = (T + fused::BT - 1) / fused::BT * p.n_ob;
+  MX_REQUIRE(r->blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "winograd: grid too large");
   // MX_WINOGRAD_FUSED=1 / 0 forces the fused / unfused kernels (tests, tuning).
-  bool fused_path = fused::prefer_fused(blocks * G, p.nslab);
+  r->fused = fused::prefer_fused(r->blocks * r->G, p.nslab);
   if (const char* e = std::getenv("MX_WINOGRAD_FUSED"))
-    if (e[0] == '0' || e[0] == '1') fused_path = e[0] == '1';
-  if (!fused_path) return winograd_unfused(d, x, w, bias, y, flip, s);
+    if (e[0] == '0' || e[0] == '1') r->fused = e[0] == '1';
+  const int64_t u_plain = 16 * int64_t(p.Cout) * p.C * 4;
+  const int64_t per_image = 16 * (int64_t(p.Cin) + p.Cout) * p.TH * p.TW * 4;
+  const int64_t fit = ws_limit > u_plain ? (ws_limit - u_plain) / per_image : 0;
+  if (!r->fused && fit < 1) r->fused = true;
+  if (!r->fused) {
+    const int64_t passes = (d.n + fit - 1) / fit;
+    r->chunk = (d.n + passes - 1) / passes;
+    r->unfused_bytes = u_plain + per_image * r->chunk;
+  }
+  return MX_OK;
+}
+
+// The convolution d of x with filter w (read flipped and channel-swapped when
+// `flip`), Winograd F(2x2,3x3), plus bias.
+int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y, bool flip,
+                 int64_t ws_limit, hipStream_t s) {
+  RunPlan r;
+  MX_TRY(plan_run(d, ws_limit, &r));
+  fused::Args& p = r.p;
+  if (p.T == 0) return MX_OK;
+  if (!r.fused) return winograd_unfused(d, x, w, bias, y, flip, r.chunk, s);
+  p.bias = bias;
   Scratch U;
-  MX_TRY(U.alloc(size_t(u_bytes), s));
+  MX_TRY(U.alloc(size_t(p.u_bytes), s));
   p.U = U.as<float>();
-  hipLaunchKernelGGL(fused::filter_kernel, dim3(blocks_for(int64_t(G) * (p.Cpad / 2) * p.Opad)), dim3(256), 0, s, w,
-                     U.as<float>(), p.C, p.O, p.Cpad, p.Opad, G, flip);
+  hipLaunchKernelGGL(fused::filter_kernel, dim3(blocks_for(int64_t(r.G) * (p.Cpad / 2) * p.Opad)), dim3(256), 0, s,
+                     w, U.as<float>(), p.C, p.O, p.Cpad, p.Opad, r.G, flip);
   MX_HIP(hipGetLastError());
   p.x = x;
   p.y = y;
-  p.x_bytes = x_bytes;
-  p.y_bytes = y_bytes;
-  p.T = int(T);
-  const dim3 grid{unsigned(blocks), unsigned(G), 1u};
+  const dim3 grid{unsigned(r.blocks), unsigned(r.G), 1u};
   if (p.C % fused::BK)
     hipLaunchKernelGGL(fused::wino_fused_kernel<true>, grid, dim3(256), 0, s, p);
   else
@@ -819,18 +859,19 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   MX_HIP(hipGetLastError());
   return MX_OK;
 }
-}  // namespace
 
-int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
-                     hipStream_t s) {
-  return winograd_run(d, x, w, bias, y, false, s);
-}
-
-// dw of the 3x3 stride-1 layer d (any padding): the fused adjoint kernel
-// over K ranges of tiles sized so the launch fills every CU twice, then a
-// fixed-order sum of the ranges' partials.
-int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, hipStream_t s) {
+// Launch plan of the Winograd weight gradient: K ranges of output tiles sized
+// so the launch fills every CU twice (at least four slabs each), as few as
+// the workspace budget requires for their partials (one range writes dw
+// directly, with no scratch).
+struct DwRunPlan {
   fused_dw::Args p{};
+  int G = 1;
+  int64_t blocks = 0, ranges = 1, n_dw = 0;
+};
+
+int plan_dw_run(const mx_conv2d_desc& d, int64_t ws_limit, DwRunPlan* r) {
+  fused_dw::Args& p = r->p;
   p.Cin = int(d.cin);
   p.H = int(d.h);
   p.W = int(d.w);
@@ -839,9 +880,9 @@ int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const floa
   p.OW = int(d.ow);
   p.ph = int(d.ph);
   p.pw = int(d.pw);
-  const int G = int(d.groups);
-  p.C = p.Cin / G;
-  p.O = p.Cout / G;
+  r->G = int(d.groups);
+  p.C = p.Cin / r->G;
+  p.O = p.Cout / r->G;
   p.TH = (p.OH + 1) / 2;
   p.TW = (p.OW + 1) / 2;
   p.n_ob = (p.O + fused_dw::BO - 1) / fused_dw::BO;
@@ -849,46 +890,61 @@ int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const floa
   p.f_tw = mfma::fast_div(uint32_t(p.TW));
   p.f_thw = mfma::fast_div(uint32_t(p.TH * p.TW));
   // The caller splits batches so both operands stay buffer-addressable.
-  const int64_t x_bytes = d.n * int64_t(p.Cin) * p.H * p.W * 4;
-  const int64_t dy_bytes = d.n * int64_t(p.Cout) * p.OH * p.OW * 4;
+  p.x_bytes = d.n * int64_t(p.Cin) * p.H * p.W * 4;
+  p.dy_bytes = d.n * int64_t(p.Cout) * p.OH * p.OW * 4;
   const int64_t T = d.n * int64_t(p.TH) * p.TW;
-  MX_REQUIRE(x_bytes < mfma::kBufMaxBytes && dy_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
+  MX_REQUIRE(p.x_bytes < mfma::kBufMaxBytes && p.dy_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
              "winograd dweight: an operand exceeds the 2 GiB bound");
-  const int64_t n_dw = int64_t(p.Cout) * p.C * 9;
-  const int64_t blocks = int64_t(p.n_ob) * p.n_cb * G;
-  // Ranges: two resident workgroups per CU in one wave of the launch, at
-  // least four slabs each.
+  r->n_dw = int64_t(p.Cout) * p.C * 9;
+  r->blocks = int64_t(p.n_ob) * p.n_cb * r->G;
   int64_t per_cu = 2;
   if (const char* e = std::getenv("MX_WINO_DW_PER_CU")) per_cu = std::max(1, std::atoi(e));
-  const int64_t want = std::max<int64_t>(1, (per_cu * int64_t(cu_count()) + blocks - 1) / blocks);
+  int64_t want = std::max<int64_t>(1, (per_cu * int64_t(cu_count()) + r->blocks - 1) / r->blocks);
+  const int64_t fit = ws_limit / (r->n_dw * 4);
+  want = fit >= 2 ? std::min(want, fit) : 1;
   int64_t kps = (T + want - 1) / want;
   kps = std::max<int64_t>(kps, 4 * fused_dw::BK);
   kps = (kps + fused_dw::BK - 1) / fused_dw::BK * fused_dw::BK;
-  const int64_t ranges = (T + kps - 1) / kps;
-  MX_REQUIRE(blocks * ranges <= INT32_MAX && G <= 65535, MX_ERR_UNSUPPORTED, "winograd dweight: grid too large");
+  r->ranges = std::max<int64_t>(1, (T + kps - 1) / kps);
+  MX_REQUIRE(r->blocks * r->ranges <= INT32_MAX && r->G <= 65535, MX_ERR_UNSUPPORTED,
+             "winograd dweight: grid too large");
   p.kps = int(kps);
   p.T = int(T);
+  return MX_OK;
+}
+}  // namespace
+
+int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+                     int64_t ws_limit, hipStream_t s) {
+  return winograd_run(d, x, w, bias, y, false, ws_limit, s);
+}
+
+// dw of the 3x3 stride-1 layer d (any padding): the fused adjoint kernel
+// over K ranges of tiles, then a fixed-order sum of the ranges' partials.
+int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, int64_t ws_limit,
+                             hipStream_t s) {
+  DwRunPlan r;
+  MX_TRY(plan_dw_run(d, ws_limit, &r));
+  fused_dw::Args& p = r.p;
   p.x = x;
   p.dy = dy;
-  p.x_bytes = x_bytes;
-  p.dy_bytes = dy_bytes;
   Scratch ws;
-  if (ranges > 1) {
-    MX_TRY(ws.alloc(size_t(ranges) * size_t(n_dw) * 4, s));
+  if (r.ranges > 1) {
+    MX_TRY(ws.alloc(size_t(r.ranges) * size_t(r.n_dw) * 4, s));
     p.out = ws.as<float>();
   } else {
     p.out = dw;
   }
-  hipLaunchKernelGGL(fused_dw::wino_dw_kernel, dim3(unsigned(blocks / G * ranges), unsigned(G)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(fused_dw::wino_dw_kernel, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)), dim3(256), 0,
+                     s, p);
   MX_HIP(hipGetLastError());
-  if (ranges > 1) return conv::sum_partials(ws.as<float>(), int(ranges), n_dw, dw, s);
+  if (r.ranges > 1) return conv::sum_partials(ws.as<float>(), int(r.ranges), r.n_dw, dw, s);
   return MX_OK;
 }
 
-// dx of the 3x3 stride-1 layer d: the forward convolution of dy
-// [N][Cout][OH][OW] with the flipped filter at padding 2 - p, whose output is
-// [N][Cin][H][W] since H = OH + 2 (2 - p) - 2.  Needs p <= 2.
-int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, hipStream_t s) {
+namespace {
+// The transposed description of a Winograd input gradient (see below).
+mx_conv2d_desc dinput_as_forward(const mx_conv2d_desc& d) {
   mx_conv2d_desc t = d;
   t.cin = d.cout;
   t.h = d.oh;
@@ -898,7 +954,45 @@ int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const floa
   t.pw = 2 - d.pw;
   t.oh = d.h;
   t.ow = d.w;
-  return winograd_run(t, dy, w, nullptr, dx, true, s);
+  return t;
+}
+}  // namespace
+
+// Kernels a Winograd call of `phase` launches and the scratch it counts
+// against the workspace budget.
+int winograd_describe(const mx_conv2d_desc& d, int phase, int64_t ws_limit, std::string* variant,
+                      int64_t* ws_bytes) {
+  if (phase == MX_CONV_DWEIGHT) {
+    DwRunPlan r;
+    MX_TRY(plan_dw_run(d, ws_limit, &r));
+    *variant = r.ranges > 1 ? "wino_dw_kernel+ranges" : "wino_dw_kernel";
+    *ws_bytes = r.ranges > 1 ? r.ranges * r.n_dw * 4 : 0;
+    return MX_OK;
+  }
+  RunPlan r;
+  MX_TRY(plan_run(phase == MX_CONV_DINPUT ? dinput_as_forward(d) : d, ws_limit, &r));
+  if (r.fused) {
+    *variant = cat("wino_fused_kernel<", r.p.C % fused::BK ? "ragged" : "even", ">");
+    *ws_bytes = 0;
+  } else {
+    // U, V and M are fresh mx_malloc blocks (256-byte aligned).
+    const mx_gemm_desc gd = unfused_gemm_desc(r.G, r.p.O, r.p.C, r.chunk * r.p.TH * r.p.TW);
+    const float* aligned = reinterpret_cast<const float*>(uintptr_t(256));
+    char gname[96];
+    MX_TRY(mx_gemm_variant(&gd, aligned, aligned, gname, sizeof gname));
+    *variant = cat("wino_unfused(", gname, ")", r.chunk < d.n ? "+chunks" : "");
+    *ws_bytes = r.unfused_bytes;
+  }
+  if (phase == MX_CONV_DINPUT) *variant += "+flip";
+  return MX_OK;
+}
+
+// dx of the 3x3 stride-1 layer d: the forward convolution of dy
+// [N][Cout][OH][OW] with the flipped filter at padding 2 - p, whose output is
+// [N][Cin][H][W] since H = OH + 2 (2 - p) - 2.  Needs p <= 2.
+int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, int64_t ws_limit,
+                            hipStream_t s) {
+  return winograd_run(dinput_as_forward(d), dy, w, nullptr, dx, true, ws_limit, s);
 }
 
 }  // namespace mx

@@ -103,6 +103,13 @@ bool native_conv(const at::Tensor& input, const at::Tensor& weight, bool transpo
          weight.scalar_type() == at::kFloat && is_vk(input) && is_vk(weight);
 }
 
+// Name a gpu_timing_stats() entry: the main kernel of the call.
+std::string kernel_label(const mx_conv2d_desc& d, int phase, int algo) {
+  if (!gpu_timing_enabled()) return {};
+  char buf[128];
+  return mx_conv2d_kernel_name(&d, phase, algo, buf, sizeof buf) == MX_OK ? std::string(buf) : "conv2d";
+}
+
 int choose(const mx_conv2d_desc& d, int phase, int requested) {
   int algo = 0;
   TVK_MX(mx_conv2d_select(&d, phase, requested, &algo));
@@ -134,6 +141,7 @@ at::Tensor convolution_overrideable(const at::Tensor& input, const at::Tensor& w
   }
   at::Tensor y = at::empty({d.n, d.cout, d.oh, d.ow}, input.options().memory_format(at::MemoryFormat::Contiguous));
   const int algo = choose(d, MX_CONV_FORWARD, forward_algo());
+  GpuTimer timer(kernel_label(d, MX_CONV_FORWARD, algo));
   TVK_MX(mx_conv2d_forward(&d, x.data_ptr<float>(), w.data_ptr<float>(), b.defined() ? b.data_ptr<float>() : nullptr,
                            y.data_ptr<float>(), algo, current_stream()));
   counters().kernel_launches++;
@@ -164,6 +172,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
     dx = at::empty(input.sizes(), opts);
     const at::Tensor w = packed(weight);
     const int algo = choose(d, MX_CONV_DINPUT, backward_algo(d, MX_CONV_DINPUT));
+    GpuTimer timer(kernel_label(d, MX_CONV_DINPUT, algo));
     TVK_MX(mx_conv2d_backward_input(&d, dy.data_ptr<float>(), w.data_ptr<float>(), dx.data_ptr<float>(), algo,
                                     current_stream()));
     counters().kernel_launches++;
@@ -179,11 +188,23 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
       dbp = db.data_ptr<float>();
       count_selection(std::string("selected_dbias_") + (algo == MX_CONV_ALGO_IMPLICIT_GEMM ? "fused_dweight" : "reduce"));
     }
+    if (algo == MX_CONV_ALGO_IMPLICIT_GEMM) {
+      // Split plan counters under the reference's names
+      // (tests/test_conv_dispatch.py:274-284).
+      mx_conv2d_plan_info plan{};
+      TVK_MX(mx_conv2d_plan(&d, MX_CONV_DWEIGHT, algo, output_mask[2] ? 1 : 0, &plan));
+      count_selection("dweight_tiled_dispatches");
+      count_selection("dweight_tiled_split_count_total", uint64_t(plan.splits));
+      count_selection("dweight_tiled_split_span_total", uint64_t(plan.span));
+      count_selection("dweight_tiled_workspace_bytes_total", uint64_t(plan.workspace_bytes));
+    }
+    GpuTimer timer(kernel_label(d, MX_CONV_DWEIGHT, algo));
     TVK_MX(mx_conv2d_backward_weight(&d, x.data_ptr<float>(), dy.data_ptr<float>(), dw.data_ptr<float>(), dbp, algo,
                                      current_stream()));
     counters().kernel_launches++;
   } else if (output_mask[2]) {
-    choose(d, MX_CONV_DBIAS, backward_algo(d, MX_CONV_DBIAS));
+    const int algo = choose(d, MX_CONV_DBIAS, backward_algo(d, MX_CONV_DBIAS));
+    GpuTimer timer(kernel_label(d, MX_CONV_DBIAS, algo));
     TVK_MX(mx_conv2d_backward_bias(&d, dy.data_ptr<float>(), db.data_ptr<float>(), current_stream()));
     counters().kernel_launches++;
   }

@@ -40,7 +40,7 @@ EXPORTS = [
     "mx_group_norm_forward", "mx_group_norm_backward", "mx_batch_norm_forward", "mx_batch_norm_backward",
     "mx_unary_f32", "mx_unary_backward_f32", "mx_upsample_nearest2d", "mx_upsample_nearest2d_backward",
     "mx_softmax_f32", "mx_softmax_backward_f32", "mx_mse_loss_f32", "mx_mse_loss_backward_f32", "mx_copy_rows",
-    "mx_foreach_f32",
+    "mx_foreach_f32", "mx_conv2d_plan", "mx_gemm_variant",
 ]
 
 
@@ -53,6 +53,11 @@ class MXError(RuntimeError):
 class ConvDesc(C.Structure):
     _fields_ = [(n, C.c_int64) for n in
                 ("n", "cin", "h", "w", "cout", "kh", "kw", "sh", "sw", "ph", "pw", "dh", "dw", "groups", "oh", "ow")]
+
+
+class ConvPlanInfo(C.Structure):
+    _fields_ = [("algo", C.c_int), ("tile", C.c_int), ("splits", C.c_int64), ("span", C.c_int64),
+                ("workspace_bytes", C.c_int64), ("variant", C.c_char * 256)]
 
 
 class GemmDesc(C.Structure):
@@ -143,6 +148,8 @@ def lib() -> C.CDLL:
             "mx_conv2d_dweight_plan": ([C.POINTER(ConvDesc), C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)], i32),
             "mx_conv2d_kernel_name": ([C.POINTER(ConvDesc), i32, i32, C.c_char_p, C.c_size_t], i32),
             "mx_gemm_f32": ([C.POINTER(GemmDesc), vp, vp, vp, vp, vp], i32),
+            "mx_gemm_variant": ([C.POINTER(GemmDesc), vp, vp, C.c_char_p, C.c_size_t], i32),
+            "mx_conv2d_plan": ([C.POINTER(ConvDesc), i32, i32, i32, C.POINTER(ConvPlanInfo)], i32),
             "mx_adamw_step": ([C.POINTER(AdamWTensor), i64, C.POINTER(AdamWHParams), C.POINTER(i64), vp], i32),
             "mx_group_norm_forward": ([vp, vp, vp, i64, i64, i64, i64, C.c_float, vp, vp, vp, vp], i32),
             "mx_group_norm_backward": ([vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp], i32),
@@ -210,8 +217,9 @@ def conv2d_select(d: ConvDesc, phase: int, requested: int = ALGO_AUTO) -> int:
     return out.value
 
 
-def gemm(a, b, c, *, bias=None, alpha=1.0, beta=0.0, bias_kind=None, stream=None) -> None:
-    """c[b] = alpha * a[b] @ b[b] + beta * bias for 2-D or 3-D strided torch tensors (any device layout)."""
+def gemm_desc(a, b, c, *, bias=None, alpha=1.0, beta=0.0, bias_kind=None) -> GemmDesc:
+    """Descriptor of c[b] = alpha * a[b] @ b[b] + beta * bias for 2-D or 3-D strided tensors
+    (any object with torch's shape / stride / storage_offset / dim accessors)."""
     batched = a.dim() == 3
     m, k = a.shape[-2], a.shape[-1]
     n = b.shape[-1]
@@ -222,7 +230,6 @@ def gemm(a, b, c, *, bias=None, alpha=1.0, beta=0.0, bias_kind=None, stream=None
                  b_stride_k=b.stride(-2), b_stride_n=b.stride(-1),
                  c_offset=c.storage_offset(), c_stride_b=c.stride(0) if batched else 0, ldc=c.stride(-2),
                  alpha=alpha, beta=beta, bias_kind=BIAS_NONE)
-    bias_base = None
     if bias is not None:
         if bias_kind is None:
             bias_kind = BIAS_COL if bias.dim() == 1 else BIAS_MATRIX
@@ -237,10 +244,24 @@ def gemm(a, b, c, *, bias=None, alpha=1.0, beta=0.0, bias_kind=None, stream=None
             d.bias_stride_m, d.bias_stride_n = e.stride(-2), e.stride(-1)
             if batched:
                 d.bias_stride_b = e.stride(0)
-        bias_base = bias.untyped_storage().data_ptr()
     assert c.stride(-1) == 1, "output rows must be contiguous"
+    return d
+
+
+def gemm(a, b, c, *, bias=None, alpha=1.0, beta=0.0, bias_kind=None, stream=None) -> None:
+    """c[b] = alpha * a[b] @ b[b] + beta * bias for 2-D or 3-D strided torch tensors (any device layout)."""
+    d = gemm_desc(a, b, c, bias=bias, alpha=alpha, beta=beta, bias_kind=bias_kind)
+    bias_base = bias.untyped_storage().data_ptr() if bias is not None else None
     check(lib().mx_gemm_f32(C.byref(d), a.untyped_storage().data_ptr(), b.untyped_storage().data_ptr(), bias_base,
                             c.untyped_storage().data_ptr(), stream))
+
+
+def gemm_variant(d: GemmDesc, a_base: int = 256, b_base: int = 256) -> str:
+    """Kernel instantiation mx_gemm_f32 launches for descriptor d with operand
+    storages at these addresses (only their alignment matters)."""
+    buf = C.create_string_buffer(128)
+    check(lib().mx_gemm_variant(C.byref(d), a_base, b_base, buf, 128))
+    return buf.value.decode()
 
 
 def adamw_step(params, grads, exp_avgs, exp_avg_sqs, *, lr, beta1, beta2, eps, weight_decay, steps=None,
@@ -382,6 +403,15 @@ def conv2d_kernel_name(d: ConvDesc, phase: int, algo: int = ALGO_AUTO) -> str:
     buf = C.create_string_buffer(128)
     check(lib().mx_conv2d_kernel_name(C.byref(d), phase, algo, buf, 128))
     return buf.value.decode()
+
+
+def conv2d_plan(d: ConvDesc, phase: int, algo: int = ALGO_AUTO, with_bias: bool = True) -> dict:
+    """Plan of one conv call (mx_conv2d_plan): algorithm, tile, K splits and
+    span, workspace bytes, and the kernel instantiations it launches."""
+    info = ConvPlanInfo()
+    check(lib().mx_conv2d_plan(C.byref(d), phase, algo, 1 if with_bias else 0, C.byref(info)))
+    return {"algo": info.algo, "tile": info.tile, "splits": info.splits, "span": info.span,
+            "workspace_bytes": info.workspace_bytes, "variant": info.variant.decode()}
 
 
 def dweight_plan(d: ConvDesc):
