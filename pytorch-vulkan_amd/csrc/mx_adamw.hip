@@ -19,7 +19,11 @@
 //   v = v * beta2 + ((1 - beta2) * g) * g
 //   p = p + (-lr/bc1 * m) / (sqrt(v) / sqrt(bc2) + eps)
 // with bc1 = 1 - beta1^step and bc2 = 1 - beta2^step in double, in that
-// order, and no multiply-add contraction other than the lerp's.
+// order, and no multiply-add contraction other than the lerp's.  With a
+// grad_scale (torch's GradScaler through aten::_fused_adamw_) the gradient is
+// divided by it first and the unscaled gradient is written back, before
+// maximize negates it, as torch's fused AdamW does; a non-zero found_inf
+// skips the whole step.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -37,7 +41,7 @@ constexpr int kChunk = 256 * 4 * kVec;      // elements per chunk
 
 struct AdamEntry {
   float* p;
-  const float* g;
+  float* g;  // written only with a grad_scale (the unscaled gradient)
   float* m;
   float* v;
   float* vmax;
@@ -94,12 +98,12 @@ __device__ __forceinline__ float nan_max(float a, float b) {
   return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
 }
 
+// g is the (already unscaled) gradient.
 template <bool AMS>
 __device__ __forceinline__ void update(float& p, float g, float& m, float& v, float* vmax_slot, const Coef& c,
-                                       const AdamHP& hp, float scale) {
+                                       const AdamHP& hp) {
 #pragma clang fp contract(off)
   if (hp.maximize) g = -g;
-  if (hp.grad_scale) g = g / scale;
   p = p * c.wdf;
   // torch's vectorised lerp: one fused multiply-add, fma(w, end-self, self)
   // for small weights, fma(w-1, end-self, end) otherwise.
@@ -151,12 +155,20 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamEntry* __restrict_
         v4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.v + i));
         if constexpr (AMS) x4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.vmax + i));
       }
+      if (hp.grad_scale) {
+#pragma unroll
+        for (int u = 0; u < kVec; ++u) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) g4[u][j] = g4[u][j] / scale;
+          __builtin_nontemporal_store(g4[u], reinterpret_cast<f32x4*>(e.g + base + u * 1024));
+        }
+      }
 #pragma unroll
       for (int u = 0; u < kVec; ++u)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           float pp = p4[u][j], mm = m4[u][j], vv = v4[u][j], xx = AMS ? x4[u][j] : 0.f;
-          update<AMS>(pp, g4[u][j], mm, vv, &xx, c, hp, scale);
+          update<AMS>(pp, g4[u][j], mm, vv, &xx, c, hp);
           p4[u][j] = pp;
           m4[u][j] = mm;
           v4[u][j] = vv;
@@ -189,12 +201,17 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamEntry* __restrict_
           vv[j] = in ? e.v[i] : 0.f;
           xx[j] = (AMS && in) ? e.vmax[i] : 0.f;
         }
+        if (hp.grad_scale) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) update<AMS>(pp[j], gg[j], mm[j], vv[j], &xx[j], c, hp, scale);
+          for (int j = 0; j < 4; ++j) gg[j] = gg[j] / scale;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) update<AMS>(pp[j], gg[j], mm[j], vv[j], &xx[j], c, hp);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t i = base + u * 1024 + j;
           if (i < e.numel) {
+            if (hp.grad_scale) e.g[i] = gg[j];
             e.p[i] = pp[j];
             e.m[i] = mm[j];
             e.v[i] = vv[j];
@@ -215,8 +232,9 @@ struct Interval {
 };
 
 // For each entry j, the latest earlier entry i whose memory conflicts with j
-// (one of them writes bytes the other reads or writes), or -1.
-std::vector<int64_t> latest_conflict(const mx_adamw_tensor* t, int64_t n, bool ams) {
+// (one of them writes bytes the other reads or writes), or -1.  Gradients are
+// written when `grads_written` (a grad_scale unscales them in place).
+std::vector<int64_t> latest_conflict(const mx_adamw_tensor* t, int64_t n, bool ams, bool grads_written) {
   std::vector<Interval> iv;
   iv.reserve(size_t(n) * 5);
   for (int64_t i = 0; i < n; ++i) {
@@ -226,7 +244,7 @@ std::vector<int64_t> latest_conflict(const mx_adamw_tensor* t, int64_t n, bool a
       if (ptr) iv.push_back({reinterpret_cast<uintptr_t>(ptr), reinterpret_cast<uintptr_t>(ptr) + bytes, i, w});
     };
     add(t[i].param, true);
-    add(t[i].grad, false);
+    add(t[i].grad, grads_written);
     add(t[i].exp_avg, true);
     add(t[i].exp_avg_sq, true);
     if (ams) add(t[i].max_exp_avg_sq, true);
@@ -270,7 +288,7 @@ extern "C" int mx_adamw_step(const mx_adamw_tensor* tensors, int64_t count, cons
     MX_REQUIRE(t.step_dev || t.step >= 1, MX_ERR_INVALID, "fused AdamW batch: step must be positive");
   }
   hipStream_t s = resolve_stream(stream);
-  const std::vector<int64_t> conf = latest_conflict(tensors, count, ams);
+  const std::vector<int64_t> conf = latest_conflict(tensors, count, ams, h.grad_scale != nullptr);
   AdamHP hp{};
   hp.lr = h.lr;
   hp.beta1 = h.beta1;
