@@ -15,6 +15,7 @@
 #include <torch/extension.h>
 
 #include <array>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -59,9 +60,14 @@ namespace {
 constexpr int kMaxDev = 64;
 thread_local std::array<c10::StreamId, kMaxDev> tl_stream{};  // 0 = default stream
 
+// Side streams: a fixed pool per device, created on first use and handed out
+// round-robin (as CUDA's stream pool does), so code that asks for a new
+// stream per iteration reuses the same few HIP streams.
+constexpr int kPoolSize = 32;
 std::mutex g_stream_mu;
 std::array<void*, kMaxDev> g_default{};
-std::array<std::vector<void*>, kMaxDev> g_pool;  // id k >= 1 -> g_pool[dev][k-1]
+std::array<std::array<void*, kPoolSize>, kMaxDev> g_pool{};  // id k >= 1 -> g_pool[dev][k-1]
+std::array<uint32_t, kMaxDev> g_next{};
 
 }  // namespace
 
@@ -87,8 +93,17 @@ void* stream_for_id(c10::DeviceIndex device, c10::StreamId id) {
     }
     return g_default[dev];
   }
-  TORCH_CHECK(id >= 1 && size_t(id) <= g_pool[dev].size(), "vulkan: unknown stream id ", id);
+  TORCH_CHECK(id >= 1 && id <= kPoolSize && g_pool[dev][size_t(id - 1)], "vulkan: unknown stream id ", id);
   return g_pool[dev][size_t(id - 1)];
+}
+
+// Number of side streams created on `device` so far (at most kPoolSize).
+int stream_pool_size(int device) {
+  TORCH_CHECK(device >= 0 && device < kMaxDev, "vulkan: device index out of range");
+  std::lock_guard<std::mutex> lock(g_stream_mu);
+  int n = 0;
+  for (void* s : g_pool[device]) n += s != nullptr;
+  return n;
 }
 
 void* current_stream() {
@@ -97,15 +112,19 @@ void* current_stream() {
 }
 
 static c10::StreamId new_stream_id(int dev) {
-  const int prev = cur_dev();
-  if (prev != dev) TVK_MX(mx_set_device(dev));
-  void* s = nullptr;
-  const int rc = mx_stream_create(&s);
-  if (prev != dev) mx_set_device(prev);
-  TORCH_CHECK(rc == MX_OK, mx_last_error());
+  TORCH_CHECK(dev >= 0 && dev < kMaxDev, "vulkan: device index out of range");
   std::lock_guard<std::mutex> lock(g_stream_mu);
-  g_pool[dev].push_back(s);
-  return c10::StreamId(g_pool[dev].size());
+  const uint32_t slot = g_next[dev]++ % kPoolSize;
+  if (!g_pool[dev][slot]) {
+    const int prev = cur_dev();
+    if (prev != dev) TVK_MX(mx_set_device(dev));
+    void* s = nullptr;
+    const int rc = mx_stream_create(&s);
+    if (prev != dev) mx_set_device(prev);
+    TORCH_CHECK(rc == MX_OK, mx_last_error());
+    g_pool[dev][slot] = s;
+  }
+  return c10::StreamId(slot + 1);
 }
 
 // ---------------------------------------------------------------- allocator
@@ -374,8 +393,103 @@ TORCH_LIBRARY_IMPL(_, PrivateUse1, m) {
   m.fallback(torch::CppFunction::makeFromBoxedFunction<&tvk::cpu_fallback_boxed>());
 }
 
+// ------------------------------------------------------------------ GPU timing
+namespace tvk {
+namespace {
+struct TimedPair {
+  std::string name;
+  void* start;
+  void* end;
+  double host_ms;
+};
+std::mutex g_timing_mu;
+std::vector<TimedPair> g_timing_pending;
+std::map<std::string, GpuTiming> g_timing;
+
+double now_ms() {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+}  // namespace
+
+bool gpu_timing_enabled() {
+  const char* v = std::getenv("TORCH_VULKAN_PROFILE_TIMESTAMPS");
+  return v && std::strcmp(v, "1") == 0;
+}
+
+GpuTimer::GpuTimer(std::string name) {
+  if (!gpu_timing_enabled()) return;
+  name_ = std::move(name);
+  stream_ = current_stream();
+  TVK_MX(mx_event_create(&start_, 1));
+  TVK_MX(mx_event_record(start_, stream_));
+  host_t0_ = now_ms();
+}
+
+GpuTimer::~GpuTimer() {
+  if (!start_) return;
+  void* end = nullptr;
+  if (mx_event_create(&end, 1) != MX_OK || mx_event_record(end, stream_) != MX_OK) {
+    mx_event_destroy(start_);
+    if (end) mx_event_destroy(end);
+    return;
+  }
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  g_timing_pending.push_back({name_, start_, end, now_ms() - host_t0_});
+}
+
+std::map<std::string, GpuTiming> gpu_timing_stats() {
+  std::vector<TimedPair> pending;
+  {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    pending.swap(g_timing_pending);
+  }
+  std::map<std::string, GpuTiming> add;
+  for (const TimedPair& t : pending) {
+    float ms = 0.f;
+    const bool ok = mx_event_synchronize(t.end) == MX_OK && mx_event_elapsed_ms(t.start, t.end, &ms) == MX_OK;
+    mx_event_destroy(t.start);
+    mx_event_destroy(t.end);
+    GpuTiming& a = add[t.name];
+    a.samples++;
+    a.host_eval_ms += t.host_ms;
+    if (ok) a.shader_ms += ms;
+  }
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  for (const auto& [name, a] : add) {
+    GpuTiming& g = g_timing[name];
+    g.samples += a.samples;
+    g.shader_ms += a.shader_ms;
+    g.host_eval_ms += a.host_eval_ms;
+  }
+  return g_timing;
+}
+
+void reset_gpu_timing_stats() {
+  gpu_timing_stats();
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  g_timing.clear();
+}
+
+}  // namespace tvk
+
 // ------------------------------------------------------------------- pybind
 namespace {
+
+
+py::dict gpu_timing_dict() {
+  py::dict res;
+  for (const auto& [name, v] : tvk::gpu_timing_stats()) {
+    py::dict d;
+    d["samples"] = v.samples;
+    d["shader_ms"] = v.shader_ms;
+    d["host_eval_ms"] = v.host_eval_ms;
+    // Buffers stay resident on the device: there is no per-op upload or download.
+    d["upload_ms"] = 0.0;
+    d["download_ms"] = 0.0;
+    res[py::str(name)] = std::move(d);
+  }
+  return res;
+}
 
 py::dict execution_stats() {
   auto& c = tvk::counters();
@@ -465,6 +579,9 @@ PYBIND11_MODULE(_C, m) {
         .exchangeStream(c10::Stream(c10::Stream::UNSAFE, c10::Device(c10::DeviceType::PrivateUse1, d), stream_id));
   });
   m.def("_stream_ptr", [](int64_t id, int device) { return reinterpret_cast<uintptr_t>(tvk::stream_for_id(device, id)); });
+  m.def("_stream_pool_size", [](int device) { return tvk::stream_pool_size(device); });
+  m.def("_gpu_timing_stats", &gpu_timing_dict);
+  m.def("_reset_gpu_timing_stats", &tvk::reset_gpu_timing_stats);
   m.def("_manual_seed", [](uint64_t seed) {
     for (int d = 0; d < std::max(1, device_count()); ++d) {
       auto& g = tvk::default_generator(c10::DeviceIndex(d));

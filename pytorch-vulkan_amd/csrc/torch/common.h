@@ -30,6 +30,7 @@ int cur_dev();
 void* current_stream();
 // Stream object for c10 stream ids.
 void* stream_for_id(c10::DeviceIndex device, c10::StreamId id);
+int stream_pool_size(int device);
 
 c10::Allocator* allocator();
 
@@ -55,6 +56,32 @@ void clear_selection_stats();
 // Host fallback bookkeeping: increments the counter, honours
 // TORCH_VULKAN_FORBID_CPU_FALLBACK and TORCH_VULKAN_TRACE_FALLBACK.
 void note_cpu_fallback(const char* what);
+
+// Opt-in GPU timing of the hot-path ops (TORCH_VULKAN_PROFILE_TIMESTAMPS=1,
+// the reference's knob, csrc/vulkan_context.cpp:368-404): a scope records a
+// HIP event pair on the current stream around the op's launches under `name`
+// (the kernel the op runs); gpu_timing_stats() waits for the pairs and sums
+// them per name.  When the knob is off a scope costs one getenv.
+bool gpu_timing_enabled();
+class GpuTimer {
+ public:
+  explicit GpuTimer(std::string name);
+  ~GpuTimer();
+  GpuTimer(const GpuTimer&) = delete;
+  GpuTimer& operator=(const GpuTimer&) = delete;
+
+ private:
+  std::string name_;
+  void* start_ = nullptr;
+  void* stream_ = nullptr;
+  double host_t0_ = 0;
+};
+struct GpuTiming {
+  uint64_t samples = 0;
+  double shader_ms = 0, host_eval_ms = 0;
+};
+std::map<std::string, GpuTiming> gpu_timing_stats();
+void reset_gpu_timing_stats();
 
 inline bool is_vk(const at::Tensor& t) { return t.defined() && t.device().type() == c10::DeviceType::PrivateUse1; }
 

@@ -87,6 +87,7 @@ void run(const Lists& l, double lr, double beta1, double beta2, double eps, doub
     hp.found_inf = fi_t.data_ptr<float>();
   }
   int64_t launches = 0;
+  GpuTimer timer(gpu_timing_enabled() ? (l.vmax ? "adamw_kernel<amsgrad>" : "adamw_kernel") : "");
   TVK_MX(mx_adamw_step(tab.data(), int64_t(n), &hp, &launches, current_stream()));
   counters().kernel_launches += uint64_t(launches);
   counters().adamw_launches += uint64_t(launches);

@@ -62,6 +62,14 @@ void run_gemm(const at::Tensor& a, const at::Tensor& b, at::Tensor& out, int64_t
     d.bias_offset = bias->storage_offset();
     bias_ptr = static_cast<const float*>(bias->storage().data());
   }
+  std::string label;
+  if (gpu_timing_enabled()) {
+    char buf[128];
+    label = mx_gemm_variant(&d, static_cast<const float*>(a.storage().data()),
+                            static_cast<const float*>(b.storage().data()), buf, sizeof buf) == MX_OK
+                ? std::string(buf) : "gemm";
+  }
+  GpuTimer timer(label);
   TVK_MX(mx_gemm_f32(&d, static_cast<const float*>(a.storage().data()), static_cast<const float*>(b.storage().data()),
                      bias_ptr, static_cast<float*>(out.storage().mutable_data()), current_stream()));
   counters().kernel_launches++;

@@ -35,6 +35,7 @@ from . import _C  # noqa: E402  (registers PrivateUse1 as "vulkan", hooks, alloc
 __all__ = [
     "is_available", "device_count", "current_device", "set_device", "synchronize", "device_name",
     "execution_stats", "reset_execution_stats", "conv_dispatch_stats", "clear_conv_dispatch_cache",
+    "gpu_timing_stats", "reset_gpu_timing_stats",
     "memory_stats", "empty_cache", "queue_stats", "performance_options", "Stream", "Event",
     "current_stream", "default_stream", "set_stream", "stream", "manual_seed", "manual_seed_all",
     "device",
@@ -110,6 +111,20 @@ def queue_stats() -> dict:
     """Launch counter under the reference's key name (``recorded_ops``)."""
     s = _C._execution_stats()
     return {"recorded_ops": s["kernel_launches"], "adamw_launches": s["adamw_launches"]}
+
+
+def gpu_timing_stats() -> dict:
+    """Per-kernel GPU time of the conv / GEMM / AdamW ops since the last reset,
+    recorded when ``TORCH_VULKAN_PROFILE_TIMESTAMPS=1`` (the reference's
+    opt-in knob): ``{kernel: {"samples", "shader_ms", "host_eval_ms",
+    "upload_ms", "download_ms"}}``.  Waits for the timed work to finish.
+    ``shader_ms`` is the time between HIP events recorded around each op on
+    its stream; buffers never leave the device, so upload / download are 0."""
+    return dict(_C._gpu_timing_stats())
+
+
+def reset_gpu_timing_stats() -> None:
+    _C._reset_gpu_timing_stats()
 
 
 def conv_dispatch_stats() -> dict:

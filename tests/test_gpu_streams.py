@@ -207,3 +207,21 @@ def test_copy_overlaps_compute(vk, long_operands):
     t_both = min(_timed(vk, both) for _ in range(3))
     assert torch.equal(dst.cpu(), h)
     assert t_both < 0.9 * (t_copy + t_gemm), f"copy {t_copy:.2f}, gemm {t_gemm:.2f}, both {t_both:.2f} ms"
+
+
+def test_new_streams_come_from_a_fixed_pool(vk):
+    """Stream() hands out the device's pooled HIP streams round-robin: a
+    thousand requests create at most the pool's 32 streams, and each stream
+    still orders its own work."""
+    from torch_vulkan import _C
+    streams = [vk.Stream() for _ in range(1000)]
+    assert _C._stream_pool_size(0) <= 32
+    assert len({s.stream_id for s in streams}) <= 32
+    x = torch.arange(1 << 16, dtype=torch.float32).to("vulkan")
+    for s in streams[:40]:
+        s.wait_stream(vk.current_stream())
+        with vk.stream(s):
+            y = x * 2
+        s.synchronize()
+        assert torch.equal(y.cpu(), torch.arange(1 << 16, dtype=torch.float32) * 2)
+    assert _C._stream_pool_size(0) <= 32

@@ -477,6 +477,38 @@ def test_torch_optim_adamw_fused_runs_on_device(amsgrad, vk):
     assert vk.execution_stats()["cpu_fallback_calls"] == fb
 
 
+@pytest.mark.parametrize("maximize", [False, True])
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_fused_adamw_grad_scale_and_found_inf(no_fallback, amsgrad, maximize):
+    """aten::_fused_adamw_ under a GradScaler: with found_inf == 0 the
+    gradients are divided by grad_scale, the unscaled gradients are written
+    back (before maximize negates them) and the step runs; with found_inf == 1
+    nothing changes.  Compared with CPU torch._fused_adamw_ bit for bit on the
+    gradients and within rel 1e-4 / abs 1e-5 on parameters and moments."""
+    torch.manual_seed(21)
+    shapes = [(37, 5), (4099,), (3,)]
+    kw = dict(lr=3e-3, beta1=0.85, beta2=0.995, weight_decay=0.02, eps=1e-7, amsgrad=amsgrad, maximize=maximize)
+    for found in (0.0, 1.0):
+        cpu = {k: [torch.randn(sh) * (4.0 if k == "g" else 1.0) for sh in shapes] for k in ("p", "g")}
+        cpu["m"] = [torch.randn(sh) * 0.1 for sh in shapes]
+        cpu["v"] = [torch.rand(sh) * 0.01 for sh in shapes]
+        cpu["x"] = [v.clone() * 1.5 for v in cpu["v"]] if amsgrad else []
+        steps_c = [torch.tensor(3.0) for _ in shapes]
+        dev = {k: [t.to("vulkan") for t in ts] for k, ts in cpu.items()}
+        steps_d = [t.to("vulkan") for t in steps_c]
+        scale, inf = torch.tensor(8.0), torch.tensor(found)
+        torch._fused_adamw_(cpu["p"], cpu["g"], cpu["m"], cpu["v"], cpu["x"], steps_c, grad_scale=scale,
+                            found_inf=inf, **kw)
+        torch._fused_adamw_(dev["p"], dev["g"], dev["m"], dev["v"], dev["x"], steps_d,
+                            grad_scale=scale.to("vulkan"), found_inf=inf.to("vulkan"), **kw)
+        for k in ("g", "p", "m", "v", "x"):
+            for c, d in zip(cpu[k], dev[k]):
+                if k == "g":
+                    assert torch.equal(d.cpu(), c), f"found_inf={found}: gradient not unscaled as torch does"
+                else:
+                    torch.testing.assert_close(d.cpu(), c, rtol=1e-4, atol=1e-5)
+
+
 def test_fallback_is_counted_and_forbiddable(vk, monkeypatch):
     x = torch.randn(5).to("vulkan")
     before = vk.execution_stats()["cpu_fallback_calls"]
@@ -485,3 +517,77 @@ def test_fallback_is_counted_and_forbiddable(vk, monkeypatch):
     monkeypatch.setenv("TORCH_VULKAN_FORBID_CPU_FALLBACK", "1")
     with pytest.raises(RuntimeError, match="forbidden"):
         torch.exp(x)
+
+
+def test_gpu_timing_stats(vk, monkeypatch):
+    """gpu_timing_stats() (the reference's torch_vulkan.gpu_timing_stats,
+    opt-in through TORCH_VULKAN_PROFILE_TIMESTAMPS=1) reports the kernels of
+    timed conv / GEMM / AdamW ops with their GPU time, and nothing while off."""
+    vk.reset_gpu_timing_stats()
+    x = torch.randn(2, 16, 12, 12).to("vulkan").requires_grad_()
+    w = torch.randn(16, 16, 3, 3).to("vulkan").requires_grad_()
+    F.conv2d(x, w, padding=1)
+    assert vk.gpu_timing_stats() == {}
+    monkeypatch.setenv("TORCH_VULKAN_PROFILE_TIMESTAMPS", "1")
+    y = F.conv2d(x, w, padding=1)
+    y.backward(torch.ones_like(y))
+    a = torch.randn(300, 200).to("vulkan")
+    a @ a.t()
+    p = torch.nn.Parameter(torch.randn(1000).to("vulkan"))
+    p.grad = torch.randn(1000).to("vulkan")
+    from torch_vulkan.optim import AdamW as VkAdamW
+    VkAdamW([p]).step()
+    stats = vk.gpu_timing_stats()
+    names = " ".join(stats)
+    for kind in ("conv_fwd_kernel", "conv_dx_kernel", "conv_dw_kernel", "gemm_kernel", "adamw_kernel"):
+        assert kind in names, (kind, stats)
+    for name, v in stats.items():
+        assert v["samples"] >= 1 and v["shader_ms"] > 0 and v["host_eval_ms"] >= 0, (name, v)
+        assert v["upload_ms"] == 0 and v["download_ms"] == 0
+    monkeypatch.delenv("TORCH_VULKAN_PROFILE_TIMESTAMPS")
+    before = {k: v["samples"] for k, v in vk.gpu_timing_stats().items()}
+    a @ a.t()
+    assert {k: v["samples"] for k, v in vk.gpu_timing_stats().items()} == before
+    vk.reset_gpu_timing_stats()
+    assert vk.gpu_timing_stats() == {}
+
+
+@pytest.mark.parametrize("budget_mb", ["1", "64"])
+def test_weight_split_scales_to_workspace_through_torch(vk, monkeypatch, budget_mb):
+    """/root/reference/tests/test_conv_dispatch.py:255-297 through the vulkan
+    device: a many-way dWeight split forced around the weight-gradient call
+    shrinks to the TORCH_VULKAN_CONV_WORKSPACE_MB budget (the dispatch
+    counters record splits, span and workspace), and dW / dB match float64."""
+    monkeypatch.setenv("TORCH_VULKAN_CONV_BACKWARD_ALGO", "optimized")
+    monkeypatch.setenv("TORCH_VULKAN_CONV_WORKSPACE_MB", budget_mb)
+    g = torch.Generator().manual_seed(31)
+    x, w, b = torch.randn(1, 48, 64, 64, generator=g), torch.randn(96, 48, 3, 3, generator=g) * 0.05, torch.randn(96)
+    gy = torch.randn(1, 96, 64, 64, generator=g)
+    prior = vk.conv_dispatch_stats()
+    monkeypatch.setenv("MX_CONV_PLAN", "5,512")
+    _, dw, db = torch.ops.aten.convolution_backward.default(
+        gy.to("vulkan"), x.to("vulkan"), w.to("vulkan"), [96], [1, 1], [1, 1], [1, 1], False, [0, 0], 1,
+        [False, True, True])
+    monkeypatch.delenv("MX_CONV_PLAN")
+    stats = vk.conv_dispatch_stats()
+    delta = {k: stats.get(k, 0) - prior.get(k, 0) for k in stats}
+    parts, span = delta["dweight_tiled_split_count_total"], delta["dweight_tiled_split_span_total"]
+    assert delta["dweight_tiled_dispatches"] == 1 and parts >= 2
+    assert (parts - 1) * span < 64 * 64 <= parts * span
+    assert delta["dweight_tiled_workspace_bytes_total"] <= int(budget_mb) << 20
+    refs = conv_refs(x, w, b, gy, (1, 1), (1, 1), (1, 1), 1)
+    assert_close_mag(dw, *refs["dw"], what="dw")
+    assert_close_mag(db, *refs["db"], what="db")
+
+
+def test_forced_split_rejects_zero_workspace_through_torch(vk, monkeypatch):
+    """/root/reference/tests/test_conv_dispatch.py:302-313."""
+    monkeypatch.setenv("TORCH_VULKAN_CONV_BACKWARD_ALGO", "optimized")
+    monkeypatch.setenv("TORCH_VULKAN_CONV_WORKSPACE_MB", "0")
+    monkeypatch.setenv("MX_CONV_PLAN", "5,2")
+    x = torch.zeros((1, 9, 1, 257), device="vulkan")
+    w = torch.zeros((17, 9, 1, 1), device="vulkan")
+    go = torch.zeros((1, 17, 1, 257), device="vulkan")
+    with pytest.raises(RuntimeError, match="[Ww]orkspace"):
+        torch.ops.aten.convolution_backward.default(go, x, w, [17], [1, 1], [0, 0], [1, 1], False, [0, 0], 1,
+                                                    [False, True, False])
