@@ -1,25 +1,127 @@
 """Opt-in fused AdamW for ``"vulkan"`` parameters.
 
-Same API, state keys and checkpoint behaviour as the reference's
-torch_vulkan/optim.py:13-75: state is created lazily with ``zeros_like``, the
-step is a host int (a tensor step restored from a ``torch.optim.AdamW``
-checkpoint is converted), and every parameter group is updated by one call of
-``torch.ops.torch_vulkan.adamw_step_batch_`` (or the AMSGrad variant), which
-the backend runs as a single multi-tensor launch.  ``torch.optim.AdamW(fused=True)``
-also runs on the device (``aten::_fused_adamw_``).
+Interface of the reference's ``torch_vulkan.optim.AdamW``
+(torch_vulkan/optim.py:13-75 there): the constructor keywords ``lr``,
+``betas``, ``eps``, ``weight_decay``, ``batched`` and ``amsgrad``, and per
+parameter the state keys of ``torch.optim.AdamW`` (``step``, ``exp_avg``,
+``exp_avg_sq``, ``max_exp_avg_sq``), so checkpoints move between this
+optimizer and torch's.
+
+How it runs here: each parameter group becomes one ``_GroupStep`` -- the
+parameters that have gradients, their moment buffers and their host step
+counts -- which is handed to the backend's custom ops
+(``torch.ops.torch_vulkan.adamw_step_batch_`` / ``adamw_amsgrad_step_batch_``,
+schemas of csrc/ops/adamw.cpp:307-317).  The backend turns one batch call into
+one multi-tensor launch over every tensor of the group (a new launch only where
+two entries alias).  ``batched=False`` issues one call per parameter instead
+(``adamw_step_`` for plain AdamW; the AMSGrad variant has no single-tensor op,
+so it gets a one-entry batch).  ``torch.optim.AdamW(fused=True)`` also runs on
+the device, through ``aten::_fused_adamw_``.
 """
 from __future__ import annotations
 
+from dataclasses import dataclass, field
+
 import torch
+
+_ops = None
+
+
+def _backend_ops():
+    global _ops
+    if _ops is None:
+        _ops = torch.ops.torch_vulkan
+    return _ops
+
+
+def _check_hyperparameters(lr, betas, eps, weight_decay):
+    beta1, beta2 = betas
+    problems = [name for name, ok in (("lr", lr >= 0), ("eps", eps >= 0), ("weight_decay", weight_decay >= 0),
+                                      ("beta1", 0 <= beta1 < 1), ("beta2", 0 <= beta2 < 1)) if not ok]
+    if problems:
+        raise ValueError(f"AdamW: out-of-range hyperparameter(s) {', '.join(problems)} "
+                         f"(lr={lr}, betas={betas}, eps={eps}, weight_decay={weight_decay})")
+
+
+def _host_step(value) -> int:
+    """A step count as a Python int (torch.optim checkpoints store a tensor)."""
+    return int(value.item()) if isinstance(value, torch.Tensor) else int(value)
+
+
+@dataclass
+class _GroupStep:
+    """The tensors of one parameter group that take part in this step."""
+    amsgrad: bool
+    params: list = field(default_factory=list)
+    grads: list = field(default_factory=list)
+    exp_avgs: list = field(default_factory=list)
+    exp_avg_sqs: list = field(default_factory=list)
+    max_exp_avg_sqs: list = field(default_factory=list)
+    steps: list = field(default_factory=list)
+
+    def add(self, p, state):
+        self.params.append(p)
+        self.grads.append(p.grad)
+        self.exp_avgs.append(state["exp_avg"])
+        self.exp_avg_sqs.append(state["exp_avg_sq"])
+        if self.amsgrad:
+            self.max_exp_avg_sqs.append(state["max_exp_avg_sq"])
+        self.steps.append(state["step"])
+
+    def lists(self, sl=slice(None)):
+        out = [self.params[sl], self.grads[sl], self.exp_avgs[sl], self.exp_avg_sqs[sl]]
+        if self.amsgrad:
+            out.append(self.max_exp_avg_sqs[sl])
+        return out
+
+    def launch(self, hyper, batched):
+        ops = _backend_ops()
+        batch_op = ops.adamw_amsgrad_step_batch_ if self.amsgrad else ops.adamw_step_batch_
+        if batched:
+            batch_op(*self.lists(), *hyper, self.steps)
+            return
+        for i in range(len(self.params)):
+            if self.amsgrad:
+                batch_op(*self.lists(slice(i, i + 1)), *hyper, self.steps[i:i + 1])
+            else:
+                ops.adamw_step_(*(lst[i] for lst in self.lists()), *hyper, self.steps[i])
 
 
 class AdamW(torch.optim.Optimizer):
+    """Decoupled-weight-decay Adam whose update runs as multi-tensor gfx950
+    launches (see the module docstring)."""
+
     def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2, batched=True,
                  amsgrad=False):
-        if lr < 0 or eps < 0 or weight_decay < 0 or not all(0 <= b < 1 for b in betas):
-            raise ValueError("Invalid AdamW hyperparameters")
-        super().__init__(params, dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, batched=batched,
-                                      amsgrad=amsgrad))
+        _check_hyperparameters(lr, betas, eps, weight_decay)
+        defaults = {"lr": lr, "betas": betas, "eps": eps, "weight_decay": weight_decay, "batched": batched,
+                    "amsgrad": amsgrad}
+        super().__init__(params, defaults)
+
+    def _state_of(self, p, amsgrad):
+        """The parameter's state, created on first use; the step advanced by one."""
+        state = self.state[p]
+        state.setdefault("step", 0)
+        # Missing buffers start at zero (a fresh parameter, or a checkpoint
+        # written without AMSGrad that is resumed with it).
+        for key in ("exp_avg", "exp_avg_sq") + (("max_exp_avg_sq",) if amsgrad else ()):
+            if key not in state:
+                state[key] = torch.zeros_like(p, memory_format=torch.preserve_format)
+        state["step"] = _host_step(state["step"]) + 1
+        return state
+
+    def _collect(self, group) -> _GroupStep:
+        batch = _GroupStep(amsgrad=bool(group["amsgrad"]))
+        for p in group["params"]:
+            g = p.grad
+            if g is None:
+                continue
+            if g.is_sparse:
+                raise RuntimeError("torch_vulkan AdamW: sparse gradients are not supported")
+            if p.device.type != "vulkan":
+                raise RuntimeError(f"torch_vulkan AdamW: parameter on {p.device}, expected a vulkan tensor")
+            batch.add(p, self._state_of(p, batch.amsgrad))
+        return batch
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -28,44 +130,10 @@ class AdamW(torch.optim.Optimizer):
             with torch.enable_grad():
                 loss = closure()
         for group in self.param_groups:
-            beta1, beta2 = group["betas"]
-            params, grads, m1, m2, mx, steps = [], [], [], [], [], []
-            for p in group["params"]:
-                if p.grad is None:
-                    continue
-                if p.grad.is_sparse:
-                    raise RuntimeError("Vulkan AdamW does not support sparse gradients")
-                if p.device.type != "vulkan":
-                    raise RuntimeError("Vulkan AdamW only supports Vulkan parameters")
-                state = self.state[p]
-                if not state:
-                    state["step"] = 0
-                    state["exp_avg"] = torch.zeros_like(p)
-                    state["exp_avg_sq"] = torch.zeros_like(p)
-                    if group["amsgrad"]:
-                        state["max_exp_avg_sq"] = torch.zeros_like(p)
-                if isinstance(state["step"], torch.Tensor):
-                    state["step"] = int(state["step"].item())
-                state["step"] += 1
-                params.append(p)
-                grads.append(p.grad)
-                m1.append(state["exp_avg"])
-                m2.append(state["exp_avg_sq"])
-                if group["amsgrad"]:
-                    mx.append(state["max_exp_avg_sq"])
-                steps.append(state["step"])
-            if not params:
+            batch = self._collect(group)
+            if not batch.params:
                 continue
-            hp = (group["lr"], beta1, beta2, group["eps"], group["weight_decay"])
-            if group["amsgrad"]:
-                if group.get("batched", True):
-                    torch.ops.torch_vulkan.adamw_amsgrad_step_batch_(params, grads, m1, m2, mx, *hp, steps)
-                else:
-                    for args in zip(params, grads, m1, m2, mx, steps):
-                        torch.ops.torch_vulkan.adamw_amsgrad_step_batch_(*[[a] for a in args[:5]], *hp, [args[5]])
-            elif group.get("batched", True):
-                torch.ops.torch_vulkan.adamw_step_batch_(params, grads, m1, m2, *hp, steps)
-            else:
-                for p, g, a, b, s in zip(params, grads, m1, m2, steps):
-                    torch.ops.torch_vulkan.adamw_step_(p, g, a, b, *hp, s)
+            beta1, beta2 = group["betas"]
+            hyper = (group["lr"], beta1, beta2, group["eps"], group["weight_decay"])
+            batch.launch(hyper, group.get("batched", True))
         return loss
