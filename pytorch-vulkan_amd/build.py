@@ -8,9 +8,10 @@ Outputs (next to the Python package so they travel with the source tree):
   torch_vulkan/_C.so     PrivateUse1 "vulkan" operator surface (C++ against
                          the installed torch headers), linked to libmx.so.
 
-Both link the HIP runtime that ships inside the installed torch wheel
+libmx.so links the HIP runtime that ships inside the installed torch wheel
 (torch/lib/libamdhip64.so) so that a process which imports torch never loads
-a second HIP runtime.
+a second HIP runtime; with a wheel that has none (a CPU-only torch, which the
+drop-in surface supports) it links ROCm's own runtime (ROCM_PATH/lib).
 """
 from __future__ import annotations
 
@@ -116,6 +117,28 @@ def stale(target: Path, deps: list[Path]) -> bool:
     return any(d.stat().st_mtime > t for d in deps)
 
 
+def hip_runtime_dir(torch_lib: str) -> str:
+    """Directory of the HIP runtime libmx.so links and finds at run time: the
+    torch wheel's own copy when it ships one, else ROCm's."""
+    if any(Path(torch_lib).glob("libamdhip64.so*")):
+        return torch_lib
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib"
+    if any(rocm.glob("libamdhip64.so*")):
+        return str(rocm)
+    raise RuntimeError(f"no libamdhip64.so in {torch_lib} or {rocm}: the HIP runtime is needed to link libmx.so")
+
+
+def link_mx(objs, out: Path, runtime_dir: str) -> None:
+    """Plain host link (non-relocatable device code needs no device link
+    step); hipcc would add -lamdhip64 from /opt/rocm even where torch ships
+    its own runtime."""
+    tmp = out.with_name(out.name + ".tmp")
+    cxx = os.environ.get("CXX", "g++")
+    run([cxx, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+         f"-L{runtime_dir}", f"-Wl,-rpath,{runtime_dir}", "-lamdhip64", "-Wl,--no-undefined"])
+    tmp.replace(out)
+
+
 def build_mx(jobs: int, incremental: bool) -> Path:
     BUILD.mkdir(exist_ok=True)
     OUT.mkdir(exist_ok=True)
@@ -132,13 +155,7 @@ def build_mx(jobs: int, incremental: bool) -> Path:
         wait_all([ex.submit(compile_hip, c) for c in todo])
     lib = OUT / "libmx.so"
     if not incremental or stale(lib, objs):
-        tmp = OUT / "libmx.so.tmp"
-        # Plain host link (non-relocatable device code needs no device link
-        # step); hipcc would add -lamdhip64 from /opt/rocm (a second runtime).
-        cxx = os.environ.get("CXX", "g++")
-        run([cxx, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-             f"-L{torch_lib}", f"-Wl,-rpath,{torch_lib}", "-lamdhip64", "-Wl,--no-undefined"])
-        tmp.replace(lib)
+        link_mx(objs, lib, hip_runtime_dir(torch_lib))
     return lib
 
 

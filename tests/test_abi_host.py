@@ -38,6 +38,30 @@ def test_library_links_torch_hip_runtime_only():
     assert "libamdhip64" in out and "torch/lib" in out
 
 
+def test_link_resolves_without_the_wheels_hip_runtime(tmp_path):
+    """With a torch wheel that ships no HIP runtime (CPU-only torch) libmx.so
+    links ROCm's: the link of the built objects succeeds against an empty
+    torch lib directory and the library's rpath then points at ROCm."""
+    import glob
+    import subprocess
+    import sys
+    sys.path.insert(0, os.path.join(REPO, "pytorch-vulkan_amd"))
+    import build
+    objs = sorted(glob.glob(os.path.join(REPO, "pytorch-vulkan_amd", "_build", "mx_*.o")))
+    if len(objs) < len(build.MX_SOURCES):
+        pytest.skip("objects not built (run build.py first)")
+    empty = tmp_path / "torch_lib"
+    empty.mkdir()
+    runtime = build.hip_runtime_dir(str(empty))
+    assert runtime != str(empty) and glob.glob(os.path.join(runtime, "libamdhip64.so*"))
+    out = tmp_path / "libmx.so"
+    build.link_mx(objs, out, runtime)
+    dyn = subprocess.run(["readelf", "-d", str(out)], capture_output=True, text=True).stdout
+    assert "libamdhip64" in dyn and runtime in dyn and "torch/lib" not in dyn
+    ldd = subprocess.run(["ldd", str(out)], capture_output=True, text=True).stdout
+    assert "not found" not in ldd and runtime in ldd
+
+
 def test_conv_check_fills_output_shape(mx):
     d = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (1, 1))
     assert (d.oh, d.ow) == (56, 56)
