@@ -211,6 +211,23 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
 int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const float* dy,
                               float* dw, float* db, int algo, void* stream);
 
+/* Allocation-free dWeight / dBias.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory while they run (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, algorithms and results as mx_conv2d_backward_weight, but
+ * every scratch buffer (split-K partials, Winograd range partials, the partial
+ * gradient of a batch run in chunks) lives in a library-owned device array of
+ * MX_NOALLOC_SCRATCH_BYTES per GPU instead of the allocator: plans are sized
+ * to fit it (and TORCH_VULKAN_CONV_WORKSPACE_MB), and a call whose smallest
+ * plan still needs more fails with MX_ERR_WORKSPACE before any launch.  No
+ * hipMalloc / hipFree / allocator call is made.  Every call on a GPU shares
+ * that GPU's array and overwrites what it reads, so nothing needs clearing;
+ * calls that overlap in time on one GPU (other streams, other threads) race
+ * and must be serialised by the caller. */
+#define MX_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int mx_conv2d_backward_weight_noalloc(const mx_conv2d_desc* desc, const float* x, const float* dy, float* dw,
+                                      float* db, int algo, void* stream);
+
 /* db only (conv2d_backward_bias_reduce.comp:10-24). */
 int mx_conv2d_backward_bias(const mx_conv2d_desc* desc, const float* dy, float* db, void* stream);
 

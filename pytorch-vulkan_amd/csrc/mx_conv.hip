@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -700,7 +701,7 @@ int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, co
 int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, int64_t ws_limit,
                             hipStream_t s);
 int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, int64_t ws_limit,
-                             hipStream_t s);
+                             float* ext, hipStream_t s);
 int winograd_describe(const mx_conv2d_desc& d, int phase, int64_t ws_limit, std::string* variant, int64_t* ws_bytes);
 
 namespace conv {
@@ -956,9 +957,27 @@ int mx_conv2d_backward_bias(const mx_conv2d_desc* desc, const float* dy, float* 
   MX_ABI_END
 }
 
-int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const float* dy, float* dw, float* db,
-                              int algo, void* stream) {
-  MX_ABI_BEGIN
+}  // extern "C"
+
+// Scratch of mx_conv2d_backward_weight_noalloc: one array per GPU, in the
+// library's code object, so calls allocate nothing.  Host code uses the device
+// address hipGetSymbolAddress returns for the current GPU (noalloc_scratch),
+// never the array's name.
+namespace mx {
+namespace noalloc {
+__device__ __align__(256) float scratch[MX_NOALLOC_SCRATCH_BYTES / 4];
+}  // namespace noalloc
+}  // namespace mx
+
+namespace {
+
+// dW (+ dB) of one call.  Scratch (split-K partials, the Winograd range
+// partials, the partial gradients of a batch split into chunks) comes from
+// `ext` when the caller provides `ext_bytes` of it, else from the
+// stream-ordered allocator; with `ext` every plan is sized to fit and nothing
+// is allocated.
+int dweight_impl(const mx_conv2d_desc* desc, const float* x, const float* dy, float* dw, float* db, int algo,
+                 float* ext, int64_t ext_bytes, void* stream) {
   mx_conv2d_desc d = *desc;
   MX_TRY(checked_desc(&d));
   MX_REQUIRE(x && dy, MX_ERR_INVALID, "conv2d dweight: null tensor");
@@ -968,6 +987,7 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
   MX_TRY(select_algo(d, MX_CONV_DWEIGHT, algo, &chosen));
   int64_t limit = 0;
   MX_TRY(conv::workspace_limit(&limit));
+  if (ext) limit = std::min(limit, ext_bytes);
   hipStream_t s = resolve_stream(stream);
   if (chosen == MX_CONV_ALGO_DIRECT || chosen == MX_CONV_ALGO_REDUCE) {
     ConvArgs p = make_args(d);
@@ -990,20 +1010,32 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
     MX_REQUIRE(nc > 0, MX_ERR_UNSUPPORTED, "conv2d dweight: one image or the weights exceed the 2 GiB operand bound");
     if (nc < d.n) {
       // Sum of the chunks' gradients: the first chunk writes dw / db, the
-      // others go through a scratch copy added in chunk order.
+      // others go through a scratch copy added in chunk order.  With a caller
+      // workspace that copy takes its tail and the chunks plan within the rest.
       const int64_t nw = d.cout * (d.cin / d.groups) * d.kh * d.kw;
+      const int64_t tmp_bytes = (nw + (db ? d.cout : 0)) * 4;
       Scratch tmp;
-      MX_TRY(tmp.alloc(size_t(nw + (db ? d.cout : 0)) * 4, s));
-      float* tw = tmp.as<float>();
+      float* tw = nullptr;
+      int64_t sub_bytes = 0;
+      if (ext) {
+        MX_REQUIRE(tmp_bytes <= limit, MX_ERR_WORKSPACE, "conv2d dweight: the partial gradient of a chunked batch (",
+                   tmp_bytes, " bytes) exceeds the ", limit, "-byte workspace");
+        sub_bytes = (limit - tmp_bytes) / 256 * 256;
+        tw = ext + sub_bytes / 4;
+      } else {
+        MX_TRY(tmp.alloc(size_t(tmp_bytes), s));
+        tw = tmp.as<float>();
+      }
       float* tb = db ? tw + nw : nullptr;
       for (int64_t n0 = 0; n0 < d.n; n0 += nc) {
         const mx_conv2d_desc c = batch_slice(d, std::min(nc, d.n - n0));
         const float* xc = x + n0 * d.cin * d.h * d.w;
         const float* dyc = dy + n0 * d.cout * d.oh * d.ow;
+        float* sub_ext = ext ? ext : nullptr;
         if (n0 == 0) {
-          MX_TRY(mx_conv2d_backward_weight(&c, xc, dyc, dw, db, chosen, stream));
+          MX_TRY(dweight_impl(&c, xc, dyc, dw, db, chosen, sub_ext, sub_bytes, stream));
         } else {
-          MX_TRY(mx_conv2d_backward_weight(&c, xc, dyc, tw, tb, chosen, stream));
+          MX_TRY(dweight_impl(&c, xc, dyc, tw, tb, chosen, sub_ext, sub_bytes, stream));
           MX_TRY(mx_add_f32(dw, dw, tw, 1.f, nw, stream));
           if (db) MX_TRY(mx_add_f32(db, db, tb, 1.f, d.cout, stream));
         }
@@ -1012,7 +1044,7 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
     }
   }
   if (chosen == MX_CONV_ALGO_WINOGRAD) {
-    MX_TRY(winograd_backward_weight(d, x, dy, dw, limit, s));
+    MX_TRY(winograd_backward_weight(d, x, dy, dw, limit, ext, s));
     return db ? mx_conv2d_backward_bias(desc, dy, db, stream) : MX_OK;
   }
   DwPlan f;
@@ -1020,14 +1052,60 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
   ConvArgs& p = f.p;
   if (f.gp.splits == 1) return conv::conv_dw_launch(p, f.gp.tile, f.amode, f.bmode, s);
   Scratch ws, wsdb;
-  MX_TRY(ws.alloc(size_t(f.ws_bytes), s));
-  p.ws = ws.as<float>();
-  if (db) {
-    MX_TRY(wsdb.alloc(size_t(f.db_bytes), s));
-    p.ws_db = wsdb.as<float>();
+  if (ext) {
+    // The plan fits: ws_bytes + db_bytes <= limit <= ext_bytes.
+    p.ws = ext;
+    p.ws_db = db ? ext + f.ws_bytes / 4 : nullptr;
+  } else {
+    MX_TRY(ws.alloc(size_t(f.ws_bytes), s));
+    p.ws = ws.as<float>();
+    if (db) {
+      MX_TRY(wsdb.alloc(size_t(f.db_bytes), s));
+      p.ws_db = wsdb.as<float>();
+    }
   }
   MX_TRY(conv::conv_dw_launch(p, f.gp.tile, f.amode, f.bmode, s));
   return conv::conv_dw_finalize(p, dw, db, s);
+}
+
+constexpr int64_t kNoAllocBytes = MX_NOALLOC_SCRATCH_BYTES;
+constexpr int kNoAllocDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kNoAllocDevices] = {};
+
+// The current GPU's copy of `scratch`, looked up on the first call there.
+int noalloc_scratch(float** out) {
+  const int dev = current_device();
+  MX_REQUIRE(dev >= 0 && dev < kNoAllocDevices, MX_ERR_INVALID, "device ", dev, " out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    MX_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(mx::noalloc::scratch)));
+    MX_REQUIRE(ptr, MX_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch array");
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return MX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const float* dy, float* dw, float* db,
+                              int algo, void* stream) {
+  MX_ABI_BEGIN
+  return dweight_impl(desc, x, dy, dw, db, algo, nullptr, 0, stream);
+  MX_ABI_END
+}
+
+int mx_conv2d_backward_weight_noalloc(const mx_conv2d_desc* desc, const float* x, const float* dy, float* dw,
+                                      float* db, int algo, void* stream) {
+  MX_ABI_BEGIN
+  MX_REQUIRE(desc, MX_ERR_INVALID, "conv2d dweight: null descriptor");
+  float* ws = nullptr;
+  MX_TRY(noalloc_scratch(&ws));
+  return dweight_impl(desc, x, dy, dw, db, algo, ws, kNoAllocBytes, stream);
   MX_ABI_END
 }
 

@@ -921,24 +921,26 @@ int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, co
 
 // dw of the 3x3 stride-1 layer d (any padding): the fused adjoint kernel
 // over K ranges of tiles, then a fixed-order sum of the ranges' partials.
+// The partials go to `ext` when the caller provides the workspace (at least
+// ws_limit bytes), else to a stream-ordered allocation.
 int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, int64_t ws_limit,
-                             hipStream_t s) {
+                             float* ext, hipStream_t s) {
   DwRunPlan r;
   MX_TRY(plan_dw_run(d, ws_limit, &r));
   fused_dw::Args& p = r.p;
   p.x = x;
   p.dy = dy;
   Scratch ws;
-  if (r.ranges > 1) {
+  float* partials = ext;
+  if (r.ranges > 1 && !ext) {
     MX_TRY(ws.alloc(size_t(r.ranges) * size_t(r.n_dw) * 4, s));
-    p.out = ws.as<float>();
-  } else {
-    p.out = dw;
+    partials = ws.as<float>();
   }
+  p.out = r.ranges > 1 ? partials : dw;
   hipLaunchKernelGGL(fused_dw::wino_dw_kernel, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)), dim3(256), 0,
                      s, p);
   MX_HIP(hipGetLastError());
-  if (r.ranges > 1) return conv::sum_partials(ws.as<float>(), int(r.ranges), r.n_dw, dw, s);
+  if (r.ranges > 1) return conv::sum_partials(partials, int(r.ranges), r.n_dw, dw, s);
   return MX_OK;
 }
 

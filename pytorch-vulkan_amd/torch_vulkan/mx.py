@@ -40,7 +40,7 @@ EXPORTS = [
     "mx_group_norm_forward", "mx_group_norm_backward", "mx_batch_norm_forward", "mx_batch_norm_backward",
     "mx_unary_f32", "mx_unary_backward_f32", "mx_upsample_nearest2d", "mx_upsample_nearest2d_backward",
     "mx_softmax_f32", "mx_softmax_backward_f32", "mx_mse_loss_f32", "mx_mse_loss_backward_f32", "mx_copy_rows",
-    "mx_foreach_f32", "mx_conv2d_plan", "mx_gemm_variant",
+    "mx_foreach_f32", "mx_conv2d_plan", "mx_gemm_variant", "mx_conv2d_backward_weight_noalloc",
 ]
 
 
@@ -144,6 +144,7 @@ def lib() -> C.CDLL:
             "mx_conv2d_forward": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
             "mx_conv2d_backward_input": ([C.POINTER(ConvDesc), vp, vp, vp, i32, vp], i32),
             "mx_conv2d_backward_weight": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
+            "mx_conv2d_backward_weight_noalloc": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
             "mx_conv2d_backward_bias": ([C.POINTER(ConvDesc), vp, vp, vp], i32),
             "mx_conv2d_dweight_plan": ([C.POINTER(ConvDesc), C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)], i32),
             "mx_conv2d_kernel_name": ([C.POINTER(ConvDesc), i32, i32, C.c_char_p, C.c_size_t], i32),
@@ -205,6 +206,15 @@ def conv2d_backward_input(d: ConvDesc, dy, w, dx, algo=ALGO_AUTO, stream=None) -
 
 def conv2d_backward_weight(d: ConvDesc, x, dy, dw, db, algo=ALGO_AUTO, stream=None) -> None:
     check(lib().mx_conv2d_backward_weight(C.byref(d), ptr(x), ptr(dy), ptr(dw), ptr(db), algo, stream))
+
+
+NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # MX_NOALLOC_SCRATCH_BYTES
+
+
+def conv2d_backward_weight_noalloc(d: ConvDesc, x, dy, dw, db, algo=ALGO_AUTO, stream=None) -> None:
+    """mx_conv2d_backward_weight without any device allocation (library-owned
+    scratch; overlapping calls on one GPU race)."""
+    check(lib().mx_conv2d_backward_weight_noalloc(C.byref(d), ptr(x), ptr(dy), ptr(dw), ptr(db), algo, stream))
 
 
 def conv2d_backward_bias(d: ConvDesc, dy, db, stream=None) -> None:
