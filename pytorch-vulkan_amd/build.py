@@ -7,6 +7,8 @@ Outputs (next to the Python package so they travel with the source tree):
                          every gfx950 kernel, built with hipcc.
   torch_vulkan/_C.so     PrivateUse1 "vulkan" operator surface (C++ against
                          the installed torch headers), linked to libmx.so.
+  torch_vulkan/libmxprobe.so  HBM stream probes used by bench.py (not part of
+                         the C ABI).
 
 libmx.so links the HIP runtime that ships inside the installed torch wheel
 (torch/lib/libamdhip64.so) so that a process which imports torch never loads
@@ -159,6 +161,21 @@ def build_mx(jobs: int, incremental: bool) -> Path:
     return lib
 
 
+def build_probe(incremental: bool) -> Path:
+    """torch_vulkan/libmxprobe.so: bench.py's HBM stream probes
+    (csrc/bench/mx_stream_probe.hip), kept apart from the C ABI library."""
+    BUILD.mkdir(exist_ok=True)
+    _, torch_lib = torch_paths()
+    src = CSRC / "bench" / "mx_stream_probe.hip"
+    obj = BUILD / "mx_stream_probe.o"
+    if not incremental or stale(obj, [src]):
+        compile_hip([hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+    lib = OUT / "libmxprobe.so"
+    if not incremental or stale(lib, [obj]):
+        link_mx([obj], lib, hip_runtime_dir(torch_lib))
+    return lib
+
+
 def build_ext(jobs: int, incremental: bool) -> Path:
     BUILD.mkdir(exist_ok=True)
     incs, torch_lib = torch_paths()
@@ -200,6 +217,7 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     if args.only in (None, "mx"):
         print("built", build_mx(args.j, args.incremental))
+        print("built", build_probe(args.incremental))
     if args.only in (None, "ext"):
         print("built", build_ext(args.j, args.incremental))
     return 0

@@ -1,0 +1,118 @@
+// HBM stream probes for bench.py: the access patterns of the multi-tensor
+// AdamW kernel (mx_adamw.hip) with trivial arithmetic, so the benchmark can
+// report AdamW against what the same pattern reaches on the same GPU in the
+// same run.  Measurement infrastructure only: not part of the drop-in C ABI
+// (include/mx.h) and not used by the operator surface.
+//
+//   int mxp_stream(int kind, float* const* bufs, int64_t n, int per_cu, void* stream)
+//
+//   kind 0  copy:       bufs[1][i] = bufs[0][i]                      (1 read, 1 write)
+//   kind 1  read:       sum of bufs[0..3][i], one value per workgroup (4 reads)
+//   kind 2  AdamW mix:  bufs[0], bufs[2], bufs[3] updated in place from
+//                       themselves and bufs[1]                        (4 reads, 3 writes)
+//
+// n must be a multiple of 4096 (one chunk); buffers 16-byte aligned.  Chunks
+// of 4096 elements are dealt round-robin to per_cu * CUs workgroups, a thread
+// issues all its 128-bit loads of a chunk before any arithmetic, and every
+// access is non-temporal -- the AdamW kernel's scheme.  Returns 0, or the HIP
+// error code.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kVec = 4;                 // float4 per stream per thread per chunk
+constexpr int kChunk = 256 * 4 * kVec;  // elements per chunk
+
+__global__ __launch_bounds__(256) void copy_kernel(const float* __restrict__ a, float* __restrict__ b,
+                                                   int64_t chunks) {
+  for (int64_t ch = blockIdx.x; ch < chunks; ch += gridDim.x) {
+    const int64_t base = ch * kChunk + int64_t(threadIdx.x) * 4;
+    f32x4 v[kVec];
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a + base + u * 1024));
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) __builtin_nontemporal_store(v[u], reinterpret_cast<f32x4*>(b + base + u * 1024));
+  }
+}
+
+__global__ __launch_bounds__(256) void read_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                   const float* __restrict__ c, const float* __restrict__ d,
+                                                   float* __restrict__ out, int64_t chunks) {
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t ch = blockIdx.x; ch < chunks; ch += gridDim.x) {
+    const int64_t base = ch * kChunk + int64_t(threadIdx.x) * 4;
+    f32x4 v[4 * kVec];
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      const int64_t i = base + u * 1024;
+      v[4 * u + 0] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a + i));
+      v[4 * u + 1] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(b + i));
+      v[4 * u + 2] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(c + i));
+      v[4 * u + 3] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(d + i));
+    }
+#pragma unroll
+    for (int q = 0; q < 4 * kVec; ++q) s += v[q];
+  }
+  // One store per workgroup keeps the loads live.
+  __shared__ float part[256];
+  part[threadIdx.x] = s[0] + s[1] + s[2] + s[3];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int i = 0; i < 256; ++i) t += part[i];
+    out[blockIdx.x] = t;
+  }
+}
+
+__global__ __launch_bounds__(256) void mix_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                  float* __restrict__ m, float* __restrict__ v, int64_t chunks) {
+  for (int64_t ch = blockIdx.x; ch < chunks; ch += gridDim.x) {
+    const int64_t base = ch * kChunk + int64_t(threadIdx.x) * 4;
+    f32x4 P[kVec], G[kVec], M[kVec], V[kVec];
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      const int64_t i = base + u * 1024;
+      P[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + i));
+      G[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g + i));
+      M[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(m + i));
+      V[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(v + i));
+    }
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      M[u] = M[u] * 0.5f + G[u];
+      V[u] = V[u] * 0.5f + G[u];
+      P[u] = P[u] * 0.5f + M[u] - V[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      const int64_t i = base + u * 1024;
+      __builtin_nontemporal_store(P[u], reinterpret_cast<f32x4*>(p + i));
+      __builtin_nontemporal_store(M[u], reinterpret_cast<f32x4*>(m + i));
+      __builtin_nontemporal_store(V[u], reinterpret_cast<f32x4*>(v + i));
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int mxp_stream(int kind, float* const* bufs, int64_t n, int per_cu, void* stream) {
+  if (n <= 0 || n % kChunk != 0 || per_cu <= 0 || kind < 0 || kind > 2) return int(hipErrorInvalidValue);
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return int(e);
+  const int64_t chunks = n / kChunk;
+  const unsigned grid = unsigned(std::min<int64_t>(chunks, int64_t(cus) * per_cu));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (kind == 0)
+    hipLaunchKernelGGL(copy_kernel, dim3(grid), dim3(256), 0, s, bufs[0], bufs[1], chunks);
+  else if (kind == 1)
+    hipLaunchKernelGGL(read_kernel, dim3(grid), dim3(256), 0, s, bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], chunks);
+  else
+    hipLaunchKernelGGL(mix_kernel, dim3(grid), dim3(256), 0, s, bufs[0], bufs[1], bufs[2], bufs[3], chunks);
+  return int(hipGetLastError());
+}

@@ -126,6 +126,7 @@ WINOGRAD_GEOMETRIES = [
 ]
 WINOGRAD_MODES = [
     {"MX_WINOGRAD_FUSED": "1"},
+    {},
     *[{"MX_WINOGRAD_FUSED": "0", "MX_GEMM_TILE": str(t)} for t in range(4)],
     *[{"MX_WINOGRAD_FUSED": "0", "MX_GEMM_TILE": str(t), "TORCH_VULKAN_CONV_WORKSPACE_MB": "1"} for t in range(4)],
     {"TORCH_VULKAN_CONV_WORKSPACE_MB": "0"},
@@ -205,9 +206,13 @@ def layout_operands(m, n, k, layout, batch=None):
 
 # ------------------------------------------------------------------ configuration calls
 def c1_calls():
-    """C1 as bench.py runs it: one 3x3 layer, forward + dInput + dWeight + dBias."""
+    """C1 as bench.py runs it: one 3x3 layer, forward + dInput + dWeight + dBias,
+    forward and dInput on Winograd, dWeight on the implicit GEMM; and the same
+    layer with every phase on the implicit GEMM (its comparison line)."""
     g = ((8, 64, 56, 56), 64, (3, 3), (1, 1), (1, 1), (1, 1), 1)
-    return [{"kind": "conv", "geometry": g, "phase": ph, "algo": "c1", "with_bias": True} for ph in (0, 1, 2)]
+    routed = [("winograd", 0), ("winograd", 1), ("implicit_gemm", 2)]
+    implicit = [("implicit_gemm", ph) for ph in (0, 1, 2)]
+    return [{"kind": "conv", "geometry": g, "phase": ph, "algo": a, "with_bias": True} for a, ph in routed + implicit]
 
 
 def c2_calls():

@@ -30,8 +30,7 @@ def conv_desc(mx, g):
 
 
 def algo_code(mx, name):
-    return {"auto": mx.ALGO_AUTO, "implicit_gemm": mx.ALGO_IMPLICIT_GEMM, "winograd": mx.ALGO_WINOGRAD,
-            "c1": mx.ALGO_AUTO}[name]
+    return {"auto": mx.ALGO_AUTO, "implicit_gemm": mx.ALGO_IMPLICIT_GEMM, "winograd": mx.ALGO_WINOGRAD}[name]
 
 
 def conv_variants(mx, g, phase, algo, with_bias):
