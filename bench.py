@@ -657,6 +657,35 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir):
     return out
 
 
+def sq_summary(directory, xcds=8, cus=256):
+    """Markdown table of SQ counters per launch class from a rocprofv3 --pmc
+    CSV directory (SQ_* with GRBM_GUI_ACTIVE): mean per dispatch, and derived
+    figures -- kernel cycles (GRBM_GUI_ACTIVE sums the XCDs), MFMA busy as a
+    share of every SIMD's cycles (SQ_VALU_MFMA_BUSY_CYCLES sums the SIMDs:
+    each instruction's matrix-core cycles) and the share of wave-resident
+    cycles spent waiting on dependencies (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES)."""
+    import csv
+    import glob
+    vals = defaultdict(lambda: defaultdict(list))
+    for path in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            vals[kernel_class(r["Kernel_Name"])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    names = ["SQ_WAVES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_VALU_MFMA_BUSY_CYCLES",
+             "SQ_WAVE_CYCLES", "SQ_WAIT_INST_ANY", "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE"]
+    out = ["| launch class | dispatches | " + " | ".join(n.replace("SQ_", "") for n in names) +
+           " | kernel us | MFMA busy | waiting |", "|---|" + "---:|" * (len(names) + 4)]
+    for k, c in sorted(vals.items(), key=lambda kv: -sum(kv[1].get("SQ_VALU_MFMA_BUSY_CYCLES", [0]))):
+        m = {n: sum(v) / len(v) for n, v in c.items()}
+        if not m.get("SQ_WAVES"):
+            continue
+        cyc = m.get("GRBM_GUI_ACTIVE", 0) / xcds
+        busy = m.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / (4 * cus * cyc) if cyc else 0
+        wait = m.get("SQ_WAIT_INST_ANY", 0) / m["SQ_WAVE_CYCLES"] if m.get("SQ_WAVE_CYCLES") else 0
+        out.append(f"| `{k}` | {len(c.get('SQ_WAVES', []))} | " + " | ".join(f"{m.get(n, 0):.0f}" for n in names) +
+                   f" | {cyc / 2400:.1f} | {100 * busy:.1f}% | {100 * wait:.1f}% |")
+    return "\n".join(out)
+
+
 WINOGRAD_KERNELS = ("filter_kernel", "wino_fused_kernel",   # fused path
                     "wino_filter_kernel", "wino_input_kernel", "wino_output_kernel", "gemm_kernel")
 WINOGRAD_CALL_START = ("filter_kernel", "wino_filter_kernel")  # first dispatch of every Winograd call
@@ -793,6 +822,8 @@ def main(argv=None):
     ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_LOG"),
                     help="kernel time per ABI call of each launch class from a rocprofv3 kernel trace of a "
                          "bench.py run, next to that run's live per-call time")
+    ap.add_argument("--sq-summary", metavar="PMC_DIR",
+                    help="markdown table of SQ counters (and MFMA busy share) per launch class from a --pmc CSV dir")
     ap.add_argument("--stats-table", nargs=2, metavar=("KERNEL_STATS_CSV", "STEPS_RUN"),
                     help="markdown tables (per launch class, per kernel) from a rocprofv3 --stats CSV")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -804,6 +835,9 @@ def main(argv=None):
         return 0
     if args.trace_summary:
         print(json.dumps(trace_summary(*args.trace_summary), indent=1))
+        return 0
+    if args.sq_summary:
+        print(sq_summary(args.sq_summary))
         return 0
     if args.stats_table:
         print(stats_table(*args.stats_table))
