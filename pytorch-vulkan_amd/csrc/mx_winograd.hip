@@ -449,6 +449,241 @@ bool prefer_fused(int64_t workgroups, int nslab) {
 
 }  // namespace fused
 
+// ------------------------------------------------------------ pipelined fused kernel
+// The fused kernel's schedule is serial per slab: wait for the slab's loads,
+// transform and store them to LDS, barrier, products, barrier.  Both waves of
+// a SIMD reach each phase together, so nothing overlaps the products.  This
+// variant stages slab s + 1 while the products of slab s run:
+//   - two LDS stages (filter and patches each), as separate arrays so the
+//     compiler knows that the stores of one never alias the reads of the
+//     other, and one barrier per slab;
+//   - the products of a slab in quads of coordinates (first k step of all
+//     four, then the second), so a product and the next one on the same
+//     accumulator are eight MFMAs apart;
+//   - slab s + 1's filter copy and patch transform stored between the
+//     products of the first quads, slab s + 2's loads issued after them.
+// Same arguments, U' layout and epilogue as the fused kernel; 96 KB of LDS,
+// one workgroup per CU.
+namespace pipe {
+using fused::A_FLOATS;
+using fused::A_PASSES;
+using fused::B_FLOATS;
+using fused::BK;
+using fused::BO;
+using fused::BT;
+using fused::f32x2;
+using fused::ROW_A;
+using fused::ROW_B;
+using mfma::f32x4;
+using mfma::i32x4;
+using mfma::kOffNone;
+
+template <bool RAGGED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void wino_pipe_kernel(fused::Args p) {
+  __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs0[B_FLOATS];
+  __shared__ __attribute__((aligned(16))) float As1[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs1[B_FLOATS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y;
+  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
+  const int ob = b % p.n_ob, tb = b / p.n_ob;
+  const int o0 = ob * BO, t0 = tb * BT;
+
+  // Loads as in the fused kernel: filter rows from L2, one input patch per
+  // thread.
+  const i32x4 ru = mfma::buffer_rsrc(p.U, p.u_bytes);
+  const int a_row = tid >> 5, a_f4 = tid & 31;
+  const uint32_t a_off = uint32_t(
+      ((((int64_t(g) * 16 + (a_row >> 2)) * p.nslab) * 4 + (a_row & 3)) * int64_t(p.Opad) * 2 + 2 * o0 + 4 * a_f4) *
+      4);
+  const uint32_t a_sstep = uint32_t(4) * p.Opad * 2 * 4;
+  const uint32_t a_qstep = uint32_t(2) * p.nslab * a_sstep;
+  const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
+  const int b_t = (tid & 15) | ((tid >> 1) & 16);
+  const int b_c = ((tid >> 4) & 1) | ((tid >> 5) & 6);
+  uint32_t row_off[4];
+  uint32_t col_ok = 0;
+  {
+    const int t = t0 + b_t;
+    const bool tok = t < p.T;
+    const uint32_t tt = tok ? uint32_t(t) : 0u;
+    const uint32_t img = mfma::fdiv(tt, p.f_thw);
+    const uint32_t pos = tt - img * uint32_t(p.TH * p.TW);
+    const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
+    const int y0 = int(2 * ty) - p.ph, x0 = int(2 * tx) - p.pw;
+    const int64_t plane = (int64_t(img) * p.Cin + int64_t(g) * p.C + b_c) * p.H;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int iy = y0 + r;
+      row_off[r] = (tok && unsigned(iy) < unsigned(p.H)) ? uint32_t(((plane + iy) * p.W + x0) * 4) : kOffNone;
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) col_ok |= (unsigned(x0 + cc) < unsigned(p.W) ? 1u : 0u) << cc;
+  }
+  const uint32_t x_sstep = uint32_t(BK) * p.H * p.W * 4;
+  const int nslab = p.nslab;
+
+  f32x4 av[A_PASSES];
+  float d[16];
+  auto load = [&](int slab) {
+    const uint32_t sa = uint32_t(slab) * a_sstep, sx = uint32_t(slab) * x_sstep;
+#pragma unroll
+    for (int q = 0; q < A_PASSES; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
+    // x0 may be -1 (left padding): row_off + 4 * cc is then computed modulo
+    // 2^32 and only used when column cc is inside the image.
+    const uint32_t cmask = (!RAGGED || slab * BK + b_c < p.C) ? col_ok : 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        d[r * 4 + cc] = mfma::bload(rx, ((cmask >> cc) & 1u) ? row_off[r] + 4u * cc : kOffNone, sx);
+  };
+  auto store = [&](float* As, float* Bs) {
+    float* const a_st = As + a_row * ROW_A + 4 * a_f4;
+    float* const b_st = Bs + (b_c >> 1) * ROW_B + 2 * b_t + (b_c & 1);
+#pragma unroll
+    for (int q = 0; q < A_PASSES; ++q) *reinterpret_cast<f32x4*>(a_st + q * 8 * ROW_A) = av[q];
+    float z[16];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      z[0 * 4 + cc] = d[0 * 4 + cc] - d[2 * 4 + cc];
+      z[1 * 4 + cc] = d[1 * 4 + cc] + d[2 * 4 + cc];
+      z[2 * 4 + cc] = d[2 * 4 + cc] - d[1 * 4 + cc];
+      z[3 * 4 + cc] = d[1 * 4 + cc] - d[3 * 4 + cc];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      b_st[(r * 4 + 0) * 4 * ROW_B] = z[r * 4 + 0] - z[r * 4 + 2];
+      b_st[(r * 4 + 1) * 4 * ROW_B] = z[r * 4 + 1] + z[r * 4 + 2];
+      b_st[(r * 4 + 2) * 4 * ROW_B] = z[r * 4 + 2] - z[r * 4 + 1];
+      b_st[(r * 4 + 3) * 4 * ROW_B] = z[r * 4 + 1] - z[r * 4 + 3];
+    }
+  };
+
+  const int wo = wave >> 1, wt = wave & 1;
+  const int kq = lane >> 4, li = lane & 15;
+  f32x4 acc[16][2];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Slab s from stage (Ac, Bc); slab s + 1 (in registers) to stage (An, Bn);
+  // slab s + 2 requested.  Past the last slab the loads re-read it and the
+  // spare stage is written but never read: no branch in the schedule.
+  // Four chunks fenced by scheduling barriers: quad 0 of the products with
+  // the staging of slab s + 1 and the loads of slab s + 2, then quads 1-3;
+  // each chunk also reads the next quad's fragments.
+  auto step = [&](const float* Ac, const float* Bc, float* An, float* Bn, int s) {
+    // The loaded values count as produced here, so no part of the transform
+    // is hoisted above the previous barrier to sit right behind the loads.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(d[i]));
+#pragma unroll
+    for (int q = 0; q < A_PASSES; ++q) asm volatile("" : "+v"(av[q]));
+    const f32x2* const a_frag = reinterpret_cast<const f32x2*>(Ac + kq * ROW_A + 2 * (wo * 32 + li));
+    const f32x2* const b_frag = reinterpret_cast<const f32x2*>(Bc + kq * ROW_B + 2 * (wt * 16 + li));
+    f32x2 fa0[4], fa1[4], fb[4];
+    auto frags = [&](int q) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 4 * q + j;
+        fb[j] = b_frag[t * 2 * ROW_B];
+        fa0[j] = a_frag[t * 2 * ROW_A];
+        fa1[j] = a_frag[t * 2 * ROW_A + 16];
+      }
+    };
+    // Coordinates in quads: the first k step of all four, then the second,
+    // so a product and the next one on the same accumulator are eight MFMAs
+    // apart.
+    auto quad = [&](int q) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int t = 4 * q + j;
+          acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0[j][h], fb[j][h], acc[t][0], 0, 0, 0);
+          acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1[j][h], fb[j][h], acc[t][1], 0, 0, 0);
+        }
+    };
+    frags(0);
+    quad(0);
+    store(An, Bn);
+    load(min(s + 2, nslab - 1));
+    frags(1);
+    __builtin_amdgcn_sched_barrier(0);
+    // Quads 1-3: the next quad's fragment reads go out after the first two
+    // products, so they land while the rest of the quad runs.
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      quad(q);
+      if (q < 3) {
+        frags(q + 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 14, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __syncthreads();
+  };
+
+  load(0);
+  store(As0, Bs0);
+  load(min(1, nslab - 1));
+  __syncthreads();
+  // The host pads the channels to a multiple of 16: an even slab count.
+  for (int s = 0; s < nslab; s += 2) {
+    step(As0, Bs0, As1, Bs1, s);
+    step(As1, Bs1, As0, Bs0, s + 1);
+  }
+
+  // Output transform (the fused kernel's epilogue).
+  const int t = t0 + wt * 16 + li;
+  if (t >= p.T) return;
+  const uint32_t img = mfma::fdiv(uint32_t(t), p.f_thw);
+  const uint32_t pos = uint32_t(t) - img * uint32_t(p.TH * p.TW);
+  const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
+  const int oy = int(2 * ty), ox = int(2 * tx);
+  const bool right = ox + 1 < p.OW, below = oy + 1 < p.OH;
+  float bias_v[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
+      bias_v[i][v] = (p.bias && o < p.O) ? p.bias[g * p.O + o] : 0.f;
+    }
+  const i32x4 ry = mfma::buffer_rsrc(p.y, p.y_bytes);
+  const uint32_t row_step = uint32_t(p.OW) * 4u;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
+      float m[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) m[q] = acc[q][i][v];
+      float r0[4], r1[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        r0[c] = m[c] + m[4 + c] + m[8 + c];
+        r1[c] = m[4 + c] - m[8 + c] - m[12 + c];
+      }
+      const float bb = bias_v[i][v];
+      const bool ok = o < p.O;
+      const uint32_t off =
+          uint32_t(((img * uint32_t(p.Cout) + uint32_t(g * p.O + o)) * uint32_t(p.OH) + uint32_t(oy)) *
+                       uint32_t(p.OW) +
+                   uint32_t(ox)) *
+          4u;
+      mfma::bstore(r0[0] + r0[1] + r0[2] + bb, ry, ok ? off : kOffNone, 0);
+      mfma::bstore(r0[1] - r0[2] - r0[3] + bb, ry, (ok && right) ? off + 4u : kOffNone, 0);
+      mfma::bstore(r1[0] + r1[1] + r1[2] + bb, ry, (ok && below) ? off + row_step : kOffNone, 0);
+      mfma::bstore(r1[1] - r1[2] - r1[3] + bb, ry, (ok && below && right) ? off + row_step + 4u : kOffNone, 0);
+    }
+}
+}  // namespace pipe
+
 // ------------------------------------------------------------ fused dWeight
 // Weight gradient of a 3x3 stride-1 layer as the adjoint of the forward
 // transform: with M_t = U_t V_t and Y = A^T M A, U = G w G^T,
@@ -779,6 +1014,7 @@ struct RunPlan {
   int G = 1;
   int64_t blocks = 0;
   bool fused = true;
+  bool pipe = false;          // the pipelined fused kernel (channels padded to 16)
   int64_t chunk = 0;          // images per unfused pass
   int64_t unfused_bytes = 0;  // U, V and M of one pass
 };
@@ -817,8 +1053,18 @@ int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
   p.T = int(T);
   r->blocks = (T + fused::BT - 1) / fused::BT * p.n_ob;
   MX_REQUIRE(r->blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "winograd: grid too large");
-  // MX_WINOGRAD_FUSED=1 / 0 forces the fused / unfused kernels (tests, tuning).
-  r->fused = fused::prefer_fused(r->blocks * r->G, p.nslab);
+  // The pipelined fused kernel holds 96 KB of LDS, one workgroup per CU, so
+  // it pays where the grid fits the CUs once: measured on MI355X it beats
+  // the fused kernel on C1's layer (196 workgroups of 8 slabs: 23.6 vs 25.4
+  // us per call) and the unfused passes on 512-channel layers with 256
+  // workgroups of 64 slabs (116 vs 130 us); with long walks and fewer than
+  // half the CUs busy the unfused passes stay ahead (64 workgroups of 64
+  // slabs: 48 vs 115 us).
+  const int64_t cus = cu_count(), wgs = r->blocks * r->G;
+  const bool pipe_fits = wgs <= cus && (p.nslab <= 16 || 2 * wgs >= cus);
+  // MX_WINOGRAD_FUSED=1 / 0 forces the fused / unfused kernels and
+  // MX_WINOGRAD_PIPE=1 / 0 the pipelined / serial fused kernel (tests, tuning).
+  r->fused = pipe_fits || fused::prefer_fused(wgs, p.nslab);
   if (const char* e = std::getenv("MX_WINOGRAD_FUSED"))
     if (e[0] == '0' || e[0] == '1') r->fused = e[0] == '1';
   const int64_t u_plain = 16 * int64_t(p.Cout) * p.C * 4;
@@ -829,6 +1075,17 @@ int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
     const int64_t passes = (d.n + fit - 1) / fit;
     r->chunk = (d.n + passes - 1) / passes;
     r->unfused_bytes = u_plain + per_image * r->chunk;
+  }
+  r->pipe = pipe_fits;
+  if (const char* e = std::getenv("MX_WINOGRAD_PIPE"))
+    if (e[0] == '0' || e[0] == '1') r->pipe = e[0] == '1';
+  r->pipe = r->pipe && r->fused;
+  if (r->pipe) {
+    // Two slabs per loop trip: channels padded to 16 (zero filter rows).
+    p.Cpad = (p.C + 2 * fused::BK - 1) / (2 * fused::BK) * (2 * fused::BK);
+    p.nslab = p.Cpad / fused::BK;
+    p.u_bytes = int64_t(r->G) * 16 * p.Cpad * p.Opad * 4;
+    MX_REQUIRE(p.u_bytes < mfma::kBufMaxBytes, MX_ERR_UNSUPPORTED, "winograd: the transformed filter exceeds 2 GiB");
   }
   return MX_OK;
 }
@@ -846,12 +1103,23 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   Scratch U;
   MX_TRY(U.alloc(size_t(p.u_bytes), s));
   p.U = U.as<float>();
-  hipLaunchKernelGGL(fused::filter_kernel, dim3(blocks_for(int64_t(r.G) * (p.Cpad / 2) * p.Opad)), dim3(256), 0, s,
-                     w, U.as<float>(), p.C, p.O, p.Cpad, p.Opad, r.G, flip);
-  MX_HIP(hipGetLastError());
   p.x = x;
   p.y = y;
   const dim3 grid{unsigned(r.blocks), unsigned(r.G), 1u};
+  // 64-thread blocks: a small filter (64 x 64 is 2,048 threads) then spreads
+  // over 32 CUs instead of 8, and its scattered reads queue on more of them.
+  const int64_t filter_threads = int64_t(r.G) * (p.Cpad / 2) * p.Opad;
+  hipLaunchKernelGGL(fused::filter_kernel, dim3(unsigned(std::min<int64_t>((filter_threads + 63) / 64, 1 << 20))),
+                     dim3(64), 0, s, w, U.as<float>(), p.C, p.O, p.Cpad, p.Opad, r.G, flip);
+  MX_HIP(hipGetLastError());
+  if (r.pipe) {
+    if (p.C % (2 * fused::BK))
+      hipLaunchKernelGGL(pipe::wino_pipe_kernel<true>, grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(pipe::wino_pipe_kernel<false>, grid, dim3(256), 0, s, p);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
   if (p.C % fused::BK)
     hipLaunchKernelGGL(fused::wino_fused_kernel<true>, grid, dim3(256), 0, s, p);
   else
@@ -973,7 +1241,10 @@ int winograd_describe(const mx_conv2d_desc& d, int phase, int64_t ws_limit, std:
   }
   RunPlan r;
   MX_TRY(plan_run(phase == MX_CONV_DINPUT ? dinput_as_forward(d) : d, ws_limit, &r));
-  if (r.fused) {
+  if (r.pipe) {
+    *variant = cat("wino_pipe_kernel<", r.p.C % (2 * fused::BK) ? "ragged" : "even", ">");
+    *ws_bytes = 0;
+  } else if (r.fused) {
     *variant = cat("wino_fused_kernel<", r.p.C % fused::BK ? "ragged" : "even", ">");
     *ws_bytes = 0;
   } else {

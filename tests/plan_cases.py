@@ -125,7 +125,8 @@ WINOGRAD_GEOMETRIES = [
     ((8, 64, 8, 8), 64, (3, 3), (1, 1), (1, 1), (1, 1), 1),  # 1 MiB budget: two image chunks
 ]
 WINOGRAD_MODES = [
-    {"MX_WINOGRAD_FUSED": "1"},
+    {"MX_WINOGRAD_FUSED": "1", "MX_WINOGRAD_PIPE": "0"},
+    {"MX_WINOGRAD_FUSED": "1", "MX_WINOGRAD_PIPE": "1"},
     {},
     *[{"MX_WINOGRAD_FUSED": "0", "MX_GEMM_TILE": str(t)} for t in range(4)],
     *[{"MX_WINOGRAD_FUSED": "0", "MX_GEMM_TILE": str(t), "TORCH_VULKAN_CONV_WORKSPACE_MB": "1"} for t in range(4)],
