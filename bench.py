@@ -481,19 +481,35 @@ def cpu_setup(torch):
     cores = min(affinity, quota) if quota else affinity
     torch.set_num_threads(cores)
     model = None
+    lscpu = {}
     try:
         import subprocess
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        model = next((l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name")), None)
+        lscpu = {k.strip(): v.strip() for k, v in (l.split(":", 1) for l in out.splitlines() if ":" in l)}
+        model = lscpu.get("Model name")
     except Exception:  # noqa: BLE001 (lscpu missing: fall back to /proc/cpuinfo)
         pass
+    cpuinfo = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                if cpuinfo:
+                    break  # the first processor's block is enough
+                continue
+            k, v = line.split(":", 1)
+            cpuinfo.setdefault(k.strip(), v.strip())
+    except Exception:  # noqa: BLE001
+        pass
     if model is None:
-        try:
-            model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-        except Exception:  # noqa: BLE001
-            model = "unknown"
+        model = cpuinfo.get("model name", "unknown")
+    # Virtual machines often report only "AMD EPYC": family / model / stepping
+    # (family 25 is Zen 3-4, 26 Zen 5), clocks and caches tell hosts apart.
+    host = {"family": cpuinfo.get("cpu family"), "model": cpuinfo.get("model"), "stepping": cpuinfo.get("stepping"),
+            "mhz": cpuinfo.get("cpu MHz"), "max_mhz": lscpu.get("CPU max MHz"), "l3": lscpu.get("L3 cache"),
+            "sockets": lscpu.get("Socket(s)"), "hypervisor": lscpu.get("Hypervisor vendor"),
+            "avx512": "avx512f" in cpuinfo.get("flags", "")}
     return {"cores": cores, "threads": torch.get_num_threads(), "cpu_model": model, "affinity": affinity,
-            "cgroup_quota": quota}
+            "cgroup_quota": quota, "cpu_host": {k: v for k, v in host.items() if v not in (None, "")}}
 
 
 def cpu_time(fn, warmup, reps):
@@ -998,7 +1014,8 @@ def main(argv=None):
         tflops, sample_flops, times = cpu_conv_stack(torch, 4, 3)
         result["cpu_baseline"] = {
             "value": round(tflops, 4), "unit": "TFLOP/s", "cores": host["threads"], "kind": "reference",
-            "cpu_model": host["cpu_model"], "affinity_cores": host["affinity"], "cgroup_cpu_quota": host["cgroup_quota"],
+            "cpu_model": host["cpu_model"], "cpu_host": host["cpu_host"], "affinity_cores": host["affinity"],
+            "cgroup_cpu_quota": host["cgroup_quota"],
             "sample": f"CPU PyTorch {torch.__version__} F.conv2d + autograd over the same 53-layer stack at batch 4 "
                       f"instead of 64 ({sample_flops / 1e9:.1f} GFLOP per pass, median of {len(times)} passes "
                       f"after 1 warm-up, {host['threads']} threads)",
