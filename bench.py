@@ -641,6 +641,7 @@ def cpu_conv_stack(torch, batch, reps):
 def kernel_class(name: str) -> str:
     """Demangled dispatch name -> the label bench uses for its launch class."""
     import re
+    name = name.replace("conv_dx_phases_kernel", "conv_dx_kernel")  # fused stride phases: the same tile class
     for kind in ("conv_fwd_kernel", "conv_dx_kernel", "conv_dw_kernel"):
         if kind in name:
             m = re.search(r"Cfg<(\d+), (\d+), (\d+),", name)

@@ -629,10 +629,14 @@ std::string dx_variant(const DxPlan& f) {
   for (size_t i = 0; i < f.phases.size(); ++i) {
     const ConvArgs& q = f.phases[i];
     if (q.K == 0) continue;
+    // Phases sharing a loader run as one conv_dx_phases_kernel launch.
+    int same = 0;
+    for (size_t j = 0; j < f.phases.size(); ++j) same += f.phases[j].K != 0 && f.bmodes[j] == f.bmodes[i];
     const char* b = f.bmodes[i] == conv::B_VEC ? "PosQuad"
                     : conv::blocked_channels(q.Cout_g) ? "PhaseGather<blocked>" : "PhaseGather";
-    std::string n = cat("conv_dx_kernel<", tile_name(f.gp.tile, MX_CONV_DINPUT), ",", f.vec_a ? "RVEC" : "RSCALAR",
-                        ",", b, ">", f.gp.splits > 1 ? "+split" : "", f.zfill ? "+zfill" : "");
+    std::string n = cat(same > 1 ? "conv_dx_phases_kernel<" : "conv_dx_kernel<", tile_name(f.gp.tile, MX_CONV_DINPUT),
+                        ",", f.vec_a ? "RVEC" : "RSCALAR", ",", b, ">", f.gp.splits > 1 ? "+split" : "",
+                        f.zfill ? "+zfill" : "");
     if (std::find(names.begin(), names.end(), n) == names.end()) names.push_back(n);
   }
   std::string out;
@@ -926,11 +930,21 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
     }
     if (set.n > 0) MX_TRY(conv::conv_dx_pack_weights(p, set, wt.as<float>(), s));
   }
-  for (size_t i = 0; i < f.phases.size(); ++i) {
-    ConvArgs& q = f.phases[i];
-    if (q.K == 0) continue;
-    q.ws = ws.as<float>();
-    MX_TRY(conv::conv_dx_launch(q, f.gp.tile, f.vec_a ? Mode::RVEC : Mode::RSCALAR, f.bmodes[i], s));
+  // The reached phases in one launch per operand loader (up to four each).
+  for (int bmode : {int(conv::B_GATHER), int(conv::B_VEC)}) {
+    conv::DxPhaseSet set{};
+    set.G = p.G;
+    for (size_t i = 0; i < f.phases.size(); ++i) {
+      ConvArgs& q = f.phases[i];
+      if (q.K == 0 || f.bmodes[i] != bmode) continue;
+      q.ws = ws.as<float>();
+      set.q[set.n++] = q;
+      if (set.n == conv::kMaxFusedPhases) {
+        MX_TRY(conv::conv_dx_launch_set(set, f.gp.tile, f.vec_a ? Mode::RVEC : Mode::RSCALAR, bmode, s));
+        set.n = 0;
+      }
+    }
+    if (set.n > 0) MX_TRY(conv::conv_dx_launch_set(set, f.gp.tile, f.vec_a ? Mode::RVEC : Mode::RSCALAR, bmode, s));
   }
   if (f.gp.splits > 1) return conv::conv_sum_splits(ws.as<float>(), f.gp.splits, f.out_elems, dx, nullptr, 1, 1, s);
   return MX_OK;

@@ -581,6 +581,14 @@ enum BMode : int { B_GATHER = 0, B_VEC = 1 };
 
 int conv_fwd_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t s);
 int conv_dx_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t s);
+// Up to kMaxFusedPhases stride phases of one dInput (same tile, loaders and
+// split count) in one launch.
+constexpr int kMaxFusedPhases = 4;
+struct DxPhaseSet {
+  ConvArgs q[kMaxFusedPhases];
+  int n, G;
+};
+int conv_dx_launch_set(const DxPhaseSet& set, int tile, Mode ma, int bmode, hipStream_t s);
 int conv_dw_launch(const ConvArgs& p, int tile, int amode, int bmode, hipStream_t s);
 // Weight packing of several dInput stride phases in one launch.
 constexpr int kMaxPackPhases = 16;

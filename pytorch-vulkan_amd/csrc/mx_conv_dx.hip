@@ -66,14 +66,13 @@ __global__ void conv_dx_zero_kernel(float* __restrict__ dx, int64_t n) {
   for (; i < n; i += stride) dx[i] = 0.f;
 }
 
+// One output tile (linear index `lin`, K split `split`, group g) of one
+// stride phase.
 template <class C, Mode MA, class LB>
-MX_TILE_KERNEL(C) void conv_dx_kernel(ConvArgs p) {
-  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
-  const int g = blockIdx.z;
+__device__ __forceinline__ void dx_tile(const ConvArgs& p, int g, int lin, int split, float* smem) {
   int tm, tn;
-  tile_coords(xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), p.tiles_m, p.tiles_n, tm, tn);
+  tile_coords(lin, p.tiles_m, p.tiles_n, tm, tn);
   const int row0 = tm * C::BM, col0 = tn * C::BN;
-  const int split = blockIdx.y;
   const int k0 = split * p.kps, k1 = min(p.K, k0 + p.kps);
   BufStridedLoader<C::BM, C::BK, MA> la;  // element (ci, k) = wt[g][k][ci]
   la.init(p.wt + int64_t(g) * p.K * p.Cin_g, int64_t(p.K) * p.Cin_g * 4, 1, p.Cin_g, row0, p.M, k0, k1);
@@ -136,6 +135,26 @@ MX_TILE_KERNEL(C) void conv_dx_kernel(ConvArgs p) {
   });
 }
 
+template <class C, Mode MA, class LB>
+MX_TILE_KERNEL(C) void conv_dx_kernel(ConvArgs p) {
+  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
+  dx_tile<C, MA, LB>(p, blockIdx.z, xcd_remap(blockIdx.x, p.tiles_m * p.tiles_n), blockIdx.y, smem);
+}
+
+// Several stride phases in one launch (blockIdx.z = phase * G + group): the
+// phases of a strided layer are each a fraction of its positions, and run one
+// after another their launches leave most of the GPU idle.  The grid covers
+// the phase with the most tiles; the others' surplus workgroups exit.
+template <class C, Mode MA, class LB>
+MX_TILE_KERNEL(C) void conv_dx_phases_kernel(DxPhaseSet set) {
+  __shared__ __attribute__((aligned(16))) float smem[C::SMEM_FLOATS];
+  const int ph = int(blockIdx.z) / set.G, g = int(blockIdx.z) - ph * set.G;
+  const ConvArgs& p = set.q[ph];
+  const int lin = xcd_remap(blockIdx.x, gridDim.x);
+  if (lin >= p.tiles_m * p.tiles_n) return;
+  dx_tile<C, MA, LB>(p, g, lin, blockIdx.y, smem);
+}
+
 template <class C, Mode MA>
 int launch_b(ConvArgs p, int bmode, hipStream_t s) {
   p.tiles_m = (p.M + C::BM - 1) / C::BM;
@@ -157,6 +176,35 @@ int launch_a(const ConvArgs& p, Mode ma, int bmode, hipStream_t s) {
   return launch_b<C, Mode::RSCALAR>(p, bmode, s);
 }
 
+template <class C, Mode MA>
+int launch_set_b(DxPhaseSet set, int bmode, hipStream_t s) {
+  int most = 0;
+  for (int i = 0; i < set.n; ++i) {
+    ConvArgs& q = set.q[i];
+    q.tiles_m = (q.M + C::BM - 1) / C::BM;
+    q.tiles_n = (q.Ncols + C::BN - 1) / C::BN;
+    most = std::max(most, q.tiles_m * q.tiles_n);
+  }
+  const dim3 grid(unsigned(most), unsigned(set.q[0].splits), unsigned(set.G * set.n));
+  if (bmode == B_VEC)
+    hipLaunchKernelGGL((conv_dx_phases_kernel<C, MA, PosQuadLoader<C::BN, C::BK, true>>), grid, dim3(kThreads), 0, s,
+                       set);
+  else if (blocked_channels(set.q[0].Cout_g))
+    hipLaunchKernelGGL((conv_dx_phases_kernel<C, MA, PhaseGatherLoader<C::BN, C::BK, true>>), grid, dim3(kThreads), 0,
+                       s, set);
+  else
+    hipLaunchKernelGGL((conv_dx_phases_kernel<C, MA, PhaseGatherLoader<C::BN, C::BK, false>>), grid, dim3(kThreads),
+                       0, s, set);
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
+template <class C>
+int launch_set_a(const DxPhaseSet& set, Mode ma, int bmode, hipStream_t s) {
+  if (ma == Mode::RVEC) return launch_set_b<C, Mode::RVEC>(set, bmode, s);
+  return launch_set_b<C, Mode::RSCALAR>(set, bmode, s);
+}
+
 int grid_for(int64_t total) { return int(std::min<int64_t>((total + 255) / 256, 1 << 20)); }
 
 }  // namespace
@@ -173,6 +221,17 @@ int conv_dx_zero(float* dx, int64_t n, hipStream_t s) {
   hipLaunchKernelGGL(conv_dx_zero_kernel, dim3(grid_for((n + 3) / 4)), dim3(256), 0, s, dx, n);
   MX_HIP(hipGetLastError());
   return MX_OK;
+}
+
+int conv_dx_launch_set(const DxPhaseSet& set, int tile, Mode ma, int bmode, hipStream_t s) {
+  if (set.n == 1) return conv_dx_launch(set.q[0], tile, ma, bmode, s);
+  switch (tile) {
+    case TALL: return launch_set_a<TileTall>(set, ma, bmode, s);
+    case WIDE: return launch_set_a<TileWide>(set, ma, bmode, s);
+    case SQ: return launch_set_a<TileSq>(set, ma, bmode, s);
+    case FLAT: return launch_set_a<TileFlat>(set, ma, bmode, s);
+    default: return launch_set_a<TileSmallShallow>(set, ma, bmode, s);
+  }
 }
 
 int conv_dx_launch(const ConvArgs& p, int tile, Mode ma, int bmode, hipStream_t s) {
