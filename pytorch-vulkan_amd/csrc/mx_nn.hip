@@ -389,6 +389,137 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_fused_kernel(const float* __r
   }
 }
 
+// Register-resident variants of the two kernels above for groups that fit a
+// workgroup's registers (at most 16 float4 per thread, 16-byte aligned
+// planes): each element is read from HBM once instead of three times
+// (forward) or twice (backward).  Every thread holds exactly the elements
+// the multi-pass kernel's loops give it, in the same order, so the sums and
+// the results are bit-identical to that kernel's.
+template <int NPT>
+__global__ __launch_bounds__(kThreads) void gn_fwd_regs_kernel(const float* __restrict__ x,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ beta, int C, int G, int hw,
+                                                               float eps, float* __restrict__ y,
+                                                               float* __restrict__ mean, float* __restrict__ rstd) {
+  __shared__ float red[kWavesPerBlock];
+  const int ng = blockIdx.x;
+  const int n = ng / G, g = ng - (ng / G) * G, cpg = C / G;
+  const int count = cpg * hw, count4 = count / 4;
+  const int64_t base = (int64_t(n) * C + int64_t(g) * cpg) * hw;
+  const float4* p4 = reinterpret_cast<const float4*>(x + base);
+  float4 v[NPT];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int i = threadIdx.x + kThreads * j;
+    v[j] = i < count4 ? p4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < count4) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+  const float m = block_sum(s, red) / float(count);
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    if (threadIdx.x + kThreads * j < count4) {
+      const float a = v[j].x - m, b = v[j].y - m, c = v[j].z - m, d = v[j].w - m;
+      sq += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  const float inv = 1.f / sqrtf(block_sum(sq, red) / float(count) + eps);
+  if (threadIdx.x == 0) {
+    mean[ng] = m;
+    rstd[ng] = inv;
+  }
+  const int c0 = g * cpg;
+  float4* q4 = reinterpret_cast<float4*>(y + base);
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int i = threadIdx.x + kThreads * j;
+    if (i >= count4) continue;
+    const int c = c0 + (4 * i) / hw;
+    const float a = gamma ? inv * gamma[c] : inv, b = beta ? beta[c] : 0.f;
+    q4[i] = make_float4((v[j].x - m) * a + b, (v[j].y - m) * a + b, (v[j].z - m) * a + b, (v[j].w - m) * a + b);
+  }
+}
+
+// Backward: wave w holds channels w, w + 4, ... of the group and lanes the
+// plane's float4 lane, lane + 64, ... (np of them per channel), for dy and x.
+template <int NPT>
+__global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __restrict__ dy,
+                                                               const float* __restrict__ x,
+                                                               const float* __restrict__ mean,
+                                                               const float* __restrict__ rstd,
+                                                               const float* __restrict__ gamma, int C, int G, int hw,
+                                                               float* __restrict__ dx, float* __restrict__ part_dy,
+                                                               float* __restrict__ part_dyx) {
+  __shared__ float sdy[kGnMaxCpg], sdyx[kGnMaxCpg];
+  __shared__ float tot[2];
+  const int ng = blockIdx.x;
+  const int n = ng / G, g = ng - (ng / G) * G, cpg = C / G;
+  const int64_t base = (int64_t(n) * C + int64_t(g) * cpg) * hw;
+  const float mu = mean[ng], inv = rstd[ng];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int hw4 = hw / 4, np = (hw4 + 63) / 64;
+  const float4* g4 = reinterpret_cast<const float4*>(dy + base);
+  const float4* x4 = reinterpret_cast<const float4*>(x + base);
+  float4 gv[NPT], xv[NPT];
+  // Element k of this thread: channel wave + 4 (k / np), plane float4 lane + 64 (k % np).
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const int ci = wave + kWavesPerBlock * (k / np), i = lane + 64 * (k % np);
+    const bool ok = ci < cpg && i < hw4;
+    gv[k] = ok ? g4[int64_t(ci) * hw4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    xv[k] = ok ? x4[int64_t(ci) * hw4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int cb = 0; cb * kWavesPerBlock < cpg; ++cb) {
+    const int ci = wave + kWavesPerBlock * cb;
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+      if (k / np != cb || lane + 64 * (k % np) >= hw4) continue;
+      const float4 gg = gv[k], v = xv[k];
+      a += (gg.x + gg.y) + (gg.z + gg.w);
+      b += (gg.x * (v.x - mu) + gg.y * (v.y - mu)) + (gg.z * (v.z - mu) + gg.w * (v.w - mu));
+    }
+    if (ci < cpg) {
+      a = wave_sum(a);
+      b = wave_sum(b);
+      if (lane == 0) {
+        sdy[ci] = a;
+        sdyx[ci] = b;
+        const int64_t r = int64_t(n) * C + int64_t(g) * cpg + ci;
+        part_dy[r] = a;
+        part_dyx[r] = b;
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sv = 0.f, svx = 0.f;
+    for (int ci = 0; ci < cpg; ++ci) {
+      const float w = gamma ? gamma[g * cpg + ci] : 1.f;
+      sv += w * sdy[ci];
+      svx += w * sdyx[ci];
+    }
+    tot[0] = sv;
+    tot[1] = svx;
+  }
+  __syncthreads();
+  if (!dx) return;
+  const float cnt = float(cpg * hw);
+  const float kk = -inv * inv * inv * (tot[1] / cnt);
+  const float q = -inv * (tot[0] / cnt);
+  float4* d4 = reinterpret_cast<float4*>(dx + base);
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const int ci = wave + kWavesPerBlock * (k / np), i = lane + 64 * (k % np);
+    if (ci >= cpg || i >= hw4) continue;
+    const float pc = gamma ? inv * gamma[g * cpg + ci] : inv;
+    const float4 gg = gv[k], v = xv[k];
+    d4[int64_t(ci) * hw4 + i] = make_float4(pc * gg.x + kk * (v.x - mu) + q, pc * gg.y + kk * (v.y - mu) + q,
+                                            pc * gg.z + kk * (v.z - mu) + q, pc * gg.w + kk * (v.w - mu) + q);
+  }
+}
+
 // ---------------------------------------------------------------- BatchNorm
 // One thread per channel: merge the N rows of channel c.  Training: batch
 // mean / inverse std (0 when var == eps == 0, as torch's InvStd) and the
@@ -636,6 +767,38 @@ __global__ __launch_bounds__(kThreads) void upsample_nearest_grad_kernel(const f
   }
 }
 
+// Exact 2x in both axes (iw even, 8-byte aligned x, 16-byte aligned y): a
+// thread reads two neighbouring inputs (8 bytes) and writes their 2x2 blocks
+// as two 16-byte rows.  32-bit indices (the host checks the sizes).
+__global__ __launch_bounds__(kThreads) void upsample2x_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                              uint32_t rows, uint32_t half_w) {
+  const uint32_t total = rows * half_w;
+  for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
+    const uint32_t row = t / half_w, j = t - row * half_w;  // row = plane * ih + input row
+    const float2 a = reinterpret_cast<const float2*>(x)[t];
+    const float4 v = make_float4(a.x, a.x, a.y, a.y);
+    float4* out = reinterpret_cast<float4*>(y) + (2 * row) * half_w + j;
+    out[0] = v;
+    out[half_w] = v;
+  }
+}
+
+// Its gradient: the 2x2 block of each input summed in row-major output order
+// (((0 + d00) + d01) + d10) + d11, torch's CPU order.
+__global__ __launch_bounds__(kThreads) void upsample2x_grad_kernel(const float* __restrict__ dy,
+                                                                   float* __restrict__ dx, uint32_t rows,
+                                                                   uint32_t half_w) {
+  const uint32_t total = rows * half_w;
+  for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
+    const uint32_t row = t / half_w, j = t - row * half_w;
+    const float4* in = reinterpret_cast<const float4*>(dy) + (2 * row) * half_w + j;
+    const float4 r0 = in[0], r1 = in[half_w];
+    // From a zero start, as the general kernel (a sum of negative zeros is +0).
+    reinterpret_cast<float2*>(dx)[t] = make_float2((((0.f + r0.x) + r0.y) + r1.x) + r1.y,
+                                                   (((0.f + r0.z) + r0.w) + r1.z) + r1.w);
+  }
+}
+
 // ------------------------------------------------------------------ softmax
 // Last axis (inner == 1): one wave per row.  y = exp(x - max) * (1 / sum).
 __global__ __launch_bounds__(kThreads) void softmax_last_kernel(const float* __restrict__ x, float* __restrict__ y,
@@ -670,6 +833,80 @@ __global__ __launch_bounds__(kThreads) void softmax_last_grad_kernel(const float
   for (int i = lane; i < len; i += 64) s += g[i] * p[i];
   s = wave_sum(s);
   for (int i = lane; i < len; i += 64) dx[r * len + i] = p[i] * (g[i] - s);
+}
+
+// Rows of len % 4 == 0 floats (16-byte aligned), len <= 256 NV: one wave per
+// row holding it in registers, lane l owning float4s l, l + 64, ...; each
+// element is read once and its exponential computed once.
+template <int NV>
+__global__ __launch_bounds__(kThreads) void softmax_rows_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                int64_t rows, int len) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float4* p = reinterpret_cast<const float4*>(x + r * len);
+  float4* q = reinterpret_cast<float4*>(y + r * len);
+  const int n4 = len / 4;
+  float e[NV][4];
+  float m = -std::numeric_limits<float>::infinity();
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = lane + 64 * j;
+    const float4 v = i < n4 ? p[i] : make_float4(m, m, m, m);
+    e[j][0] = v.x;
+    e[j][1] = v.y;
+    e[j][2] = v.z;
+    e[j][3] = v.w;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) m = (e[j][c] > m || e[j][c] != e[j][c]) ? e[j][c] : m;
+  }
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const bool ok = lane + 64 * j < n4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      e[j][c] = expf(e[j][c] - m);
+      if (ok) s += e[j][c];
+    }
+  }
+  const float inv = 1.f / wave_sum(s);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = lane + 64 * j;
+    if (i < n4) q[i] = make_float4(e[j][0] * inv, e[j][1] * inv, e[j][2] * inv, e[j][3] * inv);
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(kThreads) void softmax_rows_grad_kernel(const float* __restrict__ dy,
+                                                                     const float* __restrict__ y,
+                                                                     float* __restrict__ dx, int64_t rows, int len) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float4* g4 = reinterpret_cast<const float4*>(dy + r * len);
+  const float4* p4 = reinterpret_cast<const float4*>(y + r * len);
+  float4* d4 = reinterpret_cast<float4*>(dx + r * len);
+  const int n4 = len / 4;
+  float4 gv[NV], pv[NV];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = lane + 64 * j;
+    gv[j] = i < n4 ? g4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    pv[j] = i < n4 ? p4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < n4) s += ((gv[j].x * pv[j].x + gv[j].y * pv[j].y) + gv[j].z * pv[j].z) + gv[j].w * pv[j].w;
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = lane + 64 * j;
+    if (i < n4)
+      d4[i] = make_float4(pv[j].x * (gv[j].x - s), pv[j].y * (gv[j].y - s), pv[j].z * (gv[j].z - s),
+                          pv[j].w * (gv[j].w - s));
+  }
 }
 
 // Axis with inner > 1: one thread per (outer, inner) column, loads coalesced
@@ -785,6 +1022,14 @@ void launch_copy_rows(void* dst, int64_t dst_pitch, const void* src, int64_t src
 
 int launch_rows(int64_t rows) { return int((rows + kWavesPerBlock - 1) / kWavesPerBlock); }
 
+// Smallest register-array size of {1, 2, 4, 8, 16} holding `need` float4 per
+// thread (0: more than 16).
+int regs_for(int64_t need) {
+  for (int r = 1; r <= 16; r *= 2)
+    if (need <= r) return r;
+  return 0;
+}
+
 NearestAxis nearest_axis(int64_t in, int64_t out, double scale) {
   NearestAxis a{int(in), int(out), 0.f, 2};
   if (out == in)
@@ -828,6 +1073,26 @@ int mx_group_norm_forward(const float* x, const float* gamma, const float* beta,
   const int64_t cpg64 = c / groups;
   if (cpg64 <= kGnMaxCpg && cpg64 * hw <= INT32_MAX && n * groups <= INT32_MAX) {
     const bool vec4 = hw % 4 == 0 && aligned16(x) && aligned16(y);
+    const int npt = vec4 ? regs_for((cpg64 * hw / 4 + kThreads - 1) / kThreads) : 0;
+    const dim3 grid(unsigned(n * groups));
+    const int C = int(c), G = int(groups), HW = int(hw);
+    switch (npt) {
+      case 1: hipLaunchKernelGGL(gn_fwd_regs_kernel<1>, grid, dim3(kThreads), 0, s, x, gamma, beta, C, G, HW, eps, y,
+                                 mean, rstd); break;
+      case 2: hipLaunchKernelGGL(gn_fwd_regs_kernel<2>, grid, dim3(kThreads), 0, s, x, gamma, beta, C, G, HW, eps, y,
+                                 mean, rstd); break;
+      case 4: hipLaunchKernelGGL(gn_fwd_regs_kernel<4>, grid, dim3(kThreads), 0, s, x, gamma, beta, C, G, HW, eps, y,
+                                 mean, rstd); break;
+      case 8: hipLaunchKernelGGL(gn_fwd_regs_kernel<8>, grid, dim3(kThreads), 0, s, x, gamma, beta, C, G, HW, eps, y,
+                                 mean, rstd); break;
+      case 16: hipLaunchKernelGGL(gn_fwd_regs_kernel<16>, grid, dim3(kThreads), 0, s, x, gamma, beta, C, G, HW, eps,
+                                  y, mean, rstd); break;
+      default: break;
+    }
+    if (npt) {
+      MX_HIP(hipGetLastError());
+      return MX_OK;
+    }
     if (vec4)
       hipLaunchKernelGGL(gn_fwd_fused_kernel<true>, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, x, gamma, beta,
                          int(c), int(groups), int(hw), eps, y, mean, rstd);
@@ -891,12 +1156,28 @@ int mx_group_norm_backward(const float* dy, const float* x, const float* mean, c
   const bool vec = hw % 4 == 0 && aligned16(x) && aligned16(dy) && (!dx || aligned16(dx));
   const int cpg = int(c / groups);
   if (cpg <= kGnMaxCpg && int64_t(cpg) * hw <= INT32_MAX && n * groups <= INT32_MAX) {
-    if (vec)
-      hipLaunchKernelGGL(gn_bwd_fused_kernel<true>, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, dy, x, mean,
-                         rstd, gamma, int(c), int(groups), int(hw), dx, sdy, sdyx);
-    else
-      hipLaunchKernelGGL(gn_bwd_fused_kernel<false>, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, dy, x, mean,
-                         rstd, gamma, int(c), int(groups), int(hw), dx, sdy, sdyx);
+    const int npt = vec ? regs_for(int64_t((cpg + kWavesPerBlock - 1) / kWavesPerBlock) * ((hw / 4 + 63) / 64)) : 0;
+    const dim3 grid(unsigned(n * groups));
+    const int C = int(c), G = int(groups), HW = int(hw);
+    switch (npt) {
+      case 1: hipLaunchKernelGGL(gn_bwd_regs_kernel<1>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
+                                 HW, dx, sdy, sdyx); break;
+      case 2: hipLaunchKernelGGL(gn_bwd_regs_kernel<2>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
+                                 HW, dx, sdy, sdyx); break;
+      case 4: hipLaunchKernelGGL(gn_bwd_regs_kernel<4>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
+                                 HW, dx, sdy, sdyx); break;
+      case 8: hipLaunchKernelGGL(gn_bwd_regs_kernel<8>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
+                                 HW, dx, sdy, sdyx); break;
+      case 16: hipLaunchKernelGGL(gn_bwd_regs_kernel<16>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
+                                  HW, dx, sdy, sdyx); break;
+      default:
+        if (vec)
+          hipLaunchKernelGGL(gn_bwd_fused_kernel<true>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G, HW,
+                             dx, sdy, sdyx);
+        else
+          hipLaunchKernelGGL(gn_bwd_fused_kernel<false>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
+                             HW, dx, sdy, sdyx);
+    }
     MX_HIP(hipGetLastError());
     if (dgamma || dbeta) {
       hipLaunchKernelGGL(gn_affine_kernel, dim3(int((c + 255) / 256)), dim3(256), 0, s, sdy, sdyx, rstd, int(n),
@@ -1072,8 +1353,17 @@ int mx_upsample_nearest2d(const float* x, int64_t planes, int64_t ih, int64_t iw
   if (planes == 0) return MX_OK;
   MX_REQUIRE(x && y, MX_ERR_INVALID, "mx_upsample_nearest2d: null tensor");
   hipStream_t s = resolve_stream(stream);
+  const NearestAxis ah = nearest_axis(ih, oh, scale_h), aw = nearest_axis(iw, ow, scale_w);
+  if (ah.mode == 1 && aw.mode == 1 && iw % 2 == 0 && (reinterpret_cast<uintptr_t>(x) & 7) == 0 && aligned16(y) &&
+      planes * oh * ow <= INT32_MAX) {
+    const uint32_t rows = uint32_t(planes * ih), half_w = uint32_t(iw / 2);
+    hipLaunchKernelGGL(upsample2x_kernel, dim3(grid_for(int64_t(rows) * half_w)), dim3(kThreads), 0, s, x, y, rows,
+                       half_w);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
   hipLaunchKernelGGL(upsample_nearest_kernel, dim3(grid_for(planes * oh * ow)), dim3(kThreads), 0, s, x, y, planes,
-                     nearest_axis(ih, oh, scale_h), nearest_axis(iw, ow, scale_w));
+                     ah, aw);
   MX_HIP(hipGetLastError());
   return MX_OK;
   MX_ABI_END
@@ -1089,8 +1379,17 @@ int mx_upsample_nearest2d_backward(const float* dy, int64_t planes, int64_t ih, 
   if (planes == 0) return MX_OK;
   MX_REQUIRE(dy && dx, MX_ERR_INVALID, "mx_upsample_nearest2d_backward: null tensor");
   hipStream_t s = resolve_stream(stream);
+  const NearestAxis ah = nearest_axis(ih, oh, scale_h), aw = nearest_axis(iw, ow, scale_w);
+  if (ah.mode == 1 && aw.mode == 1 && iw % 2 == 0 && aligned16(dy) && (reinterpret_cast<uintptr_t>(dx) & 7) == 0 &&
+      planes * oh * ow <= INT32_MAX) {
+    const uint32_t rows = uint32_t(planes * ih), half_w = uint32_t(iw / 2);
+    hipLaunchKernelGGL(upsample2x_grad_kernel, dim3(grid_for(int64_t(rows) * half_w)), dim3(kThreads), 0, s, dy, dx,
+                       rows, half_w);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
   hipLaunchKernelGGL(upsample_nearest_grad_kernel, dim3(grid_for(planes * ih * iw)), dim3(kThreads), 0, s, dy, dx,
-                     planes, nearest_axis(ih, oh, scale_h), nearest_axis(iw, ow, scale_w));
+                     planes, ah, aw);
   MX_HIP(hipGetLastError());
   return MX_OK;
   MX_ABI_END
@@ -1105,7 +1404,14 @@ int mx_softmax_f32(const float* x, int64_t outer, int64_t axis, int64_t inner, f
   if (inner == 1) {
     MX_REQUIRE(axis <= INT32_MAX && outer <= int64_t(INT32_MAX) * kWavesPerBlock, MX_ERR_INVALID,
                "mx_softmax_f32: size exceeds int32");
-    hipLaunchKernelGGL(softmax_last_kernel, dim3(launch_rows(outer)), dim3(kThreads), 0, s, x, y, outer, int(axis));
+    const int nv = (axis % 4 == 0 && aligned16(x) && aligned16(y)) ? regs_for((axis / 4 + 63) / 64) : 0;
+    const dim3 grid(launch_rows(outer));
+    switch (nv) {
+      case 1: hipLaunchKernelGGL(softmax_rows_kernel<1>, grid, dim3(kThreads), 0, s, x, y, outer, int(axis)); break;
+      case 2: hipLaunchKernelGGL(softmax_rows_kernel<2>, grid, dim3(kThreads), 0, s, x, y, outer, int(axis)); break;
+      case 4: hipLaunchKernelGGL(softmax_rows_kernel<4>, grid, dim3(kThreads), 0, s, x, y, outer, int(axis)); break;
+      default: hipLaunchKernelGGL(softmax_last_kernel, grid, dim3(kThreads), 0, s, x, y, outer, int(axis));
+    }
   } else {
     hipLaunchKernelGGL(softmax_inner_kernel, dim3(grid_for(outer * inner)), dim3(kThreads), 0, s, x, y, outer, axis,
                        inner);
@@ -1125,8 +1431,19 @@ int mx_softmax_backward_f32(const float* dy, const float* y, int64_t outer, int6
   if (inner == 1) {
     MX_REQUIRE(axis <= INT32_MAX && outer <= int64_t(INT32_MAX) * kWavesPerBlock, MX_ERR_INVALID,
                "mx_softmax_backward_f32: size exceeds int32");
-    hipLaunchKernelGGL(softmax_last_grad_kernel, dim3(launch_rows(outer)), dim3(kThreads), 0, s, dy, y, dx, outer,
-                       int(axis));
+    const int nv =
+        (axis % 4 == 0 && aligned16(dy) && aligned16(y) && aligned16(dx)) ? regs_for((axis / 4 + 63) / 64) : 0;
+    const dim3 grid(launch_rows(outer));
+    switch (nv) {
+      case 1: hipLaunchKernelGGL(softmax_rows_grad_kernel<1>, grid, dim3(kThreads), 0, s, dy, y, dx, outer, int(axis));
+        break;
+      case 2: hipLaunchKernelGGL(softmax_rows_grad_kernel<2>, grid, dim3(kThreads), 0, s, dy, y, dx, outer, int(axis));
+        break;
+      case 4: hipLaunchKernelGGL(softmax_rows_grad_kernel<4>, grid, dim3(kThreads), 0, s, dy, y, dx, outer, int(axis));
+        break;
+      default:
+        hipLaunchKernelGGL(softmax_last_grad_kernel, grid, dim3(kThreads), 0, s, dy, y, dx, outer, int(axis));
+    }
   } else {
     hipLaunchKernelGGL(softmax_inner_grad_kernel, dim3(grid_for(outer * inner)), dim3(kThreads), 0, s, dy, y, dx,
                        outer, axis, inner);

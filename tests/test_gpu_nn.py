@@ -90,6 +90,8 @@ def close(actual, ref, mag=None, rtol=RTOL, atol=ATOL, what=""):
 GN_CASES = [((2, 8, 4, 5), 4), ((1, 12, 3, 7), 3), ((2, 16, 8), 8), ((2, 4, 1, 1), 2),
             ((2, 64, 16, 16), 32), ((4, 128, 32, 32), 32), ((2, 512, 8, 8), 32), ((1, 32, 6, 6), 32),
             ((2, 256, 64, 64), 32),
+            # register-resident kernels: 16 float4 per thread (C4's level-0 shape), 2 and 8
+            ((2, 128, 64, 64), 32), ((3, 64, 16, 32), 16), ((2, 96, 32, 32), 24),
             # more than 1024 channels per group: the row-statistics path
             ((1, 2048, 2, 2), 1), ((2, 1030, 3, 1), 1)]
 
@@ -216,7 +218,9 @@ def test_abi_unary_misaligned_views(mx):
 
 NEAREST = [((2, 3, 5, 7), (10, 14), None), ((1, 7, 3, 5), (7, 13), None), ((2, 3, 9, 11), (4, 3), None),
            ((1, 2, 1, 7), (3, 1), None), ((1, 2, 7, 9), (7, 9), None), ((2, 3, 5, 7), None, (1.7, 2.3)),
-           ((2, 3, 13, 11), None, (.6, .7)), ((2, 3, 7, 9), None, (1.001, 1.5)), ((16, 256, 16, 16), None, (2.0, 2.0))]
+           ((2, 3, 13, 11), None, (.6, .7)), ((2, 3, 7, 9), None, (1.001, 1.5)), ((16, 256, 16, 16), None, (2.0, 2.0)),
+           # exact 2x with an even width: the vector kernels
+           ((2, 3, 6, 8), (12, 16), None), ((1, 5, 3, 2), None, (2.0, 2.0))]
 
 
 @pytest.mark.parametrize("shape,size,scales", NEAREST)
@@ -240,7 +244,7 @@ def test_abi_upsample_nearest(mx, shape, size, scales):
 
 @pytest.mark.parametrize("shape,dim", [((2, 3, 5), 0), ((2, 3, 5), 1), ((2, 3, 5), 2), ((2, 4, 3, 7), -3),
                                        ((3, 13, 2), 1), ((1, 7, 32), -1), ((64, 256, 256), -1), ((4, 3000), 1),
-                                       ((7, 1), 1)])
+                                       ((7, 1), 1), ((3, 512), 1), ((2, 1000), -1), ((5, 12), 1)])
 def test_abi_softmax(mx, shape, dim):
     rng = np.random.default_rng(62)
     x = (rng.standard_normal(shape) * 5).astype(np.float32)
