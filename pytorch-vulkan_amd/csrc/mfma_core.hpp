@@ -85,6 +85,9 @@ extern "C" __device__ float mx_raw_buffer_load_f32(i32x4 rsrc, int voffset, int 
     "llvm.amdgcn.raw.buffer.load.f32");
 extern "C" __device__ f32x4 mx_raw_buffer_load_v4f32(i32x4 rsrc, int voffset, int soffset, int aux) __asm(
     "llvm.amdgcn.raw.buffer.load.v4f32");
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+extern "C" __device__ f32x2 mx_raw_buffer_load_v2f32(i32x4 rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.buffer.load.v2f32");
 // Vector-memory store through the same resource: a store at an offset past
 // the extent (kOffNone) is dropped by the range check.
 extern "C" __device__ void mx_raw_buffer_store_f32(float v, i32x4 rsrc, int voffset, int soffset, int aux) __asm(
@@ -108,6 +111,9 @@ __device__ __forceinline__ float bload(const i32x4& r, uint32_t voff, uint32_t s
 }
 __device__ __forceinline__ f32x4 bload4(const i32x4& r, uint32_t voff, uint32_t soff) {
   return mx_raw_buffer_load_v4f32(r, int(voff), int(soff), 0);
+}
+__device__ __forceinline__ f32x2 bload2(const i32x4& r, uint32_t voff, uint32_t soff) {
+  return mx_raw_buffer_load_v2f32(r, int(voff), int(soff), 0);
 }
 __device__ __forceinline__ void bstore(float v, const i32x4& r, uint32_t voff, uint32_t soff) {
   mx_raw_buffer_store_f32(v, r, int(voff), int(soff), 0);

@@ -726,6 +726,23 @@ struct Args {
   mfma::FastDiv f_thw, f_tw;
 };
 
+// A workgroup decodes the tiles of its range once, in chunks of up to
+// kChunk tiles, into a table in LDS.  Row offsets are in bytes and leave out
+// the channel term, which each lane adds (saturating, so a sentinel stays out
+// of range); kRowNone marks a row outside the image or a tile past the range.
+constexpr int kChunk = 512;
+constexpr uint32_t kRowNone = 0x80000000u;
+constexpr uint32_t kXRare = 1u << 5, kYRare = 1u << 6;
+struct alignas(16) TileEntry {
+  uint32_t xrow[4];  // x patch rows (columns x0 .. x0 + 3)
+  uint32_t yrow[2];  // dy tile rows (columns ox, ox + 1)
+  int xfirst;        // element offset of the patch's top-left corner (may be negative)
+  // bits 0-3: x column cc inside the image; 4: dy column ox + 1 inside;
+  // kXRare / kYRare: a row segment may leave the tensor for some channel;
+  // 8-11: x row r inside; 12-13: dy row r inside.
+  uint32_t bits;
+};
+
 // Tile t -> image and the top-left output coordinate (2 ty, 2 tx).
 __device__ __forceinline__ void tile_origin(uint32_t t, const Args& p, uint32_t& img, int& oy, int& ox) {
   img = mfma::fdiv(t, p.f_thw);
@@ -737,6 +754,7 @@ __device__ __forceinline__ void tile_origin(uint32_t t, const Args& p, uint32_t&
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void wino_dw_kernel(Args p) {
   __shared__ __attribute__((aligned(16))) float smem[A_FLOATS + B_FLOATS];
+  __shared__ TileEntry tiles[kChunk];
   float* As = smem;
   float* Bs = smem + A_FLOATS;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -749,7 +767,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int o0 = ob * BO, c0 = cb * BC;
   const int k_begin = range * p.kps;
   const int k_end = min(p.T, k_begin + p.kps);
-  const int nslab = (k_end - k_begin + BK - 1) / BK;
 
   // dy: the thread owns output channel a_o of the block and slab tiles
   // 2 a_kq and 2 a_kq + 1 (the k pair one MFMA lane multiplies).
@@ -763,55 +780,78 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const bool c_ok = c0 + b_c < p.C;
   const uint32_t x_chan = uint32_t(g * p.C + c0 + b_c);
 
-  float gy[2][4];  // two 2x2 dy tiles
-  float d[16];     // one 4x4 x patch
+  // Each row of the x patch and of a dy tile is one 16- or 8-byte load at
+  // the row's first column; a row outside the image reads zeros.  Columns
+  // outside the image read the neighbouring row's values and are zeroed in
+  // store() from the column bits.  A tile whose rows may start before the
+  // tensor or end past it (only at the tensor's first and last rows) is read
+  // again element by element in store(), after the slab's loads have landed,
+  // so the rare path adds no wait to the common one and no load it keeps is
+  // ever partly out of range.
+  const int HW = p.H * p.W, OHW = p.OH * p.OW;  // the tensors hold fewer than 2^29 floats
+  const int x_elems = int(p.x_bytes >> 2), dy_elems = int(p.dy_bytes >> 2);
+  const uint32_t xc_bytes = c_ok ? x_chan * uint32_t(HW) * 4u : kRowNone;
+  const uint32_t yc_bytes = o_ok ? dy_chan * uint32_t(OHW) * 4u : kRowNone;
+  f32x4 xr[4];          // the x patch's rows
+  uint32_t xbits;       // the patch's TileEntry::bits
+  f32x2 yr[2][2];       // the dy tiles' rows
+  uint32_t ybits[2];
   auto load = [&](int slab) {
-    const int kb = k_begin + slab * BK;
-    {
-      const int t = kb + b_t;
-      const bool tok = c_ok && t < k_end;
-      uint32_t img;
-      int oy, ox;
-      tile_origin(tok ? uint32_t(t) : 0u, p, img, oy, ox);
-      const int y0 = oy - p.ph, x0 = ox - p.pw;
-      const uint32_t plane = (img * uint32_t(p.Cin) + x_chan) * uint32_t(p.H);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int iy = y0 + r;
-        const bool rok = tok && unsigned(iy) < unsigned(p.H);
-        // x0 may be negative (left padding): the offset wraps modulo 2^32 and
-        // is only used for columns inside the image.
-        const uint32_t row = (plane + uint32_t(iy)) * uint32_t(p.W) * 4u + uint32_t(x0) * 4u;
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-          const bool ok = rok && unsigned(x0 + cc) < unsigned(p.W);
-          d[r * 4 + cc] = mfma::bload(rx, ok ? row + 4u * cc : kOffNone, 0);
-        }
-      }
-    }
+    const TileEntry* ex = &tiles[slab * BK + b_t];
+    const uint4 xo = *reinterpret_cast<const uint4*>(ex->xrow);
+    xbits = ex->bits;
+    xr[0] = mfma::bload4(rx, __builtin_elementwise_add_sat(xo.x, xc_bytes), 0);
+    xr[1] = mfma::bload4(rx, __builtin_elementwise_add_sat(xo.y, xc_bytes), 0);
+    xr[2] = mfma::bload4(rx, __builtin_elementwise_add_sat(xo.z, xc_bytes), 0);
+    xr[3] = mfma::bload4(rx, __builtin_elementwise_add_sat(xo.w, xc_bytes), 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int t = kb + 2 * a_kq + j;
-      const bool tok = o_ok && t < k_end;
-      uint32_t img;
-      int oy, ox;
-      tile_origin(tok ? uint32_t(t) : 0u, p, img, oy, ox);
-      const uint32_t plane = (img * uint32_t(p.Cout) + dy_chan) * uint32_t(p.OH);
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const bool rok = tok && oy + r < p.OH;
-        const uint32_t row = ((plane + uint32_t(oy + r)) * uint32_t(p.OW) + uint32_t(ox)) * 4u;
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const bool ok = rok && ox + cc < p.OW;
-          gy[j][r * 2 + cc] = mfma::bload(rdy, ok ? row + 4u * cc : kOffNone, 0);
-        }
-      }
+      const TileEntry* ey = &tiles[slab * BK + 2 * a_kq + j];
+      const uint2 yo = *reinterpret_cast<const uint2*>(ey->yrow);
+      ybits[j] = ey->bits;
+      yr[j][0] = mfma::bload2(rdy, __builtin_elementwise_add_sat(yo.x, yc_bytes), 0);
+      yr[j][1] = mfma::bload2(rdy, __builtin_elementwise_add_sat(yo.y, yc_bytes), 0);
     }
   };
   float* const a_st = As + a_kq * ROW_A + 2 * a_o;                       // [coord][kq][o][2]
   float* const b_st = Bs + (b_t >> 1) * ROW_B + 2 * b_c + (b_t & 1);    // [coord][kq][c][2]
-  auto store = [&]() {
+  auto store = [&](int slab) {
+    if (xbits & kXRare) {
+      const int first = tiles[slab * BK + b_t].xfirst + int(x_chan) * HW;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const bool ok = c_ok && ((xbits >> (8 + r)) & 1u) && ((xbits >> cc) & 1u);
+          xr[r][cc] = mfma::bload(rx, ok ? uint32_t(first + r * p.W + cc) * 4u : kOffNone, 0);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (ybits[j] & kYRare) {
+        // Row 0 of a tile inside the range is always inside the image.
+        const int first = int(tiles[slab * BK + 2 * a_kq + j].yrow[0] >> 2) + int(dy_chan) * OHW;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+          for (int cc = 0; cc < 2; ++cc) {
+            const bool ok = o_ok && ((ybits[j] >> (12 + r)) & 1u) && (cc == 0 || ((ybits[j] >> 4) & 1u));
+            yr[j][r][cc] = mfma::bload(rdy, ok ? uint32_t(first + r * p.OW + cc) * 4u : kOffNone, 0);
+          }
+      }
+    float gy[2][4];  // two 2x2 dy tiles
+    float d[16];     // one 4x4 x patch
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        gy[j][r * 2] = yr[j][r][0];
+        gy[j][r * 2 + 1] = ((ybits[j] >> 4) & 1u) ? yr[j][r][1] : 0.f;
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) d[r * 4 + cc] = ((xbits >> cc) & 1u) ? xr[r][cc] : 0.f;
     // dM = A g A^T, A = [[1,0],[1,1],[1,-1],[0,-1]], for both tiles.
     float m[2][16];
 #pragma unroll
@@ -881,14 +921,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
   };
 
-  load(0);
-  for (int sl = 0; sl < nslab; ++sl) {
-    store();
+  for (int k0 = k_begin; k0 < k_end; k0 += kChunk) {
+    const int k1 = min(k_end, k0 + kChunk);
+    const int nslab = (k1 - k0 + BK - 1) / BK;
+    for (int i = tid; i < nslab * BK; i += mfma::kThreads) {
+      const int t = k0 + i;
+      const bool tok = t < k1;
+      uint32_t img;
+      int oy, ox;
+      tile_origin(tok ? uint32_t(t) : 0u, p, img, oy, ox);
+      const int y0 = oy - p.ph, x0 = ox - p.pw;
+      TileEntry e;
+      e.xfirst = int(img) * p.Cin * HW + y0 * p.W + x0;
+      const int yfirst = int(img) * p.Cout * OHW + oy * p.OW + ox;
+      uint32_t bits = uint32_t(ox + 1 < p.OW) << 4;
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) bits |= uint32_t(unsigned(x0 + cc) < unsigned(p.W)) << cc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = tok && unsigned(y0 + r) < unsigned(p.H);
+        bits |= uint32_t(ok) << (8 + r);
+        e.xrow[r] = ok ? uint32_t(e.xfirst + r * p.W) * 4u : kRowNone;
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const bool ok = tok && oy + r < p.OH;
+        bits |= uint32_t(ok) << (12 + r);
+        e.yrow[r] = ok ? uint32_t(yfirst + r * p.OW) * 4u : kRowNone;
+      }
+      // Checked for the largest channel, so every channel's lanes agree.
+      if (e.xfirst < 0 || e.xfirst + 3 * p.W + 4 + (p.Cin - 1) * HW > x_elems) bits |= kXRare;
+      if (yfirst + p.OW + 2 + (p.Cout - 1) * OHW > dy_elems) bits |= kYRare;
+      e.bits = bits;
+      tiles[i] = e;
+    }
     __syncthreads();
-    load(min(sl + 1, nslab - 1));  // the last slab re-reads itself: no branch around the loads
-    __builtin_amdgcn_sched_barrier(0);
-    mma();
-    __syncthreads();
+    load(0);
+    for (int sl = 0; sl < nslab; ++sl) {
+      store(sl);
+      __syncthreads();
+      load(min(sl + 1, nslab - 1));  // the last slab re-reads itself: no branch around the loads
+      __builtin_amdgcn_sched_barrier(0);
+      mma();
+      __syncthreads();
+    }
   }
 
   // dw = G^T dU G, G = [[1,0,0],[1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]].

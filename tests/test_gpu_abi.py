@@ -320,7 +320,16 @@ def test_conv_winograd_dinput(mx, monkeypatch, case, fused):
     close(dx, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd dx")
 
 
-@pytest.mark.parametrize("case", WINO_CASES, ids=[f"w{i}" for i in range(len(WINO_CASES))])
+# Tensors smaller than one patch row or whose rows straddle the tensor's
+# ends: the weight gradient's row loads give way to element loads there.
+WINO_DW_CASES = WINO_CASES + [
+    ((1, 1, 1, 2), 1, (3, 3), (1, 1), (1, 1), (1, 1), 1),
+    ((1, 2, 3, 3), 1, (3, 3), (1, 1), (2, 2), (1, 1), 1),
+    ((2, 1, 5, 3), 3, (3, 3), (1, 1), (1, 2), (1, 1), 1),
+]
+
+
+@pytest.mark.parametrize("case", WINO_DW_CASES, ids=[f"w{i}" for i in range(len(WINO_DW_CASES))])
 def test_conv_winograd_dweight(mx, case):
     """Weight gradient (and the bias gradient beside it) of a 3x3 stride-1
     layer through the Winograd adjoint against float64 CPU torch at the
@@ -364,6 +373,22 @@ def test_conv_winograd_dweight_batch_chunks(mx, monkeypatch):
     mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, db, mx.ALGO_WINOGRAD, stream())
     close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, atol=1e-4, mag=refs["dw"][1], what="winograd chunked dw")
     close(db, refs["db"][0], mag=refs["db"][1], what="chunked db")
+
+
+def test_conv_winograd_dweight_one_range(mx, monkeypatch):
+    """No workspace for partials: one tile range of 1798 tiles, which the
+    kernel decodes in several table chunks (the last one ragged), with ragged
+    input- and output-channel blocks."""
+    xs, cout = (2, 16, 58, 62), 24
+    x, w, b = conv_inputs(xs, cout, (3, 3), 1, seed=27)
+    d = mx.conv_desc(xs, w.shape, (1, 1), (1, 1), (1, 1), 1)
+    monkeypatch.setenv("TORCH_VULKAN_CONV_WORKSPACE_MB", "0")
+    assert mx.conv2d_plan(d, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD, False)["variant"] == "wino_dw_kernel"
+    dy = torch.randn((xs[0], cout, d.oh, d.ow), generator=torch.Generator().manual_seed(28))
+    ref, mag = conv_refs(x, w, None, dy, (1, 1), (1, 1), (1, 1), 1)["dw"]
+    dw = torch.full(w.shape, float("nan"), device="cuda")
+    mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, None, mx.ALGO_WINOGRAD, stream())
+    close(dw, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd dw, one range")
 
 
 def test_conv_winograd_dinput_batch_chunks(mx, monkeypatch):
