@@ -189,6 +189,83 @@ struct Args {
   mfma::FastDiv f_thw, f_tw;
 };
 
+// A thread's 4x4 input patch for one slab: each row is one 16-byte load at
+// the row's first column, the slab's channel offset added in 32-bit
+// arithmetic.  Rows outside the image keep the kOffNone offset and read
+// zeros; columns outside it read the neighbouring row's values and are
+// zeroed in patch().  A patch whose rows would start before the tensor or end
+// past it (only at the tensor's first and last rows) is read again element by
+// element in fix(), after which no value kept comes from a load that was
+// partly out of range.
+struct PatchRows {
+  uint32_t row_off[4];  // byte offset of row r's first column, kOffNone off the image
+  uint32_t col_ok;      // bit cc: column cc inside the image
+  uint32_t f_off, l_off;  // offsets of the first and last rows inside the image (0 when none)
+  f32x4 xr[4];
+  uint32_t sx;          // slab offset of the rows held
+  bool whole;           // the row loads were inside the tensor
+
+  __device__ __forceinline__ void init(int64_t plane, int y0, int x0, bool tok, int H, int W) {
+    f_off = l_off = 0;
+    bool seen = false;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int iy = y0 + r;
+      const bool ok = tok && unsigned(iy) < unsigned(H);
+      // x0 may be negative (left padding): the offset is then taken modulo
+      // 2^32, and fix() re-reads the one patch whose row starts before the
+      // tensor.
+      row_off[r] = ok ? uint32_t(((plane + iy) * W + x0) * 4) : kOffNone;
+      if (ok && !seen) f_off = row_off[r];
+      if (ok) l_off = row_off[r];
+      seen = seen || ok;
+    }
+    col_ok = 0;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) col_ok |= (unsigned(x0 + cc) < unsigned(W) ? 1u : 0u) << cc;
+  }
+  // Rows of the slab at byte offset s; a channel past the group's (padding)
+  // reads zeros.
+  __device__ __forceinline__ void load(const i32x4& rx, uint32_t s, uint32_t x_bytes, bool chan_ok) {
+    sx = s;
+    whole = !chan_ok | ((int(f_off + s) >= 0) & (l_off + s + 16u <= x_bytes));  // no short-circuit branch
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xr[r] = mfma::bload4(rx, chan_ok ? row_off[r] + s : kOffNone, 0);
+  }
+  __device__ __forceinline__ void fix(const i32x4& rx) {
+    if (!whole) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        // Offsets formed here, not hoisted out of the slab loop into 16
+        // registers held for the whole kernel.
+        uint32_t ro = row_off[r];
+        asm volatile("" : "+v"(ro));
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+          xr[r][cc] = mfma::bload(rx, ((col_ok >> cc) & 1u) ? ro + 4u * cc : kOffNone, sx);
+      }
+    }
+  }
+  // The same patch element by element (one load per element inside the
+  // image, the slab in the scalar offset), for the two-workgroup fused
+  // kernel, where the row loads' column selects and the rare re-read cost
+  // more than the twelve loads they save.
+  __device__ __forceinline__ void load_elements(const i32x4& rx, uint32_t s, bool chan_ok, float (&d)[16]) const {
+    const uint32_t cmask = chan_ok ? col_ok : 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc)
+        d[r * 4 + cc] = mfma::bload(rx, ((cmask >> cc) & 1u) ? row_off[r] + 4u * cc : kOffNone, s);
+  }
+  __device__ __forceinline__ void patch(float (&d)[16]) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) d[r * 4 + cc] = ((col_ok >> cc) & 1u) ? xr[r][cc] : 0.f;
+  }
+};
+
 // U' for the padded (c, o) range, zero outside the real one: channel c of
 // coordinate t at [g][t][c / 8][(c % 8) / 2][o][c % 2].
 // With `flip`, w is the layer filter [G*C][O][3][3] of an input gradient:
@@ -282,8 +359,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // floats ([k pair][tile][2]) -- distinct banks.
   const int b_t = (tid & 15) | ((tid >> 1) & 16);
   const int b_c = ((tid >> 4) & 1) | ((tid >> 5) & 6);
-  uint32_t row_off[4];
-  uint32_t col_ok = 0;
+  PatchRows px;
   {
     const int t = t0 + b_t;
     const bool tok = t < p.T;
@@ -293,13 +369,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
     const int y0 = int(2 * ty) - p.ph, x0 = int(2 * tx) - p.pw;
     const int64_t plane = (int64_t(img) * p.Cin + int64_t(g) * p.C + b_c) * p.H;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int iy = y0 + r;
-      row_off[r] = (tok && unsigned(iy) < unsigned(p.H)) ? uint32_t(((plane + iy) * p.W + x0) * 4) : kOffNone;
-    }
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) col_ok |= (unsigned(x0 + cc) < unsigned(p.W) ? 1u : 0u) << cc;
+    px.init(plane, y0, x0, tok, p.H, p.W);
   }
   const uint32_t x_sstep = uint32_t(BK) * p.H * p.W * 4;
 
@@ -310,14 +380,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint32_t sa = uint32_t(slab) * a_sstep, sx = uint32_t(slab) * x_sstep;
 #pragma unroll
     for (int q = 0; q < A_PASSES; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
-    // x0 may be -1 (left padding): row_off + 4 * cc is then computed modulo
-    // 2^32 and only used when column cc is inside the image.
-    const uint32_t cmask = (!RAGGED || slab * BK + b_c < p.C) ? col_ok : 0u;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc)
-        d[r * 4 + cc] = mfma::bload(rx, ((cmask >> cc) & 1u) ? row_off[r] + 4u * cc : kOffNone, sx);
+    px.load_elements(rx, sx, !RAGGED || slab * BK + b_c < p.C, d);
   };
   float* const a_st = As + a_row * ROW_A + 4 * a_f4;
   float* const b_st = Bs + (b_c >> 1) * ROW_B + 2 * b_t + (b_c & 1);
@@ -472,6 +535,7 @@ using fused::BK;
 using fused::BO;
 using fused::BT;
 using fused::f32x2;
+using fused::PatchRows;
 using fused::ROW_A;
 using fused::ROW_B;
 using mfma::f32x4;
@@ -502,8 +566,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
   const int b_t = (tid & 15) | ((tid >> 1) & 16);
   const int b_c = ((tid >> 4) & 1) | ((tid >> 5) & 6);
-  uint32_t row_off[4];
-  uint32_t col_ok = 0;
+  PatchRows px;
   {
     const int t = t0 + b_t;
     const bool tok = t < p.T;
@@ -513,37 +576,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
     const int y0 = int(2 * ty) - p.ph, x0 = int(2 * tx) - p.pw;
     const int64_t plane = (int64_t(img) * p.Cin + int64_t(g) * p.C + b_c) * p.H;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int iy = y0 + r;
-      row_off[r] = (tok && unsigned(iy) < unsigned(p.H)) ? uint32_t(((plane + iy) * p.W + x0) * 4) : kOffNone;
-    }
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) col_ok |= (unsigned(x0 + cc) < unsigned(p.W) ? 1u : 0u) << cc;
+    px.init(plane, y0, x0, tok, p.H, p.W);
   }
   const uint32_t x_sstep = uint32_t(BK) * p.H * p.W * 4;
   const int nslab = p.nslab;
 
   f32x4 av[A_PASSES];
-  float d[16];
   auto load = [&](int slab) {
     const uint32_t sa = uint32_t(slab) * a_sstep, sx = uint32_t(slab) * x_sstep;
 #pragma unroll
     for (int q = 0; q < A_PASSES; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
-    // x0 may be -1 (left padding): row_off + 4 * cc is then computed modulo
-    // 2^32 and only used when column cc is inside the image.
-    const uint32_t cmask = (!RAGGED || slab * BK + b_c < p.C) ? col_ok : 0u;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc)
-        d[r * 4 + cc] = mfma::bload(rx, ((cmask >> cc) & 1u) ? row_off[r] + 4u * cc : kOffNone, sx);
+    px.load(rx, sx, uint32_t(p.x_bytes), !RAGGED || slab * BK + b_c < p.C);
   };
   auto store = [&](float* As, float* Bs) {
     float* const a_st = As + a_row * ROW_A + 4 * a_f4;
     float* const b_st = Bs + (b_c >> 1) * ROW_B + 2 * b_t + (b_c & 1);
 #pragma unroll
     for (int q = 0; q < A_PASSES; ++q) *reinterpret_cast<f32x4*>(a_st + q * 8 * ROW_A) = av[q];
+    float d[16];
+    px.patch(d);
     float z[16];
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
@@ -576,8 +627,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto step = [&](const float* Ac, const float* Bc, float* An, float* Bn, int s) {
     // The loaded values count as produced here, so no part of the transform
     // is hoisted above the previous barrier to sit right behind the loads.
+    px.fix(rx);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(d[i]));
+    for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(px.xr[r]));
 #pragma unroll
     for (int q = 0; q < A_PASSES; ++q) asm volatile("" : "+v"(av[q]));
     const f32x2* const a_frag = reinterpret_cast<const f32x2*>(Ac + kq * ROW_A + 2 * (wo * 32 + li));
@@ -628,6 +680,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
 
   load(0);
+  px.fix(rx);
   store(As0, Bs0);
   load(min(1, nslab - 1));
   __syncthreads();
