@@ -10,11 +10,11 @@ Prints ONE JSON line.  The headline (`value`) is BASELINE.json's Conv2D
 fwd+bwd FP32 TFLOP/s on its largest single-GPU Conv2D configuration, C3: the
 53 convolutions of ResNet-50 v1.5 at batch 64, 224x224, each run forward +
 dInput + dWeight (the stem needs no dInput), 3x3 stride-1 layers routed to
-Winograd F(2x2,3x3) as the configuration states: their forwards, and their
+Winograd F(2x2,3x3) as the configuration states: their forwards, their
 input gradients, which are 3x3 stride-1 convolutions of dy with the flipped
-filter (dWeight stays on the implicit GEMM).  A "step" is one pass of
+filter, and their weight gradients, the adjoint of the transform.  A "step" is one pass of
 every layer; inputs are resident in HBM before timing.  `components` holds
-C1 (single conv layer fwd+dX+dW+dB, forward and dInput on Winograd; c1_implicit
+C1 (single conv layer fwd+dX+dW+dB, every phase on Winograd; c1_implicit
 the same on the implicit GEMM only), C2 (Linear addmm fwd+bwd, 8192x4096x4096),
 C5 (multi-tensor AdamW, 250 tensors, GB/s), C4 (the diffusion U-Net training
 step on the "vulkan" device, TFLOP/s of its convolutions and bmm over the
@@ -163,11 +163,12 @@ def build_c3(torch, mx, L, batch, winograd=True):
     return calls, total, executed
 
 
-# C1 routing: forward and dInput (both 3x3 stride-1 correlations) on Winograd
-# F(2x2,3x3), the fastest correct kernels for this layer (rel 1e-3 parity);
-# dWeight with the fused dBias on the implicit GEMM.  C1_IMPLICIT keeps every
-# phase on the implicit GEMM (rel 1e-4 parity) for comparison.
-C1_ROUTED = ("winograd", "winograd", "implicit_gemm")
+# C1 routing: forward and dInput (both 3x3 stride-1 correlations) and the
+# weight gradient (the transform's adjoint, dBias in the same launch) on
+# Winograd F(2x2,3x3), the fastest correct kernels for this layer (rel 1e-3
+# parity).  C1_IMPLICIT keeps every phase on the implicit GEMM (rel 1e-4
+# parity) for comparison.
+C1_ROUTED = ("winograd", "winograd", "winograd")
 C1_IMPLICIT = ("implicit_gemm", "implicit_gemm", "implicit_gemm")
 
 
@@ -972,8 +973,8 @@ def main(argv=None):
                               "frac_of_4r3w_probe": round(gbs / ceiling["adamw_mix_4r3w"], 4),
                               "roofline": roof, "kernels": breakdown(agg_c)}
             else:
-                desc = {"c1": "C1: Conv2D 8x64x56x56 3x3 fwd+dX+dW+dB; forward and dInput on Winograd F(2x2,3x3) "
-                              "(rel 1e-3 parity), dWeight + dBias on the implicit GEMM",
+                desc = {"c1": "C1: Conv2D 8x64x56x56 3x3 fwd+dX+dW+dB; every phase on Winograd F(2x2,3x3) "
+                              "(rel 1e-3 parity), dBias in the weight-gradient launch",
                         "c1_implicit": "C1 with every phase on the implicit GEMM (rel 1e-4 parity)",
                         "c2": "C2: Linear addmm 8192x4096x4096 fwd + dX + dW + db"}[key]
                 comps[key] = {"workload": desc, "ms_per_step": round(ms, 4),

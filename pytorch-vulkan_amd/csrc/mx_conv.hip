@@ -704,9 +704,10 @@ int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, co
                      int64_t ws_limit, hipStream_t s);
 int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, int64_t ws_limit,
                             hipStream_t s);
-int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, int64_t ws_limit,
-                             float* ext, hipStream_t s);
-int winograd_describe(const mx_conv2d_desc& d, int phase, int64_t ws_limit, std::string* variant, int64_t* ws_bytes);
+int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, float* db,
+                             int64_t ws_limit, float* ext, hipStream_t s);
+int winograd_describe(const mx_conv2d_desc& d, int phase, bool with_bias, int64_t ws_limit, std::string* variant,
+                      int64_t* ws_bytes);
 
 namespace conv {
 // Scratch budget of one convolution call (split-K partials, the Winograd
@@ -753,8 +754,7 @@ int describe(const mx_conv2d_desc* desc, int phase, int algo, int with_bias, mx_
   if (phase == MX_CONV_DBIAS) {
     name = chosen == MX_CONV_ALGO_DIRECT ? "conv_db_direct_kernel" : "conv_db_reduce_kernel";
   } else if (chosen == MX_CONV_ALGO_WINOGRAD) {
-    MX_TRY(winograd_describe(d, phase, limit, &name, &r.workspace_bytes));
-    if (phase == MX_CONV_DWEIGHT && with_bias) name += " conv_db_reduce_kernel";
+    MX_TRY(winograd_describe(d, phase, with_bias != 0, limit, &name, &r.workspace_bytes));
   } else if (chosen == MX_CONV_ALGO_DIRECT) {
     name = phase == MX_CONV_FORWARD  ? "conv_fwd_direct_kernel"
            : phase == MX_CONV_DINPUT ? "conv_dx_direct_kernel"
@@ -1058,8 +1058,7 @@ int dweight_impl(const mx_conv2d_desc* desc, const float* x, const float* dy, fl
     }
   }
   if (chosen == MX_CONV_ALGO_WINOGRAD) {
-    MX_TRY(winograd_backward_weight(d, x, dy, dw, limit, ext, s));
-    return db ? mx_conv2d_backward_bias(desc, dy, db, stream) : MX_OK;
+    return winograd_backward_weight(d, x, dy, dw, db, limit, ext, s);
   }
   DwPlan f;
   MX_TRY(plan_dweight(d, x, dy, dw, db, limit, &f));

@@ -612,6 +612,10 @@ int conv_sum_splits(const float* ws, int splits, int64_t n, float* out, const fl
 // finalize: 64 elements per workgroup, four interleaved phases of splits),
 // for few elements over many splits.
 int sum_partials(const float* ws, int splits, int64_t n, float* out, hipStream_t s);
+// The same for two arrays of partials in one launch: ws [splits][n] into
+// out and ws_db [splits][n_db] into out_db.
+int sum_partials(const float* ws, const float* ws_db, int splits, int64_t n, int n_db, float* out, float* out_db,
+                 hipStream_t s);
 
 }  // namespace conv
 }  // namespace mx

@@ -265,5 +265,10 @@ int sum_partials(const float* ws, int splits, int64_t n, float* out, hipStream_t
   return launch_finalize(ws, nullptr, out, nullptr, n, 0, splits, s);
 }
 
+int sum_partials(const float* ws, const float* ws_db, int splits, int64_t n, int n_db, float* out, float* out_db,
+                 hipStream_t s) {
+  return launch_finalize(ws, ws_db, out, out_db, n, out_db ? n_db : 0, splits, s);
+}
+
 }  // namespace conv
 }  // namespace mx

@@ -42,7 +42,8 @@
 
 namespace mx {
 namespace conv {
-int sum_partials(const float* ws, int splits, int64_t n, float* out, hipStream_t s);
+int sum_partials(const float* ws, const float* ws_db, int splits, int64_t n, int n_db, float* out, float* out_db,
+                 hipStream_t s);
 }
 namespace {
 
@@ -774,6 +775,7 @@ struct Args {
   const float* x;   // [N][Cin][H][W]
   const float* dy;  // [N][Cout][OH][OW]
   float* out;       // [range][G][O][C][3][3]
+  float* out_db;    // [range][G][O] dBias partials, or null
   int64_t x_bytes, dy_bytes;
   int Cin, H, W, Cout, OH, OW, ph, pw, C, O, TH, TW, T, n_ob, n_cb, kps;
   mfma::FastDiv f_thw, f_tw;
@@ -849,6 +851,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   uint32_t xbits;       // the patch's TileEntry::bits
   f32x2 yr[2][2];       // the dy tiles' rows
   uint32_t ybits[2];
+  float dsum = 0.f;     // this thread's dy values, for dBias
   auto load = [&](int slab) {
     const TileEntry* ex = &tiles[slab * BK + b_t];
     const uint4 xo = *reinterpret_cast<const uint4*>(ex->xrow);
@@ -901,6 +904,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         gy[j][r * 2] = yr[j][r][0];
         gy[j][r * 2 + 1] = ((ybits[j] >> 4) & 1u) ? yr[j][r][1] : 0.f;
       }
+    dsum += ((gy[0][0] + gy[0][1]) + (gy[0][2] + gy[0][3])) + ((gy[1][0] + gy[1][1]) + (gy[1][2] + gy[1][3]));
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -1018,6 +1022,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       mma();
       __syncthreads();
     }
+  }
+
+  // dBias of the range: every dy element lies in exactly one tile, and the
+  // workgroups of the first input-channel block read each one once; the four
+  // lanes of an output channel (a_kq = 0..3, adjacent) hold its slab tiles.
+  if (p.out_db && cb == 0) {
+    float t = dsum;
+    t += __shfl_xor(t, 1);
+    t += __shfl_xor(t, 2);
+    if (a_kq == 0 && o_ok) p.out_db[(int64_t(range) * gridDim.y + g) * p.O + o0 + a_o] = t;
   }
 
   // dw = G^T dU G, G = [[1,0,0],[1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]].
@@ -1264,10 +1278,11 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
 struct DwRunPlan {
   fused_dw::Args p{};
   int G = 1;
-  int64_t blocks = 0, ranges = 1, n_dw = 0;
+  int64_t blocks = 0, ranges = 1, n_dw = 0, n_db = 0;
 };
 
-int plan_dw_run(const mx_conv2d_desc& d, int64_t ws_limit, DwRunPlan* r) {
+// with_db: the kernel also writes the dBias partials (Cout per range).
+int plan_dw_run(const mx_conv2d_desc& d, int64_t ws_limit, bool with_db, DwRunPlan* r) {
   fused_dw::Args& p = r->p;
   p.Cin = int(d.cin);
   p.H = int(d.h);
@@ -1293,11 +1308,12 @@ int plan_dw_run(const mx_conv2d_desc& d, int64_t ws_limit, DwRunPlan* r) {
   MX_REQUIRE(p.x_bytes < mfma::kBufMaxBytes && p.dy_bytes < mfma::kBufMaxBytes && T <= INT32_MAX, MX_ERR_UNSUPPORTED,
              "winograd dweight: an operand exceeds the 2 GiB bound");
   r->n_dw = int64_t(p.Cout) * p.C * 9;
+  r->n_db = with_db ? p.Cout : 0;
   r->blocks = int64_t(p.n_ob) * p.n_cb * r->G;
   int64_t per_cu = 2;
   if (const char* e = std::getenv("MX_WINO_DW_PER_CU")) per_cu = std::max(1, std::atoi(e));
   int64_t want = std::max<int64_t>(1, (per_cu * int64_t(cu_count()) + r->blocks - 1) / r->blocks);
-  const int64_t fit = ws_limit / (r->n_dw * 4);
+  const int64_t fit = ws_limit / ((r->n_dw + r->n_db) * 4);
   want = fit >= 2 ? std::min(want, fit) : 1;
   int64_t kps = (T + want - 1) / want;
   kps = std::max<int64_t>(kps, 4 * fused_dw::BK);
@@ -1316,28 +1332,31 @@ int winograd_forward(const mx_conv2d_desc& d, const float* x, const float* w, co
   return winograd_run(d, x, w, bias, y, false, ws_limit, s);
 }
 
-// dw of the 3x3 stride-1 layer d (any padding): the fused adjoint kernel
-// over K ranges of tiles, then a fixed-order sum of the ranges' partials.
-// The partials go to `ext` when the caller provides the workspace (at least
-// ws_limit bytes), else to a stream-ordered allocation.
-int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, int64_t ws_limit,
-                             float* ext, hipStream_t s) {
+// dw (and db when given) of the 3x3 stride-1 layer d (any padding): the
+// fused adjoint kernel over K ranges of tiles, then a fixed-order sum of the
+// ranges' partials.  The partials go to `ext` when the caller provides the
+// workspace (at least ws_limit bytes), else to a stream-ordered allocation.
+int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const float* dy, float* dw, float* db,
+                             int64_t ws_limit, float* ext, hipStream_t s) {
   DwRunPlan r;
-  MX_TRY(plan_dw_run(d, ws_limit, &r));
+  MX_TRY(plan_dw_run(d, ws_limit, db != nullptr, &r));
   fused_dw::Args& p = r.p;
   p.x = x;
   p.dy = dy;
   Scratch ws;
   float* partials = ext;
   if (r.ranges > 1 && !ext) {
-    MX_TRY(ws.alloc(size_t(r.ranges) * size_t(r.n_dw) * 4, s));
+    MX_TRY(ws.alloc(size_t(r.ranges) * size_t(r.n_dw + r.n_db) * 4, s));
     partials = ws.as<float>();
   }
+  float* const partials_db = r.ranges > 1 ? partials + r.ranges * r.n_dw : nullptr;
   p.out = r.ranges > 1 ? partials : dw;
+  p.out_db = db ? (r.ranges > 1 ? partials_db : db) : nullptr;
   hipLaunchKernelGGL(fused_dw::wino_dw_kernel, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)), dim3(256), 0,
                      s, p);
   MX_HIP(hipGetLastError());
-  if (r.ranges > 1) return conv::sum_partials(partials, int(r.ranges), r.n_dw, dw, s);
+  if (r.ranges > 1)
+    return conv::sum_partials(partials, partials_db, int(r.ranges), r.n_dw, int(r.n_db), dw, db, s);
   return MX_OK;
 }
 
@@ -1359,13 +1378,13 @@ mx_conv2d_desc dinput_as_forward(const mx_conv2d_desc& d) {
 
 // Kernels a Winograd call of `phase` launches and the scratch it counts
 // against the workspace budget.
-int winograd_describe(const mx_conv2d_desc& d, int phase, int64_t ws_limit, std::string* variant,
+int winograd_describe(const mx_conv2d_desc& d, int phase, bool with_bias, int64_t ws_limit, std::string* variant,
                       int64_t* ws_bytes) {
   if (phase == MX_CONV_DWEIGHT) {
     DwRunPlan r;
-    MX_TRY(plan_dw_run(d, ws_limit, &r));
+    MX_TRY(plan_dw_run(d, ws_limit, with_bias, &r));
     *variant = r.ranges > 1 ? "wino_dw_kernel+ranges" : "wino_dw_kernel";
-    *ws_bytes = r.ranges > 1 ? r.ranges * r.n_dw * 4 : 0;
+    *ws_bytes = r.ranges > 1 ? r.ranges * (r.n_dw + r.n_db) * 4 : 0;
     return MX_OK;
   }
   RunPlan r;

@@ -208,10 +208,10 @@ def layout_operands(m, n, k, layout, batch=None):
 # ------------------------------------------------------------------ configuration calls
 def c1_calls():
     """C1 as bench.py runs it: one 3x3 layer, forward + dInput + dWeight + dBias,
-    forward and dInput on Winograd, dWeight on the implicit GEMM; and the same
+    every phase on Winograd (dBias in the weight-gradient launch); and the same
     layer with every phase on the implicit GEMM (its comparison line)."""
     g = ((8, 64, 56, 56), 64, (3, 3), (1, 1), (1, 1), (1, 1), 1)
-    routed = [("winograd", 0), ("winograd", 1), ("implicit_gemm", 2)]
+    routed = [("winograd", 0), ("winograd", 1), ("winograd", 2)]
     implicit = [("implicit_gemm", ph) for ph in (0, 1, 2)]
     return [{"kind": "conv", "geometry": g, "phase": ph, "algo": a, "with_bias": True} for a, ph in routed + implicit]
 

@@ -378,17 +378,19 @@ def test_conv_winograd_dweight_batch_chunks(mx, monkeypatch):
 def test_conv_winograd_dweight_one_range(mx, monkeypatch):
     """No workspace for partials: one tile range of 1798 tiles, which the
     kernel decodes in several table chunks (the last one ragged), with ragged
-    input- and output-channel blocks."""
+    input- and output-channel blocks; dBias comes out of the same launch."""
     xs, cout = (2, 16, 58, 62), 24
     x, w, b = conv_inputs(xs, cout, (3, 3), 1, seed=27)
     d = mx.conv_desc(xs, w.shape, (1, 1), (1, 1), (1, 1), 1)
     monkeypatch.setenv("TORCH_VULKAN_CONV_WORKSPACE_MB", "0")
-    assert mx.conv2d_plan(d, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD, False)["variant"] == "wino_dw_kernel"
+    assert mx.conv2d_plan(d, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD, True)["variant"] == "wino_dw_kernel"
     dy = torch.randn((xs[0], cout, d.oh, d.ow), generator=torch.Generator().manual_seed(28))
-    ref, mag = conv_refs(x, w, None, dy, (1, 1), (1, 1), (1, 1), 1)["dw"]
+    refs = conv_refs(x, w, b, dy, (1, 1), (1, 1), (1, 1), 1)
     dw = torch.full(w.shape, float("nan"), device="cuda")
-    mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, None, mx.ALGO_WINOGRAD, stream())
-    close(dw, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd dw, one range")
+    db = torch.full(b.shape, float("nan"), device="cuda")
+    mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, db, mx.ALGO_WINOGRAD, stream())
+    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, atol=1e-4, mag=refs["dw"][1], what="winograd dw, one range")
+    close(db, refs["db"][0], mag=refs["db"][1], what="db beside winograd dw, one range")
 
 
 def test_conv_winograd_dinput_batch_chunks(mx, monkeypatch):
