@@ -169,13 +169,16 @@ enum mx_conv_phase { MX_CONV_FORWARD = 0, MX_CONV_DINPUT = 1, MX_CONV_DWEIGHT = 
  * requested explicitly, the input gradient of a 3x3 stride-1 dilation-1 layer
  * with padding <= 2 (an addition: the reference's Winograd is forward only;
  * AUTO never picks it for dInput); REDUCE is the no-scratch dWeight / dBias
- * reduction. */
+ * reduction; DEPTHWISE is the forward of a layer with groups == cin and any
+ * channel multiplier (conv2d_depthwise.comp:15-41; candidate rule
+ * csrc/ops/convolution.cpp:361, chosen by AUTO when cin >= 8 as at :462). */
 enum mx_conv_algo {
   MX_CONV_ALGO_AUTO = 0,
   MX_CONV_ALGO_DIRECT = 1,
   MX_CONV_ALGO_IMPLICIT_GEMM = 2,
   MX_CONV_ALGO_WINOGRAD = 3,
-  MX_CONV_ALGO_REDUCE = 4
+  MX_CONV_ALGO_REDUCE = 4,
+  MX_CONV_ALGO_DEPTHWISE = 5
 };
 
 /* Validation and output shape: convolution_params

@@ -113,6 +113,87 @@ __global__ void conv_dw_direct_kernel(ConvArgs p) {
   }
 }
 
+// Depthwise forward (groups == Cin, Cout = m * Cin; conv2d_depthwise.comp:15-41).
+// One workgroup per (image, input channel, 16 x 64 output tile): the input
+// patch the tile reads (halo and zero padding included) is staged once in LDS
+// and all m output channels that read this input channel are computed from
+// it, so x is read from HBM once per tile and y written once.  Wave w owns
+// output rows 4w .. 4w+3 of the tile, lane l output column l.  Each output
+// starts from its bias and adds the taps in (kh, kw) order, as the shader
+// does; a padded tap adds 0 * w.  A patch larger than the LDS budget (very
+// large dilation) reads x directly (kStaged = false).
+constexpr int kDwTileW = 64, kDwTileH = 16, kDwRowsPerWave = 4;
+constexpr int kDwLdsFloats = 12288;  // 48 KiB
+
+struct DepthwiseArgs {
+  ConvArgs p;
+  int tiles_w, tiles_h;
+  int64_t tiles;
+  int patch_h, patch_w;  // staged input rows / columns of one tile
+};
+
+template <bool kStaged>
+__global__ __launch_bounds__(256) void conv_depthwise_kernel(DepthwiseArgs a) {
+  __shared__ float patch[kStaged ? kDwLdsFloats : 1];
+  const ConvArgs& p = a.p;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = p.Cout_g;
+  for (int64_t t = blockIdx.x; t < a.tiles; t += gridDim.x) {
+    const int tw = int(t % a.tiles_w);
+    const int th = int((t / a.tiles_w) % a.tiles_h);
+    const int64_t plane = t / (int64_t(a.tiles_w) * a.tiles_h);  // img * Cin + ic
+    const int ic = int(plane % p.Cin);
+    const int img = int(plane / p.Cin);
+    const float* xp = p.x + plane * p.HW;
+    const int oh0 = th * kDwTileH, ow0 = tw * kDwTileW;
+    const int ih0 = oh0 * p.sh - p.ph, iw0 = ow0 * p.sw - p.pw;
+    if constexpr (kStaged) {
+      const int n = a.patch_h * a.patch_w;
+      for (int e = threadIdx.x; e < n; e += 256) {
+        const int r = e / a.patch_w, c = e - r * a.patch_w;
+        const int ih = ih0 + r, iw = iw0 + c;
+        patch[e] = (ih >= 0 && ih < p.H && iw >= 0 && iw < p.W) ? xp[ih * p.W + iw] : 0.f;
+      }
+      __syncthreads();
+    }
+    const int ow = ow0 + lane;
+    const int orow = wave * kDwRowsPerWave;
+    for (int j = 0; j < m; ++j) {
+      const int oc = ic * m + j;
+      const float* wk = p.w + int64_t(oc) * p.KK;
+      const float b = p.bias ? p.bias[oc] : 0.f;
+      float acc[kDwRowsPerWave];
+#pragma unroll
+      for (int r = 0; r < kDwRowsPerWave; ++r) acc[r] = b;
+      for (int kh = 0; kh < p.KH; ++kh)
+        for (int kw = 0; kw < p.KW; ++kw) {
+          const float wv = wk[kh * p.KW + kw];
+          const int c = lane * p.sw + kw * p.dw;
+#pragma unroll
+          for (int r = 0; r < kDwRowsPerWave; ++r) {
+            const int rr = (orow + r) * p.sh + kh * p.dh;
+            float xv;
+            if constexpr (kStaged) {
+              // rr <= 15 sh + (KH-1) dh < patch_h and c <= 63 sw + (KW-1) dw < patch_w.
+              xv = patch[rr * a.patch_w + c];
+            } else {
+              const int ih = ih0 + rr, iw = iw0 + c;
+              xv = (ih >= 0 && ih < p.H && iw >= 0 && iw < p.W) ? xp[ih * p.W + iw] : 0.f;
+            }
+            acc[r] += xv * wv;
+          }
+        }
+      float* yp = p.out + (int64_t(img) * p.Cout + oc) * p.OHOW;
+#pragma unroll
+      for (int r = 0; r < kDwRowsPerWave; ++r) {
+        const int oh = oh0 + orow + r;
+        if (oh < p.OH && ow < p.OW) yp[oh * p.OW + ow] = acc[r];
+      }
+    }
+    if constexpr (kStaged) __syncthreads();  // the next tile restages the patch
+  }
+}
+
 // No-scratch dWeight: one workgroup per weight, strided partial sums and a
 // fixed LDS tree (conv2d_backward_weight_reduce.comp:13-38).
 __global__ __launch_bounds__(256) void conv_dw_reduce_kernel(ConvArgs p) {
@@ -238,6 +319,36 @@ ConvArgs make_args(const mx_conv2d_desc& d) {
   return p;
 }
 
+bool depthwise_staged(const mx_conv2d_desc& d) {
+  const int64_t ph = (kDwTileH - 1) * d.sh + (d.kh - 1) * d.dh + 1;
+  const int64_t pw = (kDwTileW - 1) * d.sw + (d.kw - 1) * d.dw + 1;
+  return ph * pw <= kDwLdsFloats;
+}
+
+int conv_depthwise_forward(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+                           hipStream_t s) {
+  DepthwiseArgs a{};
+  a.p = make_args(d);
+  a.p.x = x;
+  a.p.w = w;
+  a.p.bias = bias;
+  a.p.out = y;
+  a.tiles_w = int((d.ow + kDwTileW - 1) / kDwTileW);
+  a.tiles_h = int((d.oh + kDwTileH - 1) / kDwTileH);
+  a.tiles = d.n * d.cin * a.tiles_w * a.tiles_h;
+  if (a.tiles == 0) return MX_OK;
+  const dim3 grid(unsigned(std::min<int64_t>(a.tiles, 1 << 20)));
+  if (depthwise_staged(d)) {
+    a.patch_h = int((kDwTileH - 1) * d.sh + (d.kh - 1) * d.dh + 1);
+    a.patch_w = int((kDwTileW - 1) * d.sw + (d.kw - 1) * d.dw + 1);
+    hipLaunchKernelGGL(conv_depthwise_kernel<true>, grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(conv_depthwise_kernel<false>, grid, dim3(256), 0, s, a);
+  }
+  MX_HIP(hipGetLastError());
+  return MX_OK;
+}
+
 int linear_blocks(int64_t total) { return int(std::min<int64_t>((total + 255) / 256, 1 << 20)); }
 
 // Images per launch of the implicit-GEMM kernels: their loaders address each
@@ -273,6 +384,8 @@ bool winograd_applicable(const mx_conv2d_desc& d) {
 int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
   const int64_t cin_g = d.cin / d.groups, cout_g = d.cout / d.groups;
   const int64_t rows = d.n * d.oh * d.ow, cols = cin_g * d.kh * d.kw;
+  MX_REQUIRE(requested >= MX_CONV_ALGO_AUTO && requested <= MX_CONV_ALGO_DEPTHWISE, MX_ERR_INVALID,
+             "conv2d: unknown algorithm ", requested);
   switch (phase) {
     case MX_CONV_FORWARD:
       if (requested == MX_CONV_ALGO_WINOGRAD) {
@@ -284,6 +397,10 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
       }
       MX_REQUIRE(requested != MX_CONV_ALGO_REDUCE, MX_ERR_UNSUPPORTED,
                  "reduce is not a forward convolution algorithm");
+      if (requested == MX_CONV_ALGO_DEPTHWISE)
+        MX_REQUIRE(d.groups == d.cin, MX_ERR_UNSUPPORTED,
+                   "Forced Vulkan convolution forward candidate depthwise exceeds device limits, workspace "
+                   "budget, or operator applicability");
       if (requested != MX_CONV_ALGO_AUTO) {
         *algo = requested;
         return MX_OK;
@@ -293,6 +410,8 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
       // direct kernel's per-output loop once the GEMM has real depth.
       if (winograd_applicable(d) && d.groups >= 4 && cin_g >= 16 && cout_g >= 16 && rows >= 2048)
         *algo = MX_CONV_ALGO_WINOGRAD;
+      else if (d.groups == d.cin && d.cin >= 8)
+        *algo = MX_CONV_ALGO_DEPTHWISE;
       else if (cols >= 8 && rows >= 32 && cout_g * cols >= 64)
         *algo = MX_CONV_ALGO_IMPLICIT_GEMM;
       else
@@ -308,7 +427,7 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
         *algo = MX_CONV_ALGO_WINOGRAD;
         return MX_OK;
       }
-      MX_REQUIRE(requested != MX_CONV_ALGO_REDUCE, MX_ERR_UNSUPPORTED,
+      MX_REQUIRE(requested != MX_CONV_ALGO_REDUCE && requested != MX_CONV_ALGO_DEPTHWISE, MX_ERR_UNSUPPORTED,
                  "dinput supports direct, implicit_gemm and winograd only");
       if (requested != MX_CONV_ALGO_AUTO) {
         *algo = requested;
@@ -328,6 +447,8 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
         *algo = MX_CONV_ALGO_WINOGRAD;
         return MX_OK;
       }
+      MX_REQUIRE(requested != MX_CONV_ALGO_DEPTHWISE, MX_ERR_UNSUPPORTED,
+                 "depthwise is a forward convolution algorithm");
       if (requested != MX_CONV_ALGO_AUTO) {
         *algo = requested;
         return MX_OK;
@@ -755,6 +876,8 @@ int describe(const mx_conv2d_desc* desc, int phase, int algo, int with_bias, mx_
     name = chosen == MX_CONV_ALGO_DIRECT ? "conv_db_direct_kernel" : "conv_db_reduce_kernel";
   } else if (chosen == MX_CONV_ALGO_WINOGRAD) {
     MX_TRY(winograd_describe(d, phase, with_bias != 0, limit, &name, &r.workspace_bytes));
+  } else if (chosen == MX_CONV_ALGO_DEPTHWISE) {
+    name = depthwise_staged(d) ? "conv_depthwise_kernel<staged>" : "conv_depthwise_kernel<global>";
   } else if (chosen == MX_CONV_ALGO_DIRECT) {
     name = phase == MX_CONV_FORWARD  ? "conv_fwd_direct_kernel"
            : phase == MX_CONV_DINPUT ? "conv_dx_direct_kernel"
@@ -837,6 +960,7 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
     }
   }
   if (chosen == MX_CONV_ALGO_WINOGRAD) return winograd_forward(d, x, w, bias, y, limit, s);
+  if (chosen == MX_CONV_ALGO_DEPTHWISE) return conv_depthwise_forward(d, x, w, bias, y, s);
   if (chosen == MX_CONV_ALGO_DIRECT) {
     ConvArgs p = make_args(d);
     p.x = x;
@@ -1132,6 +1256,8 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
     name = info.variant;
   } else if (info.algo == MX_CONV_ALGO_WINOGRAD) {
     name = phase == MX_CONV_DWEIGHT ? "wino_dw_kernel" : "wino_filter_kernel";
+  } else if (info.algo == MX_CONV_ALGO_DEPTHWISE) {
+    name = "conv_depthwise_kernel";
   } else if (info.algo == MX_CONV_ALGO_DIRECT) {
     name = phase == MX_CONV_FORWARD  ? "conv_fwd_direct_kernel"
            : phase == MX_CONV_DINPUT ? "conv_dx_direct_kernel"

@@ -25,6 +25,7 @@ const char* algo_name(int algo) {
     case MX_CONV_ALGO_IMPLICIT_GEMM: return "implicit_gemm";
     case MX_CONV_ALGO_WINOGRAD: return "winograd_f2";
     case MX_CONV_ALGO_REDUCE: return "reduce";
+    case MX_CONV_ALGO_DEPTHWISE: return "depthwise";
     default: return "auto";
   }
 }
@@ -38,7 +39,8 @@ std::string env_or(const char* name, const char* dflt) {
 int forward_algo() {
   const std::string a = env_or("TORCH_VULKAN_CONV_ALGO", "auto");
   if (a == "auto") return MX_CONV_ALGO_AUTO;
-  if (a == "direct" || a == "depthwise") return MX_CONV_ALGO_DIRECT;
+  if (a == "direct") return MX_CONV_ALGO_DIRECT;
+  if (a == "depthwise") return MX_CONV_ALGO_DEPTHWISE;
   if (a == "tiled" || a == "implicit_gemm") return MX_CONV_ALGO_IMPLICIT_GEMM;
   if (a == "winograd") return MX_CONV_ALGO_WINOGRAD;
   TORCH_CHECK(false, "TORCH_VULKAN_CONV_ALGO has an invalid algorithm (forward: auto/direct/tiled/depthwise/winograd)");

@@ -22,7 +22,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmx.so")
 MX_OK, MX_ERR_INVALID, MX_ERR_UNSUPPORTED, MX_ERR_OOM, MX_ERR_HIP, MX_ERR_WORKSPACE = range(6)
 MX_COPY_H2D, MX_COPY_D2H, MX_COPY_D2D = 1, 2, 3
 MX_CONV_FORWARD, MX_CONV_DINPUT, MX_CONV_DWEIGHT, MX_CONV_DBIAS = range(4)
-ALGO_AUTO, ALGO_DIRECT, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_REDUCE = range(5)
+ALGO_AUTO, ALGO_DIRECT, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_REDUCE, ALGO_DEPTHWISE = range(6)
 BIAS_NONE, BIAS_COL, BIAS_MATRIX = range(3)
 ABI_VERSION = 2  # struct layouts of include/mx.h
 

@@ -97,6 +97,25 @@ def test_planner_mirrors_reference_heuristic(mx):
             assert mx.conv2d_select(d, phase) == mx.ALGO_IMPLICIT_GEMM
 
 
+def test_depthwise_selection(mx):
+    """Depthwise forward: AUTO for groups == cin >= 8 (csrc/ops/convolution.cpp:462),
+    forced only where groups == cin (:361), never for a gradient."""
+    dw = mx.conv_desc((2, 32, 28, 28), (64, 1, 3, 3), (1, 1), (1, 1), (1, 1), 32)
+    assert mx.conv2d_select(dw, mx.MX_CONV_FORWARD) == mx.ALGO_DEPTHWISE
+    assert mx.conv2d_kernel_name(dw, mx.MX_CONV_FORWARD) == "conv_depthwise_kernel"
+    small = mx.conv_desc((1, 4, 8, 8), (4, 1, 3, 3), (1, 1), (1, 1), (1, 1), 4)
+    assert mx.conv2d_select(small, mx.MX_CONV_FORWARD) == mx.ALGO_DIRECT
+    assert mx.conv2d_select(small, mx.MX_CONV_FORWARD, mx.ALGO_DEPTHWISE) == mx.ALGO_DEPTHWISE
+    grouped = mx.conv_desc((1, 16, 8, 8), (16, 8, 3, 3), (1, 1), (1, 1), (1, 1), 2)
+    with pytest.raises(mx.MXError, match="depthwise"):
+        mx.conv2d_select(grouped, mx.MX_CONV_FORWARD, mx.ALGO_DEPTHWISE)
+    for phase in (mx.MX_CONV_DINPUT, mx.MX_CONV_DWEIGHT):
+        with pytest.raises(mx.MXError):
+            mx.conv2d_select(dw, phase, mx.ALGO_DEPTHWISE)
+    with pytest.raises(mx.MXError, match="unknown algorithm"):
+        mx.conv2d_select(dw, mx.MX_CONV_FORWARD, 9)
+
+
 def test_forced_inapplicable_algorithm_raises(mx):
     strided = mx.conv_desc((1, 8, 9, 9), (8, 8, 3, 3), (2, 2), (1, 1))
     with pytest.raises(mx.MXError, match="winograd"):
