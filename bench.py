@@ -733,9 +733,11 @@ def sq_summary(directory, xcds=8, cus=256):
     return "\n".join(out)
 
 
-WINOGRAD_KERNELS = ("filter_kernel", "wino_fused_kernel",   # fused path
+WINOGRAD_KERNELS = ("filter_kernel", "wino_ws_kernel",   # fused path
                     "wino_filter_kernel", "wino_input_kernel", "wino_output_kernel", "gemm_kernel")
-WINOGRAD_CALL_START = ("filter_kernel", "wino_filter_kernel")  # first dispatch of every Winograd call
+# First dispatch of a Winograd call: its filter transform, or the fused
+# kernel itself when that transforms the filter (no filter launch before it).
+WINOGRAD_CALL_START = ("filter_kernel", "wino_filter_kernel")
 BEFORE_HELPERS = ("conv_fwd_pack_kernel", "conv_dx_pack_kernel")       # run before their tile kernel
 AFTER_HELPERS = ("conv_dw_finalize_kernel", "conv_sum_splits_kernel")   # run after it
 
@@ -817,7 +819,8 @@ def trace_summary(trace_csv, bench_log):
             # the Winograd weight gradient; its range sum follows as a helper
             owner[i] = last_tile = "winograd_dweight"
         elif label in WINOGRAD_KERNELS:
-            wino_calls += label in WINOGRAD_CALL_START
+            wino_calls += label in WINOGRAD_CALL_START or (
+                label == "wino_ws_kernel" and (i == 0 or seq[i - 1][0] != "filter_kernel"))
             owner[i] = "winograd_dinput" if (wino_dx and wino_calls % 2 == 0) else "winograd_forward"
         elif label in AFTER_HELPERS or label == "conv_dx_zero_kernel":
             owner[i] = last_tile
@@ -935,7 +938,7 @@ def main(argv=None):
     value = flops_step / (dt / args.steps) / 1e12
     log(f"headline: {ms_step:.3f} ms/step, {value:.2f} TFLOP/s")
     _, agg = run_steps(torch, L, calls, args.steps, 0, timing=True)
-    roof = roofline_from(agg, "mfma")
+    roof = roofline_from(agg, "mfma", executed_step / flops_step)
     if args.workload == "c3" and not args.no_winograd and os.path.exists(TRAFFIC_FILE):
         traffic = json.load(open(TRAFFIC_FILE)).get("kernels", {}).get(roof["kernel"])
         if traffic:

@@ -19,9 +19,11 @@
 //
 // Fused kernel (the default): one workgroup computes 64 output channels x 32
 // tiles for all 16 coordinates.  Per slab of 8 input channels it stages the
-// transformed filter U (precomputed once per call, [G][16][Cpad][Opad], output
-// channels contiguous, zero padded) and transforms the 4x4 input patches it
-// loads straight into LDS, so V never goes to HBM; the 16 products run as
+// transformed filter U (precomputed once per call by the filter launch,
+// [G][16][Cpad][Opad], output channels contiguous, zero padded, or for
+// short channel walks transformed from w in the kernel) and transforms the
+// 4x4 input patches it loads straight into LDS, so V never goes to HBM; the
+// 16 products run as
 // v_mfma_f32_16x16x4f32 with each wave holding all 16 coordinates of a 32
 // channel x 16 tile block, so the output transform A^T M A and the bias are
 // applied in registers and M never goes to HBM either.
@@ -183,9 +185,10 @@ static_assert(BK * BT == mfma::kThreads, "one input patch per thread per slab");
 struct Args {
   const float* x;    // [N][Cin][H][W]
   const float* U;    // [G][16][nslab][4][Opad][2]
+  const float* w;    // the layer filter, for kernels that transform it themselves
   const float* bias;
   float* y;          // [N][Cout][OH][OW]
-  int64_t x_bytes, u_bytes, y_bytes;
+  int64_t x_bytes, u_bytes, y_bytes, w_bytes;
   int Cin, H, W, Cout, OH, OW, ph, pw, C, O, Cpad, Opad, TH, TW, T, n_ob, nslab;
   mfma::FastDiv f_thw, f_tw;
 };
@@ -275,6 +278,27 @@ struct PatchRows {
 // One thread per (g, channel pair c, c + 1, o), o fastest: the two channels
 // of a pair are adjacent in U', so each coordinate is one 8-byte store and a
 // wave writes 512 contiguous bytes.
+// u = G k G^T for one 3x3 filter k (row-major), G = [[1,0,0],[1/2,1/2,1/2],
+// [1/2,-1/2,1/2],[0,0,1]].  The filter launch and the kernels that transform
+// the filter themselves share this arithmetic, so their U' are bit-identical.
+__device__ __forceinline__ void filter_math(const float (&k)[9], float (&u)[16]) {
+  float z[4][3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    z[0][j] = k[j];
+    z[1][j] = 0.5f * (k[j] + k[3 + j] + k[6 + j]);
+    z[2][j] = 0.5f * (k[j] - k[3 + j] + k[6 + j]);
+    z[3][j] = k[6 + j];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    u[r * 4 + 0] = z[r][0];
+    u[r * 4 + 1] = 0.5f * (z[r][0] + z[r][1] + z[r][2]);
+    u[r * 4 + 2] = 0.5f * (z[r][0] - z[r][1] + z[r][2]);
+    u[r * 4 + 3] = z[r][2];
+  }
+}
+
 __device__ __forceinline__ void filter_transform(const float* __restrict__ w, int C, int O, int g, int o, int c,
                                                  bool flip, float (&u)[16]) {
   if (o >= O || c >= C) {
@@ -292,21 +316,7 @@ __device__ __forceinline__ void filter_transform(const float* __restrict__ w, in
 #pragma unroll
     for (int j = 0; j < 9; ++j) k[j] = src[j];
   }
-  float z[4][3];
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    z[0][j] = k[j];
-    z[1][j] = 0.5f * (k[j] + k[3 + j] + k[6 + j]);
-    z[2][j] = 0.5f * (k[j] - k[3 + j] + k[6 + j]);
-    z[3][j] = k[6 + j];
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    u[r * 4 + 0] = z[r][0];
-    u[r * 4 + 1] = 0.5f * (z[r][0] + z[r][1] + z[r][2]);
-    u[r * 4 + 2] = 0.5f * (z[r][0] - z[r][1] + z[r][2]);
-    u[r * 4 + 3] = z[r][2];
-  }
+  filter_math(k, u);
 }
 
 __global__ void filter_kernel(const float* __restrict__ w, float* __restrict__ U, int C, int O, int Cpad, int Opad,
@@ -330,205 +340,37 @@ __global__ void filter_kernel(const float* __restrict__ w, float* __restrict__ U
   }
 }
 
-template <bool RAGGED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void wino_fused_kernel(Args p) {
-  __shared__ __attribute__((aligned(16))) float smem[A_FLOATS + B_FLOATS];
-  float* As = smem;
-  float* Bs = smem + A_FLOATS;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = blockIdx.y;
-  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
-  const int ob = b % p.n_ob, tb = b / p.n_ob;
-  const int o0 = ob * BO, t0 = tb * BT;
-
-  // Filter loads: pass q copies row r = tid / 32 + 8 q (coordinate r / 4,
-  // k pair r % 4) of the slab, floats 4 * (tid % 32) .. + 3 of its 128.
-  const i32x4 ru = mfma::buffer_rsrc(p.U, p.u_bytes);
-  const int a_row = tid >> 5, a_f4 = tid & 31;
-  const uint32_t a_off = uint32_t(
-      ((((int64_t(g) * 16 + (a_row >> 2)) * p.nslab) * 4 + (a_row & 3)) * int64_t(p.Opad) * 2 + 2 * o0 + 4 * a_f4) *
-      4);
-  const uint32_t a_sstep = uint32_t(4) * p.Opad * 2 * 4;           // one slab
-  const uint32_t a_qstep = uint32_t(2) * p.nslab * a_sstep;        // two coordinates
-
-  // Input patch: channel b_c of the slab, tile t0 + b_t; four row offsets (or
-  // kOffNone off the image) and a column mask, the slab's channel offset in
-  // the scalar offset.
-  const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
-  // Lanes 0-15 and 16-31 of a half-wave take the two channels of a pair for
-  // the same 16 tiles, so the half-wave's V stores cover 32 consecutive
-  // floats ([k pair][tile][2]) -- distinct banks.
-  const int b_t = (tid & 15) | ((tid >> 1) & 16);
-  const int b_c = ((tid >> 4) & 1) | ((tid >> 5) & 6);
-  PatchRows px;
-  {
-    const int t = t0 + b_t;
-    const bool tok = t < p.T;
-    const uint32_t tt = tok ? uint32_t(t) : 0u;
-    const uint32_t img = mfma::fdiv(tt, p.f_thw);
-    const uint32_t pos = tt - img * uint32_t(p.TH * p.TW);
-    const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
-    const int y0 = int(2 * ty) - p.ph, x0 = int(2 * tx) - p.pw;
-    const int64_t plane = (int64_t(img) * p.Cin + int64_t(g) * p.C + b_c) * p.H;
-    px.init(plane, y0, x0, tok, p.H, p.W);
-  }
-  const uint32_t x_sstep = uint32_t(BK) * p.H * p.W * 4;
-
-  // Register staging of the next slab: filter (from L2) and input patches.
-  f32x4 av[A_PASSES];
-  float d[16];
-  auto load = [&](int slab) {
-    const uint32_t sa = uint32_t(slab) * a_sstep, sx = uint32_t(slab) * x_sstep;
-#pragma unroll
-    for (int q = 0; q < A_PASSES; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
-    px.load_elements(rx, sx, !RAGGED || slab * BK + b_c < p.C, d);
-  };
-  float* const a_st = As + a_row * ROW_A + 4 * a_f4;
-  float* const b_st = Bs + (b_c >> 1) * ROW_B + 2 * b_t + (b_c & 1);
-  auto store = [&]() {
-#pragma unroll
-    for (int q = 0; q < A_PASSES; ++q) *reinterpret_cast<f32x4*>(a_st + q * 8 * ROW_A) = av[q];
-    // V = B^T d B
-    float z[16];
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      z[0 * 4 + cc] = d[0 * 4 + cc] - d[2 * 4 + cc];
-      z[1 * 4 + cc] = d[1 * 4 + cc] + d[2 * 4 + cc];
-      z[2 * 4 + cc] = d[2 * 4 + cc] - d[1 * 4 + cc];
-      z[3 * 4 + cc] = d[1 * 4 + cc] - d[3 * 4 + cc];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      b_st[(r * 4 + 0) * 4 * ROW_B] = z[r * 4 + 0] - z[r * 4 + 2];
-      b_st[(r * 4 + 1) * 4 * ROW_B] = z[r * 4 + 1] + z[r * 4 + 2];
-      b_st[(r * 4 + 2) * 4 * ROW_B] = z[r * 4 + 2] - z[r * 4 + 1];
-      b_st[(r * 4 + 3) * 4 * ROW_B] = z[r * 4 + 1] - z[r * 4 + 3];
-    }
-  };
-
-  // Wave (wo, wt) owns output channels wo*32 .. +31 (two 16-row blocks) and
-  // tiles wt*16 .. +15 of the workgroup tile, for all 16 coordinates.
-  const int wo = wave >> 1, wt = wave & 1;
-  const int kq = lane >> 4, li = lane & 15;
-  f32x4 acc[16][2];
-#pragma unroll
-  for (int t = 0; t < 16; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const f32x2* const a_frag = reinterpret_cast<const f32x2*>(As + kq * ROW_A + 2 * (wo * 32 + li));
-  const f32x2* const b_frag = reinterpret_cast<const f32x2*>(Bs + kq * ROW_B + 2 * (wt * 16 + li));
-
-  auto mma = [&]() {
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const f32x2 fb = b_frag[t * 2 * ROW_B];        // 4 rows of ROW_B floats per coordinate
-      const f32x2 fa0 = a_frag[t * 2 * ROW_A];
-      const f32x2 fa1 = a_frag[t * 2 * ROW_A + 16];  // channels + 16
-      acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0[0], fb[0], acc[t][0], 0, 0, 0);
-      acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1[0], fb[0], acc[t][1], 0, 0, 0);
-      acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0[1], fb[1], acc[t][0], 0, 0, 0);
-      acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1[1], fb[1], acc[t][1], 0, 0, 0);
-    }
-    // The fragment reads (merged in pairs: three per two coordinates) run two
-    // coordinate pairs ahead of the products that use them.
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-#pragma unroll
-    for (int t = 0; t < 6; ++t) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-  };
-
-  const int nslab = p.nslab;
-  load(0);
-  for (int s = 0; s < nslab; ++s) {
-    store();
-    __syncthreads();
-    load(min(s + 1, nslab - 1));  // the last slab re-reads itself: no branch around the loads
-    // The next slab's global loads are issued before any product.
-    __builtin_amdgcn_sched_barrier(0);
-    mma();
-    __syncthreads();
-  }
-
-  // Output transform.  16x16x4 layout: lane l, register v holds row
-  // 4 * (l / 16) + v (output channel) and column l % 16 (tile).
-  const int t = t0 + wt * 16 + li;
-  if (t >= p.T) return;
-  const uint32_t img = mfma::fdiv(uint32_t(t), p.f_thw);
-  const uint32_t pos = uint32_t(t) - img * uint32_t(p.TH * p.TW);
-  const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
-  const int oy = int(2 * ty), ox = int(2 * tx);
-  const bool right = ox + 1 < p.OW, below = oy + 1 < p.OH;
-  // All bias values before the first store: stores and loads share the
-  // vector-memory counter, so a load between stores would make each later
-  // store wait for the earlier ones.
-  float bias_v[2][4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
-      bias_v[i][v] = (p.bias && o < p.O) ? p.bias[g * p.O + o] : 0.f;
-    }
-  // y (below 2^31 bytes: the caller splits batches) as a buffer resource:
-  // positions outside the image or channels past O store to kOffNone and are
-  // dropped, so the 32 stores need no branches.
-  const i32x4 ry = mfma::buffer_rsrc(p.y, p.y_bytes);
-  const uint32_t row_step = uint32_t(p.OW) * 4u;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
-    float m[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) m[q] = acc[q][i][v];
-    float r0[4], r1[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      r0[c] = m[c] + m[4 + c] + m[8 + c];
-      r1[c] = m[4 + c] - m[8 + c] - m[12 + c];
-    }
-    const float bb = bias_v[i][v];
-    const bool ok = o < p.O;
-    const uint32_t off = uint32_t(((img * uint32_t(p.Cout) + uint32_t(g * p.O + o)) * uint32_t(p.OH) + uint32_t(oy)) *
-                                      uint32_t(p.OW) + uint32_t(ox)) * 4u;
-    mfma::bstore(r0[0] + r0[1] + r0[2] + bb, ry, ok ? off : kOffNone, 0);
-    mfma::bstore(r0[1] - r0[2] - r0[3] + bb, ry, (ok && right) ? off + 4u : kOffNone, 0);
-    mfma::bstore(r1[0] + r1[1] + r1[2] + bb, ry, (ok && below) ? off + row_step : kOffNone, 0);
-    mfma::bstore(r1[1] - r1[2] - r1[3] + bb, ry, (ok && below && right) ? off + row_step + 4u : kOffNone, 0);
-  }
-}
-
-// The fused kernel keeps one slab of loads in flight per workgroup and two
-// workgroups fit on a CU, so with long channel walks it needs most CUs
-// doubly occupied to hide HBM latency: measured on MI355X it wins from 1.5
-// workgroups per CU up (392 and more at 256 CUs) and loses below with 512
-// channels (256 workgroups of 64 slabs: 149 vs 123 us).  Short walks win
-// at any count (64 channels, 196 workgroups of 8 slabs: 24 vs 41 us), since
-// the unfused passes' V and M round trips then dominate.
+// Fused (warp-specialized kernel) or unfused passes.  The fused kernel holds
+// one workgroup per CU, so a launch with long channel walks and fewer
+// workgroups than half the CUs leaves the chip idle where the unfused passes'
+// batched GEMM spreads the same work: measured on MI355X, 512 channels at
+// 8x8, batch 16 (64 workgroups of 64 slabs) run 89.5 us fused and 47.6
+// unfused.  From half the CUs up, or with short walks (<= 16 slabs, where
+// the unfused passes' V and M round trips dominate), the fused kernel wins:
+// 16 x 256 x 16^2 (128 workgroups of 32 slabs) 49.8 vs 58.0 us, C1's layer
+// 18.2 vs 21.2, every 3x3 layer of the C3 and C4 stacks 8-20% faster.
 bool prefer_fused(int64_t workgroups, int nslab) {
-  return 2 * workgroups >= 3 * int64_t(cu_count()) || nslab <= 16;
+  return 2 * workgroups >= int64_t(cu_count()) || nslab <= 16;
 }
 
 }  // namespace fused
 
-// ------------------------------------------------------------ pipelined fused kernel
-// The fused kernel's schedule is serial per slab: wait for the slab's loads,
-// transform and store them to LDS, barrier, products, barrier.  Both waves of
-// a SIMD reach each phase together, so nothing overlaps the products.  This
-// variant stages slab s + 1 while the products of slab s run:
-//   - two LDS stages (filter and patches each), as separate arrays so the
-//     compiler knows that the stores of one never alias the reads of the
-//     other, and one barrier per slab;
-//   - the products of a slab in quads of coordinates (first k step of all
-//     four, then the second), so a product and the next one on the same
-//     accumulator are eight MFMAs apart;
-//   - slab s + 1's filter copy and patch transform stored between the
-//     products of the first quads, slab s + 2's loads issued after them.
-// Same arguments, U' layout and epilogue as the fused kernel; 96 KB of LDS,
-// one workgroup per CU.
-namespace pipe {
+// ------------------------------------------------------------ warp-specialized fused kernel
+// A workgroup of eight waves in two roles.  Waves 0-3 (consumers) run only
+// the fragment reads and MFMAs of slab s, then the output transform; waves
+// 4-7 (producers) load slab s + 2 and transform slab s + 1 (the input patches
+// by B^T d B, the filter copied from U' or transformed from w) into the
+// other of two LDS stages.  Each SIMD holds one wave of each role, so its
+// matrix core runs one wave's products while the other wave's staging
+// instructions issue; had every wave done both, as in a single-role kernel,
+// the staging would issue between the products (measured on MI355X: C1's
+// layer 21.2 -> 18.2 us, the C3 / C4 3x3 layers 8-20% faster than the
+// single-role kernels this one replaced).  One barrier per slab, reached by
+// both roles the same number of times (1 + nslab).  The products run by
+// quads of coordinates (the first k step of four coordinates, then the
+// second), so a product and the next one on the same accumulator are eight
+// MFMAs apart.  96 KB of LDS: one workgroup per CU.
+namespace ws {
 using fused::A_FLOATS;
 using fused::A_PASSES;
 using fused::B_FLOATS;
@@ -543,8 +385,14 @@ using mfma::f32x4;
 using mfma::i32x4;
 using mfma::kOffNone;
 
-template <bool RAGGED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void wino_pipe_kernel(fused::Args p) {
+// FILT: 0 reads U' (written by the filter launch); 1 / 2 have the producers
+// transform the layer filter w themselves (2: flipped and channel-swapped,
+// for an input gradient), so no filter launch runs.  Producer thread (kq, o)
+// then loads the 3x3 filters of output channel o0 + o, slab channels 2 kq and
+// 2 kq + 1, and stores their 16 coordinates as 8-byte pairs (a wave writes
+// 512 contiguous bytes per coordinate).
+template <bool RAGGED, int FILT>
+__global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
   __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
   __shared__ __attribute__((aligned(16))) float Bs0[B_FLOATS];
   __shared__ __attribute__((aligned(16))) float As1[A_FLOATS];
@@ -554,85 +402,131 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
   const int ob = b % p.n_ob, tb = b / p.n_ob;
   const int o0 = ob * BO, t0 = tb * BT;
+  const int nslab = p.nslab;  // even: the host pads the channels to 16
 
-  // Loads as in the fused kernel: filter rows from L2, one input patch per
-  // thread.
-  const i32x4 ru = mfma::buffer_rsrc(p.U, p.u_bytes);
-  const int a_row = tid >> 5, a_f4 = tid & 31;
-  const uint32_t a_off = uint32_t(
-      ((((int64_t(g) * 16 + (a_row >> 2)) * p.nslab) * 4 + (a_row & 3)) * int64_t(p.Opad) * 2 + 2 * o0 + 4 * a_f4) *
-      4);
-  const uint32_t a_sstep = uint32_t(4) * p.Opad * 2 * 4;
-  const uint32_t a_qstep = uint32_t(2) * p.nslab * a_sstep;
-  const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
-  const int b_t = (tid & 15) | ((tid >> 1) & 16);
-  const int b_c = ((tid >> 4) & 1) | ((tid >> 5) & 6);
-  PatchRows px;
-  {
-    const int t = t0 + b_t;
-    const bool tok = t < p.T;
-    const uint32_t tt = tok ? uint32_t(t) : 0u;
-    const uint32_t img = mfma::fdiv(tt, p.f_thw);
-    const uint32_t pos = tt - img * uint32_t(p.TH * p.TW);
-    const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
-    const int y0 = int(2 * ty) - p.ph, x0 = int(2 * tx) - p.pw;
-    const int64_t plane = (int64_t(img) * p.Cin + int64_t(g) * p.C + b_c) * p.H;
-    px.init(plane, y0, x0, tok, p.H, p.W);
+  if (wave >= 4) {
+    // ---- producers: the pipelined kernel's loads and stores, thread ptid.
+    const int ptid = tid - 256;
+    const i32x4 ru = mfma::buffer_rsrc(p.U, p.u_bytes);
+    const int a_row = ptid >> 5, a_f4 = ptid & 31;
+    const uint32_t a_off = uint32_t(
+        ((((int64_t(g) * 16 + (a_row >> 2)) * p.nslab) * 4 + (a_row & 3)) * int64_t(p.Opad) * 2 + 2 * o0 +
+         4 * a_f4) *
+        4);
+    const uint32_t a_sstep = uint32_t(4) * p.Opad * 2 * 4;
+    const uint32_t a_qstep = uint32_t(2) * p.nslab * a_sstep;
+    const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
+    const int b_t = (ptid & 15) | ((ptid >> 1) & 16);
+    const int b_c = ((ptid >> 4) & 1) | ((ptid >> 5) & 6);
+    PatchRows px;
+    {
+      const int t = t0 + b_t;
+      const bool tok = t < p.T;
+      const uint32_t tt = tok ? uint32_t(t) : 0u;
+      const uint32_t img = mfma::fdiv(tt, p.f_thw);
+      const uint32_t pos = tt - img * uint32_t(p.TH * p.TW);
+      const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
+      const int y0 = int(2 * ty) - p.ph, x0 = int(2 * tx) - p.pw;
+      const int64_t plane = (int64_t(img) * p.Cin + int64_t(g) * p.C + b_c) * p.H;
+      px.init(plane, y0, x0, tok, p.H, p.W);
+    }
+    const uint32_t x_sstep = uint32_t(BK) * p.H * p.W * 4;
+    const i32x4 rw = mfma::buffer_rsrc(p.w, FILT ? p.w_bytes : 0);
+    const int f_o = ptid & 63, f_kq = ptid >> 6;
+    const bool f_ook = o0 + f_o < p.O;
+    // Byte offset of filter (o0 + f_o, channel c): forward w[g*O + o][c],
+    // flipped w[g*C + c][o].
+    auto f_off = [&](int c) {
+      const int64_t e = FILT == 2 ? (int64_t(g) * p.C + c) * p.O + o0 + f_o : (int64_t(g) * p.O + o0 + f_o) * p.C + c;
+      return (f_ook && c < p.C) ? uint32_t(e * 36) : kOffNone;
+    };
+    f32x4 av[FILT ? 1 : A_PASSES];
+    f32x4 wv[2][2];
+    float wl[2];
+    auto load = [&](int slab) {
+      const uint32_t sa = uint32_t(slab) * a_sstep, sx = uint32_t(slab) * x_sstep;
+      if constexpr (FILT) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t off = f_off(slab * BK + 2 * f_kq + j);
+          wv[j][0] = mfma::bload4(rw, off, 0);
+          wv[j][1] = mfma::bload4(rw, off, 16);
+          wl[j] = mfma::bload(rw, off, 32);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < A_PASSES; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
+      }
+      px.load(rx, sx, uint32_t(p.x_bytes), !RAGGED || slab * BK + b_c < p.C);
+    };
+    auto store = [&](float* As, float* Bs) {
+      px.fix(rx);
+      float* const b_st = Bs + (b_c >> 1) * ROW_B + 2 * b_t + (b_c & 1);
+      if constexpr (FILT) {
+        float u[2][16];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float v[9] = {wv[j][0][0], wv[j][0][1], wv[j][0][2], wv[j][0][3], wv[j][1][0],
+                              wv[j][1][1], wv[j][1][2], wv[j][1][3], wl[j]};
+          float k[9];
+#pragma unroll
+          for (int e = 0; e < 9; ++e) k[e] = FILT == 2 ? v[8 - e] : v[e];
+          fused::filter_math(k, u[j]);
+        }
+        float* const a_st = As + f_kq * ROW_A + 2 * f_o;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) *reinterpret_cast<f32x2*>(a_st + t * 4 * ROW_A) = f32x2{u[0][t], u[1][t]};
+      } else {
+        float* const a_st = As + a_row * ROW_A + 4 * a_f4;
+#pragma unroll
+        for (int q = 0; q < A_PASSES; ++q) *reinterpret_cast<f32x4*>(a_st + q * 8 * ROW_A) = av[q];
+      }
+      float d[16];
+      px.patch(d);
+      float z[16];
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        z[0 * 4 + cc] = d[0 * 4 + cc] - d[2 * 4 + cc];
+        z[1 * 4 + cc] = d[1 * 4 + cc] + d[2 * 4 + cc];
+        z[2 * 4 + cc] = d[2 * 4 + cc] - d[1 * 4 + cc];
+        z[3 * 4 + cc] = d[1 * 4 + cc] - d[3 * 4 + cc];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        b_st[(r * 4 + 0) * 4 * ROW_B] = z[r * 4 + 0] - z[r * 4 + 2];
+        b_st[(r * 4 + 1) * 4 * ROW_B] = z[r * 4 + 1] + z[r * 4 + 2];
+        b_st[(r * 4 + 2) * 4 * ROW_B] = z[r * 4 + 2] - z[r * 4 + 1];
+        b_st[(r * 4 + 3) * 4 * ROW_B] = z[r * 4 + 1] - z[r * 4 + 3];
+      }
+    };
+    load(0);
+    store(As0, Bs0);
+    load(1);
+    __syncthreads();  // stage 0 holds slab 0
+    // Trip s stores slab s + 1 into the stage slab s - 1 used (the consumers
+    // finished reading it before the previous barrier) and loads slab s + 2;
+    // past the last slab nothing is stored.
+    for (int s = 0; s < nslab; s += 2) {
+      store(As1, Bs1);             // slab s + 1 (s + 1 < nslab: nslab is even)
+      load(min(s + 2, nslab - 1));
+      __syncthreads();
+      if (s + 2 < nslab) {
+        store(As0, Bs0);           // slab s + 2
+        load(min(s + 3, nslab - 1));
+      }
+      __syncthreads();
+    }
+    return;
   }
-  const uint32_t x_sstep = uint32_t(BK) * p.H * p.W * 4;
-  const int nslab = p.nslab;
 
-  f32x4 av[A_PASSES];
-  auto load = [&](int slab) {
-    const uint32_t sa = uint32_t(slab) * a_sstep, sx = uint32_t(slab) * x_sstep;
-#pragma unroll
-    for (int q = 0; q < A_PASSES; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
-    px.load(rx, sx, uint32_t(p.x_bytes), !RAGGED || slab * BK + b_c < p.C);
-  };
-  auto store = [&](float* As, float* Bs) {
-    float* const a_st = As + a_row * ROW_A + 4 * a_f4;
-    float* const b_st = Bs + (b_c >> 1) * ROW_B + 2 * b_t + (b_c & 1);
-#pragma unroll
-    for (int q = 0; q < A_PASSES; ++q) *reinterpret_cast<f32x4*>(a_st + q * 8 * ROW_A) = av[q];
-    float d[16];
-    px.patch(d);
-    float z[16];
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      z[0 * 4 + cc] = d[0 * 4 + cc] - d[2 * 4 + cc];
-      z[1 * 4 + cc] = d[1 * 4 + cc] + d[2 * 4 + cc];
-      z[2 * 4 + cc] = d[2 * 4 + cc] - d[1 * 4 + cc];
-      z[3 * 4 + cc] = d[1 * 4 + cc] - d[3 * 4 + cc];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      b_st[(r * 4 + 0) * 4 * ROW_B] = z[r * 4 + 0] - z[r * 4 + 2];
-      b_st[(r * 4 + 1) * 4 * ROW_B] = z[r * 4 + 1] + z[r * 4 + 2];
-      b_st[(r * 4 + 2) * 4 * ROW_B] = z[r * 4 + 2] - z[r * 4 + 1];
-      b_st[(r * 4 + 3) * 4 * ROW_B] = z[r * 4 + 1] - z[r * 4 + 3];
-    }
-  };
-
+  // ---- consumers: wave (wo, wt) owns output channels wo*32 .. +31 and tiles
+  // wt*16 .. +15 of the block, for all 16 coordinates.
   const int wo = wave >> 1, wt = wave & 1;
   const int kq = lane >> 4, li = lane & 15;
   f32x4 acc[16][2];
 #pragma unroll
   for (int t = 0; t < 16; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Slab s from stage (Ac, Bc); slab s + 1 (in registers) to stage (An, Bn);
-  // slab s + 2 requested.  Past the last slab the loads re-read it and the
-  // spare stage is written but never read: no branch in the schedule.
-  // Four chunks fenced by scheduling barriers: quad 0 of the products with
-  // the staging of slab s + 1 and the loads of slab s + 2, then quads 1-3;
-  // each chunk also reads the next quad's fragments.
-  auto step = [&](const float* Ac, const float* Bc, float* An, float* Bn, int s) {
-    // The loaded values count as produced here, so no part of the transform
-    // is hoisted above the previous barrier to sit right behind the loads.
-    px.fix(rx);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(px.xr[r]));
-#pragma unroll
-    for (int q = 0; q < A_PASSES; ++q) asm volatile("" : "+v"(av[q]));
+  auto slab = [&](const float* Ac, const float* Bc) {
     const f32x2* const a_frag = reinterpret_cast<const f32x2*>(Ac + kq * ROW_A + 2 * (wo * 32 + li));
     const f32x2* const b_frag = reinterpret_cast<const f32x2*>(Bc + kq * ROW_B + 2 * (wt * 16 + li));
     f32x2 fa0[4], fa1[4], fb[4];
@@ -645,9 +539,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         fa1[j] = a_frag[t * 2 * ROW_A + 16];
       }
     };
-    // Coordinates in quads: the first k step of all four, then the second,
-    // so a product and the next one on the same accumulator are eight MFMAs
-    // apart.
+    // Coordinates in quads, as in the pipelined kernel.
     auto quad = [&](int q) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -659,15 +551,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
     };
     frags(0);
-    quad(0);
-    store(An, Bn);
-    load(min(s + 2, nslab - 1));
-    frags(1);
-    __builtin_amdgcn_sched_barrier(0);
-    // Quads 1-3: the next quad's fragment reads go out after the first two
-    // products, so they land while the rest of the quad runs.
 #pragma unroll
-    for (int q = 1; q < 4; ++q) {
+    for (int q = 0; q < 4; ++q) {
       quad(q);
       if (q < 3) {
         frags(q + 1);
@@ -677,18 +562,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
   };
-
-  load(0);
-  px.fix(rx);
-  store(As0, Bs0);
-  load(min(1, nslab - 1));
-  __syncthreads();
-  // The host pads the channels to a multiple of 16: an even slab count.
+  __syncthreads();  // stage 0 holds slab 0
   for (int s = 0; s < nslab; s += 2) {
-    step(As0, Bs0, As1, Bs1, s);
-    step(As1, Bs1, As0, Bs0, s + 1);
+    slab(As0, Bs0);
+    __syncthreads();
+    slab(As1, Bs1);
+    __syncthreads();
   }
 
   // Output transform (the fused kernel's epilogue).
@@ -736,7 +616,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       mfma::bstore(r1[1] - r1[2] - r1[3] + bb, ry, (ok && below && right) ? off + row_step + 4u : kOffNone, 0);
     }
 }
-}  // namespace pipe
+}  // namespace ws
 
 // ------------------------------------------------------------ fused dWeight
 // Weight gradient of a 3x3 stride-1 layer as the adjoint of the forward
@@ -1157,7 +1037,7 @@ struct RunPlan {
   int G = 1;
   int64_t blocks = 0;
   bool fused = true;
-  bool pipe = false;          // the pipelined fused kernel (channels padded to 16)
+  bool filt = false;          // the fused kernel transforms the filter itself (no filter launch)
   int64_t chunk = 0;          // images per unfused pass
   int64_t unfused_bytes = 0;  // U, V and M of one pass
 };
@@ -1175,7 +1055,9 @@ int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
   r->G = int(d.groups);
   p.C = p.Cin / r->G;
   p.O = p.Cout / r->G;
-  p.Cpad = (p.C + fused::BK - 1) / fused::BK * fused::BK;
+  // The fused kernel runs two slabs per loop trip: channels padded to 16
+  // (zero filter rows).
+  p.Cpad = (p.C + 2 * fused::BK - 1) / (2 * fused::BK) * (2 * fused::BK);
   p.Opad = (p.O + fused::BO - 1) / fused::BO * fused::BO;
   p.TH = (p.OH + 1) / 2;
   p.TW = (p.OW + 1) / 2;
@@ -1196,18 +1078,9 @@ int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
   p.T = int(T);
   r->blocks = (T + fused::BT - 1) / fused::BT * p.n_ob;
   MX_REQUIRE(r->blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "winograd: grid too large");
-  // The pipelined fused kernel holds 96 KB of LDS, one workgroup per CU, so
-  // it pays where the grid fits the CUs once: measured on MI355X it beats
-  // the fused kernel on C1's layer (196 workgroups of 8 slabs: 23.6 vs 25.4
-  // us per call) and the unfused passes on 512-channel layers with 256
-  // workgroups of 64 slabs (116 vs 130 us); with long walks and fewer than
-  // half the CUs busy the unfused passes stay ahead (64 workgroups of 64
-  // slabs: 48 vs 115 us).
-  const int64_t cus = cu_count(), wgs = r->blocks * r->G;
-  const bool pipe_fits = wgs <= cus && (p.nslab <= 16 || 2 * wgs >= cus);
-  // MX_WINOGRAD_FUSED=1 / 0 forces the fused / unfused kernels and
-  // MX_WINOGRAD_PIPE=1 / 0 the pipelined / serial fused kernel (tests, tuning).
-  r->fused = pipe_fits || fused::prefer_fused(wgs, p.nslab);
+  const int64_t wgs = r->blocks * r->G;
+  // MX_WINOGRAD_FUSED=1 / 0 forces the fused / unfused kernels (tests, tuning).
+  r->fused = fused::prefer_fused(wgs, p.nslab);
   if (const char* e = std::getenv("MX_WINOGRAD_FUSED"))
     if (e[0] == '0' || e[0] == '1') r->fused = e[0] == '1';
   const int64_t u_plain = 16 * int64_t(p.Cout) * p.C * 4;
@@ -1219,16 +1092,19 @@ int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
     r->chunk = (d.n + passes - 1) / passes;
     r->unfused_bytes = u_plain + per_image * r->chunk;
   }
-  r->pipe = pipe_fits;
-  if (const char* e = std::getenv("MX_WINOGRAD_PIPE"))
-    if (e[0] == '0' || e[0] == '1') r->pipe = e[0] == '1';
-  r->pipe = r->pipe && r->fused;
-  if (r->pipe) {
-    // Two slabs per loop trip: channels padded to 16 (zero filter rows).
-    p.Cpad = (p.C + 2 * fused::BK - 1) / (2 * fused::BK) * (2 * fused::BK);
-    p.nslab = p.Cpad / fused::BK;
-    p.u_bytes = int64_t(r->G) * 16 * p.Cpad * p.Opad * 4;
-    MX_REQUIRE(p.u_bytes < mfma::kBufMaxBytes, MX_ERR_UNSUPPORTED, "winograd: the transformed filter exceeds 2 GiB");
+  // With at most 4 slabs the producers transform the filter themselves: the
+  // separate filter launch then costs more than its work (20 -> 24 channels
+  // at 9x11, batch 4: 12.0 -> 9.5 us); on longer walks every workgroup
+  // redoing the transform costs more than the launch (C1's layer 18.2 ->
+  // 19.0 us, 512 channels 90 -> 123 us).  MX_WINOGRAD_FILTER=0 / 1 forces the
+  // filter launch / the in-kernel transform (tests, tuning).
+  r->filt = p.nslab <= 4;
+  if (const char* e = std::getenv("MX_WINOGRAD_FILTER"))
+    if (e[0] == '0' || e[0] == '1') r->filt = e[0] == '1';
+  r->filt = r->filt && r->fused;
+  if (r->filt) {
+    p.w_bytes = int64_t(d.cout) * p.C * 9 * 4;
+    MX_REQUIRE(p.w_bytes < mfma::kBufMaxBytes, MX_ERR_UNSUPPORTED, "winograd: the filter exceeds 2 GiB");
   }
   return MX_OK;
 }
@@ -1243,30 +1119,29 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   if (p.T == 0) return MX_OK;
   if (!r.fused) return winograd_unfused(d, x, w, bias, y, flip, r.chunk, s);
   p.bias = bias;
-  Scratch U;
-  MX_TRY(U.alloc(size_t(p.u_bytes), s));
-  p.U = U.as<float>();
   p.x = x;
   p.y = y;
   const dim3 grid{unsigned(r.blocks), unsigned(r.G), 1u};
+  const bool ragged = p.C % (2 * fused::BK) != 0;
+  if (r.filt) {
+    p.w = w;
+    void (*kern)(fused::Args) = flip ? (ragged ? ws::wino_ws_kernel<true, 2> : ws::wino_ws_kernel<false, 2>)
+                                     : (ragged ? ws::wino_ws_kernel<true, 1> : ws::wino_ws_kernel<false, 1>);
+    hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, p);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
+  Scratch U;
+  MX_TRY(U.alloc(size_t(p.u_bytes), s));
+  p.U = U.as<float>();
   // 64-thread blocks: a small filter (64 x 64 is 2,048 threads) then spreads
   // over 32 CUs instead of 8, and its scattered reads queue on more of them.
   const int64_t filter_threads = int64_t(r.G) * (p.Cpad / 2) * p.Opad;
   hipLaunchKernelGGL(fused::filter_kernel, dim3(unsigned(std::min<int64_t>((filter_threads + 63) / 64, 1 << 20))),
                      dim3(64), 0, s, w, U.as<float>(), p.C, p.O, p.Cpad, p.Opad, r.G, flip);
   MX_HIP(hipGetLastError());
-  if (r.pipe) {
-    if (p.C % (2 * fused::BK))
-      hipLaunchKernelGGL(pipe::wino_pipe_kernel<true>, grid, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL(pipe::wino_pipe_kernel<false>, grid, dim3(256), 0, s, p);
-    MX_HIP(hipGetLastError());
-    return MX_OK;
-  }
-  if (p.C % fused::BK)
-    hipLaunchKernelGGL(fused::wino_fused_kernel<true>, grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL(fused::wino_fused_kernel<false>, grid, dim3(256), 0, s, p);
+  void (*kern)(fused::Args) = ragged ? ws::wino_ws_kernel<true, 0> : ws::wino_ws_kernel<false, 0>;
+  hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, p);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }
@@ -1389,11 +1264,8 @@ int winograd_describe(const mx_conv2d_desc& d, int phase, bool with_bias, int64_
   }
   RunPlan r;
   MX_TRY(plan_run(phase == MX_CONV_DINPUT ? dinput_as_forward(d) : d, ws_limit, &r));
-  if (r.pipe) {
-    *variant = cat("wino_pipe_kernel<", r.p.C % (2 * fused::BK) ? "ragged" : "even", ">");
-    *ws_bytes = 0;
-  } else if (r.fused) {
-    *variant = cat("wino_fused_kernel<", r.p.C % fused::BK ? "ragged" : "even", ">");
+  if (r.fused) {
+    *variant = cat("wino_ws_kernel<", r.p.C % (2 * fused::BK) ? "ragged" : "even", r.filt ? ",filter>" : ">");
     *ws_bytes = 0;
   } else {
     // U, V and M are fresh mx_malloc blocks (256-byte aligned).
