@@ -815,7 +815,7 @@ def trace_summary(trace_csv, bench_log):
     wino_dx = "winograd_dinput" in res["kernels"]
     wino_calls = 0
     for i, (label, _) in enumerate(seq):
-        if label == "wino_dw_kernel":
+        if label in ("wino_dw_kernel", "wino_dw_ws_kernel"):
             # the Winograd weight gradient; its range sum follows as a helper
             owner[i] = last_tile = "winograd_dweight"
         elif label in WINOGRAD_KERNELS:

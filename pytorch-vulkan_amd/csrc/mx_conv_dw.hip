@@ -94,46 +94,58 @@ MX_TILE_KERNEL(C) void conv_dw_kernel(ConvArgs p) {
 // order, so the result is the same on every run and many splits of a small
 // dW keep four times more loads in flight than one thread per element would.
 // The first n4 = n_dw / 4 groups of four (n4 = 0 unless the host found ws
-// and dw 16-byte aligned) are summed as 16-byte vectors, 256 elements per
-// workgroup; workgroups past them take the rest (dw's tail, then db) one
-// element per lane.
+// and dw 16-byte aligned) are summed as 16-byte vectors, E = 256 / Q groups
+// per workgroup; workgroups past them take the rest (dw's tail, then db) one
+// element per lane.  Each output is summed by Q lanes (chain q takes splits
+// q, q + Q, ...), whose sums are added in chain order: a fixed order for a
+// given split count.  Q = 16 when there are many splits keeps every split's
+// load in flight at once (C1's Winograd weight gradient: 98 ranges, 6 loads
+// per lane instead of 25).
+template <int Q>
 __global__ __launch_bounds__(256) void conv_dw_finalize_kernel(const float* __restrict__ ws,
                                                                const float* __restrict__ ws_db, float* __restrict__ dw,
                                                                float* __restrict__ db, int64_t n_dw, int n_db,
                                                                int splits, int64_t n4) {
-  __shared__ f32x4 part[4][64];
-  const int e = threadIdx.x & 63, q = threadIdx.x >> 6;
-  const int64_t vblocks = (n4 + 63) / 64;
+  constexpr int E = 256 / Q;
+  __shared__ f32x4 part[Q][E];
+  const int e = threadIdx.x % E, q = threadIdx.x / E;
+  const int64_t vblocks = (n4 + E - 1) / E;
   if (int64_t(blockIdx.x) < vblocks) {
-    const int64_t g4 = int64_t(blockIdx.x) * 64 + e;
+    const int64_t g4 = int64_t(blockIdx.x) * E + e;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     if (g4 < n4) {
       const f32x4* src = reinterpret_cast<const f32x4*>(ws) + g4;
       const int64_t stride4 = n_dw / 4;
 #pragma unroll 4
-      for (int sp = q; sp < splits; sp += 4) s += src[sp * stride4];
+      for (int sp = q; sp < splits; sp += Q) s += src[sp * stride4];
     }
     part[q][e] = s;
     __syncthreads();
-    if (q == 0 && g4 < n4)
-      reinterpret_cast<f32x4*>(dw)[g4] = ((part[0][e] + part[1][e]) + part[2][e]) + part[3][e];
+    if (q == 0 && g4 < n4) {
+      f32x4 t = part[0][e];
+#pragma unroll
+      for (int i = 1; i < Q; ++i) t += part[i][e];
+      reinterpret_cast<f32x4*>(dw)[g4] = t;
+    }
     return;
   }
-  const int64_t idx = 4 * n4 + (int64_t(blockIdx.x) - vblocks) * 64 + e;
+  const int64_t idx = 4 * n4 + (int64_t(blockIdx.x) - vblocks) * E + e;
   float s = 0.f;
   if (idx < n_dw) {
     const float* src = ws + idx;
 #pragma unroll 4
-    for (int sp = q; sp < splits; sp += 4) s += src[sp * n_dw];
+    for (int sp = q; sp < splits; sp += Q) s += src[sp * n_dw];
   } else if (idx < n_dw + n_db) {
     const float* src = ws_db + (idx - n_dw);
 #pragma unroll 4
-    for (int sp = q; sp < splits; sp += 4) s += src[sp * int64_t(n_db)];
+    for (int sp = q; sp < splits; sp += Q) s += src[sp * int64_t(n_db)];
   }
   part[q][e][0] = s;
   __syncthreads();
   if (q == 0) {
-    const float v = ((part[0][e][0] + part[1][e][0]) + part[2][e][0]) + part[3][e][0];
+    float v = part[0][e][0];
+#pragma unroll
+    for (int i = 1; i < Q; ++i) v += part[i][e][0];
     if (idx < n_dw) dw[idx] = v;
     else if (idx < n_dw + n_db) db[idx - n_dw] = v;
   }
@@ -248,10 +260,16 @@ int launch_finalize(const float* ws, const float* ws_db, float* out, float* db, 
   const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   const int64_t n4 = vec ? n / 4 : 0;
-  const int64_t blocks = (n4 + 63) / 64 + (n - 4 * n4 + n_db + 63) / 64;
+  const bool wide = splits >= 32;
+  const int64_t E = wide ? 16 : 64;
+  const int64_t blocks = (n4 + E - 1) / E + (n - 4 * n4 + n_db + E - 1) / E;
   MX_REQUIRE(blocks <= INT32_MAX, MX_ERR_UNSUPPORTED, "conv2d dweight: finalize grid too large");
-  hipLaunchKernelGGL(conv_dw_finalize_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, ws, ws_db, out, db, n, n_db,
-                     splits, n4);
+  if (wide)
+    hipLaunchKernelGGL(conv_dw_finalize_kernel<16>, dim3(unsigned(blocks)), dim3(256), 0, s, ws, ws_db, out, db, n,
+                       n_db, splits, n4);
+  else
+    hipLaunchKernelGGL(conv_dw_finalize_kernel<4>, dim3(unsigned(blocks)), dim3(256), 0, s, ws, ws_db, out, db, n,
+                       n_db, splits, n4);
   MX_HIP(hipGetLastError());
   return MX_OK;
 }

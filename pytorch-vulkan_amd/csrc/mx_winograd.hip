@@ -418,7 +418,16 @@ __global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
     const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
     const int b_t = (ptid & 15) | ((ptid >> 1) & 16);
     const int b_c = ((ptid >> 4) & 1) | ((ptid >> 5) & 6);
-    PatchRows px;
+    // A slab's loaded registers.  (Two sets, loading two slabs ahead,
+    // measured no faster: the producers are not waiting on load latency.)
+    struct Set {
+      f32x4 av[FILT ? 1 : A_PASSES];
+      f32x4 wv[2][2];
+      float wl[2];
+      PatchRows px;
+    };
+    Set sa_;
+    PatchRows& px = sa_.px;
     {
       const int t = t0 + b_t;
       const bool tok = t < p.T;
@@ -440,27 +449,27 @@ __global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
       const int64_t e = FILT == 2 ? (int64_t(g) * p.C + c) * p.O + o0 + f_o : (int64_t(g) * p.O + o0 + f_o) * p.C + c;
       return (f_ook && c < p.C) ? uint32_t(e * 36) : kOffNone;
     };
-    f32x4 av[FILT ? 1 : A_PASSES];
-    f32x4 wv[2][2];
-    float wl[2];
-    auto load = [&](int slab) {
+    auto load = [&](Set& r, int slab) {
       const uint32_t sa = uint32_t(slab) * a_sstep, sx = uint32_t(slab) * x_sstep;
       if constexpr (FILT) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const uint32_t off = f_off(slab * BK + 2 * f_kq + j);
-          wv[j][0] = mfma::bload4(rw, off, 0);
-          wv[j][1] = mfma::bload4(rw, off, 16);
-          wl[j] = mfma::bload(rw, off, 32);
+          r.wv[j][0] = mfma::bload4(rw, off, 0);
+          r.wv[j][1] = mfma::bload4(rw, off, 16);
+          r.wl[j] = mfma::bload(rw, off, 32);
         }
       } else {
 #pragma unroll
-        for (int q = 0; q < A_PASSES; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
+        for (int q = 0; q < A_PASSES; ++q) r.av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_qstep);
       }
-      px.load(rx, sx, uint32_t(p.x_bytes), !RAGGED || slab * BK + b_c < p.C);
+      r.px.load(rx, sx, uint32_t(p.x_bytes), !RAGGED || slab * BK + b_c < p.C);
     };
-    auto store = [&](float* As, float* Bs) {
-      px.fix(rx);
+    auto store = [&](Set& r, float* As, float* Bs) {
+      r.px.fix(rx);
+      const f32x4(&av)[FILT ? 1 : A_PASSES] = r.av;
+      const f32x4(&wv)[2][2] = r.wv;
+      const float(&wl)[2] = r.wl;
       float* const b_st = Bs + (b_c >> 1) * ROW_B + 2 * b_t + (b_c & 1);
       if constexpr (FILT) {
         float u[2][16];
@@ -482,7 +491,7 @@ __global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
         for (int q = 0; q < A_PASSES; ++q) *reinterpret_cast<f32x4*>(a_st + q * 8 * ROW_A) = av[q];
       }
       float d[16];
-      px.patch(d);
+      r.px.patch(d);
       float z[16];
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {
@@ -492,27 +501,27 @@ __global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
         z[3 * 4 + cc] = d[1 * 4 + cc] - d[3 * 4 + cc];
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        b_st[(r * 4 + 0) * 4 * ROW_B] = z[r * 4 + 0] - z[r * 4 + 2];
-        b_st[(r * 4 + 1) * 4 * ROW_B] = z[r * 4 + 1] + z[r * 4 + 2];
-        b_st[(r * 4 + 2) * 4 * ROW_B] = z[r * 4 + 2] - z[r * 4 + 1];
-        b_st[(r * 4 + 3) * 4 * ROW_B] = z[r * 4 + 1] - z[r * 4 + 3];
+      for (int i = 0; i < 4; ++i) {
+        b_st[(i * 4 + 0) * 4 * ROW_B] = z[i * 4 + 0] - z[i * 4 + 2];
+        b_st[(i * 4 + 1) * 4 * ROW_B] = z[i * 4 + 1] + z[i * 4 + 2];
+        b_st[(i * 4 + 2) * 4 * ROW_B] = z[i * 4 + 2] - z[i * 4 + 1];
+        b_st[(i * 4 + 3) * 4 * ROW_B] = z[i * 4 + 1] - z[i * 4 + 3];
       }
     };
-    load(0);
-    store(As0, Bs0);
-    load(1);
+    load(sa_, 0);
+    store(sa_, As0, Bs0);
+    load(sa_, 1);
     __syncthreads();  // stage 0 holds slab 0
     // Trip s stores slab s + 1 into the stage slab s - 1 used (the consumers
     // finished reading it before the previous barrier) and loads slab s + 2;
     // past the last slab nothing is stored.
     for (int s = 0; s < nslab; s += 2) {
-      store(As1, Bs1);             // slab s + 1 (s + 1 < nslab: nslab is even)
-      load(min(s + 2, nslab - 1));
+      store(sa_, As1, Bs1);  // slab s + 1 (s + 1 < nslab: nslab is even)
+      load(sa_, min(s + 2, nslab - 1));
       __syncthreads();
       if (s + 2 < nslab) {
-        store(As0, Bs0);           // slab s + 2
-        load(min(s + 3, nslab - 1));
+        store(sa_, As0, Bs0);  // slab s + 2
+        load(sa_, min(s + 3, nslab - 1));
       }
       __syncthreads();
     }
@@ -687,52 +696,90 @@ __device__ __forceinline__ void tile_origin(uint32_t t, const Args& p, uint32_t&
   ox = int(2 * (pos - ty * uint32_t(p.TW)));
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void wino_dw_kernel(Args p) {
-  __shared__ __attribute__((aligned(16))) float smem[A_FLOATS + B_FLOATS];
-  __shared__ TileEntry tiles[kChunk];
-  float* As = smem;
-  float* Bs = smem + A_FLOATS;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = blockIdx.y;
-  // Blocks of one tile range are consecutive, so they share an XCD and read
-  // the same x and dy tiles through its L2.
-  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
-  const int nblk = p.n_ob * p.n_cb;
-  const int range = b / nblk, ob = (b % nblk) % p.n_ob, cb = (b % nblk) / p.n_ob;
-  const int o0 = ob * BO, c0 = cb * BC;
-  const int k_begin = range * p.kps;
-  const int k_end = min(p.T, k_begin + p.kps);
-
-  // dy: the thread owns output channel a_o of the block and slab tiles
-  // 2 a_kq and 2 a_kq + 1 (the k pair one MFMA lane multiplies).
-  const i32x4 rdy = mfma::buffer_rsrc(p.dy, p.dy_bytes);
-  const int a_o = tid >> 2, a_kq = tid & 3;
-  const bool o_ok = o0 + a_o < p.O;
-  const uint32_t dy_chan = uint32_t(g * p.O + o0 + a_o);
-  // x: the thread owns input channel b_c of the block and slab tile b_t.
-  const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
-  const int b_c = tid >> 3, b_t = tid & 7;
-  const bool c_ok = c0 + b_c < p.C;
-  const uint32_t x_chan = uint32_t(g * p.C + c0 + b_c);
-
-  // Each row of the x patch and of a dy tile is one 16- or 8-byte load at
-  // the row's first column; a row outside the image reads zeros.  Columns
-  // outside the image read the neighbouring row's values and are zeroed in
-  // store() from the column bits.  A tile whose rows may start before the
-  // tensor or end past it (only at the tensor's first and last rows) is read
-  // again element by element in store(), after the slab's loads have landed,
-  // so the rare path adds no wait to the common one and no load it keeps is
-  // ever partly out of range.
+// Tiles k0 .. k0 + n - 1 of a range ending at k1 into the LDS table, by
+// `nthreads` threads; entries at or past k1 read nothing.
+__device__ __forceinline__ void decode_tiles(const Args& p, TileEntry* tiles, int k0, int k1, int n, int tid,
+                                             int nthreads) {
   const int HW = p.H * p.W, OHW = p.OH * p.OW;  // the tensors hold fewer than 2^29 floats
   const int x_elems = int(p.x_bytes >> 2), dy_elems = int(p.dy_bytes >> 2);
-  const uint32_t xc_bytes = c_ok ? x_chan * uint32_t(HW) * 4u : kRowNone;
-  const uint32_t yc_bytes = o_ok ? dy_chan * uint32_t(OHW) * 4u : kRowNone;
-  f32x4 xr[4];          // the x patch's rows
-  uint32_t xbits;       // the patch's TileEntry::bits
-  f32x2 yr[2][2];       // the dy tiles' rows
+  for (int i = tid; i < n; i += nthreads) {
+    const int t = k0 + i;
+    const bool tok = t < k1;
+    uint32_t img;
+    int oy, ox;
+    tile_origin(tok ? uint32_t(t) : 0u, p, img, oy, ox);
+    const int y0 = oy - p.ph, x0 = ox - p.pw;
+    TileEntry e;
+    e.xfirst = int(img) * p.Cin * HW + y0 * p.W + x0;
+    const int yfirst = int(img) * p.Cout * OHW + oy * p.OW + ox;
+    uint32_t bits = uint32_t(ox + 1 < p.OW) << 4;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) bits |= uint32_t(unsigned(x0 + cc) < unsigned(p.W)) << cc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = tok && unsigned(y0 + r) < unsigned(p.H);
+      bits |= uint32_t(ok) << (8 + r);
+      e.xrow[r] = ok ? uint32_t(e.xfirst + r * p.W) * 4u : kRowNone;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const bool ok = tok && oy + r < p.OH;
+      bits |= uint32_t(ok) << (12 + r);
+      e.yrow[r] = ok ? uint32_t(yfirst + r * p.OW) * 4u : kRowNone;
+    }
+    // Checked for the largest channel, so every channel's lanes agree; a
+    // tile past the range reads nothing and is never rare.
+    if (tok && (e.xfirst < 0 || e.xfirst + 3 * p.W + 4 + (p.Cin - 1) * HW > x_elems)) bits |= kXRare;
+    if (tok && yfirst + p.OW + 2 + (p.Cout - 1) * OHW > dy_elems) bits |= kYRare;
+    e.bits = bits;
+    tiles[i] = e;
+  }
+}
+
+// One thread's part of a slab: the x patch of input channel b_c for slab
+// tile b_t (one patch per thread), and the dy tiles of output channel a_o
+// for slab tiles 2 a_kq and 2 a_kq + 1 (the k pair one MFMA lane
+// multiplies), with their transforms into an LDS stage.
+//
+// Each row of the x patch and of a dy tile is one 16- or 8-byte load at the
+// row's first column; a row outside the image reads zeros.  Columns outside
+// the image read the neighbouring row's values and are zeroed in store()
+// from the column bits.  A tile whose rows may start before the tensor or end
+// past it (only at the tensor's first and last rows) is read again element
+// by element in store(), after the slab's loads have landed, so the rare path
+// adds no wait to the common one and no load it keeps is ever partly out of
+// range.
+struct SlabIO {
+  i32x4 rdy, rx;
+  int a_o, a_kq, b_c, b_t, HW, OHW, W, OW;
+  bool o_ok, c_ok;
+  uint32_t dy_chan, x_chan, xc_bytes, yc_bytes;
+  f32x4 xr[4];     // the x patch's rows
+  uint32_t xbits;  // the patch's TileEntry::bits
+  f32x2 yr[2][2];  // the dy tiles' rows
   uint32_t ybits[2];
-  float dsum = 0.f;     // this thread's dy values, for dBias
-  auto load = [&](int slab) {
+  float dsum;      // this thread's dy values, for dBias
+
+  __device__ __forceinline__ void init(const Args& p, int tid, int g, int o0, int c0) {
+    rdy = mfma::buffer_rsrc(p.dy, p.dy_bytes);
+    rx = mfma::buffer_rsrc(p.x, p.x_bytes);
+    a_o = tid >> 2;
+    a_kq = tid & 3;
+    b_c = tid >> 3;
+    b_t = tid & 7;
+    o_ok = o0 + a_o < p.O;
+    c_ok = c0 + b_c < p.C;
+    dy_chan = uint32_t(g * p.O + o0 + a_o);
+    x_chan = uint32_t(g * p.C + c0 + b_c);
+    HW = p.H * p.W;
+    OHW = p.OH * p.OW;
+    W = p.W;
+    OW = p.OW;
+    xc_bytes = c_ok ? x_chan * uint32_t(HW) * 4u : kRowNone;
+    yc_bytes = o_ok ? dy_chan * uint32_t(OHW) * 4u : kRowNone;
+    dsum = 0.f;
+  }
+  __device__ __forceinline__ void load(const TileEntry* tiles, int slab) {
     const TileEntry* ex = &tiles[slab * BK + b_t];
     const uint4 xo = *reinterpret_cast<const uint4*>(ex->xrow);
     xbits = ex->bits;
@@ -748,10 +795,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       yr[j][0] = mfma::bload2(rdy, __builtin_elementwise_add_sat(yo.x, yc_bytes), 0);
       yr[j][1] = mfma::bload2(rdy, __builtin_elementwise_add_sat(yo.y, yc_bytes), 0);
     }
-  };
-  float* const a_st = As + a_kq * ROW_A + 2 * a_o;                       // [coord][kq][o][2]
-  float* const b_st = Bs + (b_t >> 1) * ROW_B + 2 * b_c + (b_t & 1);    // [coord][kq][c][2]
-  auto store = [&](int slab) {
+  }
+  __device__ __forceinline__ void store(const TileEntry* tiles, int slab, float* As, float* Bs) {
+    float* const a_st = As + a_kq * ROW_A + 2 * a_o;                       // [coord][kq][o][2]
+    float* const b_st = Bs + (b_t >> 1) * ROW_B + 2 * b_c + (b_t & 1);    // [coord][kq][c][2]
     if (xbits & kXRare) {
       const int first = tiles[slab * BK + b_t].xfirst + int(x_chan) * HW;
 #pragma unroll
@@ -759,7 +806,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
           const bool ok = c_ok && ((xbits >> (8 + r)) & 1u) && ((xbits >> cc) & 1u);
-          xr[r][cc] = mfma::bload(rx, ok ? uint32_t(first + r * p.W + cc) * 4u : kOffNone, 0);
+          xr[r][cc] = mfma::bload(rx, ok ? uint32_t(first + r * W + cc) * 4u : kOffNone, 0);
         }
     }
 #pragma unroll
@@ -772,7 +819,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
           for (int cc = 0; cc < 2; ++cc) {
             const bool ok = o_ok && ((ybits[j] >> (12 + r)) & 1u) && (cc == 0 || ((ybits[j] >> 4) & 1u));
-            yr[j][r][cc] = mfma::bload(rdy, ok ? uint32_t(first + r * p.OW + cc) * 4u : kOffNone, 0);
+            yr[j][r][cc] = mfma::bload(rdy, ok ? uint32_t(first + r * OW + cc) * 4u : kOffNone, 0);
           }
       }
     float gy[2][4];  // two 2x2 dy tiles
@@ -827,7 +874,71 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       b_st[(r * 4 + 2) * 4 * ROW_B] = z[r * 4 + 2] - z[r * 4 + 1];
       b_st[(r * 4 + 3) * 4 * ROW_B] = z[r * 4 + 1] - z[r * 4 + 3];
     }
-  };
+  }
+  // dBias of the range: every dy element lies in exactly one tile, and the
+  // workgroups of the first input-channel block read each one once; the four
+  // lanes of an output channel (a_kq = 0..3, adjacent) hold its slab tiles.
+  __device__ __forceinline__ void write_db(const Args& p, int range, int g, int ngroups, int o0) const {
+    float t = dsum;
+    t += __shfl_xor(t, 1);
+    t += __shfl_xor(t, 2);
+    if (a_kq == 0 && o_ok) p.out_db[(int64_t(range) * ngroups + g) * p.O + o0 + a_o] = t;
+  }
+};
+
+// dw = G^T dU G, G = [[1,0,0],[1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]], of a
+// wave's 32 output x 16 input channels, written as the range's 3x3 partial.
+// 16x16x4 layout: lane l, register v holds row 4 (l / 16) + v (output
+// channel) and column l % 16 (input channel).
+__device__ __forceinline__ void write_dw(const Args& p, const f32x4 (&acc)[16][2], int range, int g, int ngroups,
+                                         int o0, int c0, int wo, int wc, int kq, int li) {
+  const int c = c0 + wc * 16 + li;
+  if (c >= p.C) return;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
+      if (o >= p.O) continue;
+      float u[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) u[q] = acc[q][i][v];
+      float z[3][4];
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const float s12 = 0.5f * (u[4 + cc] + u[8 + cc]);
+        z[0][cc] = u[cc] + s12;
+        z[1][cc] = 0.5f * (u[4 + cc] - u[8 + cc]);
+        z[2][cc] = s12 + u[12 + cc];
+      }
+      float* dst = p.out + ((int64_t(range) * ngroups + g) * p.O + o) * int64_t(p.C) * 9 + int64_t(c) * 9;
+#pragma unroll
+      for (int r = 0; r < 3; ++r) {
+        const float s12 = 0.5f * (z[r][1] + z[r][2]);
+        dst[r * 3 + 0] = z[r][0] + s12;
+        dst[r * 3 + 1] = 0.5f * (z[r][1] - z[r][2]);
+        dst[r * 3 + 2] = s12 + z[r][3];
+      }
+    }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void wino_dw_kernel(Args p) {
+  __shared__ __attribute__((aligned(16))) float smem[A_FLOATS + B_FLOATS];
+  __shared__ TileEntry tiles[kChunk];
+  float* As = smem;
+  float* Bs = smem + A_FLOATS;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y;
+  // Blocks of one tile range are consecutive, so they share an XCD and read
+  // the same x and dy tiles through its L2.
+  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
+  const int nblk = p.n_ob * p.n_cb;
+  const int range = b / nblk, ob = (b % nblk) % p.n_ob, cb = (b % nblk) / p.n_ob;
+  const int o0 = ob * BO, c0 = cb * BC;
+  const int k_begin = range * p.kps;
+  const int k_end = min(p.T, k_begin + p.kps);
+  SlabIO io;
+  io.init(p, tid, g, o0, c0);
 
   // Wave (wo, wc) owns output channels wo*32 .. +31 (two 16-row blocks) and
   // input channels wc*16 .. +15 of the block, for all 16 coordinates.
@@ -861,90 +972,119 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int k0 = k_begin; k0 < k_end; k0 += kChunk) {
     const int k1 = min(k_end, k0 + kChunk);
     const int nslab = (k1 - k0 + BK - 1) / BK;
-    for (int i = tid; i < nslab * BK; i += mfma::kThreads) {
-      const int t = k0 + i;
-      const bool tok = t < k1;
-      uint32_t img;
-      int oy, ox;
-      tile_origin(tok ? uint32_t(t) : 0u, p, img, oy, ox);
-      const int y0 = oy - p.ph, x0 = ox - p.pw;
-      TileEntry e;
-      e.xfirst = int(img) * p.Cin * HW + y0 * p.W + x0;
-      const int yfirst = int(img) * p.Cout * OHW + oy * p.OW + ox;
-      uint32_t bits = uint32_t(ox + 1 < p.OW) << 4;
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc) bits |= uint32_t(unsigned(x0 + cc) < unsigned(p.W)) << cc;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool ok = tok && unsigned(y0 + r) < unsigned(p.H);
-        bits |= uint32_t(ok) << (8 + r);
-        e.xrow[r] = ok ? uint32_t(e.xfirst + r * p.W) * 4u : kRowNone;
-      }
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const bool ok = tok && oy + r < p.OH;
-        bits |= uint32_t(ok) << (12 + r);
-        e.yrow[r] = ok ? uint32_t(yfirst + r * p.OW) * 4u : kRowNone;
-      }
-      // Checked for the largest channel, so every channel's lanes agree.
-      if (e.xfirst < 0 || e.xfirst + 3 * p.W + 4 + (p.Cin - 1) * HW > x_elems) bits |= kXRare;
-      if (yfirst + p.OW + 2 + (p.Cout - 1) * OHW > dy_elems) bits |= kYRare;
-      e.bits = bits;
-      tiles[i] = e;
-    }
+    decode_tiles(p, tiles, k0, k1, nslab * BK, tid, mfma::kThreads);
     __syncthreads();
-    load(0);
+    io.load(tiles, 0);
     for (int sl = 0; sl < nslab; ++sl) {
-      store(sl);
+      io.store(tiles, sl, As, Bs);
       __syncthreads();
-      load(min(sl + 1, nslab - 1));  // the last slab re-reads itself: no branch around the loads
+      io.load(tiles, min(sl + 1, nslab - 1));  // the last slab re-reads itself: no branch around the loads
       __builtin_amdgcn_sched_barrier(0);
       mma();
       __syncthreads();
     }
   }
+  if (p.out_db && cb == 0) io.write_db(p, range, g, gridDim.y, o0);
+  write_dw(p, acc, range, g, gridDim.y, o0, c0, wo, wc, kq, li);
+}
 
-  // dBias of the range: every dy element lies in exactly one tile, and the
-  // workgroups of the first input-channel block read each one once; the four
-  // lanes of an output channel (a_kq = 0..3, adjacent) hold its slab tiles.
-  if (p.out_db && cb == 0) {
-    float t = dsum;
-    t += __shfl_xor(t, 1);
-    t += __shfl_xor(t, 2);
-    if (a_kq == 0 && o_ok) p.out_db[(int64_t(range) * gridDim.y + g) * p.O + o0 + a_o] = t;
+// The weight gradient with the warp-specialized split of the forward kernel:
+// waves 4-7 (producers) load and transform slab s + 1 (dM and V) into the
+// other of two LDS stages while waves 0-3 (consumers) multiply slab s; one
+// barrier per slab.  A range holds at most kChunk tiles, decoded once; an odd
+// slab count runs one more slab of tiles past the range (they read nothing).
+// Producers own the dBias sums, consumers the accumulators and the
+// G^T dU G epilogue.  Same products per coordinate in the same order as the
+// single-role kernel.  106 KB of LDS stages + 16 KB tile table: one
+// workgroup of eight waves per CU.
+__global__ __launch_bounds__(512) void wino_dw_ws_kernel(Args p) {
+  __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs0[B_FLOATS];
+  __shared__ __attribute__((aligned(16))) float As1[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs1[B_FLOATS];
+  __shared__ TileEntry tiles[kChunk];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y;
+  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
+  const int nblk = p.n_ob * p.n_cb;
+  const int range = b / nblk, ob = (b % nblk) % p.n_ob, cb = (b % nblk) / p.n_ob;
+  const int o0 = ob * BO, c0 = cb * BC;
+  const int k_begin = range * p.kps;
+  const int k_end = min(p.T, k_begin + p.kps);  // the host keeps p.kps <= kChunk
+  const int nslab = ((k_end - k_begin + BK - 1) / BK + 1) & ~1;  // even, >= 2
+  decode_tiles(p, tiles, k_begin, k_end, nslab * BK, tid, 2 * mfma::kThreads);
+  __syncthreads();
+
+  if (wave >= 4) {
+    SlabIO io;
+    io.init(p, tid - mfma::kThreads, g, o0, c0);
+    io.load(tiles, 0);
+    io.store(tiles, 0, As0, Bs0);
+    io.load(tiles, 1);
+    __syncthreads();  // stage 0 holds slab 0
+    for (int s = 0; s < nslab; s += 2) {
+      io.store(tiles, s + 1, As1, Bs1);
+      io.load(tiles, min(s + 2, nslab - 1));
+      __syncthreads();
+      if (s + 2 < nslab) {
+        io.store(tiles, s + 2, As0, Bs0);
+        io.load(tiles, min(s + 3, nslab - 1));
+      }
+      __syncthreads();
+    }
+    if (p.out_db && cb == 0) io.write_db(p, range, g, gridDim.y, o0);
+    return;
   }
 
-  // dw = G^T dU G, G = [[1,0,0],[1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]].
-  // 16x16x4 layout: lane l, register v holds row 4 (l / 16) + v (output
-  // channel) and column l % 16 (input channel).
-  const int c = c0 + wc * 16 + li;
-  if (c >= p.C) return;
+  const int wo = wave >> 1, wc = wave & 1;
+  const int kq = lane >> 4, li = lane & 15;
+  f32x4 acc[16][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int t = 0; t < 16; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto slab = [&](const float* Ac, const float* Bc) {
+    const f32x2* const a_frag = reinterpret_cast<const f32x2*>(Ac + kq * ROW_A + 2 * (wo * 32 + li));
+    const f32x2* const b_frag = reinterpret_cast<const f32x2*>(Bc + kq * ROW_B + 2 * (wc * 16 + li));
+    f32x2 fa0[4], fa1[4], fb[4];
+    auto frags = [&](int q) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int o = o0 + wo * 32 + i * 16 + 4 * kq + v;
-      if (o >= p.O) continue;
-      float u[16];
-#pragma unroll
-      for (int q = 0; q < 16; ++q) u[q] = acc[q][i][v];
-      float z[3][4];
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc) {
-        const float s12 = 0.5f * (u[4 + cc] + u[8 + cc]);
-        z[0][cc] = u[cc] + s12;
-        z[1][cc] = 0.5f * (u[4 + cc] - u[8 + cc]);
-        z[2][cc] = s12 + u[12 + cc];
+      for (int j = 0; j < 4; ++j) {
+        const int t = 4 * q + j;
+        fb[j] = b_frag[t * 2 * ROW_B];
+        fa0[j] = a_frag[t * 2 * ROW_A];
+        fa1[j] = a_frag[t * 2 * ROW_A + 16];
       }
-      float* dst = p.out + ((int64_t(range) * gridDim.y + g) * p.O + o) * int64_t(p.C) * 9 + int64_t(c) * 9;
+    };
+    auto quad = [&](int q) {
 #pragma unroll
-      for (int r = 0; r < 3; ++r) {
-        const float s12 = 0.5f * (z[r][1] + z[r][2]);
-        dst[r * 3 + 0] = z[r][0] + s12;
-        dst[r * 3 + 1] = 0.5f * (z[r][1] - z[r][2]);
-        dst[r * 3 + 2] = s12 + z[r][3];
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int t = 4 * q + j;
+          acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa0[j][h], fb[j][h], acc[t][0], 0, 0, 0);
+          acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa1[j][h], fb[j][h], acc[t][1], 0, 0, 0);
+        }
+    };
+    frags(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      quad(q);
+      if (q < 3) {
+        frags(q + 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 14, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+  };
+  __syncthreads();  // stage 0 holds slab 0
+  for (int s = 0; s < nslab; s += 2) {
+    slab(As0, Bs0);
+    __syncthreads();
+    slab(As1, Bs1);
+    __syncthreads();
+  }
+  write_dw(p, acc, range, g, gridDim.y, o0, c0, wo, wc, kq, li);
 }
 
 }  // namespace fused_dw
@@ -1154,6 +1294,7 @@ struct DwRunPlan {
   fused_dw::Args p{};
   int G = 1;
   int64_t blocks = 0, ranges = 1, n_dw = 0, n_db = 0;
+  bool ws = false;  // the warp-specialized kernel (ranges of at most fused_dw::kChunk tiles)
 };
 
 // with_db: the kernel also writes the dBias partials (Cout per range).
@@ -1185,10 +1326,30 @@ int plan_dw_run(const mx_conv2d_desc& d, int64_t ws_limit, bool with_db, DwRunPl
   r->n_dw = int64_t(p.Cout) * p.C * 9;
   r->n_db = with_db ? p.Cout : 0;
   r->blocks = int64_t(p.n_ob) * p.n_cb * r->G;
+  const int64_t fit = ws_limit / ((r->n_dw + r->n_db) * 4);
+  // Warp-specialized kernel: one workgroup per CU, so ranges fill the CUs
+  // once (whole slab pairs, at most kChunk tiles each, as many as the
+  // workspace holds; one range writes dw directly).  MX_WINO_DW_WS=0 / 1
+  // forces the single-role / warp-specialized kernel (tests, tuning).
+  {
+    const int64_t want = fit >= 2 ? std::max<int64_t>(1, std::min<int64_t>(cu_count() / r->blocks, fit)) : 1;
+    int64_t kps = (T + want - 1) / want;
+    kps = (kps + 2 * fused_dw::BK - 1) / (2 * fused_dw::BK) * (2 * fused_dw::BK);
+    r->ws = kps <= fused_dw::kChunk;
+    if (const char* e = std::getenv("MX_WINO_DW_WS"))
+      if (e[0] == '0' || e[0] == '1') r->ws = e[0] == '1' && kps <= fused_dw::kChunk;
+    if (r->ws) {
+      r->ranges = std::max<int64_t>(1, (T + kps - 1) / kps);
+      MX_REQUIRE(r->blocks * r->ranges <= INT32_MAX && r->G <= 65535, MX_ERR_UNSUPPORTED,
+                 "winograd dweight: grid too large");
+      p.kps = int(kps);
+      p.T = int(T);
+      return MX_OK;
+    }
+  }
   int64_t per_cu = 2;
   if (const char* e = std::getenv("MX_WINO_DW_PER_CU")) per_cu = std::max(1, std::atoi(e));
   int64_t want = std::max<int64_t>(1, (per_cu * int64_t(cu_count()) + r->blocks - 1) / r->blocks);
-  const int64_t fit = ws_limit / ((r->n_dw + r->n_db) * 4);
   want = fit >= 2 ? std::min(want, fit) : 1;
   int64_t kps = (T + want - 1) / want;
   kps = std::max<int64_t>(kps, 4 * fused_dw::BK);
@@ -1227,8 +1388,12 @@ int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const floa
   float* const partials_db = r.ranges > 1 ? partials + r.ranges * r.n_dw : nullptr;
   p.out = r.ranges > 1 ? partials : dw;
   p.out_db = db ? (r.ranges > 1 ? partials_db : db) : nullptr;
-  hipLaunchKernelGGL(fused_dw::wino_dw_kernel, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)), dim3(256), 0,
-                     s, p);
+  if (r.ws)
+    hipLaunchKernelGGL(fused_dw::wino_dw_ws_kernel, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)),
+                       dim3(512), 0, s, p);
+  else
+    hipLaunchKernelGGL(fused_dw::wino_dw_kernel, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)),
+                       dim3(256), 0, s, p);
   MX_HIP(hipGetLastError());
   if (r.ranges > 1)
     return conv::sum_partials(partials, partials_db, int(r.ranges), r.n_dw, int(r.n_db), dw, db, s);
@@ -1258,7 +1423,7 @@ int winograd_describe(const mx_conv2d_desc& d, int phase, bool with_bias, int64_
   if (phase == MX_CONV_DWEIGHT) {
     DwRunPlan r;
     MX_TRY(plan_dw_run(d, ws_limit, with_bias, &r));
-    *variant = r.ranges > 1 ? "wino_dw_kernel+ranges" : "wino_dw_kernel";
+    *variant = cat(r.ws ? "wino_dw_ws_kernel" : "wino_dw_kernel", r.ranges > 1 ? "+ranges" : "");
     *ws_bytes = r.ranges > 1 ? r.ranges * (r.n_dw + r.n_db) * 4 : 0;
     return MX_OK;
   }
