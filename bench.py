@@ -733,7 +733,7 @@ def sq_summary(directory, xcds=8, cus=256):
     return "\n".join(out)
 
 
-WINOGRAD_KERNELS = ("filter_kernel", "wino_ws_kernel",   # fused path
+WINOGRAD_KERNELS = ("filter_kernel", "wino_ws_kernel", "wino_ws16_kernel",   # fused path
                     "wino_filter_kernel", "wino_input_kernel", "wino_output_kernel", "gemm_kernel")
 # First dispatch of a Winograd call: its filter transform, or the fused
 # kernel itself when that transforms the filter (no filter launch before it).
@@ -820,7 +820,7 @@ def trace_summary(trace_csv, bench_log):
             owner[i] = last_tile = "winograd_dweight"
         elif label in WINOGRAD_KERNELS:
             wino_calls += label in WINOGRAD_CALL_START or (
-                label == "wino_ws_kernel" and (i == 0 or seq[i - 1][0] != "filter_kernel"))
+                label in ("wino_ws_kernel", "wino_ws16_kernel") and (i == 0 or seq[i - 1][0] != "filter_kernel"))
             owner[i] = "winograd_dinput" if (wino_dx and wino_calls % 2 == 0) else "winograd_forward"
         elif label in AFTER_HELPERS or label == "conv_dx_zero_kernel":
             owner[i] = last_tile

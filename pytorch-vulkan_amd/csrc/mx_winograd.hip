@@ -625,6 +625,216 @@ __global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
       mfma::bstore(r1[1] - r1[2] - r1[3] + bb, ry, (ok && below && right) ? off + row_step + 4u : kOffNone, 0);
     }
 }
+
+// The same roles with 16 tiles per workgroup: 80 KB of LDS and at most 128
+// VGPRs, so two workgroups share a CU and one's prologue and epilogue (the
+// first slabs' loads, the output transform and its stores) overlap the
+// other's products.  Consumer wave w owns output channels w*16 .. +15 and all
+// 16 tiles; producer waves 4-5 transform the 128 input patches of a slab,
+// waves 6-7 copy the slab's filter (64 floats per thread).  Same U' layout,
+// accumulation order and epilogue as the 32-tile kernel: bit-identical.
+constexpr int BT16 = 16;
+constexpr int ROW_B16 = 2 * BT16;
+constexpr int B16_FLOATS = 16 * 4 * ROW_B16;
+
+template <bool RAGGED>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void wino_ws16_kernel(fused::Args p) {
+  __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs0[B16_FLOATS];
+  __shared__ __attribute__((aligned(16))) float As1[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs1[B16_FLOATS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.y;
+  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
+  const int ob = b % p.n_ob, tb = b / p.n_ob;
+  const int o0 = ob * BO, t0 = tb * BT16;
+  const int nslab = p.nslab;  // even: the host pads the channels to 16
+
+  if (wave >= 6) {
+    // ---- filter producers: rows a_row .. of the slab's U' block, 16 floats
+    // (four 16-byte chunks) per (coordinate, k pair) row and thread.
+    const int ptid = tid - 384;  // 0 .. 127
+    const i32x4 ru = mfma::buffer_rsrc(p.U, p.u_bytes);
+    const int a_row = ptid >> 5, a_f4 = ptid & 31;  // 4 rows per pass, 16 passes
+    const uint32_t a_off = uint32_t(
+        ((((int64_t(g) * 16 + (a_row >> 2)) * p.nslab) * 4 + (a_row & 3)) * int64_t(p.Opad) * 2 + 2 * o0 +
+         4 * a_f4) *
+        4);
+    const uint32_t a_sstep = uint32_t(4) * p.Opad * 2 * 4;
+    const uint32_t a_cstep = uint32_t(p.nslab) * a_sstep;  // one coordinate
+    f32x4 av[16];
+    auto load = [&](int slab) {
+      const uint32_t sa = uint32_t(slab) * a_sstep;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_cstep);
+    };
+    auto store = [&](float* As) {
+      float* const a_st = As + a_row * ROW_A + 4 * a_f4;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) *reinterpret_cast<f32x4*>(a_st + q * 4 * ROW_A) = av[q];
+    };
+    load(0);
+    store(As0);
+    load(1);
+    __syncthreads();
+    for (int s = 0; s < nslab; s += 2) {
+      store(As1);
+      load(min(s + 2, nslab - 1));
+      __syncthreads();
+      if (s + 2 < nslab) {
+        store(As0);
+        load(min(s + 3, nslab - 1));
+      }
+      __syncthreads();
+    }
+    return;
+  }
+  if (wave >= 4) {
+    // ---- patch producers: thread ptid owns slab tile b_t and channel b_c;
+    // a half-wave's V stores are 32 consecutive floats.
+    const int ptid = tid - 256;  // 0 .. 127
+    const i32x4 rx = mfma::buffer_rsrc(p.x, p.x_bytes);
+    const int b_t = ptid & 15;
+    const int b_c = ((ptid >> 4) & 1) | ((ptid >> 5) << 1);
+    PatchRows px;
+    {
+      const int t = t0 + b_t;
+      const bool tok = t < p.T;
+      const uint32_t tt = tok ? uint32_t(t) : 0u;
+      const uint32_t img = mfma::fdiv(tt, p.f_thw);
+      const uint32_t pos = tt - img * uint32_t(p.TH * p.TW);
+      const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
+      const int y0 = int(2 * ty) - p.ph, x0 = int(2 * tx) - p.pw;
+      const int64_t plane = (int64_t(img) * p.Cin + int64_t(g) * p.C + b_c) * p.H;
+      px.init(plane, y0, x0, tok, p.H, p.W);
+    }
+    const uint32_t x_sstep = uint32_t(BK) * p.H * p.W * 4;
+    auto load = [&](int slab) {
+      px.load(rx, uint32_t(slab) * x_sstep, uint32_t(p.x_bytes), !RAGGED || slab * BK + b_c < p.C);
+    };
+    auto store = [&](float* Bs) {
+      px.fix(rx);
+      float* const b_st = Bs + (b_c >> 1) * ROW_B16 + 2 * b_t + (b_c & 1);
+      float d[16];
+      px.patch(d);
+      float z[16];
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        z[0 * 4 + cc] = d[0 * 4 + cc] - d[2 * 4 + cc];
+        z[1 * 4 + cc] = d[1 * 4 + cc] + d[2 * 4 + cc];
+        z[2 * 4 + cc] = d[2 * 4 + cc] - d[1 * 4 + cc];
+        z[3 * 4 + cc] = d[1 * 4 + cc] - d[3 * 4 + cc];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        b_st[(i * 4 + 0) * 4 * ROW_B16] = z[i * 4 + 0] - z[i * 4 + 2];
+        b_st[(i * 4 + 1) * 4 * ROW_B16] = z[i * 4 + 1] + z[i * 4 + 2];
+        b_st[(i * 4 + 2) * 4 * ROW_B16] = z[i * 4 + 2] - z[i * 4 + 1];
+        b_st[(i * 4 + 3) * 4 * ROW_B16] = z[i * 4 + 1] - z[i * 4 + 3];
+      }
+    };
+    load(0);
+    store(Bs0);
+    load(1);
+    __syncthreads();
+    for (int s = 0; s < nslab; s += 2) {
+      store(Bs1);
+      load(min(s + 2, nslab - 1));
+      __syncthreads();
+      if (s + 2 < nslab) {
+        store(Bs0);
+        load(min(s + 3, nslab - 1));
+      }
+      __syncthreads();
+    }
+    return;
+  }
+
+  // ---- consumers: wave w owns output channels w*16 .. +15 and the 16 tiles.
+  const int kq = lane >> 4, li = lane & 15;
+  f32x4 acc[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto slab = [&](const float* Ac, const float* Bc) {
+    const f32x2* const a_frag = reinterpret_cast<const f32x2*>(Ac + kq * ROW_A + 2 * (wave * 16 + li));
+    const f32x2* const b_frag = reinterpret_cast<const f32x2*>(Bc + kq * ROW_B16 + 2 * li);
+    f32x2 fa[4], fb[4];
+    auto frags = [&](int q) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 4 * q + j;
+        fb[j] = b_frag[t * 2 * ROW_B16];
+        fa[j] = a_frag[t * 2 * ROW_A];
+      }
+    };
+    auto quad = [&](int q) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[4 * q + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[j][h], fb[j][h], acc[4 * q + j], 0, 0, 0);
+    };
+    frags(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      quad(q);
+      if (q < 3) {
+        frags(q + 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  __syncthreads();  // stage 0 holds slab 0
+  for (int s = 0; s < nslab; s += 2) {
+    slab(As0, Bs0);
+    __syncthreads();
+    slab(As1, Bs1);
+    __syncthreads();
+  }
+
+  // Output transform (the 32-tile kernel's epilogue).
+  const int t = t0 + li;
+  if (t >= p.T) return;
+  const uint32_t img = mfma::fdiv(uint32_t(t), p.f_thw);
+  const uint32_t pos = uint32_t(t) - img * uint32_t(p.TH * p.TW);
+  const uint32_t ty = mfma::fdiv(pos, p.f_tw), tx = pos - ty * uint32_t(p.TW);
+  const int oy = int(2 * ty), ox = int(2 * tx);
+  const bool right = ox + 1 < p.OW, below = oy + 1 < p.OH;
+  float bias_v[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int o = o0 + wave * 16 + 4 * kq + v;
+    bias_v[v] = (p.bias && o < p.O) ? p.bias[g * p.O + o] : 0.f;
+  }
+  const i32x4 ry = mfma::buffer_rsrc(p.y, p.y_bytes);
+  const uint32_t row_step = uint32_t(p.OW) * 4u;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int o = o0 + wave * 16 + 4 * kq + v;
+    float m[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) m[q] = acc[q][v];
+    float r0[4], r1[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      r0[c] = m[c] + m[4 + c] + m[8 + c];
+      r1[c] = m[4 + c] - m[8 + c] - m[12 + c];
+    }
+    const float bb = bias_v[v];
+    const bool ok = o < p.O;
+    const uint32_t off =
+        uint32_t(((img * uint32_t(p.Cout) + uint32_t(g * p.O + o)) * uint32_t(p.OH) + uint32_t(oy)) * uint32_t(p.OW) +
+                 uint32_t(ox)) *
+        4u;
+    mfma::bstore(r0[0] + r0[1] + r0[2] + bb, ry, ok ? off : kOffNone, 0);
+    mfma::bstore(r0[1] - r0[2] - r0[3] + bb, ry, (ok && right) ? off + 4u : kOffNone, 0);
+    mfma::bstore(r1[0] + r1[1] + r1[2] + bb, ry, (ok && below) ? off + row_step : kOffNone, 0);
+    mfma::bstore(r1[1] - r1[2] - r1[3] + bb, ry, (ok && below && right) ? off + row_step + 4u : kOffNone, 0);
+  }
+}
 }  // namespace ws
 
 // ------------------------------------------------------------ fused dWeight
@@ -1178,6 +1388,7 @@ struct RunPlan {
   int64_t blocks = 0;
   bool fused = true;
   bool filt = false;          // the fused kernel transforms the filter itself (no filter launch)
+  bool t16 = false;           // the 16-tile fused kernel (two workgroups per CU)
   int64_t chunk = 0;          // images per unfused pass
   int64_t unfused_bytes = 0;  // U, V and M of one pass
 };
@@ -1242,6 +1453,16 @@ int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
   if (const char* e = std::getenv("MX_WINOGRAD_FILTER"))
     if (e[0] == '0' || e[0] == '1') r->filt = e[0] == '1';
   r->filt = r->filt && r->fused;
+  // The 16-tile kernel (two workgroups per CU, one's prologue and epilogue
+  // under the other's products) wins while the transformed filter is small
+  // enough to stay in L2 for the twice as many workgroups that read it: 64 x
+  // 64 channels at 56^2, batch 64, 96.3 -> 84.4 us, 128 x 128 at 28^2 93.9 ->
+  // 79.5, 256 x 256 at 16^2, batch 16, 49.0 -> 34.7; at 512 x 512 (a 16.8 MB
+  // U') it loses (91.2 -> 94.9).  MX_WINOGRAD_T16=0 / 1 forces it off / on.
+  r->t16 = int64_t(p.Cpad) * p.Opad <= 256 * 256;
+  if (const char* e = std::getenv("MX_WINOGRAD_T16"))
+    if (e[0] == '0' || e[0] == '1') r->t16 = e[0] == '1';
+  r->t16 = r->t16 && r->fused && !r->filt;
   if (r->filt) {
     p.w_bytes = int64_t(d.cout) * p.C * 9 * 4;
     MX_REQUIRE(p.w_bytes < mfma::kBufMaxBytes, MX_ERR_UNSUPPORTED, "winograd: the filter exceeds 2 GiB");
@@ -1280,6 +1501,13 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   hipLaunchKernelGGL(fused::filter_kernel, dim3(unsigned(std::min<int64_t>((filter_threads + 63) / 64, 1 << 20))),
                      dim3(64), 0, s, w, U.as<float>(), p.C, p.O, p.Cpad, p.Opad, r.G, flip);
   MX_HIP(hipGetLastError());
+  if (r.t16) {
+    const dim3 grid16{unsigned((int64_t(p.T) + ws::BT16 - 1) / ws::BT16 * p.n_ob), unsigned(r.G), 1u};
+    void (*k16)(fused::Args) = ragged ? ws::wino_ws16_kernel<true> : ws::wino_ws16_kernel<false>;
+    hipLaunchKernelGGL(k16, grid16, dim3(512), 0, s, p);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
   void (*kern)(fused::Args) = ragged ? ws::wino_ws_kernel<true, 0> : ws::wino_ws_kernel<false, 0>;
   hipLaunchKernelGGL(kern, grid, dim3(512), 0, s, p);
   MX_HIP(hipGetLastError());
@@ -1430,7 +1658,8 @@ int winograd_describe(const mx_conv2d_desc& d, int phase, bool with_bias, int64_
   RunPlan r;
   MX_TRY(plan_run(phase == MX_CONV_DINPUT ? dinput_as_forward(d) : d, ws_limit, &r));
   if (r.fused) {
-    *variant = cat("wino_ws_kernel<", r.p.C % (2 * fused::BK) ? "ragged" : "even", r.filt ? ",filter>" : ">");
+    *variant = cat(r.t16 ? "wino_ws16_kernel<" : "wino_ws_kernel<", r.p.C % (2 * fused::BK) ? "ragged" : "even",
+                   r.filt ? ",filter>" : ">");
     *ws_bytes = 0;
   } else {
     // U, V and M are fresh mx_malloc blocks (256-byte aligned).

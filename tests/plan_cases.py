@@ -6,7 +6,8 @@ epilogue flags).  This module lists
 
 * the cases the GPU parity tests run (`tests/test_gpu_plans.py`), each with the
   environment that forces its plan (`MX_CONV_PLAN`, `MX_GEMM_TILE`,
-  `MX_WINOGRAD_FUSED`, `MX_WINOGRAD_FILTER`, `MX_WINO_DW_WS`, `TORCH_VULKAN_CONV_WORKSPACE_MB`), and
+  `MX_WINOGRAD_FUSED`, `MX_WINOGRAD_FILTER`, `MX_WINOGRAD_T16`, `MX_WINO_DW_WS`,
+  `TORCH_VULKAN_CONV_WORKSPACE_MB`), and
 * every call the benchmark configurations make (C1 single layer, C2 Linear,
   C3 ResNet-50 conv stack, C4 U-Net step), with the algorithm bench.py or the
   "vulkan" device requests,
@@ -125,7 +126,8 @@ WINOGRAD_GEOMETRIES = [
     ((8, 64, 8, 8), 64, (3, 3), (1, 1), (1, 1), (1, 1), 1),  # 1 MiB budget: two image chunks
 ]
 WINOGRAD_MODES = [
-    {"MX_WINOGRAD_FUSED": "1", "MX_WINOGRAD_FILTER": "0"},
+    {"MX_WINOGRAD_FUSED": "1", "MX_WINOGRAD_FILTER": "0", "MX_WINOGRAD_T16": "0"},
+    {"MX_WINOGRAD_FUSED": "1", "MX_WINOGRAD_FILTER": "0", "MX_WINOGRAD_T16": "1"},
     {"MX_WINOGRAD_FUSED": "1", "MX_WINOGRAD_FILTER": "1"},
     {"MX_WINO_DW_WS": "0"},
     {"MX_WINO_DW_WS": "1"},
