@@ -1207,6 +1207,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // G^T dU G epilogue.  Same products per coordinate in the same order as the
 // single-role kernel.  106 KB of LDS stages + 16 KB tile table: one
 // workgroup of eight waves per CU.
+// VEC_OUT (output channels a multiple of 64, input channels of 32): the
+// consumers write the block's 3x3 partial (64 x 32 x 9 floats) to LDS and
+// all eight waves copy it out as 16-byte stores of whole rows, instead of
+// each lane storing its 72 values one float at a time (C1: 14.4 MB of
+// partials, 7 us of scattered stores).
+constexpr int kResRow = BC * 9;  // floats of one output channel's row in the result tile
+
+template <bool VEC_OUT>
 __global__ __launch_bounds__(512) void wino_dw_ws_kernel(Args p) {
   __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
   __shared__ __attribute__((aligned(16))) float Bs0[B_FLOATS];
@@ -1243,9 +1251,11 @@ __global__ __launch_bounds__(512) void wino_dw_ws_kernel(Args p) {
       __syncthreads();
     }
     if (p.out_db && cb == 0) io.write_db(p, range, g, gridDim.y, o0);
-    return;
+    if constexpr (!VEC_OUT) return;
   }
-
+  if (wave >= 4) {
+    __syncthreads();  // the consumers' result tile is in LDS
+  } else {
   const int wo = wave >> 1, wc = wave & 1;
   const int kq = lane >> 4, li = lane & 15;
   f32x4 acc[16][2];
@@ -1294,7 +1304,52 @@ __global__ __launch_bounds__(512) void wino_dw_ws_kernel(Args p) {
     slab(As1, Bs1);
     __syncthreads();
   }
-  write_dw(p, acc, range, g, gridDim.y, o0, c0, wo, wc, kq, li);
+  if constexpr (!VEC_OUT) {
+    write_dw(p, acc, range, g, gridDim.y, o0, c0, wo, wc, kq, li);
+    return;
+  } else {
+    // G^T dU G as in write_dw, into the result tile: rows 0-29 in As0, 30-59
+    // in As1, 60-63 in Bs0 (the stages are free after the last barrier).
+    const int c = wc * 16 + li;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int o = wo * 32 + i * 16 + 4 * kq + v;
+        float u[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) u[q] = acc[q][i][v];
+        float z[3][4];
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const float s12 = 0.5f * (u[4 + cc] + u[8 + cc]);
+          z[0][cc] = u[cc] + s12;
+          z[1][cc] = 0.5f * (u[4 + cc] - u[8 + cc]);
+          z[2][cc] = s12 + u[12 + cc];
+        }
+        float* dst = (o < 30 ? As0 + o * kResRow : o < 60 ? As1 + (o - 30) * kResRow : Bs0 + (o - 60) * kResRow) +
+                     c * 9;
+#pragma unroll
+        for (int r = 0; r < 3; ++r) {
+          const float s12 = 0.5f * (z[r][1] + z[r][2]);
+          dst[r * 3 + 0] = z[r][0] + s12;
+          dst[r * 3 + 1] = 0.5f * (z[r][1] - z[r][2]);
+          dst[r * 3 + 2] = s12 + z[r][3];
+        }
+      }
+    __syncthreads();
+  }
+  }
+  if constexpr (VEC_OUT) {
+    // 64 rows of 288 floats (72 16-byte chunks) to [range][g][o][c][3][3].
+    float* const out = p.out + ((int64_t(range) * gridDim.y + g) * p.O + o0) * int64_t(p.C) * 9 + int64_t(c0) * 9;
+    for (int f4 = tid; f4 < BO * (kResRow / 4); f4 += 2 * mfma::kThreads) {
+      const int o = f4 / (kResRow / 4), q = f4 - o * (kResRow / 4);
+      const float* src =
+          (o < 30 ? As0 + o * kResRow : o < 60 ? As1 + (o - 30) * kResRow : Bs0 + (o - 60) * kResRow) + 4 * q;
+      *reinterpret_cast<f32x4*>(out + int64_t(o) * p.C * 9 + 4 * q) = *reinterpret_cast<const f32x4*>(src);
+    }
+  }
 }
 
 }  // namespace fused_dw
@@ -1616,9 +1671,11 @@ int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const floa
   float* const partials_db = r.ranges > 1 ? partials + r.ranges * r.n_dw : nullptr;
   p.out = r.ranges > 1 ? partials : dw;
   p.out_db = db ? (r.ranges > 1 ? partials_db : db) : nullptr;
-  if (r.ws)
-    hipLaunchKernelGGL(fused_dw::wino_dw_ws_kernel, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)),
-                       dim3(512), 0, s, p);
+  if (r.ws) {
+    const bool vec_out = p.O % fused_dw::BO == 0 && p.C % fused_dw::BC == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+    void (*kern)(fused_dw::Args) = vec_out ? fused_dw::wino_dw_ws_kernel<true> : fused_dw::wino_dw_ws_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)), dim3(512), 0, s, p);
+  }
   else
     hipLaunchKernelGGL(fused_dw::wino_dw_kernel, dim3(unsigned(r.blocks / r.G * r.ranges), unsigned(r.G)),
                        dim3(256), 0, s, p);
