@@ -214,6 +214,17 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
 int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const float* dy,
                               float* dw, float* db, int algo, void* stream);
 
+/* dx, dw and db of one layer in one call: convolution_backward's
+ * dispatch(Input), dispatch(Weight) and dispatch(Bias)
+ * (csrc/ops/convolution.cpp:667-697).  Any of dx, dw, db may be NULL (not
+ * requested).  When both gradients of a 3x3 stride-1 layer take the fused
+ * Winograd paths (algo_dx and algo_dw MX_CONV_ALGO_WINOGRAD) they run as one
+ * launch, workgroups of both kinds side by side, bit-identical to
+ * mx_conv2d_backward_input followed by mx_conv2d_backward_weight; otherwise
+ * it is those two calls. */
+int mx_conv2d_backward(const mx_conv2d_desc* desc, const float* x, const float* w, const float* dy,
+                       float* dx, float* dw, float* db, int algo_dx, int algo_dw, void* stream);
+
 /* Allocation-free dWeight / dBias.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory while they run (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -829,6 +829,8 @@ int winograd_backward_weight(const mx_conv2d_desc& d, const float* x, const floa
                              int64_t ws_limit, float* ext, hipStream_t s);
 int winograd_describe(const mx_conv2d_desc& d, int phase, bool with_bias, int64_t ws_limit, std::string* variant,
                       int64_t* ws_bytes);
+int winograd_backward(const mx_conv2d_desc& d, const float* x, const float* w, const float* dy, float* dx, float* dw,
+                      float* db, int64_t ws_limit, hipStream_t s, bool* done);
 
 namespace conv {
 // Scratch budget of one convolution call (split-K partials, the Winograd
@@ -1233,6 +1235,30 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
                               int algo, void* stream) {
   MX_ABI_BEGIN
   return dweight_impl(desc, x, dy, dw, db, algo, nullptr, 0, stream);
+  MX_ABI_END
+}
+
+int mx_conv2d_backward(const mx_conv2d_desc* desc, const float* x, const float* w, const float* dy, float* dx,
+                       float* dw, float* db, int algo_dx, int algo_dw, void* stream) {
+  MX_ABI_BEGIN
+  mx_conv2d_desc d = *desc;
+  MX_TRY(checked_desc(&d));
+  if (dx && (dw || db)) {
+    int ax = 0, aw = 0;
+    MX_TRY(select_algo(d, MX_CONV_DINPUT, algo_dx, &ax));
+    if (dw) MX_TRY(select_algo(d, MX_CONV_DWEIGHT, algo_dw, &aw));
+    if (dw && ax == MX_CONV_ALGO_WINOGRAD && aw == MX_CONV_ALGO_WINOGRAD && images_per_launch(d) >= d.n) {
+      MX_REQUIRE(x && w && dy, MX_ERR_INVALID, "conv2d backward: null tensor");
+      int64_t limit = 0;
+      MX_TRY(conv::workspace_limit(&limit));
+      bool done = false;
+      MX_TRY(winograd_backward(d, x, w, dy, dx, dw, db, limit, resolve_stream(stream), &done));
+      if (done) return MX_OK;
+    }
+  }
+  if (dx) MX_TRY(mx_conv2d_backward_input(desc, dy, w, dx, algo_dx, stream));
+  if (dw || db) MX_TRY(mx_conv2d_backward_weight(desc, x, dy, dw, db, algo_dw, stream));
+  return MX_OK;
   MX_ABI_END
 }
 

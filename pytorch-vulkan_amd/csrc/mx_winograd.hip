@@ -391,15 +391,12 @@ using mfma::kOffNone;
 // then loads the 3x3 filters of output channel o0 + o, slab channels 2 kq and
 // 2 kq + 1, and stores their 16 coordinates as 8-byte pairs (a wave writes
 // 512 contiguous bytes per coordinate).
+// The kernel body for logical block b of group g, on LDS stages the caller
+// provides (the backward kernel runs it beside the weight gradient's body).
 template <bool RAGGED, int FILT>
-__global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
-  __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
-  __shared__ __attribute__((aligned(16))) float Bs0[B_FLOATS];
-  __shared__ __attribute__((aligned(16))) float As1[A_FLOATS];
-  __shared__ __attribute__((aligned(16))) float Bs1[B_FLOATS];
+__device__ __forceinline__ void ws_body(const fused::Args& p, int b, int g, float* __restrict__ As0,
+                                        float* __restrict__ Bs0, float* __restrict__ As1, float* __restrict__ Bs1) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = blockIdx.y;
-  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
   const int ob = b % p.n_ob, tb = b / p.n_ob;
   const int o0 = ob * BO, t0 = tb * BT;
   const int nslab = p.nslab;  // even: the host pads the channels to 16
@@ -626,6 +623,15 @@ __global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
     }
 }
 
+template <bool RAGGED, int FILT>
+__global__ __launch_bounds__(512) void wino_ws_kernel(fused::Args p) {
+  __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs0[B_FLOATS];
+  __shared__ __attribute__((aligned(16))) float As1[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs1[B_FLOATS];
+  ws_body<RAGGED, FILT>(p, mfma::xcd_remap(blockIdx.x, gridDim.x), blockIdx.y, As0, Bs0, As1, Bs1);
+}
+
 // The same roles with 16 tiles per workgroup: 80 KB of LDS and at most 128
 // VGPRs, so two workgroups share a CU and one's prologue and epilogue (the
 // first slabs' loads, the output transform and its stores) overlap the
@@ -637,7 +643,10 @@ constexpr int BT16 = 16;
 constexpr int ROW_B16 = 2 * BT16;
 constexpr int B16_FLOATS = 16 * 4 * ROW_B16;
 
-template <bool RAGGED>
+// FILT 1 / 2: waves 6-7 transform the layer filter w (2: flipped and
+// channel-swapped) instead of copying U': thread (half, o) the four filters
+// of output channel o0 + o and slab channels 4 half .. 4 half + 3.
+template <bool RAGGED, int FILT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void wino_ws16_kernel(fused::Args p) {
   __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
   __shared__ __attribute__((aligned(16))) float Bs0[B16_FLOATS];
@@ -662,26 +671,78 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         4);
     const uint32_t a_sstep = uint32_t(4) * p.Opad * 2 * 4;
     const uint32_t a_cstep = uint32_t(p.nslab) * a_sstep;  // one coordinate
-    f32x4 av[16];
+    f32x4 av[FILT ? 1 : 16];
+    // In-kernel filter: the 4 x 9 taps of this thread's filters.
+    const i32x4 rw = mfma::buffer_rsrc(p.w, FILT ? p.w_bytes : 0);
+    const int f_o = ptid & 63, f_h = ptid >> 6;
+    const bool f_ook = o0 + f_o < p.O;
+    float wk[FILT ? 36 : 1];
     auto load = [&](int slab) {
-      const uint32_t sa = uint32_t(slab) * a_sstep;
+      if constexpr (FILT == 0) {
+        const uint32_t sa = uint32_t(slab) * a_sstep;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_cstep);
+        for (int q = 0; q < 16; ++q) av[q] = mfma::bload4(ru, a_off, sa + uint32_t(q) * a_cstep);
+      } else {
+        const int c = slab * BK + 4 * f_h;
+        if constexpr (FILT == 1) {
+          // w[g*O + o][c .. c + 3]: 36 contiguous floats (channels past C read
+          // the next row's or nothing and are zeroed in store()).
+          const uint32_t off = f_ook ? uint32_t(((int64_t(g) * p.O + o0 + f_o) * p.C + c) * 36) : kOffNone;
+#pragma unroll
+          for (int i = 0; i < 9; ++i) {
+            const f32x4 v = mfma::bload4(rw, off, uint32_t(i) * 16);
+            wk[4 * i] = v[0], wk[4 * i + 1] = v[1], wk[4 * i + 2] = v[2], wk[4 * i + 3] = v[3];
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t off =
+                (f_ook && c + j < p.C) ? uint32_t(((int64_t(g) * p.C + c + j) * p.O + o0 + f_o) * 36) : kOffNone;
+            const f32x4 v0 = mfma::bload4(rw, off, 0), v1 = mfma::bload4(rw, off, 16);
+            wk[9 * j] = v0[0], wk[9 * j + 1] = v0[1], wk[9 * j + 2] = v0[2], wk[9 * j + 3] = v0[3];
+            wk[9 * j + 4] = v1[0], wk[9 * j + 5] = v1[1], wk[9 * j + 6] = v1[2], wk[9 * j + 7] = v1[3];
+            wk[9 * j + 8] = mfma::bload(rw, off, 32);
+          }
+        }
+      }
     };
+    int f_slab = 0;  // slab whose taps wk holds (for the channel bound)
     auto store = [&](float* As) {
-      float* const a_st = As + a_row * ROW_A + 4 * a_f4;
+      if constexpr (FILT == 0) {
+        float* const a_st = As + a_row * ROW_A + 4 * a_f4;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) *reinterpret_cast<f32x4*>(a_st + q * 4 * ROW_A) = av[q];
+        for (int q = 0; q < 16; ++q) *reinterpret_cast<f32x4*>(a_st + q * 4 * ROW_A) = av[q];
+      } else {
+        const int c = f_slab * BK + 4 * f_h;
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          float u[2][16];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int j = 2 * pr + h;
+            float k[9];
+#pragma unroll
+            for (int e = 0; e < 9; ++e) k[e] = (c + j < p.C) ? wk[9 * j + (FILT == 2 ? 8 - e : e)] : 0.f;
+            fused::filter_math(k, u[h]);
+          }
+          float* const a_st = As + (2 * f_h + pr) * ROW_A + 2 * f_o;
+#pragma unroll
+          for (int t = 0; t < 16; ++t) *reinterpret_cast<f32x2*>(a_st + t * 4 * ROW_A) = f32x2{u[0][t], u[1][t]};
+        }
+      }
     };
     load(0);
+    f_slab = 0;
     store(As0);
     load(1);
     __syncthreads();
     for (int s = 0; s < nslab; s += 2) {
+      f_slab = s + 1;
       store(As1);
       load(min(s + 2, nslab - 1));
       __syncthreads();
       if (s + 2 < nslab) {
+        f_slab = s + 2;
         store(As0);
         load(min(s + 3, nslab - 1));
       }
@@ -1214,16 +1275,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // partials, 7 us of scattered stores).
 constexpr int kResRow = BC * 9;  // floats of one output channel's row in the result tile
 
+// The kernel body for logical block b of group g on caller-provided LDS
+// (the backward kernel runs it beside the input gradient's body).
 template <bool VEC_OUT>
-__global__ __launch_bounds__(512) void wino_dw_ws_kernel(Args p) {
-  __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
-  __shared__ __attribute__((aligned(16))) float Bs0[B_FLOATS];
-  __shared__ __attribute__((aligned(16))) float As1[A_FLOATS];
-  __shared__ __attribute__((aligned(16))) float Bs1[B_FLOATS];
-  __shared__ TileEntry tiles[kChunk];
+__device__ __forceinline__ void dw_ws_body(const Args& p, int b, int g, float* __restrict__ As0,
+                                           float* __restrict__ Bs0, float* __restrict__ As1, float* __restrict__ Bs1,
+                                           TileEntry* __restrict__ tiles) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = blockIdx.y;
-  const int b = mfma::xcd_remap(blockIdx.x, gridDim.x);
   const int nblk = p.n_ob * p.n_cb;
   const int range = b / nblk, ob = (b % nblk) % p.n_ob, cb = (b % nblk) / p.n_ob;
   const int o0 = ob * BO, c0 = cb * BC;
@@ -1352,7 +1410,49 @@ __global__ __launch_bounds__(512) void wino_dw_ws_kernel(Args p) {
   }
 }
 
+template <bool VEC_OUT>
+__global__ __launch_bounds__(512) void wino_dw_ws_kernel(Args p) {
+  __shared__ __attribute__((aligned(16))) float As0[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs0[B_FLOATS];
+  __shared__ __attribute__((aligned(16))) float As1[A_FLOATS];
+  __shared__ __attribute__((aligned(16))) float Bs1[B_FLOATS];
+  __shared__ TileEntry tiles[kChunk];
+  dw_ws_body<VEC_OUT>(p, mfma::xcd_remap(blockIdx.x, gridDim.x), blockIdx.y, As0, Bs0, As1, Bs1, tiles);
+}
+
 }  // namespace fused_dw
+
+// ------------------------------------------------------------ backward kernel
+// The input and weight gradients of one 3x3 stride-1 layer in one launch:
+// workgroups 0 .. n_dw - 1 run the weight gradient's warp-specialized body,
+// the rest the fused kernel's body on dy with the flipped filter (dx).  A
+// dependent launch costs about 3 us on MI355X even when empty, and each of
+// the two launches alone leaves CUs idle at the end (C1: 196 workgroups of
+// each on 256 CUs); together the longer weight-gradient workgroups start
+// first and the input-gradient ones fill the CUs as they free up.  Each body
+// is the one its own kernel runs, so the results are bit-identical to the
+// two separate calls.  LDS: the larger body's stages and tile table (120 KB).
+namespace bwd {
+constexpr int kFwdFloats = 2 * (fused::A_FLOATS + fused::B_FLOATS);
+constexpr int kDwStage = fused_dw::A_FLOATS + fused_dw::B_FLOATS;
+constexpr int kLdsFloats = 2 * kDwStage + fused_dw::kChunk * int(sizeof(fused_dw::TileEntry) / 4);
+static_assert(kFwdFloats <= kLdsFloats, "the input gradient's stages fit the weight gradient's");
+
+template <bool RAGGED, bool VEC_OUT>
+__global__ __launch_bounds__(512) void wino_bwd_kernel(fused::Args pf, fused_dw::Args pw, int n_dw) {
+  __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
+  const int bx = blockIdx.x;
+  if (bx < n_dw) {
+    fused_dw::dw_ws_body<VEC_OUT>(pw, mfma::xcd_remap(bx, n_dw), blockIdx.y, lds, lds + fused_dw::A_FLOATS,
+                                  lds + kDwStage, lds + kDwStage + fused_dw::A_FLOATS,
+                                  reinterpret_cast<fused_dw::TileEntry*>(lds + 2 * kDwStage));
+  } else {
+    const int n_dx = int(gridDim.x) - n_dw;
+    ws::ws_body<RAGGED, 0>(pf, mfma::xcd_remap(bx - n_dw, n_dx), blockIdx.y, lds, lds + fused::A_FLOATS,
+                           lds + fused::A_FLOATS + fused::B_FLOATS, lds + 2 * fused::A_FLOATS + fused::B_FLOATS);
+  }
+}
+}  // namespace bwd
 
 int winograd_unfused(const mx_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
                      bool flip, int64_t chunk, hipStream_t s);
@@ -1498,12 +1598,13 @@ int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
     r->chunk = (d.n + passes - 1) / passes;
     r->unfused_bytes = u_plain + per_image * r->chunk;
   }
-  // With at most 4 slabs the producers transform the filter themselves: the
-  // separate filter launch then costs more than its work (20 -> 24 channels
-  // at 9x11, batch 4: 12.0 -> 9.5 us); on longer walks every workgroup
-  // redoing the transform costs more than the launch (C1's layer 18.2 ->
-  // 19.0 us, 512 channels 90 -> 123 us).  MX_WINOGRAD_FILTER=0 / 1 forces the
-  // filter launch / the in-kernel transform (tests, tuning).
+  // With at most 4 slabs the producers transform the filter themselves: a
+  // dependent launch costs about 3 us on MI355X even when empty, more than
+  // the filter's work (20 -> 24 channels at 9x11, batch 4: 8.8 -> 6.8 us); on
+  // longer walks every workgroup redoing the transform costs more than the
+  // launch (C1's layer 18.3 -> 19.3 us, 64 x 56^2 80.6 -> 105.4).
+  // MX_WINOGRAD_FILTER=0 / 1 forces the filter launch / the in-kernel
+  // transform (tests, tuning).
   r->filt = p.nslab <= 4;
   if (const char* e = std::getenv("MX_WINOGRAD_FILTER"))
     if (e[0] == '0' || e[0] == '1') r->filt = e[0] == '1';
@@ -1517,7 +1618,7 @@ int plan_run(const mx_conv2d_desc& d, int64_t ws_limit, RunPlan* r) {
   r->t16 = int64_t(p.Cpad) * p.Opad <= 256 * 256;
   if (const char* e = std::getenv("MX_WINOGRAD_T16"))
     if (e[0] == '0' || e[0] == '1') r->t16 = e[0] == '1';
-  r->t16 = r->t16 && r->fused && !r->filt;
+  r->t16 = r->t16 && r->fused;
   if (r->filt) {
     p.w_bytes = int64_t(d.cout) * p.C * 9 * 4;
     MX_REQUIRE(p.w_bytes < mfma::kBufMaxBytes, MX_ERR_UNSUPPORTED, "winograd: the filter exceeds 2 GiB");
@@ -1539,6 +1640,15 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   p.y = y;
   const dim3 grid{unsigned(r.blocks), unsigned(r.G), 1u};
   const bool ragged = p.C % (2 * fused::BK) != 0;
+  if (r.filt && r.t16) {
+    p.w = w;
+    const dim3 grid16{unsigned((int64_t(p.T) + ws::BT16 - 1) / ws::BT16 * p.n_ob), unsigned(r.G), 1u};
+    void (*k16)(fused::Args) = flip ? (ragged ? ws::wino_ws16_kernel<true, 2> : ws::wino_ws16_kernel<false, 2>)
+                                    : (ragged ? ws::wino_ws16_kernel<true, 1> : ws::wino_ws16_kernel<false, 1>);
+    hipLaunchKernelGGL(k16, grid16, dim3(512), 0, s, p);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+  }
   if (r.filt) {
     p.w = w;
     void (*kern)(fused::Args) = flip ? (ragged ? ws::wino_ws_kernel<true, 2> : ws::wino_ws_kernel<false, 2>)
@@ -1558,7 +1668,7 @@ int winograd_run(const mx_conv2d_desc& d, const float* x, const float* w, const 
   MX_HIP(hipGetLastError());
   if (r.t16) {
     const dim3 grid16{unsigned((int64_t(p.T) + ws::BT16 - 1) / ws::BT16 * p.n_ob), unsigned(r.G), 1u};
-    void (*k16)(fused::Args) = ragged ? ws::wino_ws16_kernel<true> : ws::wino_ws16_kernel<false>;
+    void (*k16)(fused::Args) = ragged ? ws::wino_ws16_kernel<true, 0> : ws::wino_ws16_kernel<false, 0>;
     hipLaunchKernelGGL(k16, grid16, dim3(512), 0, s, p);
     MX_HIP(hipGetLastError());
     return MX_OK;
@@ -1737,6 +1847,74 @@ int winograd_describe(const mx_conv2d_desc& d, int phase, bool with_bias, int64_
 int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const float* w, float* dx, int64_t ws_limit,
                             hipStream_t s) {
   return winograd_run(dinput_as_forward(d), dy, w, nullptr, dx, true, ws_limit, s);
+}
+
+// dx, dw and db of the 3x3 stride-1 layer d in one backward launch (after
+// the flipped filter transform, before the weight gradient's range sum) when
+// both gradients take the fused Winograd paths: the input gradient the fused
+// kernel with U' from the filter launch, the weight gradient the
+// warp-specialized kernel.  *done = false (nothing launched) otherwise; the
+// caller then runs the two gradients one after the other.
+int winograd_backward(const mx_conv2d_desc& d, const float* x, const float* w, const float* dy, float* dx, float* dw,
+                      float* db, int64_t ws_limit, hipStream_t s, bool* done) {
+  *done = false;
+  if (d.ph > 2 || d.pw > 2) return MX_OK;
+  const mx_conv2d_desc t = dinput_as_forward(d);
+  RunPlan rf;
+  MX_TRY(plan_run(t, ws_limit, &rf));
+  DwRunPlan rw;
+  MX_TRY(plan_dw_run(d, ws_limit, db != nullptr, &rw));
+  if (!rf.fused || rf.filt || !rw.ws || rf.p.T == 0 || rw.p.T == 0) return MX_OK;
+  // One launch pays where the input gradient alone fits the CUs once with a
+  // short channel walk (the launch overhead and the idle CUs of two short
+  // launches then dominate): C1's layer 45.3 -> 40.1 us, 33 -> 40 channels at
+  // 17x15 20.3 -> 16.6.  Longer walks lose the 16-tile input-gradient
+  // kernel's two workgroups per CU (256 x 16^2, batch 16: 68.4 -> 82.1;
+  // 64 x 56^2, batch 64: 172 -> 185).  MX_WINOGRAD_BWD=0 / 1 forces the two
+  // launches / the one launch (where it applies).
+  bool one = rf.p.nslab <= 16 && rf.blocks * rf.G <= cu_count();
+  if (const char* e = std::getenv("MX_WINOGRAD_BWD"))
+    if (e[0] == '0' || e[0] == '1') one = e[0] == '1';
+  if (!one) return MX_OK;
+  // Input gradient: the fused kernel's arguments as winograd_run sets them.
+  fused::Args& pf = rf.p;
+  pf.bias = nullptr;
+  pf.x = dy;
+  pf.y = dx;
+  Scratch U;
+  MX_TRY(U.alloc(size_t(pf.u_bytes), s));
+  pf.U = U.as<float>();
+  const int64_t filter_threads = int64_t(rf.G) * (pf.Cpad / 2) * pf.Opad;
+  hipLaunchKernelGGL(fused::filter_kernel, dim3(unsigned(std::min<int64_t>((filter_threads + 63) / 64, 1 << 20))),
+                     dim3(64), 0, s, w, U.as<float>(), pf.C, pf.O, pf.Cpad, pf.Opad, rf.G, true);
+  MX_HIP(hipGetLastError());
+  // Weight gradient: as winograd_backward_weight sets it.
+  fused_dw::Args& pw = rw.p;
+  pw.x = x;
+  pw.dy = dy;
+  Scratch ws;
+  float* partials = nullptr;
+  if (rw.ranges > 1) {
+    MX_TRY(ws.alloc(size_t(rw.ranges) * size_t(rw.n_dw + rw.n_db) * 4, s));
+    partials = ws.as<float>();
+  }
+  float* const partials_db = rw.ranges > 1 ? partials + rw.ranges * rw.n_dw : nullptr;
+  pw.out = rw.ranges > 1 ? partials : dw;
+  pw.out_db = db ? (rw.ranges > 1 ? partials_db : db) : nullptr;
+  const bool vec_out =
+      pw.O % fused_dw::BO == 0 && pw.C % fused_dw::BC == 0 && (reinterpret_cast<uintptr_t>(pw.out) & 15) == 0;
+  const bool ragged = pf.C % (2 * fused::BK) != 0;
+  const int64_t n_dw = rw.blocks / rw.G * rw.ranges, n_dx = rf.blocks;
+  MX_REQUIRE(n_dw + n_dx <= INT32_MAX && rf.G == rw.G, MX_ERR_UNSUPPORTED, "winograd backward: grid too large");
+  void (*kern)(fused::Args, fused_dw::Args, int) =
+      ragged ? (vec_out ? bwd::wino_bwd_kernel<true, true> : bwd::wino_bwd_kernel<true, false>)
+             : (vec_out ? bwd::wino_bwd_kernel<false, true> : bwd::wino_bwd_kernel<false, false>);
+  hipLaunchKernelGGL(kern, dim3(unsigned(n_dw + n_dx), unsigned(rw.G)), dim3(512), 0, s, pf, pw, int(n_dw));
+  MX_HIP(hipGetLastError());
+  *done = true;
+  if (rw.ranges > 1)
+    return conv::sum_partials(partials, partials_db, int(rw.ranges), rw.n_dw, int(rw.n_db), dw, db, s);
+  return MX_OK;
 }
 
 }  // namespace mx

@@ -150,6 +150,10 @@ at::Tensor convolution_overrideable(const at::Tensor& input, const at::Tensor& w
   return y;
 }
 
+std::tuple<at::Tensor, at::Tensor, at::Tensor> backward_phases(const mx_conv2d_desc& d, const at::Tensor& dy,
+                                                               const at::Tensor& input, const at::Tensor& weight,
+                                                               std::array<bool, 3> output_mask, int ax, int aw);
+
 std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable(
     const at::Tensor& grad_output, const at::Tensor& input, const at::Tensor& weight, at::IntArrayRef stride,
     at::IntArrayRef padding, at::IntArrayRef dilation, bool transposed, at::IntArrayRef output_padding,
@@ -170,10 +174,43 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   const at::Tensor dy = packed(grad_output);
   at::Tensor dx, dw, db;
   auto opts = input.options().memory_format(at::MemoryFormat::Contiguous);
+  if (output_mask[0] && output_mask[1]) {
+    // Both gradients in one library call (convolution_backward's dispatch of
+    // Input, Weight and Bias, csrc/ops/convolution.cpp:667-697): where both
+    // take the fused Winograd paths the library runs them as one launch.
+    const int ax = choose(d, MX_CONV_DINPUT, backward_algo(d, MX_CONV_DINPUT));
+    const int aw = choose(d, MX_CONV_DWEIGHT, backward_algo(d, MX_CONV_DWEIGHT));
+    if (ax == MX_CONV_ALGO_WINOGRAD && aw == MX_CONV_ALGO_WINOGRAD) {
+      dx = at::empty(input.sizes(), opts);
+      dw = at::empty(weight.sizes(), weight.options().memory_format(at::MemoryFormat::Contiguous));
+      if (output_mask[2]) {
+        db = at::empty({d.cout}, weight.options());
+        count_selection("selected_dbias_fused_dweight");
+      }
+      const at::Tensor x = packed(input), w = packed(weight);
+      GpuTimer timer(kernel_label(d, MX_CONV_DWEIGHT, aw));
+      TVK_MX(mx_conv2d_backward(&d, x.data_ptr<float>(), w.data_ptr<float>(), dy.data_ptr<float>(),
+                                dx.data_ptr<float>(), dw.data_ptr<float>(), db.defined() ? db.data_ptr<float>() : nullptr,
+                                ax, aw, current_stream()));
+      counters().kernel_launches++;
+      return {dx, dw, db};
+    }
+    return backward_phases(d, dy, input, weight, output_mask, ax, aw);
+  }
+  return backward_phases(d, dy, input, weight, output_mask, -1, -1);
+}
+
+// The requested gradients one library call each.  ax / aw: algorithms
+// already chosen (and counted) for dInput / dWeight, or -1.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> backward_phases(const mx_conv2d_desc& d, const at::Tensor& dy,
+                                                               const at::Tensor& input, const at::Tensor& weight,
+                                                               std::array<bool, 3> output_mask, int ax, int aw) {
+  at::Tensor dx, dw, db;
+  auto opts = input.options().memory_format(at::MemoryFormat::Contiguous);
   if (output_mask[0]) {
     dx = at::empty(input.sizes(), opts);
     const at::Tensor w = packed(weight);
-    const int algo = choose(d, MX_CONV_DINPUT, backward_algo(d, MX_CONV_DINPUT));
+    const int algo = ax >= 0 ? ax : choose(d, MX_CONV_DINPUT, backward_algo(d, MX_CONV_DINPUT));
     GpuTimer timer(kernel_label(d, MX_CONV_DINPUT, algo));
     TVK_MX(mx_conv2d_backward_input(&d, dy.data_ptr<float>(), w.data_ptr<float>(), dx.data_ptr<float>(), algo,
                                     current_stream()));
@@ -183,7 +220,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
   if (output_mask[1]) {
     dw = at::empty(weight.sizes(), weight.options().memory_format(at::MemoryFormat::Contiguous));
     const at::Tensor x = packed(input);
-    const int algo = choose(d, MX_CONV_DWEIGHT, backward_algo(d, MX_CONV_DWEIGHT));
+    const int algo = aw >= 0 ? aw : choose(d, MX_CONV_DWEIGHT, backward_algo(d, MX_CONV_DWEIGHT));
     // dBias rides on the dWeight launch when both are requested.
     float* dbp = nullptr;
     if (output_mask[2]) {

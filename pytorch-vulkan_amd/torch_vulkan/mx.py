@@ -35,7 +35,7 @@ EXPORTS = [
     "mx_record_stream", "mx_empty_cache", "mx_memory_stats_get", "mx_memcpy", "mx_host_is_pinned",
     "mx_memcpy_async", "mx_host_malloc", "mx_host_free", "mx_fill", "mx_copy_strided",
     "mx_add_f32", "mx_scale_f32", "mx_mul_f32", "mx_sum_f32", "mx_foreach_add_scalar_f32", "mx_conv2d_check",
-    "mx_conv2d_select", "mx_conv2d_forward", "mx_conv2d_backward_input", "mx_conv2d_backward_weight",
+    "mx_conv2d_select", "mx_conv2d_forward", "mx_conv2d_backward_input", "mx_conv2d_backward_weight", "mx_conv2d_backward",
     "mx_conv2d_backward_bias", "mx_conv2d_dweight_plan", "mx_conv2d_kernel_name", "mx_gemm_f32", "mx_adamw_step",
     "mx_group_norm_forward", "mx_group_norm_backward", "mx_batch_norm_forward", "mx_batch_norm_backward",
     "mx_unary_f32", "mx_unary_backward_f32", "mx_upsample_nearest2d", "mx_upsample_nearest2d_backward",
@@ -144,6 +144,7 @@ def lib() -> C.CDLL:
             "mx_conv2d_forward": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
             "mx_conv2d_backward_input": ([C.POINTER(ConvDesc), vp, vp, vp, i32, vp], i32),
             "mx_conv2d_backward_weight": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
+            "mx_conv2d_backward": ([C.POINTER(ConvDesc), vp, vp, vp, vp, vp, vp, i32, i32, vp], i32),
             "mx_conv2d_backward_weight_noalloc": ([C.POINTER(ConvDesc), vp, vp, vp, vp, i32, vp], i32),
             "mx_conv2d_backward_bias": ([C.POINTER(ConvDesc), vp, vp, vp], i32),
             "mx_conv2d_dweight_plan": ([C.POINTER(ConvDesc), C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)], i32),
@@ -202,6 +203,11 @@ def conv2d_forward(d: ConvDesc, x, w, b, y, algo=ALGO_AUTO, stream=None) -> None
 
 def conv2d_backward_input(d: ConvDesc, dy, w, dx, algo=ALGO_AUTO, stream=None) -> None:
     check(lib().mx_conv2d_backward_input(C.byref(d), ptr(dy), ptr(w), ptr(dx), algo, stream))
+
+
+def conv2d_backward(d: ConvDesc, x, w, dy, dx, dw, db, algo_dx=ALGO_AUTO, algo_dw=ALGO_AUTO, stream=None) -> None:
+    check(lib().mx_conv2d_backward(C.byref(d), ptr(x), ptr(w), ptr(dy), ptr(dx), ptr(dw), ptr(db), algo_dx, algo_dw,
+                                   stream))
 
 
 def conv2d_backward_weight(d: ConvDesc, x, dy, dw, db, algo=ALGO_AUTO, stream=None) -> None:
