@@ -1438,7 +1438,7 @@ constexpr int kDwStage = fused_dw::A_FLOATS + fused_dw::B_FLOATS;
 constexpr int kLdsFloats = 2 * kDwStage + fused_dw::kChunk * int(sizeof(fused_dw::TileEntry) / 4);
 static_assert(kFwdFloats <= kLdsFloats, "the input gradient's stages fit the weight gradient's");
 
-template <bool RAGGED, bool VEC_OUT>
+template <bool RAGGED, bool VEC_OUT, int FILT>
 __global__ __launch_bounds__(512) void wino_bwd_kernel(fused::Args pf, fused_dw::Args pw, int n_dw) {
   __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
   const int bx = blockIdx.x;
@@ -1448,7 +1448,7 @@ __global__ __launch_bounds__(512) void wino_bwd_kernel(fused::Args pf, fused_dw:
                                   reinterpret_cast<fused_dw::TileEntry*>(lds + 2 * kDwStage));
   } else {
     const int n_dx = int(gridDim.x) - n_dw;
-    ws::ws_body<RAGGED, 0>(pf, mfma::xcd_remap(bx - n_dw, n_dx), blockIdx.y, lds, lds + fused::A_FLOATS,
+    ws::ws_body<RAGGED, FILT>(pf, mfma::xcd_remap(bx - n_dw, n_dx), blockIdx.y, lds, lds + fused::A_FLOATS,
                            lds + fused::A_FLOATS + fused::B_FLOATS, lds + 2 * fused::A_FLOATS + fused::B_FLOATS);
   }
 }
@@ -1864,15 +1864,19 @@ int winograd_backward(const mx_conv2d_desc& d, const float* x, const float* w, c
   MX_TRY(plan_run(t, ws_limit, &rf));
   DwRunPlan rw;
   MX_TRY(plan_dw_run(d, ws_limit, db != nullptr, &rw));
-  if (!rf.fused || rf.filt || !rw.ws || rf.p.T == 0 || rw.p.T == 0) return MX_OK;
-  // One launch pays where the input gradient alone fits the CUs once with a
-  // short channel walk (the launch overhead and the idle CUs of two short
-  // launches then dominate): C1's layer 45.3 -> 40.1 us, 33 -> 40 channels at
-  // 17x15 20.3 -> 16.6.  Longer walks lose the 16-tile input-gradient
-  // kernel's two workgroups per CU (256 x 16^2, batch 16: 68.4 -> 82.1;
-  // 64 x 56^2, batch 64: 172 -> 185).  MX_WINOGRAD_BWD=0 / 1 forces the two
-  // launches / the one launch (where it applies).
-  bool one = rf.p.nslab <= 16 && rf.blocks * rf.G <= cu_count();
+  if (!rf.fused || !rw.ws || rf.p.T == 0 || rw.p.T == 0) return MX_OK;
+  // One launch pays for tiny layers, where launch overhead dominates (33 ->
+  // 40 channels at 17x15: 20.2 -> 15.4 us), and where two launches of short
+  // walks (<= 8 slabs) would each leave CUs idle but together fill them at
+  // least one and a half times over, with the input gradient alone fitting
+  // the CUs once (C1's layer: 196 + 196 workgroups, 45.1 -> 39.6 us).
+  // Otherwise the 16-tile input-gradient kernel's two workgroups per CU win
+  // (64 x 28^2, batch 16: 33.3 vs 34.1; 128 x 28^2, batch 8: 46.3 vs 48.7;
+  // 256 x 16^2, batch 16: 68.9 vs 82.0).  MX_WINOGRAD_BWD=0 / 1 forces the
+  // two launches / the one launch.
+  const int64_t cus = cu_count(), n_dx32 = rf.blocks * rf.G, n_dw_all = rw.blocks * rw.ranges;
+  bool one = 4 * (n_dx32 + n_dw_all) <= cus ||
+             (rf.p.nslab <= 8 && n_dx32 <= cus && 2 * (n_dx32 + n_dw_all) >= 3 * cus);
   if (const char* e = std::getenv("MX_WINOGRAD_BWD"))
     if (e[0] == '0' || e[0] == '1') one = e[0] == '1';
   if (!one) return MX_OK;
@@ -1881,13 +1885,25 @@ int winograd_backward(const mx_conv2d_desc& d, const float* x, const float* w, c
   pf.bias = nullptr;
   pf.x = dy;
   pf.y = dx;
+  // With walks of <= 8 slabs the input-gradient workgroups transform the
+  // flipped filter themselves, saving the filter launch (C1 40.1 -> 39.6 us;
+  // 512 channels 201 -> 218, so not on long walks).  MX_WINOGRAD_FILTER=0 /
+  // 1 forces the filter launch / the in-kernel transform.
+  bool in_filt = rf.p.nslab <= 8;
+  if (const char* e = std::getenv("MX_WINOGRAD_FILTER"))
+    if (e[0] == '0' || e[0] == '1') in_filt = e[0] == '1';
   Scratch U;
-  MX_TRY(U.alloc(size_t(pf.u_bytes), s));
-  pf.U = U.as<float>();
-  const int64_t filter_threads = int64_t(rf.G) * (pf.Cpad / 2) * pf.Opad;
-  hipLaunchKernelGGL(fused::filter_kernel, dim3(unsigned(std::min<int64_t>((filter_threads + 63) / 64, 1 << 20))),
-                     dim3(64), 0, s, w, U.as<float>(), pf.C, pf.O, pf.Cpad, pf.Opad, rf.G, true);
-  MX_HIP(hipGetLastError());
+  if (in_filt) {
+    pf.w = w;
+    pf.w_bytes = int64_t(d.cout) * (d.cin / d.groups) * 9 * 4;
+  } else {
+    MX_TRY(U.alloc(size_t(pf.u_bytes), s));
+    pf.U = U.as<float>();
+    const int64_t filter_threads = int64_t(rf.G) * (pf.Cpad / 2) * pf.Opad;
+    hipLaunchKernelGGL(fused::filter_kernel, dim3(unsigned(std::min<int64_t>((filter_threads + 63) / 64, 1 << 20))),
+                       dim3(64), 0, s, w, U.as<float>(), pf.C, pf.O, pf.Cpad, pf.Opad, rf.G, true);
+    MX_HIP(hipGetLastError());
+  }
   // Weight gradient: as winograd_backward_weight sets it.
   fused_dw::Args& pw = rw.p;
   pw.x = x;
@@ -1907,8 +1923,10 @@ int winograd_backward(const mx_conv2d_desc& d, const float* x, const float* w, c
   const int64_t n_dw = rw.blocks / rw.G * rw.ranges, n_dx = rf.blocks;
   MX_REQUIRE(n_dw + n_dx <= INT32_MAX && rf.G == rw.G, MX_ERR_UNSUPPORTED, "winograd backward: grid too large");
   void (*kern)(fused::Args, fused_dw::Args, int) =
-      ragged ? (vec_out ? bwd::wino_bwd_kernel<true, true> : bwd::wino_bwd_kernel<true, false>)
-             : (vec_out ? bwd::wino_bwd_kernel<false, true> : bwd::wino_bwd_kernel<false, false>);
+      in_filt ? (ragged ? (vec_out ? bwd::wino_bwd_kernel<true, true, 2> : bwd::wino_bwd_kernel<true, false, 2>)
+                        : (vec_out ? bwd::wino_bwd_kernel<false, true, 2> : bwd::wino_bwd_kernel<false, false, 2>))
+              : (ragged ? (vec_out ? bwd::wino_bwd_kernel<true, true, 0> : bwd::wino_bwd_kernel<true, false, 0>)
+                        : (vec_out ? bwd::wino_bwd_kernel<false, true, 0> : bwd::wino_bwd_kernel<false, false, 0>));
   hipLaunchKernelGGL(kern, dim3(unsigned(n_dw + n_dx), unsigned(rw.G)), dim3(512), 0, s, pf, pw, int(n_dw));
   MX_HIP(hipGetLastError());
   *done = true;

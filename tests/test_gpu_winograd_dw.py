@@ -72,16 +72,20 @@ def test_winograd_dweight_ranges(mx, case):
 # Winograd gradients where its rule picks it (C1's layer, small layers) or
 # where MX_WINOGRAD_BWD=1 forces it, the two calls otherwise; bit-identical to
 # mx_conv2d_backward_input + mx_conv2d_backward_weight in every case.
-BWD_CASES = [((8, 64, 56, 56), 64, (1, 1), "auto"), ((3, 33, 17, 15), 40, (1, 1), "auto"),
-             ((4, 128, 14, 14), 128, (1, 1), "1"), ((2, 64, 16, 16), 128, (0, 0), "1"),
-             ((2, 40, 12, 12), 48, (2, 2), "1"), ((2, 64, 16, 16), 64, (1, 1), "0")]
+# x shape, output channels, padding, MX_WINOGRAD_BWD, MX_WINOGRAD_FILTER
+BWD_CASES = [((8, 64, 56, 56), 64, (1, 1), "auto", "auto"), ((8, 64, 56, 56), 64, (1, 1), "1", "0"),
+             ((3, 33, 17, 15), 40, (1, 1), "auto", "auto"), ((4, 128, 14, 14), 128, (1, 1), "1", "auto"),
+             ((2, 64, 16, 16), 128, (0, 0), "1", "1"), ((2, 40, 12, 12), 48, (2, 2), "1", "auto"),
+             ((2, 64, 16, 16), 64, (1, 1), "0", "auto")]
 
 
 @pytest.mark.parametrize("case", BWD_CASES, ids=[f"b{i}" for i in range(len(BWD_CASES))])
 def test_combined_backward_matches_separate_calls(mx, case, monkeypatch):
-    xs, cout, pad, mode = case
+    xs, cout, pad, mode, filt = case
     if mode != "auto":
         monkeypatch.setenv("MX_WINOGRAD_BWD", mode)
+    if filt != "auto":
+        monkeypatch.setenv("MX_WINOGRAD_FILTER", filt)
     g = torch.Generator().manual_seed(sum(xs) + cout + pad[0])
     x = torch.randn(xs, generator=g)
     w = torch.randn(cout, xs[1], 3, 3, generator=g) / math.sqrt(9 * xs[1])
