@@ -6,10 +6,12 @@
 // csrc/ops/multitensor_plan.h:22-48): one persistent launch walks a device
 // table of every tensor in 4096-element chunks dealt round-robin to the
 // workgroups.  Where the four (five) streams are 16-byte aligned a thread issues
-// all 16 (20) of its 128-bit loads for a chunk before any arithmetic -- the
-// kernel is HBM-bound, so bytes in flight per CU set its speed -- and every
-// access is non-temporal (each byte is touched once per step).  There is no 8-tensor or 65,535-workgroup cap; a new launch starts
-// only where an entry writes memory an earlier entry of the same launch uses
+// all 16 (20) of its 128-bit loads for a chunk before any arithmetic, and the
+// next chunk's loads before this chunk's stores -- the kernel is HBM-bound,
+// so bytes in flight per CU set its speed -- and every access is
+// non-temporal (each byte is touched once per step).  There is no 8-tensor
+// or 65,535-workgroup cap; a new launch starts only where an entry writes
+// memory an earlier entry of the same launch uses
 // (the reference's alias-conflict predicate, csrc/ops/adamw.cpp:207-215).
 //
 // Per-element arithmetic follows torch.optim.AdamW's single-tensor update
@@ -119,68 +121,106 @@ __device__ __forceinline__ void update(float& p, float g, float& m, float& v, fl
   p = p + (c.nss * m) / denom;
 }
 
+// Loads of one full vector chunk: element base + u * 1024 + (0..3), each
+// load instruction 4 KiB contiguous per wave.
+struct ChunkRegs {
+  f32x4 p[kVec], g[kVec], m[kVec], v[kVec], x[kVec];
+};
+
+template <bool AMS>
+__device__ __forceinline__ void load_chunk(ChunkRegs& r, const AdamEntry& e, int64_t base) {
+#pragma unroll
+  for (int u = 0; u < kVec; ++u) {
+    const int64_t i = base + u * 1024;
+    r.p[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.p + i));
+    r.g[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.g + i));
+    r.m[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.m + i));
+    r.v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.v + i));
+    if constexpr (AMS) r.x[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.vmax + i));
+  }
+}
+
 template <bool AMS>
 __global__ __launch_bounds__(256) void adamw_kernel(const AdamEntry* __restrict__ tab, AdamHP hp) {
   if (hp.found_inf && *hp.found_inf != 0.f) return;
   const float scale = hp.grad_scale ? *hp.grad_scale : 1.f;
+  const int64_t total = hp.total_chunks, stride = gridDim.x;
   // Chunks are dealt round-robin (chunk = blockIdx.x + i * gridDim.x), so the
-  // workgroups in flight stream through neighbouring memory; each finds its
-  // tensor by binary search over the table's chunk offsets.
+  // workgroups in flight stream through neighbouring memory; each finds a
+  // chunk's tensor by binary search over the table's chunk offsets (kept
+  // when the next chunk is in the same tensor).
+  auto locate = [&](int64_t ch, AdamEntry& e, int64_t& e_end, Coef& c) {
+    if (ch < e_end && ch >= e.chunk_begin) return;
+    int lo = 0, hi = hp.ntens - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tab[mid].chunk_begin <= ch) lo = mid;
+      else hi = mid - 1;
+    }
+    e = tab[lo];
+    e_end = e.chunk_begin + (e.numel + kChunk - 1) / kChunk;
+    c = coefficients(e, hp);
+  };
+  auto chunk_base = [&](const AdamEntry& e, int64_t ch) {
+    return (ch - e.chunk_begin) * kChunk + int64_t(threadIdx.x) * 4;
+  };
+  auto vector_ok = [&](const AdamEntry& e, int64_t base) { return e.vec && base + (kVec - 1) * 1024 + 3 < e.numel; };
+  int64_t ch = blockIdx.x;
+  if (ch >= total) return;
   AdamEntry e = tab[0];
   int64_t e_end = (e.numel + kChunk - 1) / kChunk;
   Coef c = coefficients(e, hp);
-  for (int64_t ch = blockIdx.x; ch < hp.total_chunks; ch += gridDim.x) {
-    if (ch >= e_end || ch < e.chunk_begin) {
-      int lo = 0, hi = hp.ntens - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tab[mid].chunk_begin <= ch) lo = mid;
-        else hi = mid - 1;
-      }
-      e = tab[lo];
-      e_end = e.chunk_begin + (e.numel + kChunk - 1) / kChunk;
-      c = coefficients(e, hp);
-    }
-    const int64_t base = (ch - e.chunk_begin) * kChunk + int64_t(threadIdx.x) * 4;
-    if (e.vec && base + (kVec - 1) * 1024 + 3 < e.numel) {
-      // Element base + u * 1024 + (0..3): each load instruction covers 4 KiB
-      // contiguous per wave.
-      f32x4 p4[kVec], g4[kVec], m4[kVec], v4[kVec], x4[kVec];
-#pragma unroll
-      for (int u = 0; u < kVec; ++u) {
-        const int64_t i = base + u * 1024;
-        p4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.p + i));
-        g4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.g + i));
-        m4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.m + i));
-        v4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.v + i));
-        if constexpr (AMS) x4[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(e.vmax + i));
-      }
+  locate(ch, e, e_end, c);
+  int64_t base = chunk_base(e, ch);
+  bool full = vector_ok(e, base);
+  // A full chunk's loads are issued one chunk ahead: the next chunk's (of
+  // whatever tensor) go out after this chunk's arithmetic and before its
+  // stores, so they are in flight while the stores drain.  Entries of one
+  // launch never share memory (the host splits launches where they would),
+  // so the early loads cannot read what the pending stores write.
+  ChunkRegs r;
+  if (full) load_chunk<AMS>(r, e, base);
+  for (; ch < total; ch += stride) {
+    const int64_t nch = ch + stride;
+    if (full) {
+      // The unscaled gradient goes out first: only the new p, m, v (and
+      // vmax) stay live across the next chunk's loads.
       if (hp.grad_scale) {
 #pragma unroll
         for (int u = 0; u < kVec; ++u) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) g4[u][j] = g4[u][j] / scale;
-          __builtin_nontemporal_store(g4[u], reinterpret_cast<f32x4*>(e.g + base + u * 1024));
+          for (int j = 0; j < 4; ++j) r.g[u][j] = r.g[u][j] / scale;
+          __builtin_nontemporal_store(r.g[u], reinterpret_cast<f32x4*>(e.g + base + u * 1024));
         }
       }
-#pragma unroll
-      for (int u = 0; u < kVec; ++u)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float pp = p4[u][j], mm = m4[u][j], vv = v4[u][j], xx = AMS ? x4[u][j] : 0.f;
-          update<AMS>(pp, g4[u][j], mm, vv, &xx, c, hp);
-          p4[u][j] = pp;
-          m4[u][j] = mm;
-          v4[u][j] = vv;
-          if constexpr (AMS) x4[u][j] = xx;
-        }
+      f32x4 np[kVec], nm[kVec], nv[kVec], nx[kVec];
 #pragma unroll
       for (int u = 0; u < kVec; ++u) {
-        const int64_t i = base + u * 1024;
-        __builtin_nontemporal_store(p4[u], reinterpret_cast<f32x4*>(e.p + i));
-        __builtin_nontemporal_store(m4[u], reinterpret_cast<f32x4*>(e.m + i));
-        __builtin_nontemporal_store(v4[u], reinterpret_cast<f32x4*>(e.v + i));
-        if constexpr (AMS) __builtin_nontemporal_store(x4[u], reinterpret_cast<f32x4*>(e.vmax + i));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float pp = r.p[u][j], mm = r.m[u][j], vv = r.v[u][j], xx = AMS ? r.x[u][j] : 0.f;
+          update<AMS>(pp, r.g[u][j], mm, vv, &xx, c, hp);
+          np[u][j] = pp;
+          nm[u][j] = mm;
+          nv[u][j] = vv;
+          if constexpr (AMS) nx[u][j] = xx;
+        }
+      }
+      const AdamEntry ce = e;
+      const int64_t cbase = base;
+      if (nch < total) {
+        locate(nch, e, e_end, c);
+        base = chunk_base(e, nch);
+        full = vector_ok(e, base);
+        if (full) load_chunk<AMS>(r, e, base);
+      }
+#pragma unroll
+      for (int u = 0; u < kVec; ++u) {
+        const int64_t i = cbase + u * 1024;
+        __builtin_nontemporal_store(np[u], reinterpret_cast<f32x4*>(ce.p + i));
+        __builtin_nontemporal_store(nm[u], reinterpret_cast<f32x4*>(ce.m + i));
+        __builtin_nontemporal_store(nv[u], reinterpret_cast<f32x4*>(ce.v + i));
+        if constexpr (AMS) __builtin_nontemporal_store(nx[u], reinterpret_cast<f32x4*>(ce.vmax + i));
       }
     } else {
       // A tensor's last (partial) chunk, or unaligned streams: element loads,
@@ -218,6 +258,12 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamEntry* __restrict_
             if constexpr (AMS) e.vmax[i] = xx[j];
           }
         }
+      }
+      if (nch < total) {
+        locate(nch, e, e_end, c);
+        base = chunk_base(e, nch);
+        full = vector_ok(e, base);
+        if (full) load_chunk<AMS>(r, e, base);
       }
     }
   }
