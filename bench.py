@@ -385,8 +385,9 @@ def run_streams(torch, reps=5):
 
 def run_stream_probes(torch, numel, reps=20):
     """The AdamW access pattern with trivial arithmetic (4 reads + 3 writes per
-    element, in place), a plain copy and a 4-stream read sweep over buffers of
-    C5's size, from libmxprobe.so; GB/s from HIP events on the current stream."""
+    element, in place), the same pattern with AdamW's per-element update, a
+    plain copy and a 4-stream read sweep over buffers of C5's size, from
+    libmxprobe.so; GB/s from HIP events on the current stream."""
     import ctypes as C
     lib = C.CDLL(os.path.join(REPO, "pytorch-vulkan_amd", "torch_vulkan", "libmxprobe.so"))
     lib.mxp_stream.argtypes = [C.c_int, C.POINTER(C.c_void_p), C.c_int64, C.c_int, C.c_void_p]
@@ -396,7 +397,8 @@ def run_stream_probes(torch, numel, reps=20):
     ptrs = (C.c_void_p * 5)(*[b.data_ptr() for b in bufs])
     st = torch.cuda.current_stream()
     out = {}
-    for name, kind, bpe in (("adamw_mix_4r3w", 2, 28), ("copy", 0, 8), ("read_4_streams", 1, 16)):
+    for name, kind, bpe in (("adamw_mix_4r3w", 2, 28), ("adamw_math_4r3w", 3, 28), ("copy", 0, 8),
+                            ("read_4_streams", 1, 16)):
         for _ in range(3):
             assert lib.mxp_stream(kind, ptrs, n, 32, st.cuda_stream) == 0
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -999,6 +1001,7 @@ def main(argv=None):
                               "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
                               "stream_probes_gb_s": ceiling,
                               "frac_of_4r3w_probe": round(gbs / ceiling["adamw_mix_4r3w"], 4),
+                              "frac_of_4r3w_math_probe": round(gbs / ceiling["adamw_math_4r3w"], 4),
                               "roofline": roof, "kernels": breakdown(agg_c)}
             else:
                 desc = {"c1": "C1: Conv2D 8x64x56x56 3x3 fwd+dX+dW+dB; every phase on Winograd F(2x2,3x3) "

@@ -10,6 +10,10 @@
 //   kind 1  read:       sum of bufs[0..3][i], one value per workgroup (4 reads)
 //   kind 2  AdamW mix:  bufs[0], bufs[2], bufs[3] updated in place from
 //                       themselves and bufs[1]                        (4 reads, 3 writes)
+//   kind 3  AdamW math: kind 2's streams with AdamW's per-element update
+//                       (two divisions and a square root, fixed
+//                       hyperparameters), next chunk's loads issued before
+//                       this chunk's stores                           (4 reads, 3 writes)
 //
 // n must be a multiple of 4096 (one chunk); buffers 16-byte aligned.  Chunks
 // of 4096 elements are dealt round-robin to per_cu * CUs workgroups, a thread
@@ -97,10 +101,64 @@ __global__ __launch_bounds__(256) void mix_kernel(float* __restrict__ p, const f
   }
 }
 
+
+// AdamW's update (mx_adamw.hip, no AMSGrad, host step) with fixed
+// coefficients, contraction off as there.
+__device__ __forceinline__ void adam_update(float& p, float g, float& m, float& v) {
+#pragma clang fp contract(off)
+  p = p * 0.99999f;
+  m = fmaf(0.1f, g - m, m);
+  v = v * 0.999f;
+  v = v + (0.001f * g) * g;
+  const float denom = sqrtf(v) / 0.0316f + 1e-8f;
+  p = p + (-0.01f * m) / denom;
+}
+
+__global__ __launch_bounds__(256) void math_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                   float* __restrict__ m, float* __restrict__ v, int64_t chunks) {
+  int64_t ch = blockIdx.x;
+  if (ch >= chunks) return;
+  f32x4 P[kVec], G[kVec], M[kVec], V[kVec];
+  auto load = [&](int64_t c) {
+    const int64_t base = c * kChunk + int64_t(threadIdx.x) * 4;
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      const int64_t i = base + u * 1024;
+      P[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + i));
+      G[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g + i));
+      M[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(m + i));
+      V[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(v + i));
+    }
+  };
+  load(ch);
+  for (; ch < chunks; ch += gridDim.x) {
+    f32x4 P2[kVec], M2[kVec], V2[kVec];
+#pragma unroll
+    for (int u = 0; u < kVec; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float pp = P[u][j], mm = M[u][j], vv = V[u][j];
+        adam_update(pp, G[u][j], mm, vv);
+        P2[u][j] = pp;
+        M2[u][j] = mm;
+        V2[u][j] = vv;
+      }
+    if (ch + gridDim.x < chunks) load(ch + gridDim.x);
+    const int64_t base = ch * kChunk + int64_t(threadIdx.x) * 4;
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      const int64_t i = base + u * 1024;
+      __builtin_nontemporal_store(P2[u], reinterpret_cast<f32x4*>(p + i));
+      __builtin_nontemporal_store(M2[u], reinterpret_cast<f32x4*>(m + i));
+      __builtin_nontemporal_store(V2[u], reinterpret_cast<f32x4*>(v + i));
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int mxp_stream(int kind, float* const* bufs, int64_t n, int per_cu, void* stream) {
-  if (n <= 0 || n % kChunk != 0 || per_cu <= 0 || kind < 0 || kind > 2) return int(hipErrorInvalidValue);
+  if (n <= 0 || n % kChunk != 0 || per_cu <= 0 || kind < 0 || kind > 3) return int(hipErrorInvalidValue);
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -112,7 +170,9 @@ extern "C" int mxp_stream(int kind, float* const* bufs, int64_t n, int per_cu, v
     hipLaunchKernelGGL(copy_kernel, dim3(grid), dim3(256), 0, s, bufs[0], bufs[1], chunks);
   else if (kind == 1)
     hipLaunchKernelGGL(read_kernel, dim3(grid), dim3(256), 0, s, bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], chunks);
-  else
+  else if (kind == 2)
     hipLaunchKernelGGL(mix_kernel, dim3(grid), dim3(256), 0, s, bufs[0], bufs[1], bufs[2], bufs[3], chunks);
+  else
+    hipLaunchKernelGGL(math_kernel, dim3(grid), dim3(256), 0, s, bufs[0], bufs[1], bufs[2], bufs[3], chunks);
   return int(hipGetLastError());
 }
