@@ -859,11 +859,20 @@ using namespace mx;
 
 namespace {
 
+// Entry points work on a copy of the caller's descriptor (checked_desc fills
+// in its output size).
+int copy_desc(const mx_conv2d_desc* desc, mx_conv2d_desc* d) {
+  MX_REQUIRE(desc, MX_ERR_INVALID, "conv2d: null descriptor");
+  *d = *desc;
+  return MX_OK;
+}
+
 // Plan of one call of `phase` (no data touched): the algorithm that runs, the
 // implicit GEMM's tile and K split, the scratch counted against the workspace
 // budget and the kernel instantiations launched.
 int describe(const mx_conv2d_desc* desc, int phase, int algo, int with_bias, mx_conv2d_plan_info* info) {
-  mx_conv2d_desc d = *desc;
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
   MX_TRY(checked_desc(&d));
   int chosen = 0;
   MX_TRY(select_algo(d, phase, algo, &chosen));
@@ -932,7 +941,8 @@ int mx_conv2d_check(mx_conv2d_desc* desc) {
 
 int mx_conv2d_select(const mx_conv2d_desc* desc, int phase, int requested, int* algo) {
   MX_ABI_BEGIN
-  mx_conv2d_desc d = *desc;
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
   MX_TRY(checked_desc(&d));
   return select_algo(d, phase, requested, algo);
   MX_ABI_END
@@ -941,7 +951,8 @@ int mx_conv2d_select(const mx_conv2d_desc* desc, int phase, int requested, int* 
 int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w, const float* bias, float* y,
                       int algo, void* stream) {
   MX_ABI_BEGIN
-  mx_conv2d_desc d = *desc;
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
   MX_TRY(checked_desc(&d));
   MX_REQUIRE(x && w && y, MX_ERR_INVALID, "conv2d forward: null tensor");
   int chosen = 0;
@@ -997,7 +1008,8 @@ int mx_conv2d_forward(const mx_conv2d_desc* desc, const float* x, const float* w
 int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const float* w, float* dx, int algo,
                              void* stream) {
   MX_ABI_BEGIN
-  mx_conv2d_desc d = *desc;
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
   MX_TRY(checked_desc(&d));
   MX_REQUIRE(dy && w && dx, MX_ERR_INVALID, "conv2d dinput: null tensor");
   int chosen = 0;
@@ -1079,7 +1091,8 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
 
 int mx_conv2d_backward_bias(const mx_conv2d_desc* desc, const float* dy, float* db, void* stream) {
   MX_ABI_BEGIN
-  mx_conv2d_desc d = *desc;
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
   MX_TRY(checked_desc(&d));
   MX_REQUIRE(dy && db, MX_ERR_INVALID, "conv2d dbias: null tensor");
   hipStream_t s = resolve_stream(stream);
@@ -1118,7 +1131,8 @@ namespace {
 // is allocated.
 int dweight_impl(const mx_conv2d_desc* desc, const float* x, const float* dy, float* dw, float* db, int algo,
                  float* ext, int64_t ext_bytes, void* stream) {
-  mx_conv2d_desc d = *desc;
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
   MX_TRY(checked_desc(&d));
   MX_REQUIRE(x && dy, MX_ERR_INVALID, "conv2d dweight: null tensor");
   if (!dw && !db) return MX_OK;
@@ -1241,7 +1255,8 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
 int mx_conv2d_backward(const mx_conv2d_desc* desc, const float* x, const float* w, const float* dy, float* dx,
                        float* dw, float* db, int algo_dx, int algo_dw, void* stream) {
   MX_ABI_BEGIN
-  mx_conv2d_desc d = *desc;
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
   MX_TRY(checked_desc(&d));
   if (dx && (dw || db)) {
     int ax = 0, aw = 0;
@@ -1312,7 +1327,8 @@ int mx_conv2d_plan(const mx_conv2d_desc* desc, int phase, int algo, int with_bia
 
 int mx_conv2d_dweight_plan(const mx_conv2d_desc* desc, int64_t* splits, int64_t* span, int64_t* workspace_bytes) {
   MX_ABI_BEGIN
-  mx_conv2d_desc d = *desc;
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
   MX_TRY(checked_desc(&d));
   int64_t limit = 0;
   MX_TRY(conv::workspace_limit(&limit));

@@ -186,3 +186,30 @@ def test_last_error_is_thread_local_and_cleared(mx):
     ok = mx.ConvDesc(n=1, cin=1, h=3, w=3, cout=1, kh=3, kw=3, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1, groups=1)
     assert mx.lib().mx_conv2d_check(C.byref(ok)) == mx.MX_OK
     assert mx.lib().mx_last_error() == b""
+
+
+def test_conv_entry_points_reject_null_descriptor(mx):
+    """Every convolution entry point returns MX_ERR_INVALID for a null
+    descriptor (before touching the device), as for any other bad argument."""
+    import ctypes as C
+    L = mx.lib()
+    algo = C.c_int()
+    info = mx.ConvPlanInfo() if hasattr(mx, "ConvPlanInfo") else None
+    buf = C.create_string_buffer(64)
+    n1, n2, n3 = C.c_int64(), C.c_int64(), C.c_int64()
+    calls = [
+        lambda: L.mx_conv2d_select(None, mx.MX_CONV_FORWARD, mx.ALGO_AUTO, C.byref(algo)),
+        lambda: L.mx_conv2d_forward(None, None, None, None, None, mx.ALGO_AUTO, None),
+        lambda: L.mx_conv2d_backward_input(None, None, None, None, mx.ALGO_AUTO, None),
+        lambda: L.mx_conv2d_backward_weight(None, None, None, None, None, mx.ALGO_AUTO, None),
+        lambda: L.mx_conv2d_backward_bias(None, None, None, None),
+        lambda: L.mx_conv2d_backward(None, None, None, None, None, None, None, mx.ALGO_AUTO, mx.ALGO_AUTO, None),
+        lambda: L.mx_conv2d_backward_weight_noalloc(None, None, None, None, None, mx.ALGO_AUTO, None),
+        lambda: L.mx_conv2d_kernel_name(None, mx.MX_CONV_FORWARD, mx.ALGO_AUTO, buf, len(buf)),
+        lambda: L.mx_conv2d_dweight_plan(None, C.byref(n1), C.byref(n2), C.byref(n3)),
+    ]
+    if info is not None:
+        calls.append(lambda: L.mx_conv2d_plan(None, mx.MX_CONV_FORWARD, mx.ALGO_AUTO, 0, C.byref(info)))
+    for call in calls:
+        with pytest.raises(mx.MXError, match="null (descriptor|argument)"):
+            mx.check(call())
