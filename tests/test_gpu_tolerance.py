@@ -114,6 +114,13 @@ def test_conv_plain_bound_beside_cpu(mx, case):
     torch.cuda.synchronize()
     record(name, "dWeight (implicit_gemm)", RTOL, DW, gwc, gwd, mwa)
     record(name, "dBias", RTOL, DB, gbc, gbd, dy.double().abs().sum((0, 2, 3)))
+    if k == 3 and s == 1:
+        # The Winograd weight gradient with its fused dBias (C1's and C3's route).
+        DW, DB = torch.empty_like(W), torch.empty_like(B)
+        mx.conv2d_backward_weight(d, X, DY, DW, DB, mx.ALGO_WINOGRAD, st)
+        torch.cuda.synchronize()
+        record(name, "dWeight (winograd)", WINOGRAD_RTOL, DW, gwc, gwd, mwa)
+        record(name, "dBias (winograd dWeight launch)", RTOL, DB, gbc, gbd, dy.double().abs().sum((0, 2, 3)))
 
 
 def test_c2_rows_plain_bound_beside_cpu(mx):
