@@ -329,8 +329,59 @@ def run_c4(torch, steps, warmup, log):
            "ms_per_step": round(dt * 1e3, 3), "value": round(flops / dt / 1e12, 3), "unit": "TFLOP/s",
            "gflop_per_step": round(flops / 1e9, 1), "params": params,
            "cpu_fallback_calls_per_step": fallbacks / steps, "host_reads_per_step": reads / steps}
+    out.update(c4_kernel_table(tv, step, steps))
     del model, opt, x, t
     return out
+
+
+def c4_kernel_table(tv, step, steps):
+    """The same training steps again with HIP events around every
+    convolution, GEMM / bmm and AdamW call on its stream
+    (TORCH_VULKAN_PROFILE_TIMESTAMPS=1): per kernel label the calls per step,
+    time per call and algorithmic TFLOP/s (direct-convolution / 2*M*N*K
+    FLOPs of the phases the call computes), the conv/GEMM kernel-summed rate
+    and the roofline of the kernel that takes the most time.  A call's time
+    covers all of its dispatches (weight packing, split-K sums)."""
+    os.environ["TORCH_VULKAN_PROFILE_TIMESTAMPS"] = "1"
+    try:
+        step()
+        tv.synchronize()
+        tv.reset_gpu_timing_stats()
+        for _ in range(steps):
+            step()
+        tv.synchronize()
+        stats = tv.gpu_timing_stats()
+    finally:
+        os.environ.pop("TORCH_VULKAN_PROFILE_TIMESTAMPS", None)
+        tv.reset_gpu_timing_stats()
+    rows = []
+    for name, v in stats.items():
+        if not v["samples"]:
+            continue
+        ms = v["shader_ms"]
+        row = {"kernel": name, "calls_per_step": round(v["samples"] / steps, 2),
+               "ms_per_step": round(ms / steps, 4), "avg_us": round(1000 * ms / v["samples"], 2)}
+        if v["flops"] > 0 and ms > 0:
+            row["tflop_s"] = round(v["flops"] / (ms * 1e-3) / 1e12, 3)
+            row["frac_of_fp32_peak"] = round(row["tflop_s"] / PEAK_FP32_TFLOPS, 4)
+        rows.append((ms, v["flops"], v["samples"], row))
+    rows.sort(key=lambda r: -r[0])
+    mm = [r for r in rows if r[1] > 0]
+    gemm_ms = sum(r[0] for r in mm)
+    gemm_flops = sum(r[1] for r in mm)
+    res = {"kernel_table": [r[3] for r in rows[:16]],
+           "timed_ms_per_step": round(sum(r[0] for r in rows) / steps, 3),
+           "conv_gemm_ms_per_step": round(gemm_ms / steps, 3)}
+    if mm:
+        ms, fl, n, row = mm[0]
+        achieved = fl / n / (ms / n * 1e-3) / 1e12
+        res["conv_gemm_kernel_tflop_s"] = round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 3)
+        res["conv_gemm_frac_of_fp32_peak"] = round(res["conv_gemm_kernel_tflop_s"] / PEAK_FP32_TFLOPS, 4)
+        res["roofline"] = {"bound": "mfma", "kernel": row["kernel"], "achieved": round(achieved, 3),
+                           "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+                           "traffic": None, "launches": n, "avg_launch_us": row["avg_us"],
+                           "timing": "HIP events around each call on its stream"}
+    return res
 
 
 def run_streams(torch, reps=5):
@@ -1035,7 +1086,8 @@ def main(argv=None):
         del calls_c
         torch.cuda.empty_cache()
         comps["c4"] = run_c4(torch, max(3, min(args.steps, 10)), 3, log)
-        log("c4", comps["c4"]["ms_per_step"], "ms/step", comps["c4"]["value"], "TFLOP/s")
+        log("c4", comps["c4"]["ms_per_step"], "ms/step", comps["c4"]["value"], "TFLOP/s; conv/GEMM kernels",
+            comps["c4"].get("conv_gemm_kernel_tflop_s"), "TFLOP/s; roofline", comps["c4"].get("roofline"))
         comps["streams"] = run_streams(torch)
         log("streams", comps["streams"])
         result["components"] = comps

@@ -225,6 +225,15 @@ int mx_conv2d_backward_weight(const mx_conv2d_desc* desc, const float* x, const 
 int mx_conv2d_backward(const mx_conv2d_desc* desc, const float* x, const float* w, const float* dy,
                        float* dx, float* dw, float* db, int algo_dx, int algo_dw, void* stream);
 
+/* *one_launch = 1 when mx_conv2d_backward with these arguments (dx and dw
+ * requested, dBias too when with_bias != 0) runs both gradients as the one
+ * Winograd launch (wino_bwd_kernel), 0 when it makes the two separate calls.
+ * No data is read.  No counterpart in the reference, whose backward
+ * dispatches gradient by gradient (csrc/ops/convolution.cpp:684-695): it lets
+ * a caller label per-kernel timing and count launches by what runs. */
+int mx_conv2d_backward_one_launch(const mx_conv2d_desc* desc, int algo_dx, int algo_dw, int with_bias,
+                                  int* one_launch);
+
 /* Allocation-free dWeight / dBias.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory while they run (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
@@ -304,7 +313,15 @@ typedef struct mx_gemm_desc {
   float alpha, beta;
   int bias_kind;
   int64_t bias_stride_b; /* bias batch stride (0 = one bias for every batch); ABI >= 2 */
+  /* Tile family (ABI >= 3), the counterpart of TORCH_VULKAN_MM_KERNEL
+   * (csrc/ops/mm.cpp:299-307, :851-854): MX_GEMM_KERNEL_AUTO lets the cost
+   * model choose, MX_GEMM_KERNEL_TILED forces the small 64x64 tile (the
+   * reference's 16x16 "tiled" kernel), MX_GEMM_KERNEL_REGISTER restricts the
+   * choice to the large register-blocked tiles (its 64x64 "register" kernel). */
+  int kernel;
 } mx_gemm_desc;
+
+enum mx_gemm_kernel { MX_GEMM_KERNEL_AUTO = 0, MX_GEMM_KERNEL_TILED = 1, MX_GEMM_KERNEL_REGISTER = 2 };
 
 int mx_gemm_f32(const mx_gemm_desc* desc, const float* a, const float* b, const float* bias,
                 float* c, void* stream);

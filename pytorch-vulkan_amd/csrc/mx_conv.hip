@@ -374,6 +374,47 @@ mx_conv2d_desc batch_slice(const mx_conv2d_desc& d, int64_t n) {
   return c;
 }
 
+// TORCH_VULKAN_CONV_TILE (csrc/ops/convolution.cpp:411-414): the reference's
+// tile menu by name (:163-169) and the implicit-GEMM tile of this build each
+// name forces.  Names keep their shape relations on this menu: base the
+// smallest tile, wide the tile widest in positions, tall the one tallest in
+// channels, the register tiles the square register-blocked ones; register3 and
+// register3_hoist only for 3x3 filters, as the reference's fixed-3x3 tiles
+// (:168-169, :369).  Unset or "auto" lets the planner choose (-1).
+struct NamedTile {
+  const char* name;
+  int tile;
+  bool fixed3x3;
+};
+constexpr NamedTile kNamedTiles[] = {{"base", conv::SMALL, false},   {"wide", conv::FLAT, false},
+                                     {"tall", conv::TALL, false},    {"register", conv::SQ, false},
+                                     {"register3", conv::WIDE, true}, {"register3_hoist", conv::SQ, true}};
+constexpr int kNamedTileCount = int(sizeof(kNamedTiles) / sizeof(kNamedTiles[0]));
+
+int tile_knob(int* idx) {
+  *idx = -1;
+  const char* v = std::getenv("TORCH_VULKAN_CONV_TILE");
+  if (!v || !*v || std::strcmp(v, "auto") == 0) return MX_OK;
+  for (int i = 0; i < kNamedTileCount; ++i)
+    if (std::strcmp(v, kNamedTiles[i].name) == 0) *idx = i;
+  MX_REQUIRE(*idx >= 0, MX_ERR_INVALID,
+             "TORCH_VULKAN_CONV_TILE must be auto/base/wide/tall/register/register3/register3_hoist");
+  return MX_OK;
+}
+
+// The tiles the planner may use for d's implicit GEMM under the knob: the
+// named tile when this phase's loaders allow it, otherwise the base tile (the
+// reference's fallback to tiled_base, :474-478).
+unsigned knob_tiles(const mx_conv2d_desc& d, unsigned allowed) {
+  int k = -1;
+  if (tile_knob(&k) != MX_OK || k < 0) return allowed;
+  const NamedTile& t = kNamedTiles[k];
+  const unsigned base = allowed & (1u << conv::SMALL);
+  if (t.fixed3x3 && !(d.kh == 3 && d.kw == 3)) return base ? base : allowed;
+  const unsigned m = allowed & (1u << t.tile);
+  return m ? m : (base ? base : allowed);
+}
+
 bool winograd_applicable(const mx_conv2d_desc& d) {
   return d.kh == 3 && d.kw == 3 && d.sh == 1 && d.sw == 1 && d.dh == 1 && d.dw == 1;
 }
@@ -386,6 +427,15 @@ int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
   const int64_t rows = d.n * d.oh * d.ow, cols = cin_g * d.kh * d.kw;
   MX_REQUIRE(requested >= MX_CONV_ALGO_AUTO && requested <= MX_CONV_ALGO_DEPTHWISE, MX_ERR_INVALID,
              "conv2d: unknown algorithm ", requested);
+  int knob = -1;
+  MX_TRY(tile_knob(&knob));
+  if (requested == MX_CONV_ALGO_IMPLICIT_GEMM && phase != MX_CONV_DBIAS && knob >= 0 &&
+      kNamedTiles[knob].fixed3x3 && !(d.kh == 3 && d.kw == 3)) {
+    static const char* names[] = {"forward", "dinput", "dweight"};
+    return set_error(MX_ERR_UNSUPPORTED, cat("Forced Vulkan convolution ", names[phase], " candidate tiled_",
+                                             kNamedTiles[knob].name,
+                                             " exceeds device limits, workspace budget, or operator applicability"));
+  }
   switch (phase) {
     case MX_CONV_FORWARD:
       if (requested == MX_CONV_ALGO_WINOGRAD) {
@@ -611,7 +661,7 @@ int plan_forward(const mx_conv2d_desc& d, const float* x, const float* w, const 
   f->padded = !f->packed && (p.K % 4 != 0 || !aligned16(w));
   f->bmode = (unpadded_1x1(p) && p.HW % 4 == 0 && aligned16(x)) ? conv::B_VEC : conv::B_GATHER;
   p.out_elems = int64_t(p.N) * p.Cout * p.OHOW;
-  MX_TRY(plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G, kSinglePassTiles, 512,
+  MX_TRY(plan_gemm(p.Cout_g, int64_t(p.N) * p.OHOW, int64_t(p.Cin_g) * p.KK, p.G, knob_tiles(d, kSinglePassTiles), 512,
                    p.out_elems, p.out_elems * 4, ws_limit, &f->gp));
   p.splits = f->gp.splits;
   p.kps = f->gp.kps;
@@ -714,8 +764,8 @@ int plan_dinput(const mx_conv2d_desc& d, const float* dy, const float* w, float*
     }
   }
   f->out_elems = int64_t(p.N) * p.Cin * p.HW;
-  MX_TRY(plan_gemm(bm, bn, std::max<int64_t>(bk, 1), p.G, kSinglePassTiles, f->any_zero ? 1 : 512, f->out_elems,
-                   f->out_elems * 4, ws_limit, &f->gp));
+  MX_TRY(plan_gemm(bm, bn, std::max<int64_t>(bk, 1), p.G, knob_tiles(d, kSinglePassTiles), f->any_zero ? 1 : 512,
+                   f->out_elems, f->out_elems * 4, ws_limit, &f->gp));
   // A 1x1 kernel is already [g][co][ci]; larger kernels are packed per phase.
   f->packed = p.KK > 1;
   f->vec_a = p.Cin_g % 4 == 0 && (f->packed || aligned16(w));
@@ -801,7 +851,7 @@ int plan_dweight(const mx_conv2d_desc& d, const float* x, const float* dy, float
   if (f->bmode == conv::B_GATHER) tiles &= ~((1u << conv::WIDE) | (1u << conv::FLAT));
   if (f->bmode == conv::B_GATHER && f->amode == conv::B_GATHER) tiles &= ~(1u << conv::TALL);
   const int64_t per_split = out * 4 + (with_db ? int64_t(p.Cout) * 4 : 0);
-  MX_TRY(plan_gemm(p.M, p.Ncols, p.K, p.G, tiles, 65535, out, per_split, ws_limit, &f->gp));
+  MX_TRY(plan_gemm(p.M, p.Ncols, p.K, p.G, knob_tiles(d, tiles), 65535, out, per_split, ws_limit, &f->gp));
   p.splits = f->gp.splits;
   p.kps = f->gp.kps;
   if (f->gp.splits > 1) {
@@ -831,6 +881,7 @@ int winograd_describe(const mx_conv2d_desc& d, int phase, bool with_bias, int64_
                       int64_t* ws_bytes);
 int winograd_backward(const mx_conv2d_desc& d, const float* x, const float* w, const float* dy, float* dx, float* dw,
                       float* db, int64_t ws_limit, hipStream_t s, bool* done);
+int winograd_backward_one_launch(const mx_conv2d_desc& d, int64_t ws_limit, bool with_db, bool* one);
 
 namespace conv {
 // Scratch budget of one convolution call (split-K partials, the Winograd
@@ -1277,6 +1328,28 @@ int mx_conv2d_backward(const mx_conv2d_desc* desc, const float* x, const float* 
   MX_ABI_END
 }
 
+int mx_conv2d_backward_one_launch(const mx_conv2d_desc* desc, int algo_dx, int algo_dw, int with_bias,
+                                  int* one_launch) {
+  MX_ABI_BEGIN
+  mx_conv2d_desc d{};
+  MX_TRY(copy_desc(desc, &d));
+  MX_REQUIRE(one_launch, MX_ERR_INVALID, "mx_conv2d_backward_one_launch: null argument");
+  MX_TRY(checked_desc(&d));
+  *one_launch = 0;
+  int ax = 0, aw = 0;
+  MX_TRY(select_algo(d, MX_CONV_DINPUT, algo_dx, &ax));
+  MX_TRY(select_algo(d, MX_CONV_DWEIGHT, algo_dw, &aw));
+  if (ax == MX_CONV_ALGO_WINOGRAD && aw == MX_CONV_ALGO_WINOGRAD && images_per_launch(d) >= d.n) {
+    int64_t limit = 0;
+    MX_TRY(conv::workspace_limit(&limit));
+    bool one = false;
+    MX_TRY(winograd_backward_one_launch(d, limit, with_bias != 0, &one));
+    *one_launch = one ? 1 : 0;
+  }
+  return MX_OK;
+  MX_ABI_END
+}
+
 int mx_conv2d_backward_weight_noalloc(const mx_conv2d_desc* desc, const float* x, const float* dy, float* dw,
                                       float* db, int algo, void* stream) {
   MX_ABI_BEGIN
@@ -1296,7 +1369,16 @@ int mx_conv2d_kernel_name(const mx_conv2d_desc* desc, int phase, int algo, char*
   if (phase == MX_CONV_DBIAS) {
     name = info.variant;
   } else if (info.algo == MX_CONV_ALGO_WINOGRAD) {
-    name = phase == MX_CONV_DWEIGHT ? "wino_dw_kernel" : "wino_filter_kernel";
+    // The variant names the kernel that carries the call: "wino_ws16_kernel<
+    // even,filter>+flip", "wino_dw_ws_kernel+ranges", or the unfused passes'
+    // batched GEMM "wino_unfused(gemm_kernel<..>)".
+    const std::string v = info.variant;
+    const size_t open = v.find('(');
+    if (open != std::string::npos) {
+      name = v.substr(open + 1, v.rfind(')') - open - 1);
+    } else {
+      name = v.substr(0, v.find_first_of("<+"));
+    }
   } else if (info.algo == MX_CONV_ALGO_DEPTHWISE) {
     name = "conv_depthwise_kernel";
   } else if (info.algo == MX_CONV_ALGO_DIRECT) {

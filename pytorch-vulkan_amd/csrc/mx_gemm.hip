@@ -183,15 +183,18 @@ constexpr TileChoice kTiles[] = {{256, 128, 2, 1.0}, {128, 256, 2, 1.0}, {128, 1
 // Cheapest tile by a wave-quantised cost model: rounds of resident tiles
 // times the time of one round (per_cu tiles per CU at the relative rate).
 // MX_GEMM_TILE=<index into kTiles> forces a tile (tuning and diagnosis; the
-// 256-wide tiles only for 16-byte operand modes).
-int pick_gemm_tile(int64_t m, int64_t n, int64_t batch, bool vec) {
+// 256-wide tiles only for 16-byte operand modes).  `kernel` (mx_gemm_kernel)
+// forces the 64x64 tile or keeps the choice among the large ones.
+int pick_gemm_tile(int64_t m, int64_t n, int64_t batch, bool vec, int kernel) {
   if (const char* e = std::getenv("MX_GEMM_TILE")) {
     const int t = std::atoi(e);
     if (t >= (vec ? 0 : 2) && t < 4) return t;
   }
+  if (kernel == MX_GEMM_KERNEL_TILED) return 3;
+  const int last = kernel == MX_GEMM_KERNEL_REGISTER ? 3 : 4;
   int best = 2;
   double best_cost = 0;
-  for (int i = vec ? 0 : 2; i < 4; ++i) {
+  for (int i = vec ? 0 : 2; i < last; ++i) {
     const TileChoice& t = kTiles[i];
     const int64_t tiles = ((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn) * batch;
     const int64_t slots = int64_t(cu_count()) * t.per_cu;
@@ -239,6 +242,8 @@ int plan_gemm(const mx_gemm_desc* d, const float* a, const float* b, const float
              MX_ERR_INVALID, "mx_gemm_f32: dimension exceeds int32");
   MX_REQUIRE(d->bias_kind >= MX_BIAS_NONE && d->bias_kind <= MX_BIAS_MATRIX, MX_ERR_INVALID,
              "mx_gemm_f32: bad bias kind");
+  MX_REQUIRE(d->kernel >= MX_GEMM_KERNEL_AUTO && d->kernel <= MX_GEMM_KERNEL_REGISTER, MX_ERR_INVALID,
+             "mx_gemm: unknown kernel class ", d->kernel);
   g->empty = d->batch == 0 || d->m == 0 || d->n == 0;
   if (g->empty) return MX_OK;
   GemmArgs& p = g->p;
@@ -268,7 +273,7 @@ int plan_gemm(const mx_gemm_desc* d, const float* a, const float* b, const float
   MX_REQUIRE(((d->m + 63) / 64) * ((d->n + 63) / 64) <= INT32_MAX, MX_ERR_INVALID, "mx_gemm_f32: too many tiles");
   g->ma = pick_mode(p.a, p.a_sm, p.a_sk, p.a_sb, p.batch, p.M, p.K);
   g->mb = pick_mode(p.b, p.b_sn, p.b_sk, p.b_sb, p.batch, p.N, p.K);
-  g->tile = pick_gemm_tile(d->m, d->n, d->batch, is_vec(g->ma) && is_vec(g->mb));
+  g->tile = pick_gemm_tile(d->m, d->n, d->batch, is_vec(g->ma) && is_vec(g->mb), d->kernel);
   return MX_OK;
 }
 

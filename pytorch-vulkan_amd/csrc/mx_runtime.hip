@@ -161,7 +161,7 @@ using namespace mx;
 extern "C" {
 
 const char* mx_last_error(void) { return g_last_error.c_str(); }
-int mx_abi_version(void) { return 2; }
+int mx_abi_version(void) { return 3; }
 
 int mx_init(int ordinal) {
   MX_ABI_BEGIN

@@ -1849,6 +1849,38 @@ int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const floa
   return winograd_run(dinput_as_forward(d), dy, w, nullptr, dx, true, ws_limit, s);
 }
 
+// Whether both Winograd gradients of the 3x3 stride-1 layer d run as one
+// backward launch (*one), with the plans that launch uses.  One launch pays
+// for tiny layers, where launch overhead dominates (33 -> 40 channels at
+// 17x15: 20.2 -> 15.4 us), and where two launches of short walks (<= 8 slabs)
+// would each leave CUs idle but together fill them at least one and a half
+// times over, with the input gradient alone fitting the CUs once (C1's layer:
+// 196 + 196 workgroups, 45.1 -> 39.6 us).  Otherwise the 16-tile
+// input-gradient kernel's two workgroups per CU win (64 x 28^2, batch 16: 33.3
+// vs 34.1; 128 x 28^2, batch 8: 46.3 vs 48.7; 256 x 16^2, batch 16: 68.9 vs
+// 82.0).  MX_WINOGRAD_BWD=0 / 1 forces the two launches / the one launch.
+static int winograd_backward_plan(const mx_conv2d_desc& d, int64_t ws_limit, bool with_db, RunPlan* rf,
+                                  DwRunPlan* rw, bool* one) {
+  *one = false;
+  if (d.ph > 2 || d.pw > 2) return MX_OK;
+  MX_TRY(plan_run(dinput_as_forward(d), ws_limit, rf));
+  MX_TRY(plan_dw_run(d, ws_limit, with_db, rw));
+  if (!rf->fused || !rw->ws || rf->p.T == 0 || rw->p.T == 0) return MX_OK;
+  const int64_t cus = cu_count(), n_dx32 = rf->blocks * rf->G, n_dw_all = rw->blocks * rw->ranges;
+  bool o = 4 * (n_dx32 + n_dw_all) <= cus ||
+           (rf->p.nslab <= 8 && n_dx32 <= cus && 2 * (n_dx32 + n_dw_all) >= 3 * cus);
+  if (const char* e = std::getenv("MX_WINOGRAD_BWD"))
+    if (e[0] == '0' || e[0] == '1') o = e[0] == '1';
+  *one = o;
+  return MX_OK;
+}
+
+int winograd_backward_one_launch(const mx_conv2d_desc& d, int64_t ws_limit, bool with_db, bool* one) {
+  RunPlan rf;
+  DwRunPlan rw;
+  return winograd_backward_plan(d, ws_limit, with_db, &rf, &rw, one);
+}
+
 // dx, dw and db of the 3x3 stride-1 layer d in one backward launch (after
 // the flipped filter transform, before the weight gradient's range sum) when
 // both gradients take the fused Winograd paths: the input gradient the fused
@@ -1858,27 +1890,10 @@ int winograd_backward_input(const mx_conv2d_desc& d, const float* dy, const floa
 int winograd_backward(const mx_conv2d_desc& d, const float* x, const float* w, const float* dy, float* dx, float* dw,
                       float* db, int64_t ws_limit, hipStream_t s, bool* done) {
   *done = false;
-  if (d.ph > 2 || d.pw > 2) return MX_OK;
-  const mx_conv2d_desc t = dinput_as_forward(d);
   RunPlan rf;
-  MX_TRY(plan_run(t, ws_limit, &rf));
   DwRunPlan rw;
-  MX_TRY(plan_dw_run(d, ws_limit, db != nullptr, &rw));
-  if (!rf.fused || !rw.ws || rf.p.T == 0 || rw.p.T == 0) return MX_OK;
-  // One launch pays for tiny layers, where launch overhead dominates (33 ->
-  // 40 channels at 17x15: 20.2 -> 15.4 us), and where two launches of short
-  // walks (<= 8 slabs) would each leave CUs idle but together fill them at
-  // least one and a half times over, with the input gradient alone fitting
-  // the CUs once (C1's layer: 196 + 196 workgroups, 45.1 -> 39.6 us).
-  // Otherwise the 16-tile input-gradient kernel's two workgroups per CU win
-  // (64 x 28^2, batch 16: 33.3 vs 34.1; 128 x 28^2, batch 8: 46.3 vs 48.7;
-  // 256 x 16^2, batch 16: 68.9 vs 82.0).  MX_WINOGRAD_BWD=0 / 1 forces the
-  // two launches / the one launch.
-  const int64_t cus = cu_count(), n_dx32 = rf.blocks * rf.G, n_dw_all = rw.blocks * rw.ranges;
-  bool one = 4 * (n_dx32 + n_dw_all) <= cus ||
-             (rf.p.nslab <= 8 && n_dx32 <= cus && 2 * (n_dx32 + n_dw_all) >= 3 * cus);
-  if (const char* e = std::getenv("MX_WINOGRAD_BWD"))
-    if (e[0] == '0' || e[0] == '1') one = e[0] == '1';
+  bool one = false;
+  MX_TRY(winograd_backward_plan(d, ws_limit, db != nullptr, &rf, &rw, &one));
   if (!one) return MX_OK;
   // Input gradient: the fused kernel's arguments as winograd_run sets them.
   fused::Args& pf = rf.p;

@@ -139,9 +139,19 @@ struct VkAllocator final : public c10::Allocator {
     const int dev = cur_dev();
     void* p = nullptr;
     if (n) {
+      const bool hot = host_hotpath_enabled();
+      mx_memory_stats before{};
+      if (hot) mx_memory_stats_get(&before);
+      const auto t0 = std::chrono::steady_clock::now();
       const int rc = mx_malloc(&p, n, current_stream());
       TORCH_CHECK_WITH(OutOfMemoryError, rc == MX_OK, "vulkan: out of device memory allocating ", n,
                        " bytes: ", mx_last_error());
+      if (hot) {
+        const auto ns = std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0);
+        mx_memory_stats after{};
+        mx_memory_stats_get(&after);
+        record_hotpath("allocator", uint64_t(ns.count()), after.device_mallocs > before.device_mallocs, n);
+      }
     }
     return {p, p, &raw_delete, c10::Device(c10::DeviceType::PrivateUse1, c10::DeviceIndex(dev))};
   }
@@ -401,7 +411,13 @@ struct TimedPair {
   void* start;
   void* end;
   double host_ms;
+  double flops;
 };
+// Event pairs wait in g_timing_pending until gpu_timing_stats() reads them;
+// past kPendingCap pairs, the ones whose work has completed are folded into
+// the totals when a new pair arrives, so a run that never reads the stats
+// holds a bounded number of events.
+constexpr size_t kPendingCap = 4096;
 std::mutex g_timing_mu;
 std::vector<TimedPair> g_timing_pending;
 std::map<std::string, GpuTiming> g_timing;
@@ -416,9 +432,84 @@ bool gpu_timing_enabled() {
   return v && std::strcmp(v, "1") == 0;
 }
 
-GpuTimer::GpuTimer(std::string name) {
-  if (!gpu_timing_enabled()) return;
+// Adds one completed pair to `into` and destroys its events.
+static void fold_pair(const TimedPair& t, std::map<std::string, GpuTiming>& into) {
+  float ms = 0.f;
+  const bool ok = mx_event_synchronize(t.end) == MX_OK && mx_event_elapsed_ms(t.start, t.end, &ms) == MX_OK;
+  mx_event_destroy(t.start);
+  mx_event_destroy(t.end);
+  GpuTiming& a = into[t.name];
+  a.samples++;
+  a.host_eval_ms += t.host_ms;
+  a.flops += t.flops;
+  if (ok) a.shader_ms += ms;
+}
+
+// With g_timing_mu held: folds every pending pair whose end event has
+// completed into g_timing (mx_event_query: 1 = complete).
+static void fold_completed_locked() {
+  std::vector<TimedPair> keep;
+  keep.reserve(g_timing_pending.size());
+  for (TimedPair& t : g_timing_pending) {
+    int done = 0;
+    if (mx_event_query(t.end, &done) == MX_OK && done)
+      fold_pair(t, g_timing);
+    else
+      keep.push_back(std::move(t));
+  }
+  g_timing_pending.swap(keep);
+}
+
+namespace {
+int64_t steady_ns() {
+  return std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+      .count();
+}
+std::mutex g_hot_mu;
+std::map<std::string, uint64_t> g_hot;
+}  // namespace
+
+bool host_hotpath_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("TORCH_VULKAN_PROFILE_HOST_HOTPATH");
+    return v && std::strcmp(v, "1") == 0;
+  }();
+  return on;
+}
+
+void record_hotpath(const char* key, uint64_t nanos, bool fresh, size_t bytes) {
+  if (!host_hotpath_enabled()) return;
+  std::lock_guard<std::mutex> lock(g_hot_mu);
+  const std::string k(key);
+  if (k == "allocator") {
+    g_hot["allocator_ns"] += nanos;
+    g_hot["allocator_calls"] += 1;
+    const char* kind = fresh ? "allocator_fresh" : "allocator_reused";
+    g_hot[std::string(kind) + "_ns"] += nanos;
+    g_hot[std::string(kind) + "_calls"] += 1;
+    if (fresh) g_hot["allocator_fresh_bytes"] += bytes;
+  } else {
+    g_hot[k + "_ns"] += nanos;
+    g_hot[k + "_count"] += 1;
+  }
+}
+
+std::map<std::string, uint64_t> hotpath_stats() {
+  std::lock_guard<std::mutex> lock(g_hot_mu);
+  std::map<std::string, uint64_t> r = g_hot;
+  for (const char* k : {"algo_hit_ns", "algo_miss_ns", "algo_hit_count", "algo_miss_count", "enqueue_ns",
+                        "enqueue_count", "allocator_ns", "allocator_calls", "allocator_fresh_ns",
+                        "allocator_fresh_calls", "allocator_fresh_bytes", "allocator_reused_ns",
+                        "allocator_reused_calls"})
+    r[k] += 0;
+  return r;
+}
+
+GpuTimer::GpuTimer(std::string name, double flops) {
+  if (host_hotpath_enabled()) hot_t0_ = steady_ns();
+  if (!gpu_timing_enabled() || name.empty()) return;
   name_ = std::move(name);
+  flops_ = flops;
   stream_ = current_stream();
   TVK_MX(mx_event_create(&start_, 1));
   TVK_MX(mx_event_record(start_, stream_));
@@ -426,6 +517,7 @@ GpuTimer::GpuTimer(std::string name) {
 }
 
 GpuTimer::~GpuTimer() {
+  if (hot_t0_ >= 0) record_hotpath("enqueue", uint64_t(steady_ns() - hot_t0_));
   if (!start_) return;
   void* end = nullptr;
   if (mx_event_create(&end, 1) != MX_OK || mx_event_record(end, stream_) != MX_OK) {
@@ -434,7 +526,8 @@ GpuTimer::~GpuTimer() {
     return;
   }
   std::lock_guard<std::mutex> lock(g_timing_mu);
-  g_timing_pending.push_back({name_, start_, end, now_ms() - host_t0_});
+  g_timing_pending.push_back({name_, start_, end, now_ms() - host_t0_, flops_});
+  if (g_timing_pending.size() > kPendingCap) fold_completed_locked();
 }
 
 std::map<std::string, GpuTiming> gpu_timing_stats() {
@@ -444,22 +537,14 @@ std::map<std::string, GpuTiming> gpu_timing_stats() {
     pending.swap(g_timing_pending);
   }
   std::map<std::string, GpuTiming> add;
-  for (const TimedPair& t : pending) {
-    float ms = 0.f;
-    const bool ok = mx_event_synchronize(t.end) == MX_OK && mx_event_elapsed_ms(t.start, t.end, &ms) == MX_OK;
-    mx_event_destroy(t.start);
-    mx_event_destroy(t.end);
-    GpuTiming& a = add[t.name];
-    a.samples++;
-    a.host_eval_ms += t.host_ms;
-    if (ok) a.shader_ms += ms;
-  }
+  for (const TimedPair& t : pending) fold_pair(t, add);
   std::lock_guard<std::mutex> lock(g_timing_mu);
   for (const auto& [name, a] : add) {
     GpuTiming& g = g_timing[name];
     g.samples += a.samples;
     g.shader_ms += a.shader_ms;
     g.host_eval_ms += a.host_eval_ms;
+    g.flops += a.flops;
   }
   return g_timing;
 }
@@ -483,6 +568,7 @@ py::dict gpu_timing_dict() {
     d["samples"] = v.samples;
     d["shader_ms"] = v.shader_ms;
     d["host_eval_ms"] = v.host_eval_ms;
+    d["flops"] = v.flops;
     // Buffers stay resident on the device: there is no per-op upload or download.
     d["upload_ms"] = 0.0;
     d["download_ms"] = 0.0;
@@ -558,8 +644,19 @@ PYBIND11_MODULE(_C, m) {
   m.def("_reset_execution_stats", &reset_execution_stats);
   m.def("_memory_stats", &memory_stats);
   m.def("_empty_cache", []() { TVK_MX(mx_empty_cache()); });
-  m.def("_conv_dispatch_stats", []() { return tvk::selection_stats(); });
-  m.def("_clear_conv_dispatch_cache", []() { tvk::clear_selection_stats(); });
+  m.def("_conv_dispatch_stats", []() {
+    // The autotune counters exist from the start, as the reference reports
+    // them (csrc/ops/convolution.cpp:528-534), plus the plan-cache size.
+    auto r = tvk::selection_stats();
+    for (const char* k : {"hits", "misses", "tunes", "evictions", "candidates_timed"}) r[k] += 0;
+    r["entries"] = tvk::conv_plan_cache_entries();
+    return r;
+  });
+  m.def("_clear_conv_plan_cache", []() { tvk::clear_conv_plan_cache(); });
+  m.def("_clear_conv_dispatch_cache", []() {
+    tvk::clear_conv_plan_cache();
+    tvk::clear_selection_stats();
+  });
   m.def("_current_stream_ptr", []() { return reinterpret_cast<uintptr_t>(tvk::current_stream()); });
   m.def("_current_stream", [](int device) {
     const c10::DeviceIndex d = c10::DeviceIndex(device < 0 ? tvk::cur_dev() : device);
@@ -590,5 +687,16 @@ PYBIND11_MODULE(_C, m) {
     }
   });
   m.def("_initial_seed", []() { return tvk::default_generator(-1).current_seed(); });
+  m.def("_get_rng_state", [](int dev) {
+    auto& g = tvk::default_generator(c10::DeviceIndex(dev));
+    std::lock_guard<std::mutex> lock(g.mutex());
+    return g.get_state();
+  });
+  m.def("_set_rng_state", [](int dev, const at::Tensor& state) {
+    auto& g = tvk::default_generator(c10::DeviceIndex(dev));
+    std::lock_guard<std::mutex> lock(g.mutex());
+    g.set_state(state);
+  });
+  m.def("_runtime_hotpath_stats", []() { return tvk::hotpath_stats(); });
   m.def("_abi_version", []() { return mx_abi_version(); });
 }

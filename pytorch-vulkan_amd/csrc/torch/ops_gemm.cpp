@@ -13,6 +13,9 @@
 #include <c10/core/DeviceGuard.h>
 #include <torch/library.h>
 
+#include <cstdlib>
+#include <cstring>
+
 #include "common.h"
 
 namespace tvk {
@@ -22,9 +25,20 @@ bool gemm_native(const at::Tensor& t) {
   return is_vk(t) && t.scalar_type() == at::kFloat && !t.is_neg() && !t.is_conj();
 }
 
+// TORCH_VULKAN_MM_KERNEL for mm / addmm (csrc/ops/mm.cpp:299-307, :851-854):
+// "register" keeps the tile choice among the large register-blocked tiles,
+// "tiled" forces the small one; any other value (or none) lets the cost model
+// choose, as the reference treats unknown values as automatic.
+int mm_kernel_knob() {
+  const char* k = std::getenv("TORCH_VULKAN_MM_KERNEL");
+  if (k && std::strcmp(k, "register") == 0) return MX_GEMM_KERNEL_REGISTER;
+  if (k && std::strcmp(k, "tiled") == 0) return MX_GEMM_KERNEL_TILED;
+  return MX_GEMM_KERNEL_AUTO;
+}
+
 // C[b] (+)= alpha * A[b] B[b] + beta * bias into a contiguous `out`.
 void run_gemm(const at::Tensor& a, const at::Tensor& b, at::Tensor& out, int64_t batch, const at::Tensor* bias,
-              float alpha, float beta) {
+              float alpha, float beta, int kernel = MX_GEMM_KERNEL_AUTO) {
   const bool batched = a.dim() == 3;
   const int64_t M = a.size(batched ? 1 : 0), K = a.size(batched ? 2 : 1), N = b.size(batched ? 2 : 1);
   mx_gemm_desc d{};
@@ -45,6 +59,7 @@ void run_gemm(const at::Tensor& a, const at::Tensor& b, at::Tensor& out, int64_t
   d.ldc = out.stride(batched ? 1 : 0);
   d.alpha = alpha;
   d.beta = beta;
+  d.kernel = kernel;
   d.bias_kind = MX_BIAS_NONE;
   const float* bias_ptr = nullptr;
   if (bias && bias->defined() && beta != 0.f) {
@@ -69,7 +84,7 @@ void run_gemm(const at::Tensor& a, const at::Tensor& b, at::Tensor& out, int64_t
                             static_cast<const float*>(b.storage().data()), buf, sizeof buf) == MX_OK
                 ? std::string(buf) : "gemm";
   }
-  GpuTimer timer(label);
+  GpuTimer timer(label, 2.0 * double(d.batch) * double(d.m) * double(d.n) * double(d.k));
   TVK_MX(mx_gemm_f32(&d, static_cast<const float*>(a.storage().data()), static_cast<const float*>(b.storage().data()),
                      bias_ptr, static_cast<float*>(out.storage().mutable_data()), current_stream()));
   counters().kernel_launches++;
@@ -94,7 +109,7 @@ at::Tensor mm_impl(const at::Tensor& self, const at::Tensor& mat2, at::Tensor* d
   const int64_t M = self.size(0), N = mat2.size(1);
   at::Tensor out = destination ? *destination : at::empty({M, N}, self.options());
   if (M == 0 || N == 0) return out;
-  run_gemm(self, mat2, out, 1, nullptr, 1.f, 0.f);
+  run_gemm(self, mat2, out, 1, nullptr, 1.f, 0.f, mm_kernel_knob());
   return out;
 }
 
@@ -138,10 +153,20 @@ at::Tensor addmm(const at::Tensor& self, const at::Tensor& mat1, const at::Tenso
     return at::addmm(self.cpu(), mat1.cpu(), mat2.cpu(), beta, alpha).to(self.device());
   }
   c10::DeviceGuard guard(self.device());
+  // TORCH_VULKAN_FUSE_ADDMM=0 (csrc/ops/mm.cpp:900-916): no bias epilogue,
+  // out = mm, scaled by alpha unless it is 1, plus beta * bias unless beta is
+  // 0 (so a NaN bias is still ignored at beta == 0).
+  const char* fuse = std::getenv("TORCH_VULKAN_FUSE_ADDMM");
+  if (fuse && std::strcmp(fuse, "0") == 0 && shape[0] > 0 && shape[1] > 0 && mat1.size(1) > 0) {
+    at::Tensor product = mm_impl(mat1, mat2, nullptr);
+    if (alpha.toFloat() != 1.0f) product = product.mul(alpha);
+    if (beta.toFloat() == 0.0f) return product;
+    return product.add(bias, beta);
+  }
   at::Tensor out = at::empty(shape, mat1.options());
   if (shape[0] == 0 || shape[1] == 0) return out;
   const at::Tensor bias_arg = self.dim() == 1 && self.size(0) == shape[1] ? self : bias;
-  run_gemm(mat1, mat2, out, 1, &bias_arg, alpha.toFloat(), beta.toFloat());
+  run_gemm(mat1, mat2, out, 1, &bias_arg, alpha.toFloat(), beta.toFloat(), mm_kernel_knob());
   return out;
 }
 

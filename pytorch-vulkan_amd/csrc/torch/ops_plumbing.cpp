@@ -252,6 +252,49 @@ const at::Tensor& resize_(const at::Tensor& self, at::IntArrayRef size, std::opt
   return self;
 }
 
+// set_ onto an existing device storage (metadata only: the tensor then
+// aliases `source` at `offset` with the given sizes and strides, contiguous
+// when `stride` is empty).  copy.deepcopy of a device tensor reaches it after
+// cloning the storage, as torch.optim checkpoints do.  The view must fit the
+// storage, as for any other device: the storage is not grown here.
+at::Tensor& set_storage_offset(at::Tensor& self, c10::Storage source, int64_t offset, at::IntArrayRef size,
+                               at::IntArrayRef stride) {
+  TORCH_CHECK(source.device().type() == c10::DeviceType::PrivateUse1 || source.nbytes() == 0,
+              "set_: expected a vulkan storage, got one on ", source.device());
+  TORCH_CHECK(offset >= 0, "set_: negative storage offset");
+  TORCH_CHECK(stride.empty() || stride.size() == size.size(), "set_: ", size.size(), " sizes but ", stride.size(),
+              " strides");
+  int64_t last = offset;  // one past the largest element index the view reaches
+  bool empty = false;
+  for (size_t i = 0; i < size.size(); ++i) {
+    TORCH_CHECK(size[i] >= 0, "set_: negative size");
+    if (size[i] == 0) empty = true;
+  }
+  if (!empty) {
+    if (stride.empty()) {
+      last += c10::multiply_integers(size);
+    } else {
+      for (size_t i = 0; i < size.size(); ++i) last += (size[i] - 1) * stride[i];
+      last += 1;
+    }
+    TORCH_CHECK(size_t(last) * self.element_size() <= source.nbytes(), "set_: a view of ", last,
+                " elements does not fit a storage of ", source.nbytes(), " bytes");
+  }
+  auto* impl = self.unsafeGetTensorImpl();
+  impl->set_storage_keep_dtype(std::move(source));
+  if (stride.empty())
+    impl->set_sizes_contiguous(size);
+  else
+    impl->set_sizes_and_strides(size, stride);
+  impl->set_storage_offset(offset);
+  return self;
+}
+
+at::Tensor& set_storage(at::Tensor& self, c10::Storage source) {
+  const int64_t n = int64_t(source.nbytes() / self.element_size());
+  return set_storage_offset(self, std::move(source), 0, {n}, {});
+}
+
 at::Scalar local_scalar_dense(const at::Tensor& self) {
   TORCH_CHECK(self.numel() == 1, "a Tensor with ", self.numel(), " elements cannot be converted to Scalar");
   c10::DeviceGuard guard(self.device());
@@ -470,6 +513,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("as_strided", TORCH_FN(tvk::as_strided));
   m.impl("_reshape_alias", TORCH_FN(tvk::reshape_alias));
   m.impl("resize_", TORCH_FN(tvk::resize_));
+  m.impl("set_.source_Storage_storage_offset", TORCH_FN(tvk::set_storage_offset));
+  m.impl("set_.source_Storage", TORCH_FN(tvk::set_storage));
   m.impl("_local_scalar_dense", TORCH_FN(tvk::local_scalar_dense));
   m.impl("fill_.Scalar", TORCH_FN(tvk::fill_scalar));
   m.impl("zero_", TORCH_FN(tvk::zero_));

@@ -38,7 +38,8 @@ __all__ = [
     "gpu_timing_stats", "reset_gpu_timing_stats",
     "memory_stats", "empty_cache", "queue_stats", "performance_options", "Stream", "Event",
     "current_stream", "default_stream", "set_stream", "stream", "manual_seed", "manual_seed_all",
-    "device",
+    "device", "is_hardware_accelerated", "runtime_hotpath_stats", "cache_stats", "clear_algorithm_cache",
+    "get_rng_state", "set_rng_state",
 ]
 
 
@@ -56,6 +57,54 @@ torch.Tensor.vulkan = _tensor_vulkan
 def is_available() -> bool:
     """True when at least one gfx950 device is visible."""
     return _C._is_available()
+
+
+def is_hardware_accelerated() -> bool:
+    """True when the device is a physical GPU (reference:
+    torch_vulkan/__init__.py:61-63, False there for a software rasteriser).
+    Every device this backend opens is a gfx950 GPU, so this is
+    ``is_available()``."""
+    return is_available()
+
+
+def runtime_hotpath_stats() -> dict:
+    """Cumulative host-side timers of the hot path, recorded when
+    ``TORCH_VULKAN_PROFILE_HOST_HOTPATH=1`` is set at start-up (the
+    reference's knob and keys): ``enqueue_ns`` / ``enqueue_count`` (host time
+    of each conv / GEMM / AdamW op's library calls), ``allocator_*`` (device
+    allocations, ``fresh`` = new device memory, ``reused`` = served from the
+    cache) and ``algo_hit_*`` / ``algo_miss_*`` (lookups in the convolution
+    autotune plan cache)."""
+    return dict(_C._runtime_hotpath_stats())
+
+
+def cache_stats() -> dict:
+    """The reference's cache counters (torch_vulkan/__init__.py:114-123).
+    HIP code objects are loaded once per process, so there is no pipeline or
+    command-sequence cache: ``pipeline_*`` and ``seq_*`` stay 0.  ``algo_*``
+    count the convolution autotune plan cache (hits, misses, evictions;
+    ``bound_algorithms`` is its size); the device allocator's cache is reported
+    as ``bound_cached_buffer_bytes`` (reserved but free bytes) and
+    ``allocator_cache_hits`` / ``allocator_device_mallocs``."""
+    conv = dict(_C._conv_dispatch_stats())
+    mem = dict(_C._memory_stats())
+    reserved = int(mem.get("reserved_bytes", 0))
+    allocated = int(mem.get("allocated_bytes", 0))
+    return {"algo_hits": int(conv.get("hits", 0)), "algo_misses": int(conv.get("misses", 0)),
+            "seq_reuses": 0, "seq_creates": 0, "algo_evictions": int(conv.get("evictions", 0)),
+            "bound_algorithms": int(conv.get("entries", 0)),
+            "bound_cached_buffer_bytes": max(0, reserved - allocated),
+            "pipeline_hits": 0, "pipeline_misses": 0, "pipeline_evictions": 0, "pipeline_entries": 0,
+            "allocator_cache_hits": int(mem.get("cache_hits", 0)),
+            "allocator_device_mallocs": int(mem.get("device_mallocs", 0))}
+
+
+def clear_algorithm_cache() -> None:
+    """Forget the convolution algorithms chosen by autotuning (the plan cache;
+    its counters stay).  The reference drops its compiled-pipeline cache here
+    (torch_vulkan/__init__.py:126-132); cached device memory is released by
+    ``empty_cache()``."""
+    _C._clear_conv_plan_cache()
 
 
 def device_count() -> int:
@@ -117,9 +166,11 @@ def gpu_timing_stats() -> dict:
     """Per-kernel GPU time of the conv / GEMM / AdamW ops since the last reset,
     recorded when ``TORCH_VULKAN_PROFILE_TIMESTAMPS=1`` (the reference's
     opt-in knob): ``{kernel: {"samples", "shader_ms", "host_eval_ms",
-    "upload_ms", "download_ms"}}``.  Waits for the timed work to finish.
-    ``shader_ms`` is the time between HIP events recorded around each op on
-    its stream; buffers never leave the device, so upload / download are 0."""
+    "upload_ms", "download_ms", "flops"}}``.  Waits for the timed work to
+    finish.  ``shader_ms`` is the time between HIP events recorded around each
+    op on its stream; ``flops`` the ops' algorithmic work (2 per multiply-add
+    of the direct convolution / GEMM); buffers never leave the device, so
+    upload / download are 0."""
     return dict(_C._gpu_timing_stats())
 
 
@@ -174,6 +225,20 @@ def seed() -> None:
 
 def seed_all() -> None:
     seed()
+
+
+def get_rng_state(device="vulkan") -> torch.Tensor:
+    """The device generator's state (seed and offset, 16 bytes), as the
+    reference's get_rng_state (torch_vulkan/__init__.py:190-193)."""
+    return _C._get_rng_state(_rng_device(device))
+
+
+def set_rng_state(state: torch.Tensor, device="vulkan") -> None:
+    _C._set_rng_state(_rng_device(device), state)
+
+
+def _rng_device(device) -> int:
+    return _validate_device(device)
 
 
 def _is_in_bad_fork() -> bool:

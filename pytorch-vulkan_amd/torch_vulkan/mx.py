@@ -24,7 +24,7 @@ MX_COPY_H2D, MX_COPY_D2H, MX_COPY_D2D = 1, 2, 3
 MX_CONV_FORWARD, MX_CONV_DINPUT, MX_CONV_DWEIGHT, MX_CONV_DBIAS = range(4)
 ALGO_AUTO, ALGO_DIRECT, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_REDUCE, ALGO_DEPTHWISE = range(6)
 BIAS_NONE, BIAS_COL, BIAS_MATRIX = range(3)
-ABI_VERSION = 2  # struct layouts of include/mx.h
+ABI_VERSION = 3  # struct layouts of include/mx.h
 
 # Every entry point declared in include/mx.h (checked by the CPU test suite).
 EXPORTS = [
@@ -41,6 +41,7 @@ EXPORTS = [
     "mx_unary_f32", "mx_unary_backward_f32", "mx_upsample_nearest2d", "mx_upsample_nearest2d_backward",
     "mx_softmax_f32", "mx_softmax_backward_f32", "mx_mse_loss_f32", "mx_mse_loss_backward_f32", "mx_copy_rows",
     "mx_foreach_f32", "mx_conv2d_plan", "mx_gemm_variant", "mx_conv2d_backward_weight_noalloc",
+    "mx_conv2d_backward_one_launch",
 ]
 
 
@@ -65,7 +66,8 @@ class GemmDesc(C.Structure):
                 ("batch", "m", "n", "k", "a_offset", "a_stride_b", "a_stride_m", "a_stride_k",
                  "b_offset", "b_stride_b", "b_stride_k", "b_stride_n", "c_offset", "c_stride_b", "ldc",
                  "bias_offset", "bias_stride_m", "bias_stride_n")] + [
-                ("alpha", C.c_float), ("beta", C.c_float), ("bias_kind", C.c_int), ("bias_stride_b", C.c_int64)]
+                ("alpha", C.c_float), ("beta", C.c_float), ("bias_kind", C.c_int), ("bias_stride_b", C.c_int64),
+                ("kernel", C.c_int)]
 
 
 class AdamWTensor(C.Structure):
@@ -149,6 +151,7 @@ def lib() -> C.CDLL:
             "mx_conv2d_backward_bias": ([C.POINTER(ConvDesc), vp, vp, vp], i32),
             "mx_conv2d_dweight_plan": ([C.POINTER(ConvDesc), C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)], i32),
             "mx_conv2d_kernel_name": ([C.POINTER(ConvDesc), i32, i32, C.c_char_p, C.c_size_t], i32),
+            "mx_conv2d_backward_one_launch": ([C.POINTER(ConvDesc), i32, i32, i32, C.POINTER(i32)], i32),
             "mx_gemm_f32": ([C.POINTER(GemmDesc), vp, vp, vp, vp, vp], i32),
             "mx_gemm_variant": ([C.POINTER(GemmDesc), vp, vp, C.c_char_p, C.c_size_t], i32),
             "mx_conv2d_plan": ([C.POINTER(ConvDesc), i32, i32, i32, C.POINTER(ConvPlanInfo)], i32),
@@ -419,6 +422,15 @@ def conv2d_kernel_name(d: ConvDesc, phase: int, algo: int = ALGO_AUTO) -> str:
     buf = C.create_string_buffer(128)
     check(lib().mx_conv2d_kernel_name(C.byref(d), phase, algo, buf, 128))
     return buf.value.decode()
+
+
+def conv2d_backward_one_launch(d: ConvDesc, algo_dx: int = ALGO_AUTO, algo_dw: int = ALGO_AUTO,
+                               with_bias: bool = True) -> bool:
+    """Whether conv2d_backward with these algorithms runs both gradients as
+    one Winograd launch (mx_conv2d_backward_one_launch)."""
+    one = C.c_int(0)
+    check(lib().mx_conv2d_backward_one_launch(C.byref(d), algo_dx, algo_dw, 1 if with_bias else 0, C.byref(one)))
+    return bool(one.value)
 
 
 def conv2d_plan(d: ConvDesc, phase: int, algo: int = ALGO_AUTO, with_bias: bool = True) -> dict:

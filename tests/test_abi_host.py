@@ -134,7 +134,7 @@ def test_forced_inapplicable_algorithm_raises(mx):
     assert mx.conv2d_select(same, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
     with pytest.raises(mx.MXError, match="winograd"):
         mx.conv2d_select(strided, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD)
-    assert mx.conv2d_kernel_name(same, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD) == "wino_dw_kernel"
+    assert mx.conv2d_kernel_name(same, mx.MX_CONV_DWEIGHT, mx.ALGO_WINOGRAD) in ("wino_dw_kernel", "wino_dw_ws_kernel")
     with pytest.raises(mx.MXError):
         mx.conv2d_select(strided, mx.MX_CONV_FORWARD, mx.ALGO_REDUCE)
 
@@ -153,6 +153,17 @@ def test_kernel_names(mx):
     assert mx.conv2d_kernel_name(c1, mx.MX_CONV_FORWARD).startswith("conv_fwd_kernel<")
     assert mx.conv2d_kernel_name(c1, mx.MX_CONV_DWEIGHT).startswith("conv_dw_kernel<")
     assert mx.conv2d_kernel_name(c1, mx.MX_CONV_FORWARD, mx.ALGO_WINOGRAD).startswith("wino")
+    # Winograd names are the kernels that carry the call (profiler names),
+    # taken from the plan's variant.
+    for phase in (mx.MX_CONV_FORWARD, mx.MX_CONV_DINPUT, mx.MX_CONV_DWEIGHT):
+        variant = mx.conv2d_plan(c1, phase, mx.ALGO_WINOGRAD)["variant"]
+        name = mx.conv2d_kernel_name(c1, phase, mx.ALGO_WINOGRAD)
+        assert variant.startswith(name) and name in ("wino_ws_kernel", "wino_ws16_kernel", "wino_dw_ws_kernel",
+                                                     "wino_dw_kernel"), (phase, name, variant)
+    # C1's two Winograd gradients run as one launch; the implicit GEMM's do not.
+    assert mx.conv2d_backward_one_launch(c1, mx.ALGO_WINOGRAD, mx.ALGO_WINOGRAD)
+    assert not mx.conv2d_backward_one_launch(c1, mx.ALGO_AUTO, mx.ALGO_AUTO)
+    assert not mx.conv2d_backward_one_launch(c1, mx.ALGO_WINOGRAD, mx.ALGO_IMPLICIT_GEMM)
 
 
 def test_gemm_rejects_bad_descriptor(mx):
@@ -206,6 +217,7 @@ def test_conv_entry_points_reject_null_descriptor(mx):
         lambda: L.mx_conv2d_backward(None, None, None, None, None, None, None, mx.ALGO_AUTO, mx.ALGO_AUTO, None),
         lambda: L.mx_conv2d_backward_weight_noalloc(None, None, None, None, None, mx.ALGO_AUTO, None),
         lambda: L.mx_conv2d_kernel_name(None, mx.MX_CONV_FORWARD, mx.ALGO_AUTO, buf, len(buf)),
+        lambda: L.mx_conv2d_backward_one_launch(None, mx.ALGO_AUTO, mx.ALGO_AUTO, 1, C.byref(algo)),
         lambda: L.mx_conv2d_dweight_plan(None, C.byref(n1), C.byref(n2), C.byref(n3)),
     ]
     if info is not None:
@@ -213,3 +225,52 @@ def test_conv_entry_points_reject_null_descriptor(mx):
     for call in calls:
         with pytest.raises(mx.MXError, match="null (descriptor|argument)"):
             mx.check(call())
+
+
+def test_tile_knob_changes_the_plan(mx, monkeypatch):
+    """TORCH_VULKAN_CONV_TILE (csrc/ops/convolution.cpp:411-414) reaches the
+    planner: C1's forward moves to the named tile of this build's menu, a
+    fixed-3x3 name on a 1x1 layer plans the base tile under AUTO and is
+    rejected when the tiled algorithm is forced, and an unknown name raises
+    the reference's message."""
+    d = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (1, 1))
+    tiles = {}
+    for name in ("base", "wide", "tall", "register", "register3", "register3_hoist"):
+        monkeypatch.setenv("TORCH_VULKAN_CONV_TILE", name)
+        tiles[name] = mx.conv2d_plan(d, mx.MX_CONV_FORWARD, mx.ALGO_IMPLICIT_GEMM)["tile"]
+        assert mx.conv2d_plan(d, mx.MX_CONV_DINPUT, mx.ALGO_IMPLICIT_GEMM)["tile"] >= 0
+        assert mx.conv2d_plan(d, mx.MX_CONV_DWEIGHT, mx.ALGO_IMPLICIT_GEMM)["tile"] >= 0
+    assert len({tiles[n] for n in ("base", "wide", "tall", "register")}) == 4, tiles
+    assert tiles["register3_hoist"] == tiles["register"]
+    monkeypatch.setenv("TORCH_VULKAN_CONV_TILE", "register3")
+    pointwise = mx.conv_desc((8, 64, 56, 56), (64, 64, 1, 1))
+    assert mx.conv2d_plan(pointwise, mx.MX_CONV_FORWARD)["tile"] == tiles["base"]
+    with pytest.raises(mx.MXError, match="tiled_register3 exceeds"):
+        mx.conv2d_select(pointwise, mx.MX_CONV_FORWARD, mx.ALGO_IMPLICIT_GEMM)
+    monkeypatch.setenv("TORCH_VULKAN_CONV_TILE", "huge")
+    with pytest.raises(mx.MXError, match="TORCH_VULKAN_CONV_TILE must be auto/base/wide/tall/register"):
+        mx.conv2d_select(d, mx.MX_CONV_FORWARD)
+    monkeypatch.setenv("TORCH_VULKAN_CONV_TILE", "auto")
+    auto = mx.conv2d_plan(d, mx.MX_CONV_FORWARD)["tile"]
+    monkeypatch.delenv("TORCH_VULKAN_CONV_TILE")
+    assert mx.conv2d_plan(d, mx.MX_CONV_FORWARD)["tile"] == auto
+
+
+def test_gemm_kernel_class_reaches_the_tile_choice(mx):
+    """mx_gemm_desc.kernel, the counterpart of TORCH_VULKAN_MM_KERNEL
+    (csrc/ops/mm.cpp:299-307): 'tiled' forces the 64x64 tile, 'register' keeps
+    the large tiles even where the cost model would pick the small one."""
+    def variant(m, n, k, kernel):
+        d = mx.GemmDesc(batch=1, m=m, n=n, k=k, a_stride_m=k, a_stride_k=1, b_stride_k=n, b_stride_n=1, ldc=n,
+                        alpha=1.0, kernel=kernel)
+        return mx.gemm_variant(d)
+    assert variant(8192, 4096, 4096, 1).startswith("gemm_kernel<64x64")
+    assert not variant(8192, 4096, 4096, 0).startswith("gemm_kernel<64x64")
+    assert not variant(8192, 4096, 4096, 2).startswith("gemm_kernel<64x64")
+    assert variant(64, 64, 64, 0).startswith("gemm_kernel<64x64")
+    assert not variant(64, 64, 64, 2).startswith("gemm_kernel<64x64")
+    import ctypes as C
+    d = mx.GemmDesc(batch=1, m=4, n=4, k=4, a_stride_m=4, a_stride_k=1, b_stride_k=4, b_stride_n=1, ldc=4, kernel=7)
+    buf = C.create_string_buffer(64)
+    with pytest.raises(mx.MXError, match="kernel class"):
+        mx.check(mx.lib().mx_gemm_variant(C.byref(d), C.c_void_p(256), C.c_void_p(256), buf, 64))

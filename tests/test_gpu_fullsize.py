@@ -10,7 +10,7 @@ does not depend on size:
 * C3 (ResNet-50 conv stack at batch 64): all 53 layers, forward / dInput /
   dWeight routed as bench.py routes them (3x3 stride-1 layers on Winograd),
   ~400 sampled outputs per phase against float64 on the host;
-* C4 (the U-Net at base width 128, 64 x 64 images, batch 2): one training
+* C4 (the U-Net at base width 128, 64 x 64 images, batch 16): one training
   step on the "vulkan" device against the same step in float64 on the CPU,
   each gradient within a small multiple of CPU FP32's own error;
 * C5 (AdamW over 250 tensors, 125M elements): one step from a state warmed for
@@ -204,10 +204,10 @@ def test_c3_conv_stack_full_size(mx):
 
 # ------------------------------------------------------------------ C4
 def test_c4_unet_full_width_step(mx):
-    """The C4 U-Net at its real width and resolution (base 128, 64 x 64),
-    batch 2, on the "vulkan" device: loss and every gradient against float64
-    CPU, each within four times CPU FP32's own error plus 1e-6 of the tensor's
-    largest gradient."""
+    """The C4 U-Net at its real configuration (base 128, 64 x 64, batch 16,
+    the step bench.py times), on the "vulkan" device: loss and every gradient
+    against float64 CPU, each within four times CPU FP32's own error plus 1e-6
+    of the tensor's largest gradient."""
     import os
 
     import torch_vulkan  # noqa: F401
@@ -217,7 +217,7 @@ def test_c4_unet_full_width_step(mx):
     try:
         torch.manual_seed(0)
         model = U.make_model()
-        x, t = U.make_inputs(batch=2)
+        x, t = U.make_inputs(batch=16)
         ref = copy.deepcopy(model).double()
         loss_ref = U.train_step_loss(ref, x.double(), t.double())
         cpu32 = copy.deepcopy(model)
