@@ -284,7 +284,7 @@ def test_conv_winograd_forward(mx, monkeypatch, case, fused):
     yref, mag = conv_refs(x, w, b, dy, stride, padding, dilation, groups)["y"]
     y = torch.empty(yref.shape, device="cuda")
     mx.conv2d_forward(d, dev(x), dev(w), dev(b), y, mx.ALGO_WINOGRAD, stream())
-    close(y, yref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd y")
+    close(y, yref, rtol=WINOGRAD_RTOL, mag=mag, what="winograd y")
 
 
 def test_conv_winograd_batch_chunks(mx, monkeypatch):
@@ -299,7 +299,7 @@ def test_conv_winograd_batch_chunks(mx, monkeypatch):
     yref, mag = conv_refs(x, w, b, dy, (1, 1), (1, 1), (1, 1), 1)["y"]
     y = torch.empty(yref.shape, device="cuda")
     mx.conv2d_forward(d, dev(x), dev(w), dev(b), y, mx.ALGO_WINOGRAD, stream())
-    close(y, yref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd chunked y")
+    close(y, yref, rtol=WINOGRAD_RTOL, mag=mag, what="winograd chunked y")
 
 
 @pytest.mark.parametrize("fused", ["1", "0"], ids=["fused", "unfused"])
@@ -317,7 +317,7 @@ def test_conv_winograd_dinput(mx, monkeypatch, case, fused):
     ref, mag = conv_refs(x, w, b, dy, stride, padding, dilation, groups)["dx"]
     dx = torch.full(ref.shape, float("nan"), device="cuda")
     mx.conv2d_backward_input(d, dev(dy), dev(w), dx, mx.ALGO_WINOGRAD, stream())
-    close(dx, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd dx")
+    close(dx, ref, rtol=WINOGRAD_RTOL, mag=mag, what="winograd dx")
 
 
 # Tensors smaller than one patch row or whose rows straddle the tensor's
@@ -342,7 +342,7 @@ def test_conv_winograd_dweight(mx, case):
     dw = torch.full(w.shape, float("nan"), device="cuda")
     db = torch.full(b.shape, float("nan"), device="cuda")
     mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, db, mx.ALGO_WINOGRAD, stream())
-    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, atol=1e-4, mag=refs["dw"][1], what="winograd dw")
+    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, mag=refs["dw"][1], what="winograd dw")
     close(db, refs["db"][0], mag=refs["db"][1], what="db beside winograd dw")
 
 
@@ -356,7 +356,7 @@ def test_conv_winograd_dweight_large_k(mx):
     ref, mag = conv_refs(x, w, None, dy, (1, 1), (1, 1), (1, 1), 1)["dw"]
     dw = torch.full(w.shape, float("nan"), device="cuda")
     mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, None, mx.ALGO_WINOGRAD, stream())
-    close(dw, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd dw (C1)")
+    close(dw, ref, rtol=WINOGRAD_RTOL, mag=mag, what="winograd dw (C1)")
 
 
 def test_conv_winograd_dweight_batch_chunks(mx, monkeypatch):
@@ -371,7 +371,7 @@ def test_conv_winograd_dweight_batch_chunks(mx, monkeypatch):
     dw = torch.full(w.shape, float("nan"), device="cuda")
     db = torch.full(b.shape, float("nan"), device="cuda")
     mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, db, mx.ALGO_WINOGRAD, stream())
-    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, atol=1e-4, mag=refs["dw"][1], what="winograd chunked dw")
+    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, mag=refs["dw"][1], what="winograd chunked dw")
     close(db, refs["db"][0], mag=refs["db"][1], what="chunked db")
 
 
@@ -389,7 +389,7 @@ def test_conv_winograd_dweight_one_range(mx, monkeypatch):
     dw = torch.full(w.shape, float("nan"), device="cuda")
     db = torch.full(b.shape, float("nan"), device="cuda")
     mx.conv2d_backward_weight(d, dev(x), dev(dy), dw, db, mx.ALGO_WINOGRAD, stream())
-    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, atol=1e-4, mag=refs["dw"][1], what="winograd dw, one range")
+    close(dw, refs["dw"][0], rtol=WINOGRAD_RTOL, mag=refs["dw"][1], what="winograd dw, one range")
     close(db, refs["db"][0], mag=refs["db"][1], what="db beside winograd dw, one range")
 
 
@@ -405,7 +405,7 @@ def test_conv_winograd_dinput_batch_chunks(mx, monkeypatch):
     ref, mag = conv_refs(x, w, b, dy, (1, 1), (1, 1), (1, 1), 1)["dx"]
     dx = torch.full(ref.shape, float("nan"), device="cuda")
     mx.conv2d_backward_input(d, dev(dy), dev(w), dx, mx.ALGO_WINOGRAD, stream())
-    close(dx, ref, rtol=WINOGRAD_RTOL, atol=1e-4, mag=mag, what="winograd chunked dx")
+    close(dx, ref, rtol=WINOGRAD_RTOL, mag=mag, what="winograd chunked dx")
 
 
 def test_conv_closed_form_1x1(mx):

@@ -77,7 +77,7 @@ def test_winograd_fixture_vs_oracle(mx, name):
     y = torch.empty(g["dy"].shape, device="cuda")
     mx.conv2d_forward(d, dev(g["x"]), dev(g["w"]), dev(g["b"]), y, mx.ALGO_WINOGRAD, stream())
     yo, my = oracle.conv2d_forward(g["x"], g["w"], g["b"], stride, padding, (1, 1), groups, winograd=True)
-    assert_close_mag(y, t(yo), t(my), rtol=WINOGRAD_RTOL, atol=1e-4, what=name)
+    assert_close_mag(y, t(yo), t(my), rtol=WINOGRAD_RTOL, what=name)
 
 
 @pytest.mark.parametrize("shape", ["addmm_5_7_11", "addmm_32_64_19", "addmm_128_256_128"])

@@ -125,7 +125,7 @@ def test_forced_winograd(vk, monkeypatch):
     x, w = torch.randn(2, 16, 12, 12, generator=g), torch.randn(24, 16, 3, 3, generator=g) / 12
     ref, mag = conv_refs(x, w, None, torch.zeros(2, 24, 12, 12), (1, 1), (1, 1), (1, 1), 1)["y"]
     y = F.conv2d(x.to("vulkan"), w.to("vulkan"), None, 1, 1)
-    assert_close_mag(y, ref, mag, rtol=1e-3, atol=1e-4, what="winograd")
+    assert_close_mag(y, ref, mag, rtol=1e-3, what="winograd")
     assert vk.conv_dispatch_stats().get("selected_forward_winograd_f2", 0) >= 1
     with pytest.raises(RuntimeError):
         F.conv2d(x.to("vulkan"), w.to("vulkan"), None, 2, 1)  # stride 2 is not Winograd-eligible
@@ -147,8 +147,8 @@ def test_backward_winograd_knob(vk, monkeypatch):
         xv, wv = x.to("vulkan").requires_grad_(), w.to("vulkan").requires_grad_()
         yv = F.conv2d(xv, wv, None, stride, 1)
         gx, gw = torch.autograd.grad(yv, (xv, wv), dy.to("vulkan"))
-        assert_close_mag(gx, *refs["dx"], rtol=1e-3, atol=1e-4, what=f"dx stride {stride}")
-        assert_close_mag(gw, *refs["dw"], rtol=1e-3, atol=1e-4, what=f"dw stride {stride}")
+        assert_close_mag(gx, *refs["dx"], rtol=1e-3, what=f"dx stride {stride}")
+        assert_close_mag(gw, *refs["dw"], rtol=1e-3, what=f"dw stride {stride}")
         stats = vk.conv_dispatch_stats()
         assert stats.get(f"selected_dinput_{algo}", 0) >= 1, stats
         assert stats.get(f"selected_dweight_{algo}", 0) >= 1, stats

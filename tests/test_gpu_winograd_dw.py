@@ -54,7 +54,7 @@ def test_winograd_dweight_ranges(mx, case):
         dw = torch.full(w.shape, float("nan"), device="cuda")
         db = torch.full((cout,), float("nan"), device="cuda") if with_db else None
         mx.conv2d_backward_weight(d, X, DY, dw, db, mx.ALGO_WINOGRAD, st)
-        assert_close_mag(dw, *refs["dw"], rtol=WINOGRAD_RTOL, atol=1e-4, what=f"dw db={with_db}")
+        assert_close_mag(dw, *refs["dw"], rtol=WINOGRAD_RTOL, what=f"dw db={with_db}")
         if with_db:
             assert_close_mag(db, *refs["db"], what="db")
         first = dw.clone() if first is None else first
@@ -109,8 +109,7 @@ def test_combined_backward_matches_separate_calls(mx, case, monkeypatch):
         for name, got, want in zip(("dx", "dw", "db"), out, sep):
             if got is not None:
                 assert torch.equal(got, want), f"{case} mask {mask}: {name} differs from the separate call"
-                rtol = WINOGRAD_RTOL if name != "db" else 1e-4
-                assert_close_mag(got, *refs[name], rtol=rtol, atol=1e-4 if name != "db" else 1e-5, what=name)
+                assert_close_mag(got, *refs[name], rtol=WINOGRAD_RTOL if name != "db" else 1e-4, what=name)
 
 
 def test_combined_backward_other_algorithms(mx):
