@@ -440,7 +440,7 @@ def run_stream_probes(torch, numel, reps=20):
     plain copy and a 4-stream read sweep over buffers of C5's size, from
     libmxprobe.so; GB/s from HIP events on the current stream."""
     import ctypes as C
-    lib = C.CDLL(os.path.join(REPO, "pytorch-vulkan_amd", "torch_vulkan", "libmxprobe.so"))
+    lib = C.CDLL(os.path.join(REPO, "libmxprobe.so"))
     lib.mxp_stream.argtypes = [C.c_int, C.POINTER(C.c_void_p), C.c_int64, C.c_int, C.c_void_p]
     lib.mxp_stream.restype = C.c_int
     n = numel // 4096 * 4096

@@ -7,7 +7,7 @@ Outputs (next to the Python package so they travel with the source tree):
                          every gfx950 kernel, built with hipcc.
   torch_vulkan/_C.so     PrivateUse1 "vulkan" operator surface (C++ against
                          the installed torch headers), linked to libmx.so.
-  torch_vulkan/libmxprobe.so  HBM stream probes used by bench.py (not part of
+  ../libmxprobe.so            HBM stream probes used by bench.py, built beside it (not part of
                          the C ABI).
 
 libmx.so links the HIP runtime that ships inside the installed torch wheel
@@ -162,15 +162,16 @@ def build_mx(jobs: int, incremental: bool) -> Path:
 
 
 def build_probe(incremental: bool) -> Path:
-    """torch_vulkan/libmxprobe.so: bench.py's HBM stream probes
-    (csrc/bench/mx_stream_probe.hip), kept apart from the C ABI library."""
+    """libmxprobe.so at the repository root, beside bench.py: its HBM stream
+    probes (csrc/bench/mx_stream_probe.hip), outside the torch_vulkan package
+    and apart from the C ABI library."""
     BUILD.mkdir(exist_ok=True)
     _, torch_lib = torch_paths()
     src = CSRC / "bench" / "mx_stream_probe.hip"
     obj = BUILD / "mx_stream_probe.o"
     if not incremental or stale(obj, [src]):
         compile_hip([hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
-    lib = OUT / "libmxprobe.so"
+    lib = Path(__file__).resolve().parent.parent / "libmxprobe.so"
     if not incremental or stale(lib, [obj]):
         link_mx([obj], lib, hip_runtime_dir(torch_lib))
     return lib

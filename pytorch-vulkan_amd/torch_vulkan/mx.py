@@ -17,7 +17,9 @@ import os
 
 import torch  # noqa: F401  (HIP runtime first, see module docstring)
 
-_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmx.so")
+# MX_LIBRARY names another build of the same C ABI (the sanitizer build of
+# pytorch-vulkan_amd/sanitize.py); by default the in-tree libmx.so.
+_LIB_PATH = os.environ.get("MX_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmx.so")
 
 MX_OK, MX_ERR_INVALID, MX_ERR_UNSUPPORTED, MX_ERR_OOM, MX_ERR_HIP, MX_ERR_WORKSPACE = range(6)
 MX_COPY_H2D, MX_COPY_D2H, MX_COPY_D2D = 1, 2, 3
