@@ -422,7 +422,21 @@ bool winograd_applicable(const mx_conv2d_desc& d) {
 // Reference heuristic (csrc/ops/convolution.cpp:423-482) restated for the
 // MFMA candidates: implicit GEMM whenever the GEMM is not degenerate, Winograd
 // only for the grouped 3x3 case the reference routes there by default.
+int select_algo_heuristic(const mx_conv2d_desc& d, int phase, int requested, int* algo);
+
+// The implicit GEMM runs one grid-z slice per group: past 65535 groups AUTO
+// takes the direct kernels and a forced implicit GEMM is refused.
 int select_algo(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
+  MX_TRY(select_algo_heuristic(d, phase, requested, algo));
+  if (*algo == MX_CONV_ALGO_IMPLICIT_GEMM && d.groups > 65535) {
+    MX_REQUIRE(requested != MX_CONV_ALGO_IMPLICIT_GEMM, MX_ERR_UNSUPPORTED,
+               "conv2d implicit GEMM: at most 65535 groups (one launch slice per group)");
+    *algo = MX_CONV_ALGO_DIRECT;
+  }
+  return MX_OK;
+}
+
+int select_algo_heuristic(const mx_conv2d_desc& d, int phase, int requested, int* algo) {
   const int64_t cin_g = d.cin / d.groups, cout_g = d.cout / d.groups;
   const int64_t rows = d.n * d.oh * d.ow, cols = cin_g * d.kh * d.kw;
   MX_REQUIRE(requested >= MX_CONV_ALGO_AUTO && requested <= MX_CONV_ALGO_DEPTHWISE, MX_ERR_INVALID,
@@ -1119,7 +1133,9 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
     }
     if (set.n > 0) MX_TRY(conv::conv_dx_pack_weights(p, set, wt.as<float>(), s));
   }
-  // The reached phases in one launch per operand loader (up to four each).
+  // The reached phases in one launch per operand loader (up to four each,
+  // fewer when phases x groups would pass the 65535 limit of grid z).
+  const int max_set = int(std::max<int64_t>(1, std::min<int64_t>(conv::kMaxFusedPhases, 65535 / p.G)));
   for (int bmode : {int(conv::B_GATHER), int(conv::B_VEC)}) {
     conv::DxPhaseSet set{};
     set.G = p.G;
@@ -1128,7 +1144,7 @@ int mx_conv2d_backward_input(const mx_conv2d_desc* desc, const float* dy, const 
       if (q.K == 0 || f.bmodes[i] != bmode) continue;
       q.ws = ws.as<float>();
       set.q[set.n++] = q;
-      if (set.n == conv::kMaxFusedPhases) {
+      if (set.n == max_set) {
         MX_TRY(conv::conv_dx_launch_set(set, f.gp.tile, f.vec_a ? Mode::RVEC : Mode::RSCALAR, bmode, s));
         set.n = 0;
       }

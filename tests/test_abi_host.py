@@ -274,3 +274,16 @@ def test_gemm_kernel_class_reaches_the_tile_choice(mx):
     buf = C.create_string_buffer(64)
     with pytest.raises(mx.MXError, match="kernel class"):
         mx.check(mx.lib().mx_gemm_variant(C.byref(d), C.c_void_p(256), C.c_void_p(256), buf, 64))
+
+
+def test_implicit_gemm_group_limit(mx):
+    """The implicit GEMM runs one grid-z slice per group: past 65535 groups
+    AUTO takes the direct kernels and a forced implicit GEMM is refused with a
+    clear error, before any launch."""
+    many = mx.conv_desc((1, 140000, 4, 4), (70000, 2, 3, 3), (1, 1), (1, 1), (1, 1), 70000)
+    for phase in (mx.MX_CONV_FORWARD, mx.MX_CONV_DINPUT, mx.MX_CONV_DWEIGHT):
+        assert mx.conv2d_select(many, phase) != mx.ALGO_IMPLICIT_GEMM
+        with pytest.raises(mx.MXError, match="at most 65535 groups"):
+            mx.conv2d_select(many, phase, mx.ALGO_IMPLICIT_GEMM)
+    fine = mx.conv_desc((1, 40000, 4, 4), (20000, 2, 3, 3), (2, 2), (1, 1), (1, 1), 20000)
+    assert mx.conv2d_select(fine, mx.MX_CONV_DINPUT, mx.ALGO_IMPLICIT_GEMM) == mx.ALGO_IMPLICIT_GEMM

@@ -164,6 +164,9 @@ CONV_CASES = [
     # small-channel layers of the C4 U-Net: 3-channel input conv and output head
     ((2, 3, 64, 64), 128, (3, 3), (1, 1), (1, 1), (1, 1), 1),
     ((2, 128, 64, 64), 3, (3, 3), (1, 1), (1, 1), (1, 1), 1),
+    # 20000 groups at stride 2: four dInput phases x 20000 groups pass the
+    # 65535 grid-z limit of one fused phase launch, so the phases split
+    ((1, 40000, 4, 4), 20000, (3, 3), (2, 2), (1, 1), (1, 1), 20000),
 ]
 
 
