@@ -165,10 +165,13 @@ enum mx_conv_phase { MX_CONV_FORWARD = 0, MX_CONV_DINPUT = 1, MX_CONV_DWEIGHT = 
 
 /* Algorithms (candidate menu of csrc/ops/convolution.cpp:161-187):
  * AUTO lets the planner choose; DIRECT is one-output-per-thread; IMPLICIT_GEMM
- * is the MFMA tile path; WINOGRAD is F(2x2,3x3) for the forward and, when
- * requested explicitly, the input gradient of a 3x3 stride-1 dilation-1 layer
- * with padding <= 2 (an addition: the reference's Winograd is forward only;
- * AUTO never picks it for dInput); REDUCE is the no-scratch dWeight / dBias
+ * is the MFMA tile path; WINOGRAD is F(2x2,3x3) for the forward, the input
+ * gradient (padding <= 2) and the weight gradient of a 3x3 stride-1
+ * dilation-1 layer (the gradients are an addition: the reference's Winograd is
+ * forward only); AUTO takes it in every phase for such layers with padding
+ * <= 2, >= 32 channels per group on both sides and >= 1024 output positions
+ * (2048 for the weight gradient), where it measures faster than the implicit GEMM on
+ * MI355X, and for the reference's grouped forward rule; REDUCE is the no-scratch dWeight / dBias
  * reduction; DEPTHWISE is the forward of a layer with groups == cin and any
  * channel multiplier (conv2d_depthwise.comp:15-41; candidate rule
  * csrc/ops/convolution.cpp:361, chosen by AUTO when cin >= 8 as at :462). */

@@ -419,9 +419,28 @@ bool winograd_applicable(const mx_conv2d_desc& d) {
   return d.kh == 3 && d.kw == 3 && d.sh == 1 && d.sw == 1 && d.dh == 1 && d.dw == 1;
 }
 
+// AUTO's Winograd rule for 3x3 stride-1 layers with at least 32 channels per
+// group on both sides, measured on MI355X per phase against the implicit GEMM
+// (kernel time, batch 1-64, 64-1024 channels, 7^2-64^2 images): from 1024
+// output positions the fused F(2x2,3x3) forward and input gradient take
+// 0.50-0.89 of the implicit GEMM's time (8x64 channels at 56^2: 17.8 vs 35.6
+// us; 16x128 at 64^2: 98 vs 184; 16x512 at 8^2: 45.5 vs 60.0) and lose only on
+// smaller layers (1x256 at 14^2: 28.8 vs 17.2); the weight gradient wins from
+// 2048 positions (0.55-0.83) and loses at 1568 (12.5 vs 11.5).  This replaces
+// the reference heuristic for these layers (its Winograd is a grouped-layer
+// forward rule, csrc/ops/convolution.cpp:454-460, kept below); every other
+// layer, and padding beyond 2, keeps the reference's choices.
+bool winograd_auto(const mx_conv2d_desc& d, int phase) {
+  if (!winograd_applicable(d) || d.ph > 2 || d.pw > 2 || d.cin / d.groups < 32 || d.cout / d.groups < 32)
+    return false;
+  return d.n * d.oh * d.ow >= (phase == MX_CONV_DWEIGHT ? 2048 : 1024);
+}
+
 // Reference heuristic (csrc/ops/convolution.cpp:423-482) restated for the
 // MFMA candidates: implicit GEMM whenever the GEMM is not degenerate, Winograd
-// only for the grouped 3x3 case the reference routes there by default.
+// for the grouped 3x3 case the reference routes there by default and, in all
+// three phases, for the 3x3 stride-1 layers where it measures faster on
+// MI355X (winograd_auto).
 int select_algo_heuristic(const mx_conv2d_desc& d, int phase, int requested, int* algo);
 
 // The implicit GEMM runs one grid-z slice per group: past 65535 groups AUTO
@@ -472,7 +491,8 @@ int select_algo_heuristic(const mx_conv2d_desc& d, int phase, int requested, int
       // Small-channel layers (a 3-channel stem or output head) still go to
       // the MFMA implicit GEMM: a mostly-empty tile row is cheaper than the
       // direct kernel's per-output loop once the GEMM has real depth.
-      if (winograd_applicable(d) && d.groups >= 4 && cin_g >= 16 && cout_g >= 16 && rows >= 2048)
+      if ((winograd_applicable(d) && d.groups >= 4 && cin_g >= 16 && cout_g >= 16 && rows >= 2048) ||
+          winograd_auto(d, MX_CONV_FORWARD))
         *algo = MX_CONV_ALGO_WINOGRAD;
       else if (d.groups == d.cin && d.cin >= 8)
         *algo = MX_CONV_ALGO_DEPTHWISE;
@@ -497,6 +517,10 @@ int select_algo_heuristic(const mx_conv2d_desc& d, int phase, int requested, int
         *algo = requested;
         return MX_OK;
       }
+      if (winograd_auto(d, MX_CONV_DINPUT)) {
+        *algo = MX_CONV_ALGO_WINOGRAD;
+        return MX_OK;
+      }
       *algo = (cin_g >= 2 && cout_g * d.kh * d.kw >= 8 && cin_g * cout_g * d.kh * d.kw >= 64 &&
                d.n * d.h * d.w >= 32)
                   ? MX_CONV_ALGO_IMPLICIT_GEMM
@@ -517,7 +541,9 @@ int select_algo_heuristic(const mx_conv2d_desc& d, int phase, int requested, int
         *algo = requested;
         return MX_OK;
       }
-      if (rows >= 64 && cout_g * cols >= 64)
+      if (winograd_auto(d, MX_CONV_DWEIGHT))
+        *algo = MX_CONV_ALGO_WINOGRAD;
+      else if (rows >= 64 && cout_g * cols >= 64)
         *algo = MX_CONV_ALGO_IMPLICIT_GEMM;
       else if (rows >= 128)
         *algo = MX_CONV_ALGO_REDUCE;

@@ -411,7 +411,7 @@ struct TimedPair {
   void* start;
   void* end;
   double host_ms;
-  double flops;
+  double flops, exec_flops;
 };
 // Event pairs wait in g_timing_pending until gpu_timing_stats() reads them;
 // past kPendingCap pairs, the ones whose work has completed are folded into
@@ -442,6 +442,7 @@ static void fold_pair(const TimedPair& t, std::map<std::string, GpuTiming>& into
   a.samples++;
   a.host_eval_ms += t.host_ms;
   a.flops += t.flops;
+  a.executed_flops += t.exec_flops;
   if (ok) a.shader_ms += ms;
 }
 
@@ -505,11 +506,12 @@ std::map<std::string, uint64_t> hotpath_stats() {
   return r;
 }
 
-GpuTimer::GpuTimer(std::string name, double flops) {
+GpuTimer::GpuTimer(std::string name, double flops, double executed_flops) {
   if (host_hotpath_enabled()) hot_t0_ = steady_ns();
   if (!gpu_timing_enabled() || name.empty()) return;
   name_ = std::move(name);
   flops_ = flops;
+  exec_flops_ = executed_flops < 0 ? flops : executed_flops;
   stream_ = current_stream();
   TVK_MX(mx_event_create(&start_, 1));
   TVK_MX(mx_event_record(start_, stream_));
@@ -526,7 +528,7 @@ GpuTimer::~GpuTimer() {
     return;
   }
   std::lock_guard<std::mutex> lock(g_timing_mu);
-  g_timing_pending.push_back({name_, start_, end, now_ms() - host_t0_, flops_});
+  g_timing_pending.push_back({name_, start_, end, now_ms() - host_t0_, flops_, exec_flops_});
   if (g_timing_pending.size() > kPendingCap) fold_completed_locked();
 }
 
@@ -545,6 +547,7 @@ std::map<std::string, GpuTiming> gpu_timing_stats() {
     g.shader_ms += a.shader_ms;
     g.host_eval_ms += a.host_eval_ms;
     g.flops += a.flops;
+    g.executed_flops += a.executed_flops;
   }
   return g_timing;
 }
@@ -569,6 +572,7 @@ py::dict gpu_timing_dict() {
     d["shader_ms"] = v.shader_ms;
     d["host_eval_ms"] = v.host_eval_ms;
     d["flops"] = v.flops;
+    d["executed_flops"] = v.executed_flops;
     // Buffers stay resident on the device: there is no per-op upload or download.
     d["upload_ms"] = 0.0;
     d["download_ms"] = 0.0;

@@ -66,9 +66,7 @@ void note_cpu_fallback(const char* what);
 // (the kernel the op runs); gpu_timing_stats() waits for the pairs and sums
 // them per name.  When the knob is off a scope costs one getenv.
 bool gpu_timing_enabled();
-// Times the ops of its scope on the current stream with two HIP events when
-// TORCH_VULKAN_PROFILE_TIMESTAMPS=1 (an empty name times nothing).  `flops`
-// is the scope's algorithmic work (2 per multiply-add), summed per name.
+
 // Host hot-path timers (TORCH_VULKAN_PROFILE_HOST_HOTPATH=1, read once, the
 // reference's knob, csrc/vulkan_context.cpp:29-58): cumulative nanoseconds and
 // counts under the reference's keys.  `key` is "enqueue" (host time of one
@@ -78,9 +76,14 @@ bool host_hotpath_enabled();
 void record_hotpath(const char* key, uint64_t nanos, bool fresh = false, size_t bytes = 0);
 std::map<std::string, uint64_t> hotpath_stats();
 
+// Times the ops of its scope on the current stream with two HIP events when
+// TORCH_VULKAN_PROFILE_TIMESTAMPS=1 (an empty name times nothing).  `flops`
+// is the scope's algorithmic work (2 per multiply-add of the direct
+// convolution / GEMM) and `executed_flops` the multiply-adds its kernels run
+// (fewer for Winograd; negative: the same as `flops`), both summed per name.
 class GpuTimer {
  public:
-  explicit GpuTimer(std::string name, double flops = 0.0);
+  explicit GpuTimer(std::string name, double flops = 0.0, double executed_flops = -1.0);
   ~GpuTimer();
   GpuTimer(const GpuTimer&) = delete;
   GpuTimer& operator=(const GpuTimer&) = delete;
@@ -90,12 +93,12 @@ class GpuTimer {
   void* start_ = nullptr;
   void* stream_ = nullptr;
   double host_t0_ = 0;
-  double flops_ = 0;
+  double flops_ = 0, exec_flops_ = 0;
   int64_t hot_t0_ = -1;  // steady-clock ns when host hot-path timing is on
 };
 struct GpuTiming {
   uint64_t samples = 0;
-  double shader_ms = 0, host_eval_ms = 0, flops = 0;
+  double shader_ms = 0, host_eval_ms = 0, flops = 0, executed_flops = 0;
 };
 std::map<std::string, GpuTiming> gpu_timing_stats();
 void reset_gpu_timing_stats();

@@ -128,6 +128,17 @@ double conv_flops(const mx_conv2d_desc& d, int phase) {
          double(d.kh) * double(d.kw);
 }
 
+// FLOPs the phase's kernels execute: Winograd F(2x2,3x3) multiplies 16
+// transformed values per 2x2 tile and channel pair where the direct
+// convolution takes 36 products (the tiles of the input gradient cover the
+// input, the others the output); the transforms are not counted.
+double conv_exec_flops(const mx_conv2d_desc& d, int phase, int algo) {
+  if (algo != MX_CONV_ALGO_WINOGRAD || phase == MX_CONV_DBIAS) return conv_flops(d, phase);
+  const int64_t th = phase == MX_CONV_DINPUT ? (d.h + 1) / 2 : (d.oh + 1) / 2;
+  const int64_t tw = phase == MX_CONV_DINPUT ? (d.w + 1) / 2 : (d.ow + 1) / 2;
+  return 2.0 * 16.0 * double(d.n) * double(th) * double(tw) * double(d.cout) * double(d.cin / d.groups);
+}
+
 const char* const kPhaseNames[] = {"forward", "dinput", "dweight", "dbias"};
 
 // TORCH_VULKAN_CONV_TILE as the caller set it ("" for unset / auto).  The
@@ -297,7 +308,8 @@ at::Tensor convolution_overrideable(const at::Tensor& input, const at::Tensor& w
                              current_stream()));
   };
   const int algo = choose(d, MX_CONV_FORWARD, forward_algo(), b.defined(), run);
-  GpuTimer timer(kernel_label(d, MX_CONV_FORWARD, algo), conv_flops(d, MX_CONV_FORWARD));
+  GpuTimer timer(kernel_label(d, MX_CONV_FORWARD, algo), conv_flops(d, MX_CONV_FORWARD),
+                 conv_exec_flops(d, MX_CONV_FORWARD, algo));
   run(algo);
   counters().kernel_launches++;
   return y;
@@ -369,19 +381,22 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> convolution_backward_overrideable
     // (convolution_backward's dispatch of Input, Weight and Bias,
     // csrc/ops/convolution.cpp:667-697).
     GpuTimer timer(gpu_timing_enabled() ? "wino_bwd_kernel" : "",
-                   conv_flops(d, MX_CONV_DINPUT) + conv_flops(d, MX_CONV_DWEIGHT));
+                   conv_flops(d, MX_CONV_DINPUT) + conv_flops(d, MX_CONV_DWEIGHT),
+                   conv_exec_flops(d, MX_CONV_DINPUT, ax) + conv_exec_flops(d, MX_CONV_DWEIGHT, aw));
     TVK_MX(mx_conv2d_backward(&d, x.data_ptr<float>(), w.data_ptr<float>(), dy.data_ptr<float>(),
                               dx.data_ptr<float>(), dw.data_ptr<float>(), dbw, ax, aw, current_stream()));
     counters().kernel_launches++;
     return {dx, dw, db};
   }
   if (output_mask[0]) {
-    GpuTimer timer(kernel_label(d, MX_CONV_DINPUT, ax), conv_flops(d, MX_CONV_DINPUT));
+    GpuTimer timer(kernel_label(d, MX_CONV_DINPUT, ax), conv_flops(d, MX_CONV_DINPUT),
+                   conv_exec_flops(d, MX_CONV_DINPUT, ax));
     run_dx(ax);
     counters().kernel_launches++;
   }
   if (output_mask[1]) {
-    GpuTimer timer(kernel_label(d, MX_CONV_DWEIGHT, aw), conv_flops(d, MX_CONV_DWEIGHT));
+    GpuTimer timer(kernel_label(d, MX_CONV_DWEIGHT, aw), conv_flops(d, MX_CONV_DWEIGHT),
+                   conv_exec_flops(d, MX_CONV_DWEIGHT, aw));
     run_dw(aw);
     counters().kernel_launches++;
   } else if (output_mask[2]) {

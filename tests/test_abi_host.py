@@ -81,11 +81,32 @@ def test_conv_validation_errors(mx, xs, ws, kw, msg):
 
 
 def test_planner_mirrors_reference_heuristic(mx):
+    """The reference's candidates (csrc/ops/convolution.cpp:423-482) except
+    for dense 3x3 stride-1 layers, which AUTO routes to Winograd in every
+    phase above the measured break-even sizes."""
     dense = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (1, 1))
-    assert mx.conv2d_select(dense, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
-    assert mx.conv2d_select(dense, mx.MX_CONV_DINPUT) == mx.ALGO_IMPLICIT_GEMM
-    assert mx.conv2d_select(dense, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    for phase in (mx.MX_CONV_FORWARD, mx.MX_CONV_DINPUT, mx.MX_CONV_DWEIGHT):
+        assert mx.conv2d_select(dense, phase) == mx.ALGO_WINOGRAD
     assert mx.conv2d_select(dense, mx.MX_CONV_DBIAS) == mx.ALGO_REDUCE
+    dense5 = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 5), (1, 1), (1, 2))
+    assert mx.conv2d_select(dense5, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
+    assert mx.conv2d_select(dense5, mx.MX_CONV_DINPUT) == mx.ALGO_IMPLICIT_GEMM
+    assert mx.conv2d_select(dense5, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    strided = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (2, 2), (1, 1))
+    assert mx.conv2d_select(strided, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
+    # Break-even sizes: 1024 output positions (forward, dInput), 2048 (dWeight).
+    b1 = mx.conv_desc((1, 64, 32, 32), (64, 64, 3, 3), (1, 1), (1, 1))     # 1024 positions
+    assert mx.conv2d_select(b1, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
+    assert mx.conv2d_select(b1, mx.MX_CONV_DINPUT) == mx.ALGO_WINOGRAD
+    assert mx.conv2d_select(b1, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    small = mx.conv_desc((1, 256, 14, 14), (256, 256, 3, 3), (1, 1), (1, 1))  # 196 positions
+    for phase in (mx.MX_CONV_FORWARD, mx.MX_CONV_DINPUT, mx.MX_CONV_DWEIGHT):
+        assert mx.conv2d_select(small, phase) == mx.ALGO_IMPLICIT_GEMM
+    thin = mx.conv_desc((16, 16, 64, 64), (64, 16, 3, 3), (1, 1), (1, 1))     # 16 input channels
+    assert mx.conv2d_select(thin, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
+    wide_pad = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (3, 3))  # padding beyond 2
+    for phase in (mx.MX_CONV_FORWARD, mx.MX_CONV_DINPUT, mx.MX_CONV_DWEIGHT):
+        assert mx.conv2d_select(wide_pad, phase) == mx.ALGO_IMPLICIT_GEMM
     grouped = mx.conv_desc((2, 128, 64, 64), (128, 16, 3, 3), (1, 1), (1, 1), (1, 1), 8)
     assert mx.conv2d_select(grouped, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
     tiny = mx.conv_desc((1, 1, 4, 4), (2, 1, 1, 1))
@@ -150,8 +171,8 @@ def test_dweight_split_plan(mx):
 
 def test_kernel_names(mx):
     c1 = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (1, 1), (1, 1))
-    assert mx.conv2d_kernel_name(c1, mx.MX_CONV_FORWARD).startswith("conv_fwd_kernel<")
-    assert mx.conv2d_kernel_name(c1, mx.MX_CONV_DWEIGHT).startswith("conv_dw_kernel<")
+    assert mx.conv2d_kernel_name(c1, mx.MX_CONV_FORWARD, mx.ALGO_IMPLICIT_GEMM).startswith("conv_fwd_kernel<")
+    assert mx.conv2d_kernel_name(c1, mx.MX_CONV_DWEIGHT, mx.ALGO_IMPLICIT_GEMM).startswith("conv_dw_kernel<")
     assert mx.conv2d_kernel_name(c1, mx.MX_CONV_FORWARD, mx.ALGO_WINOGRAD).startswith("wino")
     # Winograd names are the kernels that carry the call (profiler names),
     # taken from the plan's variant.
@@ -160,9 +181,11 @@ def test_kernel_names(mx):
         name = mx.conv2d_kernel_name(c1, phase, mx.ALGO_WINOGRAD)
         assert variant.startswith(name) and name in ("wino_ws_kernel", "wino_ws16_kernel", "wino_dw_ws_kernel",
                                                      "wino_dw_kernel"), (phase, name, variant)
-    # C1's two Winograd gradients run as one launch; the implicit GEMM's do not.
+    # C1's two Winograd gradients (AUTO's choice) run as one launch; the
+    # implicit GEMM's do not.
     assert mx.conv2d_backward_one_launch(c1, mx.ALGO_WINOGRAD, mx.ALGO_WINOGRAD)
-    assert not mx.conv2d_backward_one_launch(c1, mx.ALGO_AUTO, mx.ALGO_AUTO)
+    assert mx.conv2d_backward_one_launch(c1, mx.ALGO_AUTO, mx.ALGO_AUTO)
+    assert not mx.conv2d_backward_one_launch(c1, mx.ALGO_IMPLICIT_GEMM, mx.ALGO_IMPLICIT_GEMM)
     assert not mx.conv2d_backward_one_launch(c1, mx.ALGO_WINOGRAD, mx.ALGO_IMPLICIT_GEMM)
 
 
