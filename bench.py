@@ -472,6 +472,41 @@ def run_stream_probes(torch, numel, reps=20):
     return out
 
 
+def run_probe_sweep(torch, numel, reps=20):
+    """The 4-read / 3-write in-place mix of run_stream_probes over buffers of
+    C5's size under each memory schedule of libmxprobe.so's mxp_mix_sweep:
+    float4 per stream per thread per chunk (vec), next chunk's loads before
+    this chunk's stores (prefetch), contiguous runs of chunks per workgroup
+    instead of round-robin (contig), and workgroups per CU.  GB/s counts 28
+    bytes per element; rows sorted fastest first."""
+    import ctypes as C
+    lib = C.CDLL(os.path.join(REPO, "libmxprobe.so"))
+    lib.mxp_mix_sweep.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_void_p), C.c_int64, C.c_int, C.c_void_p]
+    lib.mxp_mix_sweep.restype = C.c_int
+    n = numel // 8192 * 8192
+    bufs = [torch.full((n,), 0.5, device="cuda") for _ in range(4)]
+    ptrs = (C.c_void_p * 4)(*[b.data_ptr() for b in bufs])
+    st = torch.cuda.current_stream()
+    rows = []
+    for vec in (1, 2, 4, 8):
+        for prefetch in (0, 1):
+            for contig in (0, 1):
+                for per_cu in (1, 2, 4, 8, 16, 32):
+                    for _ in range(3):
+                        assert lib.mxp_mix_sweep(vec, prefetch, contig, ptrs, n, per_cu, st.cuda_stream) == 0
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(st)
+                    for _ in range(reps):
+                        lib.mxp_mix_sweep(vec, prefetch, contig, ptrs, n, per_cu, st.cuda_stream)
+                    e1.record(st)
+                    e1.synchronize()
+                    rows.append({"vec": vec, "prefetch": prefetch, "contig": contig, "wg_per_cu": per_cu,
+                                 "gb_s": round(28 * n / (e0.elapsed_time(e1) / reps * 1e-3) / 1e9, 1)})
+    del bufs
+    torch.cuda.empty_cache()
+    return {"elements": n, "reps": reps, "rows": sorted(rows, key=lambda r: -r["gb_s"])}
+
+
 def run_steps(torch, L, calls, steps, warmup, timing):
     for _ in range(warmup):
         for c in calls:
@@ -942,6 +977,8 @@ def main(argv=None):
                     help="markdown table of SQ counters (and MFMA busy share) per launch class from a --pmc CSV dir")
     ap.add_argument("--stats-table", nargs=2, metavar=("KERNEL_STATS_CSV", "STEPS_RUN"),
                     help="markdown tables (per launch class, per kernel) from a rocprofv3 --stats CSV")
+    ap.add_argument("--probe-sweep", action="store_true",
+                    help="sweep the 4-read / 3-write probe's memory schedule at C5's size (one JSON object)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 layers (all three phases) to implicit GEMM")
@@ -972,6 +1009,10 @@ def main(argv=None):
     L = Launcher(mx, stream)
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 
+    if args.probe_sweep:
+        _, numel, _ = build_c5(torch, mx, L)
+        print(json.dumps(run_probe_sweep(torch, numel)), flush=True)
+        return 0
     if args.workload == "copy":
         print(json.dumps(run_copy(torch, args.steps, args.warmup)), flush=True)
         return 0

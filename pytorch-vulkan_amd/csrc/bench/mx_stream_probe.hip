@@ -155,7 +155,92 @@ __global__ __launch_bounds__(256) void math_kernel(float* __restrict__ p, const 
   }
 }
 
+// The 4-read / 3-write in-place mix with its memory schedule as parameters:
+// VEC float4 per stream per thread per chunk (chunk = 1024 * VEC elements,
+// bytes in flight per thread = 64 * VEC), PREFETCH issues the next chunk's
+// loads before this chunk's stores, CONTIG gives each workgroup one
+// contiguous run of chunks instead of dealing them round-robin.
+template <int VEC, bool PREFETCH, bool CONTIG>
+__global__ __launch_bounds__(256) void mix_sweep_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                        float* __restrict__ m, float* __restrict__ v,
+                                                        int64_t chunks) {
+  constexpr int64_t CH = 1024 * VEC;
+  const int64_t per = (chunks + gridDim.x - 1) / gridDim.x;
+  const int64_t first = CONTIG ? int64_t(blockIdx.x) * per : blockIdx.x;
+  const int64_t last = CONTIG ? std::min<int64_t>(chunks, first + per) : chunks;
+  const int64_t step = CONTIG ? 1 : gridDim.x;
+  f32x4 P[VEC], G[VEC], M[VEC], V[VEC];
+  auto load = [&](int64_t c) {
+    const int64_t base = c * CH + int64_t(threadIdx.x) * 4;
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) {
+      const int64_t i = base + u * 1024;
+      P[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + i));
+      G[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g + i));
+      M[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(m + i));
+      V[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(v + i));
+    }
+  };
+  if (first >= last) return;
+  if (PREFETCH) load(first);
+  for (int64_t ch = first; ch < last; ch += step) {
+    if (!PREFETCH) load(ch);
+    f32x4 P2[VEC], M2[VEC], V2[VEC];
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) {
+      M2[u] = M[u] * 0.5f + G[u];
+      V2[u] = V[u] * 0.5f + G[u];
+      P2[u] = P[u] * 0.5f + M2[u] - V2[u];
+    }
+    if (PREFETCH && ch + step < last) load(ch + step);
+    const int64_t base = ch * CH + int64_t(threadIdx.x) * 4;
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) {
+      const int64_t i = base + u * 1024;
+      __builtin_nontemporal_store(P2[u], reinterpret_cast<f32x4*>(p + i));
+      __builtin_nontemporal_store(M2[u], reinterpret_cast<f32x4*>(m + i));
+      __builtin_nontemporal_store(V2[u], reinterpret_cast<f32x4*>(v + i));
+    }
+  }
+}
+
+template <int VEC, bool PREFETCH, bool CONTIG>
+void launch_sweep(float* const* b, int64_t n, unsigned grid, hipStream_t s) {
+  hipLaunchKernelGGL((mix_sweep_kernel<VEC, PREFETCH, CONTIG>), dim3(grid), dim3(256), 0, s, b[0], b[1], b[2], b[3],
+                     n / (1024 * VEC));
+}
+
+template <int VEC>
+void launch_sweep_v(int prefetch, int contig, float* const* b, int64_t n, unsigned grid, hipStream_t s) {
+  if (prefetch && contig) launch_sweep<VEC, true, true>(b, n, grid, s);
+  else if (prefetch) launch_sweep<VEC, true, false>(b, n, grid, s);
+  else if (contig) launch_sweep<VEC, false, true>(b, n, grid, s);
+  else launch_sweep<VEC, false, false>(b, n, grid, s);
+}
+
 }  // namespace
+
+// The 4-read / 3-write mix under one memory schedule (mix_sweep_kernel): vec
+// in {1, 2, 4, 8}, prefetch / contig 0 or 1, per_cu workgroups per CU.  n must
+// be a multiple of 8192.
+extern "C" int mxp_mix_sweep(int vec, int prefetch, int contig, float* const* bufs, int64_t n, int per_cu,
+                             void* stream) {
+  if (n <= 0 || n % 8192 != 0 || per_cu <= 0) return int(hipErrorInvalidValue);
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return int(e);
+  const unsigned grid = unsigned(std::min<int64_t>(n / (1024 * vec), int64_t(cus) * per_cu));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (vec) {
+    case 1: launch_sweep_v<1>(prefetch, contig, bufs, n, grid, s); break;
+    case 2: launch_sweep_v<2>(prefetch, contig, bufs, n, grid, s); break;
+    case 4: launch_sweep_v<4>(prefetch, contig, bufs, n, grid, s); break;
+    case 8: launch_sweep_v<8>(prefetch, contig, bufs, n, grid, s); break;
+    default: return int(hipErrorInvalidValue);
+  }
+  return int(hipGetLastError());
+}
 
 extern "C" int mxp_stream(int kind, float* const* bufs, int64_t n, int per_cu, void* stream) {
   if (n <= 0 || n % kChunk != 0 || per_cu <= 0 || kind < 0 || kind > 3) return int(hipErrorInvalidValue);
