@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """Benchmark of the MI355X FP32 conv / GEMM / fused-AdamW path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1|c4|c5|copy] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c1|c4|c4ops|c5|copy] [--no-cpu-baseline]
     python bench.py --pmc-summary FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR
     python bench.py --trace-summary KERNEL_TRACE_CSV BENCH_LOG
     python bench.py --stats-table KERNEL_STATS_OR_TRACE_CSV STEPS_RUN
@@ -294,6 +294,22 @@ def build_c4_ops(torch, mx, L):
     return calls
 
 
+def run_c4_ops(torch, mx, L):
+    """Each C4 normalisation / activation op at its largest shape: 20 calls
+    back to back between one pair of HIP events, priced at its algorithmic
+    bytes."""
+    ops = {}
+    for label, _, nbytes, fn in build_c4_ops(torch, mx, L):
+        us = back_to_back_us(torch, fn, 20, 3)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        ops[label] = {"avg_us": round(us, 2), "algorithmic_gb_s": round(gbs, 1),
+                      "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    return {"workload": "C4 normalisation / activation kernels at the step's largest shapes: GroupNorm32 and SiLU "
+                        "on 16x128x64x64, 2x nearest 16x256x32x32->64x64, softmax over 64x256x256 scores; per op "
+                        "20 back-to-back calls between one pair of HIP events (a call's launches and the gaps "
+                        "between them), algorithmic bytes (inputs read once, outputs written once)", "ops": ops}
+
+
 def run_c4(torch, steps, warmup, log):
     """The C4 U-Net training step (forward, MSE loss, backward, fused AdamW) on
     the "vulkan" device at batch 16, 64x64; GEMM FLOPs of convolutions and
@@ -505,6 +521,21 @@ def run_probe_sweep(torch, numel, reps=20):
     del bufs
     torch.cuda.empty_cache()
     return {"elements": n, "reps": reps, "rows": sorted(rows, key=lambda r: -r["gb_s"])}
+
+
+def back_to_back_us(torch, fn, reps, warmup):
+    """Average microseconds per call of `reps` calls issued back to back on the
+    current stream between one pair of HIP events."""
+    for _ in range(warmup):
+        fn()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        fn()
+    e1.record(st)
+    e1.synchronize()
+    return 1000.0 * e0.elapsed_time(e1) / reps
 
 
 def run_steps(torch, L, calls, steps, warmup, timing):
@@ -966,8 +997,8 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["c3", "c1", "c4", "c5", "copy"], default="c3",
-                    help="c4 / c5 run only that component (for profiling); the headline stays C3")
+    ap.add_argument("--workload", choices=["c3", "c1", "c4", "c4ops", "c5", "copy"], default="c3",
+                    help="c4 / c4ops / c5 run only that component (for profiling); the headline stays C3")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="summarise four rocprofv3 --pmc output directories into per-kernel HBM bytes")
     ap.add_argument("--trace-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_LOG"),
@@ -1018,6 +1049,9 @@ def main(argv=None):
         return 0
     if args.workload == "c4":
         print(json.dumps(run_c4(torch, args.steps, args.warmup, log)), flush=True)
+        return 0
+    if args.workload == "c4ops":
+        print(json.dumps(run_c4_ops(torch, mx, L)), flush=True)
         return 0
     if args.workload == "c5":
         calls, numel, _ = build_c5(torch, mx, L)
@@ -1120,19 +1154,8 @@ def main(argv=None):
             log(key, comps[key]["value"], comps[key]["unit"])
             del calls_c, built
             torch.cuda.empty_cache()
-        calls_c = build_c4_ops(torch, mx, L)
-        dt, _ = run_steps(torch, L, calls_c, 20, 3, timing=False)
-        _, agg_c = run_steps(torch, L, calls_c, 20, 0, timing=True)
-        ops = {}
-        for label, (n_l, ms_l, _, nbytes) in agg_c.items():
-            gbs = nbytes / n_l / (ms_l / n_l * 1e-3) / 1e9
-            ops[label] = {"avg_us": round(1000 * ms_l / n_l, 2), "algorithmic_gb_s": round(gbs, 1),
-                          "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
-        comps["c4_ops"] = {"workload": "C4 normalisation / activation kernels at the step's largest shapes: "
-                                       "GroupNorm32 and SiLU on 16x128x64x64, 2x nearest 16x256x32x32->64x64, "
-                                       "softmax over 64x256x256 scores", "ops": ops}
-        log("c4_ops", {k: v["algorithmic_gb_s"] for k, v in ops.items()})
-        del calls_c
+        comps["c4_ops"] = run_c4_ops(torch, mx, L)
+        log("c4_ops", {k: v["algorithmic_gb_s"] for k, v in comps["c4_ops"]["ops"].items()})
         torch.cuda.empty_cache()
         comps["c4"] = run_c4(torch, max(3, min(args.steps, 10)), 3, log)
         log("c4", comps["c4"]["ms_per_step"], "ms/step", comps["c4"]["value"], "TFLOP/s; conv/GEMM kernels",

@@ -49,12 +49,18 @@ int grid_for(int64_t threads_needed) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Lane 0's value in every lane (read through a scalar register: lane 0 is the
+// first active lane wherever these reductions run, with the whole wave active).
+__device__ __forceinline__ float lane0(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
 // Sum over the 64 lanes of a wave, the same value returned to every lane
 // (lane 0's tree, broadcast).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
-  return __shfl(v, 0, 64);
+  return lane0(v);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -63,7 +69,37 @@ __device__ __forceinline__ float wave_max(float v) {
     const float w = __shfl_down(v, o, 64);
     v = (w > v || w != w) ? w : v;  // a NaN from either side wins
   }
-  return __shfl(v, 0, 64);
+  return lane0(v);
+}
+
+// wave_sum / wave_max of R values at once: the same tree for each value, the
+// R trees' cross-lane steps issued together so their latencies overlap.
+template <int R>
+__device__ __forceinline__ void wave_sum_n(float (&v)[R]) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float w[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) w[k] = __shfl_down(v[k], o, 64);
+#pragma unroll
+    for (int k = 0; k < R; ++k) v[k] += w[k];
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) v[k] = lane0(v[k]);
+}
+
+template <int R>
+__device__ __forceinline__ void wave_max_n(float (&v)[R]) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float w[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) w[k] = __shfl_down(v[k], o, 64);
+#pragma unroll
+    for (int k = 0; k < R; ++k) v[k] = (w[k] > v[k] || w[k] != w[k]) ? w[k] : v[k];
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) v[k] = lane0(v[k]);
 }
 
 // ------------------------------------------------------------ row statistics
@@ -213,10 +249,29 @@ __global__ void gn_affine_kernel(const float* __restrict__ sdy, const float* __r
   if (c >= C) return;
   const int g = c / (C / G);
   float dw = 0.f, db = 0.f;
-  for (int n = 0; n < N; ++n) {
-    const int64_t r = int64_t(n) * C + c;
-    dw += sdyx[r] * rstd[int64_t(n) * G + g];
-    db += sdy[r];
+  // Sixteen samples' loads go out before their sums (still added in n order):
+  // one dependent load per sample would cost a memory round trip each.
+  constexpr int kB = 16;
+  int n = 0;
+  for (; n + kB <= N; n += kB) {
+    float a[kB], b[kB], r[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const int64_t i = int64_t(n + j) * C + c;
+      a[j] = sdyx[i];
+      b[j] = sdy[i];
+      r[j] = rstd[int64_t(n + j) * G + g];
+    }
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      dw += a[j] * r[j];
+      db += b[j];
+    }
+  }
+  for (; n < N; ++n) {
+    const int64_t i = int64_t(n) * C + c;
+    dw += sdyx[i] * rstd[int64_t(n) * G + g];
+    db += sdy[i];
   }
   if (dgamma) dgamma[c] = dw;
   if (dbeta) dbeta[c] = db;
@@ -315,6 +370,10 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_fused_kernel(const float* __r
                                                                 const float* __restrict__ gamma, int C, int G, int hw,
                                                                 float* __restrict__ dx, float* __restrict__ part_dy,
                                                                 float* __restrict__ part_dyx) {
+  // No multiply-add contraction: the fused and register-resident kernels then
+  // perform the same roundings in the same order whatever the compiler's
+  // instruction scheduling, so their results are bit-identical.
+#pragma clang fp contract(off)
   __shared__ float sdy[kGnMaxCpg], sdyx[kGnMaxCpg];
   __shared__ float tot[2];
   const int ng = blockIdx.x;
@@ -407,14 +466,28 @@ __global__ __launch_bounds__(kThreads) void gn_fwd_regs_kernel(const float* __re
   const int count = cpg * hw, count4 = count / 4;
   const int64_t base = (int64_t(n) * C + int64_t(g) * cpg) * hw;
   const float4* p4 = reinterpret_cast<const float4*>(x + base);
+  const int c0 = g * cpg;
   float4 v[NPT];
-  float s = 0.f;
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
     const int i = threadIdx.x + kThreads * j;
     v[j] = i < count4 ? p4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    if (i < count4) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   }
+  // The affine parameters of each element's channel, loaded with the data:
+  // a load between the stores below would make each store wait for the
+  // earlier ones (loads and stores share one counter).
+  float ga[NPT], be[NPT];
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int i = threadIdx.x + kThreads * j;
+    const int c = c0 + (4 * min(i, count4 - 1)) / hw;
+    ga[j] = gamma ? gamma[c] : 1.f;
+    be[j] = beta ? beta[c] : 0.f;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
+    if (threadIdx.x + kThreads * j < count4) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   const float m = block_sum(s, red) / float(count);
   float sq = 0.f;
 #pragma unroll
@@ -429,21 +502,24 @@ __global__ __launch_bounds__(kThreads) void gn_fwd_regs_kernel(const float* __re
     mean[ng] = m;
     rstd[ng] = inv;
   }
-  const int c0 = g * cpg;
   float4* q4 = reinterpret_cast<float4*>(y + base);
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
     const int i = threadIdx.x + kThreads * j;
     if (i >= count4) continue;
-    const int c = c0 + (4 * i) / hw;
-    const float a = gamma ? inv * gamma[c] : inv, b = beta ? beta[c] : 0.f;
+    const float a = inv * ga[j], b = be[j];  // ga == 1 without gamma: inv * 1 == inv exactly
     q4[i] = make_float4((v[j].x - m) * a + b, (v[j].y - m) * a + b, (v[j].z - m) * a + b, (v[j].w - m) * a + b);
   }
 }
 
 // Backward: wave w holds channels w, w + 4, ... of the group and lanes the
 // plane's float4 lane, lane + 64, ... (np of them per channel), for dy and x.
-template <int NPT>
+// FULL: every one of a thread's NPT slots holds a valid float4 (channels per
+// group a multiple of 4, planes a multiple of 256 floats, NPT equal to
+// (cpg / 4) * (hw / 256)), so loads and stores carry no per-slot condition and
+// form straight-line code (a conditional store block makes the compiler wait
+// for every earlier store at its entry).
+template <int NPT, bool FULL>
 __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __restrict__ dy,
                                                                const float* __restrict__ x,
                                                                const float* __restrict__ mean,
@@ -451,7 +527,11 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __re
                                                                const float* __restrict__ gamma, int C, int G, int hw,
                                                                float* __restrict__ dx, float* __restrict__ part_dy,
                                                                float* __restrict__ part_dyx) {
-  __shared__ float sdy[kGnMaxCpg], sdyx[kGnMaxCpg];
+  // No multiply-add contraction: the fused and register-resident kernels then
+  // perform the same roundings in the same order whatever the compiler's
+  // instruction scheduling, so their results are bit-identical.
+#pragma clang fp contract(off)
+  __shared__ float sdy[kGnMaxCpg], sdyx[kGnMaxCpg], sg[kGnMaxCpg];
   __shared__ float tot[2];
   const int ng = blockIdx.x;
   const int n = ng / G, g = ng - (ng / G) * G, cpg = C / G;
@@ -466,21 +546,26 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __re
 #pragma unroll
   for (int k = 0; k < NPT; ++k) {
     const int ci = wave + kWavesPerBlock * (k / np), i = lane + 64 * (k % np);
-    const bool ok = ci < cpg && i < hw4;
+    const bool ok = FULL || (ci < cpg && i < hw4);
     gv[k] = ok ? g4[int64_t(ci) * hw4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
     xv[k] = ok ? x4[int64_t(ci) * hw4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  // The group's gamma (1 without one: inv * 1 == inv exactly) goes to LDS, so
+  // the dx stores below have neither a global load nor a branch between them
+  // (loads and stores share one counter: such a load would make each store
+  // wait for the earlier ones).
+  for (int ci = threadIdx.x; ci < cpg; ci += kThreads) sg[ci] = gamma ? gamma[g * cpg + ci] : 1.f;
   for (int cb = 0; cb * kWavesPerBlock < cpg; ++cb) {
     const int ci = wave + kWavesPerBlock * cb;
     float a = 0.f, b = 0.f;
 #pragma unroll
     for (int k = 0; k < NPT; ++k) {
-      if (k / np != cb || lane + 64 * (k % np) >= hw4) continue;
+      if (k / np != cb || (!FULL && lane + 64 * (k % np) >= hw4)) continue;
       const float4 gg = gv[k], v = xv[k];
       a += (gg.x + gg.y) + (gg.z + gg.w);
       b += (gg.x * (v.x - mu) + gg.y * (v.y - mu)) + (gg.z * (v.z - mu) + gg.w * (v.w - mu));
     }
-    if (ci < cpg) {
+    if (FULL || ci < cpg) {
       a = wave_sum(a);
       b = wave_sum(b);
       if (lane == 0) {
@@ -496,7 +581,7 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __re
   if (threadIdx.x == 0) {
     float sv = 0.f, svx = 0.f;
     for (int ci = 0; ci < cpg; ++ci) {
-      const float w = gamma ? gamma[g * cpg + ci] : 1.f;
+      const float w = sg[ci];
       sv += w * sdy[ci];
       svx += w * sdyx[ci];
     }
@@ -508,15 +593,20 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __re
   const float cnt = float(cpg * hw);
   const float kk = -inv * inv * inv * (tot[1] / cnt);
   const float q = -inv * (tot[0] / cnt);
+  // Every dx value first (into gv), then the stores: each store reads its own
+  // registers, so none waits for an earlier one to release its data.
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const float pc = inv * sg[min(wave + kWavesPerBlock * (k / np), cpg - 1)];
+    const float4 gg = gv[k], v = xv[k];
+    gv[k] = make_float4(pc * gg.x + kk * (v.x - mu) + q, pc * gg.y + kk * (v.y - mu) + q,
+                        pc * gg.z + kk * (v.z - mu) + q, pc * gg.w + kk * (v.w - mu) + q);
+  }
   float4* d4 = reinterpret_cast<float4*>(dx + base);
 #pragma unroll
   for (int k = 0; k < NPT; ++k) {
     const int ci = wave + kWavesPerBlock * (k / np), i = lane + 64 * (k % np);
-    if (ci >= cpg || i >= hw4) continue;
-    const float pc = gamma ? inv * gamma[g * cpg + ci] : inv;
-    const float4 gg = gv[k], v = xv[k];
-    d4[int64_t(ci) * hw4 + i] = make_float4(pc * gg.x + kk * (v.x - mu) + q, pc * gg.y + kk * (v.y - mu) + q,
-                                            pc * gg.z + kk * (v.z - mu) + q, pc * gg.w + kk * (v.w - mu) + q);
+    if (FULL || (ci < cpg && i < hw4)) d4[int64_t(ci) * hw4 + i] = gv[k];
   }
 }
 
@@ -835,77 +925,122 @@ __global__ __launch_bounds__(kThreads) void softmax_last_grad_kernel(const float
   for (int i = lane; i < len; i += 64) dx[r * len + i] = p[i] * (g[i] - s);
 }
 
-// Rows of len % 4 == 0 floats (16-byte aligned), len <= 256 NV: one wave per
-// row holding it in registers, lane l owning float4s l, l + 64, ...; each
-// element is read once and its exponential computed once.
-template <int NV>
+// Rows of len % 4 == 0 floats (16-byte aligned), len <= 256 NV: each wave
+// holds R consecutive rows in registers, lane l owning float4s l, l + 64, ...
+// of every row; each element is read once and its exponential computed once.
+// All R rows' loads are issued before the first reduction, so a wave keeps
+// R * NV float4 per lane in flight (short rows would otherwise leave a wave
+// waiting on one 16-byte load).  Per row the arithmetic and its order do not
+// depend on R.
+template <int NV, int R>
 __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                                 int64_t rows, int len) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  const float4* p = reinterpret_cast<const float4*>(x + r * len);
-  float4* q = reinterpret_cast<float4*>(y + r * len);
+  const int64_t r0 = (int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * R;
+  if (r0 >= rows) return;
   const int n4 = len / 4;
-  float e[NV][4];
-  float m = -std::numeric_limits<float>::infinity();
+  const float ninf = -std::numeric_limits<float>::infinity();
+  float e[R][NV][4];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int i = lane + 64 * j;
-    const float4 v = i < n4 ? p[i] : make_float4(m, m, m, m);
-    e[j][0] = v.x;
-    e[j][1] = v.y;
-    e[j][2] = v.z;
-    e[j][3] = v.w;
+  for (int k = 0; k < R; ++k) {
+    const float4* p = reinterpret_cast<const float4*>(x + (r0 + k) * len);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) m = (e[j][c] > m || e[j][c] != e[j][c]) ? e[j][c] : m;
-  }
-  m = wave_max(m);
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const bool ok = lane + 64 * j < n4;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      e[j][c] = expf(e[j][c] - m);
-      if (ok) s += e[j][c];
+    for (int j = 0; j < NV; ++j) {
+      const int i = lane + 64 * j;
+      const float4 v = (r0 + k < rows && i < n4) ? p[i] : make_float4(ninf, ninf, ninf, ninf);
+      e[k][j][0] = v.x;
+      e[k][j][1] = v.y;
+      e[k][j][2] = v.z;
+      e[k][j][3] = v.w;
     }
   }
-  const float inv = 1.f / wave_sum(s);
+  // Rows past the end hold -inf (their results are never stored).
+  float m[R], sum[R];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int i = lane + 64 * j;
-    if (i < n4) q[i] = make_float4(e[j][0] * inv, e[j][1] * inv, e[j][2] * inv, e[j][3] * inv);
+  for (int k = 0; k < R; ++k) {
+    m[k] = ninf;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) m[k] = (e[k][j][c] > m[k] || e[k][j][c] != e[k][j][c]) ? e[k][j][c] : m[k];
+  }
+  wave_max_n<R>(m);
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    sum[k] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const bool ok = lane + 64 * j < n4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        e[k][j][c] = expf(e[k][j][c] - m[k]);
+        if (ok) sum[k] += e[k][j][c];
+      }
+    }
+  }
+  wave_sum_n<R>(sum);
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    if (r0 + k >= rows) break;
+    const float inv = 1.f / sum[k];
+    float4* q = reinterpret_cast<float4*>(y + (r0 + k) * len);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int i = lane + 64 * j;
+      if (i < n4) q[i] = make_float4(e[k][j][0] * inv, e[k][j][1] * inv, e[k][j][2] * inv, e[k][j][3] * inv);
+    }
   }
 }
 
-template <int NV>
+template <int NV, int R>
 __global__ __launch_bounds__(kThreads) void softmax_rows_grad_kernel(const float* __restrict__ dy,
                                                                      const float* __restrict__ y,
                                                                      float* __restrict__ dx, int64_t rows, int len) {
+  // No multiply-add contraction: the rounding of each product does not depend
+  // on how the compiler schedules the R rows.
+#pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int64_t r = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  const float4* g4 = reinterpret_cast<const float4*>(dy + r * len);
-  const float4* p4 = reinterpret_cast<const float4*>(y + r * len);
-  float4* d4 = reinterpret_cast<float4*>(dx + r * len);
+  const int64_t r0 = (int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * R;
+  if (r0 >= rows) return;
   const int n4 = len / 4;
-  float4 gv[NV], pv[NV];
-  float s = 0.f;
+  float4 gv[R][NV], pv[R][NV];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int i = lane + 64 * j;
-    gv[j] = i < n4 ? g4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    pv[j] = i < n4 ? p4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    if (i < n4) s += ((gv[j].x * pv[j].x + gv[j].y * pv[j].y) + gv[j].z * pv[j].z) + gv[j].w * pv[j].w;
+  for (int k = 0; k < R; ++k) {
+    const float4* g4 = reinterpret_cast<const float4*>(dy + (r0 + k) * len);
+    const float4* p4 = reinterpret_cast<const float4*>(y + (r0 + k) * len);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int i = lane + 64 * j;
+      const bool ok = r0 + k < rows && i < n4;
+      gv[k][j] = ok ? g4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      pv[k][j] = ok ? p4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
-  s = wave_sum(s);
+  float sum[R];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int i = lane + 64 * j;
-    if (i < n4)
-      d4[i] = make_float4(pv[j].x * (gv[j].x - s), pv[j].y * (gv[j].y - s), pv[j].z * (gv[j].z - s),
-                          pv[j].w * (gv[j].w - s));
+  for (int k = 0; k < R; ++k) {
+    sum[k] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (lane + 64 * j < n4) {
+        const float4 g = gv[k][j], p = pv[k][j];
+        sum[k] += ((g.x * p.x + g.y * p.y) + g.z * p.z) + g.w * p.w;
+      }
+    }
+  }
+  wave_sum_n<R>(sum);
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    if (r0 + k >= rows) break;
+    const float s = sum[k];
+    float4* d4 = reinterpret_cast<float4*>(dx + (r0 + k) * len);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int i = lane + 64 * j;
+      if (i < n4)
+        d4[i] = make_float4(pv[k][j].x * (gv[k][j].x - s), pv[k][j].y * (gv[k][j].y - s),
+                            pv[k][j].z * (gv[k][j].z - s), pv[k][j].w * (gv[k][j].w - s));
+    }
   }
 }
 
@@ -1159,17 +1294,23 @@ int mx_group_norm_backward(const float* dy, const float* x, const float* mean, c
     const int npt = vec ? regs_for(int64_t((cpg + kWavesPerBlock - 1) / kWavesPerBlock) * ((hw / 4 + 63) / 64)) : 0;
     const dim3 grid(unsigned(n * groups));
     const int C = int(c), G = int(groups), HW = int(hw);
+    const bool full = npt && cpg % kWavesPerBlock == 0 && hw % 256 == 0 &&
+                      int64_t(cpg / kWavesPerBlock) * (hw / 256) == npt;
+#define MX_GN_BWD(N)                                                                                               \
+  do {                                                                                                             \
+    if (full)                                                                                                      \
+      hipLaunchKernelGGL((gn_bwd_regs_kernel<N, true>), grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G, \
+                         HW, dx, sdy, sdyx);                                                                       \
+    else                                                                                                           \
+      hipLaunchKernelGGL((gn_bwd_regs_kernel<N, false>), grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C,   \
+                         G, HW, dx, sdy, sdyx);                                                                    \
+  } while (0)
     switch (npt) {
-      case 1: hipLaunchKernelGGL(gn_bwd_regs_kernel<1>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
-                                 HW, dx, sdy, sdyx); break;
-      case 2: hipLaunchKernelGGL(gn_bwd_regs_kernel<2>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
-                                 HW, dx, sdy, sdyx); break;
-      case 4: hipLaunchKernelGGL(gn_bwd_regs_kernel<4>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
-                                 HW, dx, sdy, sdyx); break;
-      case 8: hipLaunchKernelGGL(gn_bwd_regs_kernel<8>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
-                                 HW, dx, sdy, sdyx); break;
-      case 16: hipLaunchKernelGGL(gn_bwd_regs_kernel<16>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
-                                  HW, dx, sdy, sdyx); break;
+      case 1: MX_GN_BWD(1); break;
+      case 2: MX_GN_BWD(2); break;
+      case 4: MX_GN_BWD(4); break;
+      case 8: MX_GN_BWD(8); break;
+      case 16: MX_GN_BWD(16); break;
       default:
         if (vec)
           hipLaunchKernelGGL(gn_bwd_fused_kernel<true>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G, HW,
@@ -1178,6 +1319,7 @@ int mx_group_norm_backward(const float* dy, const float* x, const float* mean, c
           hipLaunchKernelGGL(gn_bwd_fused_kernel<false>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G,
                              HW, dx, sdy, sdyx);
     }
+#undef MX_GN_BWD
     MX_HIP(hipGetLastError());
     if (dgamma || dbeta) {
       hipLaunchKernelGGL(gn_affine_kernel, dim3(int((c + 255) / 256)), dim3(256), 0, s, sdy, sdyx, rstd, int(n),
@@ -1405,11 +1547,17 @@ int mx_softmax_f32(const float* x, int64_t outer, int64_t axis, int64_t inner, f
     MX_REQUIRE(axis <= INT32_MAX && outer <= int64_t(INT32_MAX) * kWavesPerBlock, MX_ERR_INVALID,
                "mx_softmax_f32: size exceeds int32");
     const int nv = (axis % 4 == 0 && aligned16(x) && aligned16(y)) ? regs_for((axis / 4 + 63) / 64) : 0;
+    // One row per wave: the forward's exponentials and two reductions per row
+    // overlap best with other waves' memory traffic when the rows run in
+    // several rounds of waves (measured against two and four rows per wave).
     const dim3 grid(launch_rows(outer));
     switch (nv) {
-      case 1: hipLaunchKernelGGL(softmax_rows_kernel<1>, grid, dim3(kThreads), 0, s, x, y, outer, int(axis)); break;
-      case 2: hipLaunchKernelGGL(softmax_rows_kernel<2>, grid, dim3(kThreads), 0, s, x, y, outer, int(axis)); break;
-      case 4: hipLaunchKernelGGL(softmax_rows_kernel<4>, grid, dim3(kThreads), 0, s, x, y, outer, int(axis)); break;
+      case 1: hipLaunchKernelGGL((softmax_rows_kernel<1, 1>), grid, dim3(kThreads), 0, s, x, y, outer, int(axis));
+        break;
+      case 2: hipLaunchKernelGGL((softmax_rows_kernel<2, 1>), grid, dim3(kThreads), 0, s, x, y, outer, int(axis));
+        break;
+      case 4: hipLaunchKernelGGL((softmax_rows_kernel<4, 1>), grid, dim3(kThreads), 0, s, x, y, outer, int(axis));
+        break;
       default: hipLaunchKernelGGL(softmax_last_kernel, grid, dim3(kThreads), 0, s, x, y, outer, int(axis));
     }
   } else {
@@ -1433,13 +1581,16 @@ int mx_softmax_backward_f32(const float* dy, const float* y, int64_t outer, int6
                "mx_softmax_backward_f32: size exceeds int32");
     const int nv =
         (axis % 4 == 0 && aligned16(dy) && aligned16(y) && aligned16(dx)) ? regs_for((axis / 4 + 63) / 64) : 0;
-    const dim3 grid(launch_rows(outer));
+    const dim3 grid(launch_rows(outer)), grid4(launch_rows((outer + 3) / 4)), grid2(launch_rows((outer + 1) / 2));
     switch (nv) {
-      case 1: hipLaunchKernelGGL(softmax_rows_grad_kernel<1>, grid, dim3(kThreads), 0, s, dy, y, dx, outer, int(axis));
+      case 1: hipLaunchKernelGGL((softmax_rows_grad_kernel<1, 4>), grid4, dim3(kThreads), 0, s, dy, y, dx, outer,
+                                 int(axis));
         break;
-      case 2: hipLaunchKernelGGL(softmax_rows_grad_kernel<2>, grid, dim3(kThreads), 0, s, dy, y, dx, outer, int(axis));
+      case 2: hipLaunchKernelGGL((softmax_rows_grad_kernel<2, 2>), grid2, dim3(kThreads), 0, s, dy, y, dx, outer,
+                                 int(axis));
         break;
-      case 4: hipLaunchKernelGGL(softmax_rows_grad_kernel<4>, grid, dim3(kThreads), 0, s, dy, y, dx, outer, int(axis));
+      case 4: hipLaunchKernelGGL((softmax_rows_grad_kernel<4, 1>), grid, dim3(kThreads), 0, s, dy, y, dx, outer,
+                                 int(axis));
         break;
       default:
         hipLaunchKernelGGL(softmax_last_grad_kernel, grid, dim3(kThreads), 0, s, dy, y, dx, outer, int(axis));
