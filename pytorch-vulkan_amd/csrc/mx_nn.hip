@@ -55,49 +55,85 @@ __device__ __forceinline__ float lane0(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
-// Sum over the 64 lanes of a wave, the same value returned to every lane
-// (lane 0's tree, broadcast).
+// The value of lane l + o for a wave tree's step o: LDS permutes across
+// the 16-lane rows (o = 32, 16), a DPP row shift inside them (o <= 8; a lane
+// whose source lies past its row reads 0, and lane 0's tree never uses it).
+template <int O>
+__device__ __forceinline__ float lane_down(float v) {
+  if constexpr (O >= 16) {
+    return __shfl_down(v, O, 64);
+  } else {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + O, 0xf, 0xf, true));
+  }
+}
+
+__device__ __forceinline__ float max_step(float v, float w) {
+  return (w > v || w != w) ? w : v;  // a NaN from either side wins
+}
+
+// Sum over the 64 lanes of a wave, the same value returned to every lane:
+// lane 0's tree v[l] += v[l + o] for o = 32, 16, ..., 1, broadcast.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
+  v += lane_down<32>(v);
+  v += lane_down<16>(v);
+  v += lane_down<8>(v);
+  v += lane_down<4>(v);
+  v += lane_down<2>(v);
+  v += lane_down<1>(v);
   return lane0(v);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float w = __shfl_down(v, o, 64);
-    v = (w > v || w != w) ? w : v;  // a NaN from either side wins
-  }
+  v = max_step(v, lane_down<32>(v));
+  v = max_step(v, lane_down<16>(v));
+  v = max_step(v, lane_down<8>(v));
+  v = max_step(v, lane_down<4>(v));
+  v = max_step(v, lane_down<2>(v));
+  v = max_step(v, lane_down<1>(v));
   return lane0(v);
 }
 
 // wave_sum / wave_max of R values at once: the same tree for each value, the
 // R trees' cross-lane steps issued together so their latencies overlap.
+template <int O, int R>
+__device__ __forceinline__ void sum_step_n(float (&v)[R]) {
+  float w[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) w[k] = lane_down<O>(v[k]);
+#pragma unroll
+  for (int k = 0; k < R; ++k) v[k] += w[k];
+}
+
+template <int O, int R>
+__device__ __forceinline__ void max_step_n(float (&v)[R]) {
+  float w[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) w[k] = lane_down<O>(v[k]);
+#pragma unroll
+  for (int k = 0; k < R; ++k) v[k] = max_step(v[k], w[k]);
+}
+
 template <int R>
 __device__ __forceinline__ void wave_sum_n(float (&v)[R]) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float w[R];
-#pragma unroll
-    for (int k = 0; k < R; ++k) w[k] = __shfl_down(v[k], o, 64);
-#pragma unroll
-    for (int k = 0; k < R; ++k) v[k] += w[k];
-  }
+  sum_step_n<32>(v);
+  sum_step_n<16>(v);
+  sum_step_n<8>(v);
+  sum_step_n<4>(v);
+  sum_step_n<2>(v);
+  sum_step_n<1>(v);
 #pragma unroll
   for (int k = 0; k < R; ++k) v[k] = lane0(v[k]);
 }
 
 template <int R>
 __device__ __forceinline__ void wave_max_n(float (&v)[R]) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float w[R];
-#pragma unroll
-    for (int k = 0; k < R; ++k) w[k] = __shfl_down(v[k], o, 64);
-#pragma unroll
-    for (int k = 0; k < R; ++k) v[k] = (w[k] > v[k] || w[k] != w[k]) ? w[k] : v[k];
-  }
+  max_step_n<32>(v);
+  max_step_n<16>(v);
+  max_step_n<8>(v);
+  max_step_n<4>(v);
+  max_step_n<2>(v);
+  max_step_n<1>(v);
 #pragma unroll
   for (int k = 0; k < R; ++k) v[k] = lane0(v[k]);
 }
