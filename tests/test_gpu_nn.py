@@ -154,6 +154,43 @@ def test_abi_group_norm_masks_and_empty_batch(mx):
         mx.group_norm_forward(dev(x), None, None, 3, 1e-5, torch.empty_like(dev(x)), mean, rstd)
 
 
+def _lane0_tree(v):
+    """Lane 0's result of a wave's 64-lane reduction tree in float32:
+    v[l] += v[l + o] for o = 32, 16, 8, 4, 2, 1."""
+    v = np.array(v, np.float32)
+    for o in (32, 16, 8, 4, 2, 1):
+        v[:64 - o] = v[:64 - o] + v[o:]
+    return v[0]
+
+
+@pytest.mark.parametrize("channels", [4, 2])
+def test_abi_group_norm_dbeta_follows_the_lane0_tree(mx, channels):
+    """With one sample, dbeta of a channel is one wave's reduction of its
+    lanes' partial sums of dy: the register-resident backward (4 channels per
+    group: the straight-line variant; 2: the guarded one) gives lane l the
+    float4s l, l + 64, ... of the 64x64 plane, each added as (x + y) + (z + w)
+    to a running sum, and the wave combines the lanes by lane 0's tree.  The
+    float32 restatement below must match bit for bit: a tree step that read
+    the wrong lane (a shift of the wrong direction or width) rounds
+    differently on random data."""
+    rng = np.random.default_rng(404 + channels)
+    shape = (1, channels, 64, 64)
+    x = rng.standard_normal(shape).astype(np.float32)
+    g = (rng.standard_normal(shape) * np.exp2(rng.integers(-6, 7, shape))).astype(np.float32)
+    _, m_ref, r_ref = O.group_norm_forward(x, None, None, 1, 1e-5)
+    db = torch.empty(channels, device="vulkan")
+    mx.group_norm_backward(dev(g), dev(x), dev(m_ref), dev(r_ref), None, 1, None, None, db)
+    want = np.empty(channels, np.float32)
+    for c in range(channels):
+        q = g[0, c].reshape(16, 64, 4)  # [k][lane][4]: float4 lane + 64 k of the plane
+        partial = np.zeros(64, np.float32)
+        for k in range(16):
+            partial = partial + ((q[k, :, 0] + q[k, :, 1]) + (q[k, :, 2] + q[k, :, 3]))
+        want[c] = np.float32(0) + _lane0_tree(partial)
+    got = db.cpu().numpy()
+    assert np.array_equal(got.view(np.int32), want.view(np.int32)), (got, want)
+
+
 @pytest.mark.parametrize("shape", [(4, 3, 5, 6), (8, 5), (16, 64, 28, 28), (2, 24, 7, 9)])
 @pytest.mark.parametrize("training", [True, False])
 def test_abi_batch_norm(mx, shape, training):
