@@ -525,11 +525,15 @@ def run_probe_sweep(torch, numel, reps=20):
 
 def back_to_back_us(torch, fn, reps, warmup):
     """Average microseconds per call of `reps` calls issued back to back on the
-    current stream between one pair of HIP events."""
+    current stream between one pair of HIP events.  A spin kernel queued
+    before the first event keeps the GPU busy while the host issues the calls,
+    so a call shorter than its Python issue time is timed at the GPU's pace,
+    not the host's."""
     for _ in range(warmup):
         fn()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(2_000_000)
     e0.record(st)
     for _ in range(reps):
         fn()

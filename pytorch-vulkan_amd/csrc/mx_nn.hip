@@ -68,10 +68,6 @@ __device__ __forceinline__ float lane_down(float v) {
   }
 }
 
-__device__ __forceinline__ float max_step(float v, float w) {
-  return (w > v || w != w) ? w : v;  // a NaN from either side wins
-}
-
 // Sum over the 64 lanes of a wave, the same value returned to every lane:
 // lane 0's tree v[l] += v[l + o] for o = 32, 16, ..., 1, broadcast.
 __device__ __forceinline__ float wave_sum(float v) {
@@ -84,14 +80,40 @@ __device__ __forceinline__ float wave_sum(float v) {
   return lane0(v);
 }
 
+// Maximum over the 64 lanes (lane 0's tree, broadcast) with fmaxf, one
+// v_max_f32 per step.  fmaxf drops a NaN operand; the softmax kernels, its
+// only users, still give NaN for a row holding a NaN, since that element's
+// exponential, the row sum and every quotient are NaN.
 __device__ __forceinline__ float wave_max(float v) {
-  v = max_step(v, lane_down<32>(v));
-  v = max_step(v, lane_down<16>(v));
-  v = max_step(v, lane_down<8>(v));
-  v = max_step(v, lane_down<4>(v));
-  v = max_step(v, lane_down<2>(v));
-  v = max_step(v, lane_down<1>(v));
+  v = fmaxf(v, lane_down<32>(v));
+  v = fmaxf(v, lane_down<16>(v));
+  v = fmaxf(v, lane_down<8>(v));
+  v = fmaxf(v, lane_down<4>(v));
+  v = fmaxf(v, lane_down<2>(v));
+  v = fmaxf(v, lane_down<1>(v));
   return lane0(v);
+}
+
+// exp(d) for d <= 0 (or NaN), as the softmax forward needs it after taking
+// the row maximum off.  Cody and Waite's split of the argument: d * log2(e)
+// as a two-float product ph + pl (log2(e) split into its nearest float and the
+// nearest float to the remainder, the low part of d * hi recovered exactly by
+// an fma), n = rint(ph), exp(d) = 2^n * 2^((ph - n) + pl) with the hardware
+// exp2 on the reduced argument (|.| <= 0.5) and ldexp.  The error is that of
+// the exp2 plus half an ulp of the reduced argument, about 1 ulp.  No overflow
+// branch (d never exceeds 0); below ln(2^-150), half the smallest subnormal,
+// the result is 0 (also for d = -inf, where the reduction gives NaN).
+__device__ __forceinline__ float exp_nonpos(float d) {
+#pragma clang fp contract(off)
+  constexpr float kLog2eHi = 1.44269502162933349609375f;   // float(log2 e)
+  constexpr float kLog2eLo = 1.925963033500011079e-8f;     // float(log2 e - kLog2eHi)
+  constexpr float kZeroBelow = -103.972076416015625f;      // float(ln 2^-150)
+  const float ph = d * kLog2eHi;
+  float pl = __builtin_fmaf(d, kLog2eHi, -ph);
+  pl = __builtin_fmaf(d, kLog2eLo, pl);
+  const float n = __builtin_rintf(ph);
+  const float r = __builtin_ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), int(n));
+  return d < kZeroBelow ? 0.f : r;
 }
 
 // wave_sum / wave_max of R values at once: the same tree for each value, the
@@ -111,7 +133,7 @@ __device__ __forceinline__ void max_step_n(float (&v)[R]) {
 #pragma unroll
   for (int k = 0; k < R; ++k) w[k] = lane_down<O>(v[k]);
 #pragma unroll
-  for (int k = 0; k < R; ++k) v[k] = max_step(v[k], w[k]);
+  for (int k = 0; k < R; ++k) v[k] = fmaxf(v[k], w[k]);
 }
 
 template <int R>
@@ -935,15 +957,12 @@ __global__ __launch_bounds__(kThreads) void softmax_last_kernel(const float* __r
   const float* p = x + r * len;
   float* q = y + r * len;
   float m = -std::numeric_limits<float>::infinity();
-  for (int i = lane; i < len; i += 64) {
-    const float v = p[i];
-    m = (v > m || v != v) ? v : m;
-  }
+  for (int i = lane; i < len; i += 64) m = fmaxf(m, p[i]);
   m = wave_max(m);
   float s = 0.f;
-  for (int i = lane; i < len; i += 64) s += expf(p[i] - m);
+  for (int i = lane; i < len; i += 64) s += exp_nonpos(p[i] - m);
   const float inv = 1.f / wave_sum(s);
-  for (int i = lane; i < len; i += 64) q[i] = expf(p[i] - m) * inv;
+  for (int i = lane; i < len; i += 64) q[i] = exp_nonpos(p[i] - m) * inv;
 }
 
 // dx = y * (dy - sum(dy * y)) over the last axis, one wave per row.
@@ -998,7 +1017,7 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(const float* __r
 #pragma unroll
     for (int j = 0; j < NV; ++j)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) m[k] = (e[k][j][c] > m[k] || e[k][j][c] != e[k][j][c]) ? e[k][j][c] : m[k];
+      for (int c = 0; c < 4; ++c) m[k] = fmaxf(m[k], e[k][j][c]);
   }
   wave_max_n<R>(m);
 #pragma unroll
@@ -1009,7 +1028,7 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(const float* __r
       const bool ok = lane + 64 * j < n4;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        e[k][j][c] = expf(e[k][j][c] - m[k]);
+        e[k][j][c] = exp_nonpos(e[k][j][c] - m[k]);
         if (ok) sum[k] += e[k][j][c];
       }
     }
@@ -1091,14 +1110,11 @@ __global__ __launch_bounds__(kThreads) void softmax_inner_kernel(const float* __
     const float* p = x + o * axis * inner + in;
     float* q = y + o * axis * inner + in;
     float m = -std::numeric_limits<float>::infinity();
-    for (int64_t a = 0; a < axis; ++a) {
-      const float v = p[a * inner];
-      m = (v > m || v != v) ? v : m;
-    }
+    for (int64_t a = 0; a < axis; ++a) m = fmaxf(m, p[a * inner]);
     float s = 0.f;
-    for (int64_t a = 0; a < axis; ++a) s += expf(p[a * inner] - m);
+    for (int64_t a = 0; a < axis; ++a) s += exp_nonpos(p[a * inner] - m);
     const float inv = 1.f / s;
-    for (int64_t a = 0; a < axis; ++a) q[a * inner] = expf(p[a * inner] - m) * inv;
+    for (int64_t a = 0; a < axis; ++a) q[a * inner] = exp_nonpos(p[a * inner] - m) * inv;
   }
 }
 
