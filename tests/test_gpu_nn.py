@@ -297,6 +297,52 @@ def test_abi_softmax(mx, shape, dim):
     close(dx, dx_ref, mag=mag * 1e4, rtol=RTOL, atol=1e-9, what="softmax backward")
 
 
+@pytest.mark.parametrize("width,dim", [(4, 1), (8, 1), (6, 1), (4, 0)],
+                         ids=["rows4", "rows8", "last6", "inner"])
+def test_abi_softmax_exponential_accuracy(mx, width, dim):
+    """Rows [0, d, -inf, ...] have y = 1 / (1 + e^d) and e^d / (1 + e^d): the
+    forward's exponential (for arguments <= 0), one add, one division and one
+    product.  Each is within an ulp or half of one, so every output must lie
+    within 5 ulp (6e-7 relative) of float64, for d over the whole normal
+    range of e^d, on the row-per-wave, generic last-axis and inner-axis
+    kernels."""
+    rng = np.random.default_rng(7)
+    d = np.concatenate([np.linspace(-87.0, 0.0, 3001), -rng.random(3000) * 87.0, -rng.random(1000) * 1e-3])
+    d = d.astype(np.float32)
+    x = np.full((d.size, width), -np.inf, np.float32)
+    x[:, 0] = 0.0
+    x[:, 1] = d
+    e = np.exp(d.astype(np.float64))
+    want = np.zeros(x.shape)
+    want[:, 0] = 1.0 / (1.0 + e)
+    want[:, 1] = e / (1.0 + e)
+    if dim == 0:
+        x, want = np.ascontiguousarray(x.T), want.T
+    y = torch.empty(x.shape, device="vulkan")
+    mx.softmax(dev(x), dim, y)
+    got = y.cpu().numpy().astype(np.float64)
+    live = want > 0
+    rel = np.abs(got[live] - want[live]) / want[live]
+    assert rel.max() <= 6e-7, f"worst relative error {rel.max():.3g} at d = {d[np.argmax(rel) % d.size]}"
+    assert np.all(got[~live] == 0.0)
+
+
+def test_abi_softmax_special_rows_match_torch(mx):
+    """NaN, +inf, all -inf and partly masked rows give what CPU torch gives
+    (a NaN or +inf element makes its row NaN; an all -inf row is NaN)."""
+    rows = [[0.0, np.nan, 1.0, 2.0], [np.inf, 1.0, 0.0, -1.0], [-np.inf] * 4, [-np.inf, 3.0, -np.inf, 1.0],
+            [np.inf, np.inf, 0.0, 0.0], [-200.0, 0.0, -1e30, -80.0], [np.nan] * 4, [1.0, -np.inf, np.inf, np.nan]]
+    for width in (4, 6):
+        x = np.array([r + r[:width - 4] for r in rows], np.float32)
+        want = torch.softmax(torch.from_numpy(x), dim=1).numpy()
+        y = torch.empty(x.shape, device="vulkan")
+        mx.softmax(dev(x), 1, y)
+        got = y.cpu().numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(want)), f"width {width}: NaN pattern\n{got}\n{want}"
+        ok = ~np.isnan(want)
+        np.testing.assert_allclose(got[ok], want[ok], rtol=1e-6, atol=0)
+
+
 @pytest.mark.parametrize("count", [0, 1, 257, 1 << 20, 3_000_001])
 @pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
 def test_abi_mse(mx, count, reduction):
