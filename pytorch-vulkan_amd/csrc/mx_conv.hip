@@ -425,15 +425,24 @@ bool winograd_applicable(const mx_conv2d_desc& d) {
 // output positions the fused F(2x2,3x3) forward and input gradient take
 // 0.50-0.89 of the implicit GEMM's time (8x64 channels at 56^2: 17.8 vs 35.6
 // us; 16x128 at 64^2: 98 vs 184; 16x512 at 8^2: 45.5 vs 60.0) and lose only on
-// smaller layers (1x256 at 14^2: 28.8 vs 17.2); the weight gradient wins from
-// 2048 positions (0.55-0.83) and loses at 1568 (12.5 vs 11.5).  This replaces
-// the reference heuristic for these layers (its Winograd is a grouped-layer
-// forward rule, csrc/ops/convolution.cpp:454-460, kept below); every other
-// layer, and padding beyond 2, keeps the reference's choices.
+// smaller layers (1x256 at 14^2: 28.8 vs 17.2).  The weight gradient's
+// break-even follows the layer's work, not its positions: in two sweeps (342
+// and 401 layers: batch 1-32, 7^2-56^2, 32-1024 input x 32-512 output
+// channels, kernel time of each algorithm forced) it wins from
+// 2^25 multiply-adds per filter tap (positions x input channels per group x
+// output channels; 16x512 at 8^2 to 512: 46 vs 73 us) and loses below
+// (8x32 at 16^2 to 64: 11.8 vs 10.5 us); summed over each sweep it costs
+// 0.7-0.8% more than the faster algorithm per layer, a 2048-position cut
+// 8-15% more.  This replaces the reference heuristic for these layers (its
+// Winograd is a grouped-layer forward rule, csrc/ops/convolution.cpp:454-460,
+// kept below); every other layer, and padding beyond 2, keeps the
+// reference's choices.
 bool winograd_auto(const mx_conv2d_desc& d, int phase) {
   if (!winograd_applicable(d) || d.ph > 2 || d.pw > 2 || d.cin / d.groups < 32 || d.cout / d.groups < 32)
     return false;
-  return d.n * d.oh * d.ow >= (phase == MX_CONV_DWEIGHT ? 2048 : 1024);
+  const int64_t positions = d.n * d.oh * d.ow;
+  if (phase == MX_CONV_DWEIGHT) return positions * (d.cin / d.groups) * d.cout >= (int64_t(1) << 25);
+  return positions >= 1024;
 }
 
 // Reference heuristic (csrc/ops/convolution.cpp:423-482) restated for the

@@ -94,11 +94,23 @@ def test_planner_mirrors_reference_heuristic(mx):
     assert mx.conv2d_select(dense5, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
     strided = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (2, 2), (1, 1))
     assert mx.conv2d_select(strided, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
-    # Break-even sizes: 1024 output positions (forward, dInput), 2048 (dWeight).
+    # Break-even sizes: 1024 output positions (forward, dInput); for dWeight
+    # 2^25 multiply-adds per filter tap (positions x cin per group x cout).
     b1 = mx.conv_desc((1, 64, 32, 32), (64, 64, 3, 3), (1, 1), (1, 1))     # 1024 positions
     assert mx.conv2d_select(b1, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
     assert mx.conv2d_select(b1, mx.MX_CONV_DINPUT) == mx.ALGO_WINOGRAD
     assert mx.conv2d_select(b1, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    deep = mx.conv_desc((16, 512, 8, 8), (512, 512, 3, 3), (1, 1), (1, 1))  # C4's 8x8 level: 2^28
+    assert mx.conv2d_select(deep, mx.MX_CONV_DWEIGHT) == mx.ALGO_WINOGRAD
+    at = mx.conv_desc((8, 64, 16, 16), (256, 64, 3, 3), (1, 1), (1, 1))     # 2048 x 64 x 256 = 2^25
+    assert mx.conv2d_select(at, mx.MX_CONV_DWEIGHT) == mx.ALGO_WINOGRAD
+    below = mx.conv_desc((8, 64, 16, 16), (255, 64, 3, 3), (1, 1), (1, 1))  # one output channel fewer
+    assert mx.conv2d_select(below, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    thin_many = mx.conv_desc((8, 32, 16, 16), (64, 32, 3, 3), (1, 1), (1, 1))  # 2048 positions, 2^22
+    assert mx.conv2d_select(thin_many, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
+    assert mx.conv2d_select(thin_many, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    grouped_w = mx.conv_desc((16, 512, 8, 8), (512, 256, 3, 3), (1, 1), (1, 1), (1, 1), 2)  # per group 2^27
+    assert mx.conv2d_select(grouped_w, mx.MX_CONV_DWEIGHT) == mx.ALGO_WINOGRAD
     small = mx.conv_desc((1, 256, 14, 14), (256, 256, 3, 3), (1, 1), (1, 1))  # 196 positions
     for phase in (mx.MX_CONV_FORWARD, mx.MX_CONV_DINPUT, mx.MX_CONV_DWEIGHT):
         assert mx.conv2d_select(small, phase) == mx.ALGO_IMPLICIT_GEMM
