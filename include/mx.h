@@ -169,11 +169,13 @@ enum mx_conv_phase { MX_CONV_FORWARD = 0, MX_CONV_DINPUT = 1, MX_CONV_DWEIGHT = 
  * gradient (padding <= 2) and the weight gradient of a 3x3 stride-1
  * dilation-1 layer (the gradients are an addition: the reference's Winograd is
  * forward only); AUTO takes it in every phase for such layers with padding
- * <= 2, >= 32 channels per group on both sides and >= 1024 output positions
- * (for the weight gradient: >= 2^25 multiply-adds per filter tap, i.e.
- * positions x input channels per group x output channels), where it measures
- * faster than the implicit GEMM on MI355X, and for the reference's grouped
- * forward rule; REDUCE is the no-scratch dWeight / dBias
+ * <= 2 and >= 32 channels per group on both sides where it measures faster
+ * than the implicit GEMM on MI355X: forward and input gradient from 16384
+ * output positions, or from 512 when the channel walk (input channels for the
+ * forward, output channels for the input gradient) is at most 4x the channels
+ * produced; weight gradient from 2^25 multiply-adds per filter tap (positions
+ * x input channels per group x output channels); and for the reference's
+ * grouped forward rule; REDUCE is the no-scratch dWeight / dBias
  * reduction; DEPTHWISE is the forward of a layer with groups == cin and any
  * channel multiplier (conv2d_depthwise.comp:15-41; candidate rule
  * csrc/ops/convolution.cpp:361, chosen by AUTO when cin >= 8 as at :462). */

@@ -421,11 +421,18 @@ bool winograd_applicable(const mx_conv2d_desc& d) {
 
 // AUTO's Winograd rule for 3x3 stride-1 layers with at least 32 channels per
 // group on both sides, measured on MI355X per phase against the implicit GEMM
-// (kernel time, batch 1-64, 64-1024 channels, 7^2-64^2 images): from 1024
-// output positions the fused F(2x2,3x3) forward and input gradient take
-// 0.50-0.89 of the implicit GEMM's time (8x64 channels at 56^2: 17.8 vs 35.6
-// us; 16x128 at 64^2: 98 vs 184; 16x512 at 8^2: 45.5 vs 60.0) and lose only on
-// smaller layers (1x256 at 14^2: 28.8 vs 17.2).  The weight gradient's
+// (kernel time of each algorithm forced).  On typical layers the fused
+// F(2x2,3x3) forward and input gradient take 0.50-0.89 of the implicit GEMM's
+// time (8x64 channels at 56^2: 17.8 vs 35.6 us; 16x128 at 64^2: 98 vs 184;
+// 16x512 at 8^2: 45.5 vs 60.0).  They lose where their channel walk (input
+// channels for the forward, output channels for the input gradient) is long
+// against the channels they produce, which sets their workgroup count, unless
+// the layer has many positions: 16x1024 at 16^2 to 32 takes 98.5 vs 54.1 us,
+// at 56^2 (8 images) 155 vs 254.  Over 401 layers per phase (batch 1-32,
+// 7^2-56^2, 32-1024 x 32-512 channels) the rule below (Winograd from 16384
+// positions, or from 512 when the walk is at most 4x the channels produced)
+// sums to 2.0% (forward) and 2.4% (input gradient) above the faster algorithm
+// per layer, a cut at 1024 positions to 6.7% and 4.6%.  The weight gradient's
 // break-even follows the layer's work, not its positions: in two sweeps (342
 // and 401 layers: batch 1-32, 7^2-56^2, 32-1024 input x 32-512 output
 // channels, kernel time of each algorithm forced) it wins from
@@ -442,7 +449,9 @@ bool winograd_auto(const mx_conv2d_desc& d, int phase) {
     return false;
   const int64_t positions = d.n * d.oh * d.ow;
   if (phase == MX_CONV_DWEIGHT) return positions * (d.cin / d.groups) * d.cout >= (int64_t(1) << 25);
-  return positions >= 1024;
+  const int64_t walk = (phase == MX_CONV_FORWARD ? d.cin : d.cout) / d.groups;
+  const int64_t made = (phase == MX_CONV_FORWARD ? d.cout : d.cin) / d.groups;
+  return positions >= 16384 || (positions >= 512 && walk <= 4 * made);
 }
 
 // Reference heuristic (csrc/ops/convolution.cpp:423-482) restated for the

@@ -94,12 +94,30 @@ def test_planner_mirrors_reference_heuristic(mx):
     assert mx.conv2d_select(dense5, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
     strided = mx.conv_desc((8, 64, 56, 56), (64, 64, 3, 3), (2, 2), (1, 1))
     assert mx.conv2d_select(strided, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
-    # Break-even sizes: 1024 output positions (forward, dInput); for dWeight
-    # 2^25 multiply-adds per filter tap (positions x cin per group x cout).
+    # Break-even sizes.  Forward / dInput: 16384 output positions, or 512 when
+    # the channel walk (cin forward, cout dInput) is at most 4x the channels
+    # produced.  dWeight: 2^25 multiply-adds per filter tap (positions x cin
+    # per group x cout).
     b1 = mx.conv_desc((1, 64, 32, 32), (64, 64, 3, 3), (1, 1), (1, 1))     # 1024 positions
     assert mx.conv2d_select(b1, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
     assert mx.conv2d_select(b1, mx.MX_CONV_DINPUT) == mx.ALGO_WINOGRAD
     assert mx.conv2d_select(b1, mx.MX_CONV_DWEIGHT) == mx.ALGO_IMPLICIT_GEMM
+    b512 = mx.conv_desc((2, 64, 16, 16), (64, 64, 3, 3), (1, 1), (1, 1))   # 512 positions
+    assert mx.conv2d_select(b512, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
+    b511 = mx.conv_desc((1, 64, 7, 73), (64, 64, 3, 3), (1, 1), (1, 1))    # 511 positions
+    assert mx.conv2d_select(b511, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
+    walk = mx.conv_desc((16, 1024, 8, 8), (32, 1024, 3, 3), (1, 1), (1, 1))  # walk 32x the outputs
+    assert mx.conv2d_select(walk, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
+    assert mx.conv2d_select(walk, mx.MX_CONV_DINPUT) == mx.ALGO_WINOGRAD   # walks 32 output channels
+    four = mx.conv_desc((16, 512, 8, 8), (128, 512, 3, 3), (1, 1), (1, 1))   # walk exactly 4x
+    assert mx.conv2d_select(four, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
+    five = mx.conv_desc((16, 640, 8, 8), (128, 640, 3, 3), (1, 1), (1, 1))   # 5x
+    assert mx.conv2d_select(five, mx.MX_CONV_FORWARD) == mx.ALGO_IMPLICIT_GEMM
+    many = mx.conv_desc((16, 1024, 32, 32), (32, 1024, 3, 3), (1, 1), (1, 1))  # 16384 positions
+    assert mx.conv2d_select(many, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
+    dx_walk = mx.conv_desc((16, 32, 8, 8), (1024, 32, 3, 3), (1, 1), (1, 1))   # dInput walks 1024
+    assert mx.conv2d_select(dx_walk, mx.MX_CONV_DINPUT) == mx.ALGO_IMPLICIT_GEMM
+    assert mx.conv2d_select(dx_walk, mx.MX_CONV_FORWARD) == mx.ALGO_WINOGRAD
     deep = mx.conv_desc((16, 512, 8, 8), (512, 512, 3, 3), (1, 1), (1, 1))  # C4's 8x8 level: 2^28
     assert mx.conv2d_select(deep, mx.MX_CONV_DWEIGHT) == mx.ALGO_WINOGRAD
     at = mx.conv_desc((8, 64, 16, 16), (256, 64, 3, 3), (1, 1), (1, 1))     # 2048 x 64 x 256 = 2^25
