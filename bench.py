@@ -523,6 +523,92 @@ def run_probe_sweep(torch, numel, reps=20):
     return {"elements": n, "reps": reps, "rows": sorted(rows, key=lambda r: -r["gb_s"])}
 
 
+def rule_sweep_layers(kind):
+    """3x3 layers for run_rule_sweep as (batch, height, width, cin, cout,
+    padding).  "grid": square images, padding 1, power-of-two channels, at
+    most 1.2e9 multiply-adds per filter tap.  "random": 70 seeded layers with
+    non-square images, padding 0 / 1 / 2 and channel counts that are not
+    powers of two."""
+    import itertools
+    import random
+    if kind == "grid":
+        shapes = [(1, 14), (4, 7), (2, 8), (1, 16), (2, 14), (8, 7), (4, 16), (4, 14), (16, 8), (8, 16), (8, 14),
+                  (16, 16), (8, 28), (16, 28), (8, 56), (16, 56), (32, 56)]
+        out = []
+        for (n, hw), ci, co in itertools.product(shapes, (32, 64, 128, 256, 512, 1024), (32, 64, 128, 256, 512)):
+            if 2e6 <= n * hw * hw * ci * co <= 1.2e9:
+                out.append((n, hw, hw, ci, co, 1))
+        return out
+    rng = random.Random(11)
+    out = []
+    while len(out) < 70:
+        n = rng.choice([1, 2, 3, 4, 6, 8, 12, 16, 24])
+        h = rng.choice([6, 9, 10, 12, 15, 20, 24, 30, 40])
+        w = rng.choice([h, h + 3, max(4, h - 2)])
+        ci, co = rng.choice([48, 96, 192, 384, 768]), rng.choice([48, 96, 192, 384, 768])
+        pad = rng.choice([1, 1, 1, 0, 2])
+        pos = n * (h + 2 * pad - 2) * (w + 2 * pad - 2)
+        if 200 <= pos <= 40000 and pos * ci * co <= 1.5e9:
+            out.append((n, h, w, ci, co, pad))
+    return out
+
+
+def run_rule_sweep(torch, mx, kind):
+    """AUTO's Winograd rule for 3x3 stride-1 layers against both algorithms
+    forced: per layer and phase the kernel time of the implicit GEMM and of
+    Winograd (best of 3 rounds of 5 back-to-back calls) and the algorithm
+    AUTO selects; then, per phase, the summed time of AUTO's choices and of a
+    plain position cut (1024 positions for the forward / input gradient, 2048
+    for the weight gradient) as a percentage above the per-layer best."""
+    st = torch.cuda.current_stream().cuda_stream
+    phases = {"fwd": mx.MX_CONV_FORWARD, "dx": mx.MX_CONV_DINPUT, "dw": mx.MX_CONV_DWEIGHT}
+    totals = {p: [0.0, 0.0, 0.0] for p in phases}  # best, auto, position cut
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        best = 1e9
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(300_000)
+            e0.record()
+            for _ in range(5):
+                fn()
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) / 5 * 1e3)
+        return best
+
+    for n, h, w, ci, co, pad in rule_sweep_layers(kind):
+        d = mx.conv_desc((n, ci, h, w), (co, ci, 3, 3), (1, 1), (pad, pad))
+        x = torch.randn(n, ci, h, w, device="cuda")
+        wt = torch.randn(co, ci, 3, 3, device="cuda") * 0.05
+        y = torch.empty(n, co, d.oh, d.ow, device="cuda")
+        dy, dx = torch.randn_like(y), torch.empty_like(x)
+        dw, db = torch.empty_like(wt), torch.empty(co, device="cuda")
+        calls = {"fwd": lambda a: mx.conv2d_forward(d, x, wt, None, y, a, st),
+                 "dx": lambda a: mx.conv2d_backward_input(d, dy, wt, dx, a, st),
+                 "dw": lambda a: mx.conv2d_backward_weight(d, x, dy, dw, db, a, st)}
+        pos = n * d.oh * d.ow
+        row = {"n": n, "h": h, "w": w, "cin": ci, "cout": co, "pad": pad, "positions": pos}
+        for name, phase in phases.items():
+            ig = timed(lambda: calls[name](mx.ALGO_IMPLICIT_GEMM))
+            wi = timed(lambda: calls[name](mx.ALGO_WINOGRAD))
+            auto_wino = mx.conv2d_select(d, phase) == mx.ALGO_WINOGRAD
+            cut_wino = pos >= (2048 if name == "dw" else 1024)
+            t = totals[name]
+            t[0] += min(ig, wi)
+            t[1] += wi if auto_wino else ig
+            t[2] += wi if cut_wino else ig
+            row[name] = {"implicit_gemm_us": round(ig, 1), "winograd_us": round(wi, 1),
+                         "auto": "winograd" if auto_wino else "implicit_gemm"}
+        print(json.dumps(row), flush=True)
+    return {"sweep": kind, "above_best_pct": {p: {"auto": round(100 * (t[1] / t[0] - 1), 2),
+                                                  "position_cut": round(100 * (t[2] / t[0] - 1), 2)}
+                                              for p, t in totals.items()}}
+
+
 def back_to_back_us(torch, fn, reps, warmup):
     """Average microseconds per call of `reps` calls issued back to back on the
     current stream between one pair of HIP events.  A spin kernel queued
@@ -1014,6 +1100,8 @@ def main(argv=None):
                     help="markdown tables (per launch class, per kernel) from a rocprofv3 --stats CSV")
     ap.add_argument("--probe-sweep", action="store_true",
                     help="sweep the 4-read / 3-write probe's memory schedule at C5's size (one JSON object)")
+    ap.add_argument("--rule-sweep", choices=["grid", "random"],
+                    help="time both algorithms on 3x3 stride-1 layers in every phase against AUTO's Winograd rule")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 layers (all three phases) to implicit GEMM")
@@ -1044,6 +1132,9 @@ def main(argv=None):
     L = Launcher(mx, stream)
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 
+    if args.rule_sweep:
+        print(json.dumps(run_rule_sweep(torch, mx, args.rule_sweep)), flush=True)
+        return 0
     if args.probe_sweep:
         _, numel, _ = build_c5(torch, mx, L)
         print(json.dumps(run_probe_sweep(torch, numel)), flush=True)
