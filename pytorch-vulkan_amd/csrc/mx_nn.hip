@@ -507,18 +507,25 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_fused_kernel(const float* __r
 }
 
 // Register-resident variants of the two kernels above for groups that fit a
-// workgroup's registers (at most 16 float4 per thread, 16-byte aligned
-// planes): each element is read from HBM once instead of three times
-// (forward) or twice (backward).  Every thread holds exactly the elements
-// the multi-pass kernel's loops give it, in the same order, so the sums and
-// the results are bit-identical to that kernel's.
+// workgroup's registers (forward: at most 32 float4 per thread; backward: at
+// most 16 per thread of 4 or 8 waves; 16-byte aligned planes): each element
+// is read from HBM once instead of three times (forward) or twice
+// (backward).  Every thread holds exactly the elements the multi-pass
+// kernel's loops give it, in the same order, and each channel's backward sums
+// are one wave's over the same lanes and elements, so the sums and the
+// results are bit-identical to that kernel's.
 template <int NPT>
 __global__ __launch_bounds__(kThreads) void gn_fwd_regs_kernel(const float* __restrict__ x,
                                                                const float* __restrict__ gamma,
                                                                const float* __restrict__ beta, int C, int G, int hw,
                                                                float eps, float* __restrict__ y,
                                                                float* __restrict__ mean, float* __restrict__ rstd) {
+  // Up to 16 float4 per thread, each element's gamma / beta ride in
+  // registers; with 32 the group's gamma / beta go to LDS instead (the
+  // registers hold the data).
+  constexpr bool kLdsAffine = NPT > 16;
   __shared__ float red[kWavesPerBlock];
+  __shared__ float saff[kLdsAffine ? 2 * kGnMaxCpg : 1];
   const int ng = blockIdx.x;
   const int n = ng / G, g = ng - (ng / G) * G, cpg = C / G;
   const int count = cpg * hw, count4 = count / 4;
@@ -533,14 +540,22 @@ __global__ __launch_bounds__(kThreads) void gn_fwd_regs_kernel(const float* __re
   }
   // The affine parameters of each element's channel, loaded with the data:
   // a load between the stores below would make each store wait for the
-  // earlier ones (loads and stores share one counter).
-  float ga[NPT], be[NPT];
+  // earlier ones (loads and stores share one counter).  The LDS copy is read
+  // after block_sum's barriers.
+  float ga[kLdsAffine ? 1 : NPT], be[kLdsAffine ? 1 : NPT];
+  if constexpr (kLdsAffine) {
+    for (int ci = threadIdx.x; ci < cpg; ci += kThreads) {
+      saff[ci] = gamma ? gamma[c0 + ci] : 1.f;
+      saff[kGnMaxCpg + ci] = beta ? beta[c0 + ci] : 0.f;
+    }
+  } else {
 #pragma unroll
-  for (int j = 0; j < NPT; ++j) {
-    const int i = threadIdx.x + kThreads * j;
-    const int c = c0 + (4 * min(i, count4 - 1)) / hw;
-    ga[j] = gamma ? gamma[c] : 1.f;
-    be[j] = beta ? beta[c] : 0.f;
+    for (int j = 0; j < NPT; ++j) {
+      const int i = threadIdx.x + kThreads * j;
+      const int c = c0 + (4 * min(i, count4 - 1)) / hw;
+      ga[j] = gamma ? gamma[c] : 1.f;
+      be[j] = beta ? beta[c] : 0.f;
+    }
   }
   float s = 0.f;
 #pragma unroll
@@ -565,20 +580,29 @@ __global__ __launch_bounds__(kThreads) void gn_fwd_regs_kernel(const float* __re
   for (int j = 0; j < NPT; ++j) {
     const int i = threadIdx.x + kThreads * j;
     if (i >= count4) continue;
-    const float a = inv * ga[j], b = be[j];  // ga == 1 without gamma: inv * 1 == inv exactly
+    float a, b;  // gamma == 1 without one: inv * 1 == inv exactly
+    if constexpr (kLdsAffine) {
+      const int cl = (4 * i) / hw;
+      a = inv * saff[cl];
+      b = saff[kGnMaxCpg + cl];
+    } else {
+      a = inv * ga[j];
+      b = be[j];
+    }
     q4[i] = make_float4((v[j].x - m) * a + b, (v[j].y - m) * a + b, (v[j].z - m) * a + b, (v[j].w - m) * a + b);
   }
 }
 
-// Backward: wave w holds channels w, w + 4, ... of the group and lanes the
-// plane's float4 lane, lane + 64, ... (np of them per channel), for dy and x.
-// FULL: every one of a thread's NPT slots holds a valid float4 (channels per
-// group a multiple of 4, planes a multiple of 256 floats, NPT equal to
-// (cpg / 4) * (hw / 256)), so loads and stores carry no per-slot condition and
-// form straight-line code (a conditional store block makes the compiler wait
-// for every earlier store at its entry).
-template <int NPT, bool FULL>
-__global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __restrict__ dy,
+// Backward: with W waves, wave w holds channels w, w + W, ... of the group
+// and lanes the plane's float4 lane, lane + 64, ... (np of them per channel),
+// for dy and x.  W = 8 takes groups that need more than 16 float4 per thread
+// at 4 waves.  FULL: every one of a thread's NPT slots holds a valid float4
+// (channels per group a multiple of W, planes a multiple of 256 floats, NPT
+// equal to (cpg / W) * (hw / 256)), so loads and stores carry no per-slot
+// condition and form straight-line code (a conditional store block makes the
+// compiler wait for every earlier store at its entry).
+template <int NPT, bool FULL, int W>
+__global__ __launch_bounds__(64 * W) void gn_bwd_regs_kernel(const float* __restrict__ dy,
                                                                const float* __restrict__ x,
                                                                const float* __restrict__ mean,
                                                                const float* __restrict__ rstd,
@@ -603,7 +627,7 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __re
   // Element k of this thread: channel wave + 4 (k / np), plane float4 lane + 64 (k % np).
 #pragma unroll
   for (int k = 0; k < NPT; ++k) {
-    const int ci = wave + kWavesPerBlock * (k / np), i = lane + 64 * (k % np);
+    const int ci = wave + W * (k / np), i = lane + 64 * (k % np);
     const bool ok = FULL || (ci < cpg && i < hw4);
     gv[k] = ok ? g4[int64_t(ci) * hw4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
     xv[k] = ok ? x4[int64_t(ci) * hw4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -612,9 +636,9 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __re
   // the dx stores below have neither a global load nor a branch between them
   // (loads and stores share one counter: such a load would make each store
   // wait for the earlier ones).
-  for (int ci = threadIdx.x; ci < cpg; ci += kThreads) sg[ci] = gamma ? gamma[g * cpg + ci] : 1.f;
-  for (int cb = 0; cb * kWavesPerBlock < cpg; ++cb) {
-    const int ci = wave + kWavesPerBlock * cb;
+  for (int ci = threadIdx.x; ci < cpg; ci += 64 * W) sg[ci] = gamma ? gamma[g * cpg + ci] : 1.f;
+  for (int cb = 0; cb * W < cpg; ++cb) {
+    const int ci = wave + W * cb;
     float a = 0.f, b = 0.f;
 #pragma unroll
     for (int k = 0; k < NPT; ++k) {
@@ -655,7 +679,7 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __re
   // registers, so none waits for an earlier one to release its data.
 #pragma unroll
   for (int k = 0; k < NPT; ++k) {
-    const float pc = inv * sg[min(wave + kWavesPerBlock * (k / np), cpg - 1)];
+    const float pc = inv * sg[min(wave + W * (k / np), cpg - 1)];
     const float4 gg = gv[k], v = xv[k];
     gv[k] = make_float4(pc * gg.x + kk * (v.x - mu) + q, pc * gg.y + kk * (v.y - mu) + q,
                         pc * gg.z + kk * (v.z - mu) + q, pc * gg.w + kk * (v.w - mu) + q);
@@ -663,7 +687,7 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_regs_kernel(const float* __re
   float4* d4 = reinterpret_cast<float4*>(dx + base);
 #pragma unroll
   for (int k = 0; k < NPT; ++k) {
-    const int ci = wave + kWavesPerBlock * (k / np), i = lane + 64 * (k % np);
+    const int ci = wave + W * (k / np), i = lane + 64 * (k % np);
     if (FULL || (ci < cpg && i < hw4)) d4[int64_t(ci) * hw4 + i] = gv[k];
   }
 }
@@ -1209,10 +1233,10 @@ void launch_copy_rows(void* dst, int64_t dst_pitch, const void* src, int64_t src
 
 int launch_rows(int64_t rows) { return int((rows + kWavesPerBlock - 1) / kWavesPerBlock); }
 
-// Smallest register-array size of {1, 2, 4, 8, 16} holding `need` float4 per
-// thread (0: more than 16).
-int regs_for(int64_t need) {
-  for (int r = 1; r <= 16; r *= 2)
+// Smallest register-array size of {1, 2, 4, ..., cap} holding `need` float4
+// per thread (0: more than cap).
+int regs_for(int64_t need, int cap = 16) {
+  for (int r = 1; r <= cap; r *= 2)
     if (need <= r) return r;
   return 0;
 }
@@ -1260,7 +1284,7 @@ int mx_group_norm_forward(const float* x, const float* gamma, const float* beta,
   const int64_t cpg64 = c / groups;
   if (cpg64 <= kGnMaxCpg && cpg64 * hw <= INT32_MAX && n * groups <= INT32_MAX) {
     const bool vec4 = hw % 4 == 0 && aligned16(x) && aligned16(y);
-    const int npt = vec4 ? regs_for((cpg64 * hw / 4 + kThreads - 1) / kThreads) : 0;
+    const int npt = vec4 ? regs_for((cpg64 * hw / 4 + kThreads - 1) / kThreads, 32) : 0;
     const dim3 grid(unsigned(n * groups));
     const int C = int(c), G = int(groups), HW = int(hw);
     switch (npt) {
@@ -1273,6 +1297,8 @@ int mx_group_norm_forward(const float* x, const float* gamma, const float* beta,
       case 8: hipLaunchKernelGGL(gn_fwd_regs_kernel<8>, grid, dim3(kThreads), 0, s, x, gamma, beta, C, G, HW, eps, y,
                                  mean, rstd); break;
       case 16: hipLaunchKernelGGL(gn_fwd_regs_kernel<16>, grid, dim3(kThreads), 0, s, x, gamma, beta, C, G, HW, eps,
+                                  y, mean, rstd); break;
+      case 32: hipLaunchKernelGGL(gn_fwd_regs_kernel<32>, grid, dim3(kThreads), 0, s, x, gamma, beta, C, G, HW, eps,
                                   y, mean, rstd); break;
       default: break;
     }
@@ -1343,26 +1369,33 @@ int mx_group_norm_backward(const float* dy, const float* x, const float* mean, c
   const bool vec = hw % 4 == 0 && aligned16(x) && aligned16(dy) && (!dx || aligned16(dx));
   const int cpg = int(c / groups);
   if (cpg <= kGnMaxCpg && int64_t(cpg) * hw <= INT32_MAX && n * groups <= INT32_MAX) {
-    const int npt = vec ? regs_for(int64_t((cpg + kWavesPerBlock - 1) / kWavesPerBlock) * ((hw / 4 + 63) / 64)) : 0;
+    // Float4 per thread at 4 waves; groups that need more than 16 take 8.
+    const int64_t np = (hw / 4 + 63) / 64;
+    int waves = kWavesPerBlock;
+    int npt = vec ? regs_for(int64_t((cpg + waves - 1) / waves) * np) : 0;
+    if (vec && !npt) {
+      waves = 2 * kWavesPerBlock;
+      npt = regs_for(int64_t((cpg + waves - 1) / waves) * np);
+    }
     const dim3 grid(unsigned(n * groups));
     const int C = int(c), G = int(groups), HW = int(hw);
-    const bool full = npt && cpg % kWavesPerBlock == 0 && hw % 256 == 0 &&
-                      int64_t(cpg / kWavesPerBlock) * (hw / 256) == npt;
-#define MX_GN_BWD(N)                                                                                               \
+    const bool full = npt && cpg % waves == 0 && hw % 256 == 0 && int64_t(cpg / waves) * (hw / 256) == npt;
+#define MX_GN_BWD(N, W)                                                                                             \
   do {                                                                                                             \
     if (full)                                                                                                      \
-      hipLaunchKernelGGL((gn_bwd_regs_kernel<N, true>), grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G, \
-                         HW, dx, sdy, sdyx);                                                                       \
+      hipLaunchKernelGGL((gn_bwd_regs_kernel<N, true, W>), grid, dim3(64 * W), 0, s, dy, x, mean, rstd, gamma, C,   \
+                         G, HW, dx, sdy, sdyx);                                                                    \
     else                                                                                                           \
-      hipLaunchKernelGGL((gn_bwd_regs_kernel<N, false>), grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C,   \
+      hipLaunchKernelGGL((gn_bwd_regs_kernel<N, false, W>), grid, dim3(64 * W), 0, s, dy, x, mean, rstd, gamma, C,  \
                          G, HW, dx, sdy, sdyx);                                                                    \
   } while (0)
-    switch (npt) {
-      case 1: MX_GN_BWD(1); break;
-      case 2: MX_GN_BWD(2); break;
-      case 4: MX_GN_BWD(4); break;
-      case 8: MX_GN_BWD(8); break;
-      case 16: MX_GN_BWD(16); break;
+    switch (waves == kWavesPerBlock ? npt : 32 + npt) {
+      case 1: MX_GN_BWD(1, 4); break;
+      case 2: MX_GN_BWD(2, 4); break;
+      case 4: MX_GN_BWD(4, 4); break;
+      case 8: MX_GN_BWD(8, 4); break;
+      case 16: MX_GN_BWD(16, 4); break;
+      case 32 + 16: MX_GN_BWD(16, 8); break;
       default:
         if (vec)
           hipLaunchKernelGGL(gn_bwd_fused_kernel<true>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G, HW,

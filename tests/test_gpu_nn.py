@@ -163,11 +163,12 @@ def _lane0_tree(v):
     return v[0]
 
 
-@pytest.mark.parametrize("channels", [4, 2])
+@pytest.mark.parametrize("channels", [4, 2, 8, 16])
 def test_abi_group_norm_dbeta_follows_the_lane0_tree(mx, channels):
     """With one sample, dbeta of a channel is one wave's reduction of its
     lanes' partial sums of dy: the register-resident backward (4 channels per
-    group: the straight-line variant; 2: the guarded one) gives lane l the
+    group: the straight-line variant at 4 waves; 2: the guarded one; 8: the
+    8-wave variant; 16: the multi-pass kernel) gives lane l the
     float4s l, l + 64, ... of the 64x64 plane, each added as (x + y) + (z + w)
     to a running sum, and the wave combines the lanes by lane 0's tree.  The
     float32 restatement below must match bit for bit: a tree step that read
