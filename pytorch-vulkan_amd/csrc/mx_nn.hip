@@ -515,6 +515,203 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_fused_kernel(const float* __r
   }
 }
 
+// Streaming variants of the two kernels above for 16-byte aligned groups
+// whose bytes fit a buffer resource: each thread keeps a batch of float4
+// loads in flight per pass (in the element-wise pass the next batch is
+// loaded before the current one is stored), gamma / beta come from LDS, and
+// masked lanes use an out-of-range buffer offset (the load reads 0, the
+// store is dropped), so the stores form straight-line code.  Per thread the
+// elements, the order of their sums and every expression are those of the
+// loops above, so the results are bit-identical.
+typedef float nn_f32x4 __attribute__((ext_vector_type(4)));
+typedef int nn_i32x4 __attribute__((ext_vector_type(4)));
+extern "C" __device__ nn_f32x4 mx_nn_buffer_load_v4f32(nn_i32x4 rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.buffer.load.v4f32");
+extern "C" __device__ void mx_nn_buffer_store_v4f32(nn_f32x4 v, nn_i32x4 rsrc, int voffset, int soffset,
+                                                    int aux) __asm("llvm.amdgcn.raw.buffer.store.v4f32");
+constexpr int kGnBatch = 4;
+constexpr int kNnOffNone = int(0x80000000u);
+
+// Buffer resource over [base, base + bytes) (bytes < 2^31): raw addressing,
+// 32-bit elements; an offset at or past the extent reads 0 / drops the store.
+__device__ __forceinline__ nn_i32x4 nn_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  nn_i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(int(uint32_t(a)));
+  r.y = __builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32) & 0xFFFFu));
+  r.z = __builtin_amdgcn_readfirstlane(int(bytes));
+  r.w = 0x00020000;
+  return r;
+}
+
+__global__ __launch_bounds__(kThreads) void gn_fwd_stream_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ gamma,
+                                                                 const float* __restrict__ beta, int C, int G,
+                                                                 int hw, float eps, float* __restrict__ y,
+                                                                 float* __restrict__ mean,
+                                                                 float* __restrict__ rstd) {
+  __shared__ float red[kWavesPerBlock];
+  __shared__ float saff[2 * kGnMaxCpg];
+  const int ng = blockIdx.x;
+  const int n = ng / G, g = ng - (ng / G) * G, cpg = C / G;
+  const int count = cpg * hw, count4 = count / 4;
+  const int64_t base = (int64_t(n) * C + int64_t(g) * cpg) * hw;
+  const int c0 = g * cpg;
+  const nn_i32x4 rx = nn_rsrc(x + base, uint32_t(count) * 4u);
+  const nn_i32x4 ry = nn_rsrc(y + base, uint32_t(count) * 4u);
+  for (int ci = threadIdx.x; ci < cpg; ci += kThreads) {
+    saff[ci] = gamma ? gamma[c0 + ci] : 1.f;
+    saff[kGnMaxCpg + ci] = beta ? beta[c0 + ci] : 0.f;
+  }
+  auto off = [&](int i) { return i < count4 ? 16 * i : kNnOffNone; };
+  constexpr int kStep = kGnBatch * kThreads;
+  float s = 0.f;
+  for (int i0 = threadIdx.x; i0 < count4; i0 += kStep) {
+    nn_f32x4 v[kGnBatch];
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) v[u] = mx_nn_buffer_load_v4f32(rx, off(i0 + u * kThreads), 0, 0);
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u)
+      if (i0 + u * kThreads < count4) s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+  }
+  const float m = block_sum(s, red) / float(count);
+  float sq = 0.f;
+  for (int i0 = threadIdx.x; i0 < count4; i0 += kStep) {
+    nn_f32x4 v[kGnBatch];
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) v[u] = mx_nn_buffer_load_v4f32(rx, off(i0 + u * kThreads), 0, 0);
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) {
+      if (i0 + u * kThreads < count4) {
+        const float a = v[u].x - m, b = v[u].y - m, c = v[u].z - m, d = v[u].w - m;
+        sq += (a * a + b * b) + (c * c + d * d);
+      }
+    }
+  }
+  const float inv = 1.f / sqrtf(block_sum(sq, red) / float(count) + eps);
+  if (threadIdx.x == 0) {
+    mean[ng] = m;
+    rstd[ng] = inv;
+  }
+  nn_f32x4 cur[kGnBatch];
+#pragma unroll
+  for (int u = 0; u < kGnBatch; ++u) cur[u] = mx_nn_buffer_load_v4f32(rx, off(threadIdx.x + u * kThreads), 0, 0);
+  for (int i0 = threadIdx.x; i0 < count4; i0 += kStep) {
+    nn_f32x4 nxt[kGnBatch];
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) nxt[u] = mx_nn_buffer_load_v4f32(rx, off(i0 + kStep + u * kThreads), 0, 0);
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) {
+      const int i = i0 + u * kThreads;
+      const int cl = (4 * min(i, count4 - 1)) / hw;
+      const float a = inv * saff[cl], b = saff[kGnMaxCpg + cl];  // gamma == 1 without one: inv * 1 == inv
+      const nn_f32x4 v = cur[u];
+      const nn_f32x4 o = {(v.x - m) * a + b, (v.y - m) * a + b, (v.z - m) * a + b, (v.w - m) * a + b};
+      mx_nn_buffer_store_v4f32(o, ry, off(i), 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) cur[u] = nxt[u];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void gn_bwd_stream_kernel(const float* __restrict__ dy,
+                                                                 const float* __restrict__ x,
+                                                                 const float* __restrict__ mean,
+                                                                 const float* __restrict__ rstd,
+                                                                 const float* __restrict__ gamma, int C, int G,
+                                                                 int hw, float* __restrict__ dx,
+                                                                 float* __restrict__ part_dy,
+                                                                 float* __restrict__ part_dyx) {
+#pragma clang fp contract(off)
+  __shared__ float sdy[kGnMaxCpg], sdyx[kGnMaxCpg], sg[kGnMaxCpg];
+  __shared__ float tot[2];
+  const int ng = blockIdx.x;
+  const int n = ng / G, g = ng - (ng / G) * G, cpg = C / G;
+  const int count = cpg * hw, count4 = count / 4, hw4 = hw / 4;
+  const int64_t base = (int64_t(n) * C + int64_t(g) * cpg) * hw;
+  const float mu = mean[ng], inv = rstd[ng];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const nn_i32x4 rg = nn_rsrc(dy + base, uint32_t(count) * 4u);
+  const nn_i32x4 rx = nn_rsrc(x + base, uint32_t(count) * 4u);
+  for (int ci = threadIdx.x; ci < cpg; ci += kThreads) sg[ci] = gamma ? gamma[g * cpg + ci] : 1.f;
+  for (int ci = wave; ci < cpg; ci += kWavesPerBlock) {
+    float a = 0.f, b = 0.f;
+    auto coff = [&](int i) { return i < hw4 ? 16 * (ci * hw4 + i) : kNnOffNone; };
+    for (int i0 = lane; i0 < hw4; i0 += kGnBatch * 64) {
+      nn_f32x4 gv[kGnBatch], xv[kGnBatch];
+#pragma unroll
+      for (int u = 0; u < kGnBatch; ++u) {
+        gv[u] = mx_nn_buffer_load_v4f32(rg, coff(i0 + 64 * u), 0, 0);
+        xv[u] = mx_nn_buffer_load_v4f32(rx, coff(i0 + 64 * u), 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kGnBatch; ++u) {
+        if (i0 + 64 * u < hw4) {
+          const nn_f32x4 gg = gv[u], v = xv[u];
+          a += (gg.x + gg.y) + (gg.z + gg.w);
+          b += (gg.x * (v.x - mu) + gg.y * (v.y - mu)) + (gg.z * (v.z - mu) + gg.w * (v.w - mu));
+        }
+      }
+    }
+    a = wave_sum(a);
+    b = wave_sum(b);
+    if (lane == 0) {
+      sdy[ci] = a;
+      sdyx[ci] = b;
+      const int64_t r = int64_t(n) * C + int64_t(g) * cpg + ci;
+      part_dy[r] = a;
+      part_dyx[r] = b;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sv = 0.f, svx = 0.f;
+    for (int ci = 0; ci < cpg; ++ci) {
+      const float w = sg[ci];
+      sv += w * sdy[ci];
+      svx += w * sdyx[ci];
+    }
+    tot[0] = sv;
+    tot[1] = svx;
+  }
+  __syncthreads();
+  if (!dx) return;
+  const float cnt = float(count);
+  const float k = -inv * inv * inv * (tot[1] / cnt);
+  const float q = -inv * (tot[0] / cnt);
+  const nn_i32x4 rd = nn_rsrc(dx + base, uint32_t(count) * 4u);
+  auto off = [&](int i) { return i < count4 ? 16 * i : kNnOffNone; };
+  constexpr int kStep = kGnBatch * kThreads;
+  nn_f32x4 cg[kGnBatch], cx[kGnBatch];
+#pragma unroll
+  for (int u = 0; u < kGnBatch; ++u) {
+    cg[u] = mx_nn_buffer_load_v4f32(rg, off(threadIdx.x + u * kThreads), 0, 0);
+    cx[u] = mx_nn_buffer_load_v4f32(rx, off(threadIdx.x + u * kThreads), 0, 0);
+  }
+  for (int i0 = threadIdx.x; i0 < count4; i0 += kStep) {
+    nn_f32x4 ng4[kGnBatch], nx4[kGnBatch];
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) {
+      ng4[u] = mx_nn_buffer_load_v4f32(rg, off(i0 + kStep + u * kThreads), 0, 0);
+      nx4[u] = mx_nn_buffer_load_v4f32(rx, off(i0 + kStep + u * kThreads), 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) {
+      const int i = i0 + u * kThreads;
+      const float pc = inv * sg[(4 * min(i, count4 - 1)) / hw];
+      const nn_f32x4 gg = cg[u], v = cx[u];
+      const nn_f32x4 o = {pc * gg.x + k * (v.x - mu) + q, pc * gg.y + k * (v.y - mu) + q,
+                          pc * gg.z + k * (v.z - mu) + q, pc * gg.w + k * (v.w - mu) + q};
+      mx_nn_buffer_store_v4f32(o, rd, off(i), 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kGnBatch; ++u) {
+      cg[u] = ng4[u];
+      cx[u] = nx4[u];
+    }
+  }
+}
+
 // Register-resident variants of the two kernels above for groups that fit a
 // workgroup's registers (forward: at most 32 float4 per thread; backward: at
 // most 16 per thread of 4 or 8 waves; 16-byte aligned planes): each element
@@ -1315,7 +1512,10 @@ int mx_group_norm_forward(const float* x, const float* gamma, const float* beta,
       MX_HIP(hipGetLastError());
       return MX_OK;
     }
-    if (vec4)
+    if (vec4 && cpg64 * hw * 4 < (int64_t(1) << 31))
+      hipLaunchKernelGGL(gn_fwd_stream_kernel, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, x, gamma, beta,
+                         int(c), int(groups), int(hw), eps, y, mean, rstd);
+    else if (vec4)
       hipLaunchKernelGGL(gn_fwd_fused_kernel<true>, dim3(unsigned(n * groups)), dim3(kThreads), 0, s, x, gamma, beta,
                          int(c), int(groups), int(hw), eps, y, mean, rstd);
     else
@@ -1406,7 +1606,10 @@ int mx_group_norm_backward(const float* dy, const float* x, const float* mean, c
       case 16: MX_GN_BWD(16, 4); break;
       case 32 + 16: MX_GN_BWD(16, 8); break;
       default:
-        if (vec)
+        if (vec && int64_t(cpg) * hw * 4 < (int64_t(1) << 31))
+          hipLaunchKernelGGL(gn_bwd_stream_kernel, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G, HW,
+                             dx, sdy, sdyx);
+        else if (vec)
           hipLaunchKernelGGL(gn_bwd_fused_kernel<true>, grid, dim3(kThreads), 0, s, dy, x, mean, rstd, gamma, C, G, HW,
                              dx, sdy, sdyx);
         else

@@ -92,6 +92,9 @@ GN_CASES = [((2, 8, 4, 5), 4), ((1, 12, 3, 7), 3), ((2, 16, 8), 8), ((2, 4, 1, 1
             ((2, 256, 64, 64), 32),
             # register-resident kernels: 16 float4 per thread (C4's level-0 shape), 2 and 8
             ((2, 128, 64, 64), 32), ((3, 64, 16, 32), 16), ((2, 96, 32, 32), 24),
+            # more than 32768 elements per group: the streaming kernels (ragged
+            # last batch: 3600-float planes)
+            ((2, 384, 64, 64), 32), ((2, 96, 60, 60), 8),
             # more than 1024 channels per group: the row-statistics path
             ((1, 2048, 2, 2), 1), ((2, 1030, 3, 1), 1)]
 
