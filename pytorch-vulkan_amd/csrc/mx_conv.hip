@@ -605,16 +605,22 @@ const char* tile_name(int tile, int phase) {
 // with tile `ti` and K split `splits` ways of kps each, plus the finalize pass
 // that sums the partial outputs.  A CU holding n tiles runs at
 // rate * occ(n) of its share of 85% of the FP32 MFMA peak, occ rising from
-// 0.56 with one resident tile to 1 with per_cu; tiles beyond that queue.
+// 0.75 with one resident tile to 1 with per_cu; tiles beyond that queue.  The
+// finalize moves (splits + 1) outputs' bytes at an effective 3.1 TB/s.  The
+// two constants were fitted on MI355X to every (tile, split) plan of 83
+// layer phases (C3's implicit-GEMM layers and the small C1 / C4 layers, each
+// plan forced and timed): the planner's picks sum to 0.1% above the best
+// plan per layer on C3 and 1.6% on the small layers, against 0.5% and 8.9%
+// with the earlier 0.56 and 8 TB/s.
 double plan_cost(const TileInfo& ti, int64_t M, int64_t Ncols, int64_t G, int64_t splits, int64_t kps,
                  int64_t out_elems) {
   const double cu = cu_count();
   const double cu_flops = 0.85 * 157.3e12 / 256.0;
   const int64_t tiles = ((M + ti.bm - 1) / ti.bm) * ((Ncols + ti.bn - 1) / ti.bn) * G;
   const int64_t per_cu = (tiles * splits + int64_t(cu) - 1) / int64_t(cu);
-  const double occ = std::min(1.0, 0.56 + 0.44 * double(per_cu - 1) / double(ti.per_cu - 1));
+  const double occ = std::min(1.0, 0.75 + 0.25 * double(per_cu - 1) / double(ti.per_cu - 1));
   double t = double(per_cu) * 2.0 * ti.bm * ti.bn * double(kps) / (cu_flops * ti.rate * occ) + 2e-6;
-  if (splits > 1) t += double(splits + 1) * double(out_elems) * 4.0 / 8.0e12 + 3e-6;
+  if (splits > 1) t += double(splits + 1) * double(out_elems) * 4.0 / 3.1e12 + 3e-6;
   return t;
 }
 
