@@ -609,6 +609,92 @@ def run_rule_sweep(torch, mx, kind):
                                               for p, t in totals.items()}}
 
 
+def plan_sweep_layers():
+    """(x shape, cout, k, stride, pad, source) of the planner sweep: the 53
+    ResNet-50 convolutions at batch 64 (C3) and the small C1 / C4 layers."""
+    layers = {}
+    for _, xs, cout, k, stride, pad in resnet50_convs(64):
+        layers.setdefault((xs, cout, k, stride, pad), "c3")
+    for xs, co, k, s, pad in [((8, 64, 56, 56), 64, 3, 1, 1), ((16, 256, 16, 16), 768, 1, 1, 0),
+                              ((16, 768, 16, 16), 256, 1, 1, 0), ((16, 256, 8, 8), 512, 1, 1, 0),
+                              ((16, 1024, 8, 8), 512, 1, 1, 0), ((16, 128, 64, 64), 128, 3, 2, 1),
+                              ((16, 256, 16, 16), 256, 3, 2, 1), ((16, 256, 16, 16), 256, 1, 1, 0),
+                              ((16, 384, 64, 64), 128, 1, 1, 0), ((16, 512, 32, 32), 256, 1, 1, 0),
+                              ((16, 256, 32, 32), 256, 3, 2, 1), ((16, 128, 32, 32), 256, 1, 1, 0),
+                              ((16, 256, 16, 16), 512, 1, 1, 0)]:
+        layers.setdefault((xs, co, k, s, pad), "small")
+    return [(*key, src) for key, src in layers.items()]
+
+
+def run_plan_sweep(torch, mx):
+    """The convolution planner against every (tile, K split) plan: each
+    implicit-GEMM phase of the sweep's layers (phases AUTO sends to Winograd
+    are skipped) timed under every plan MX_CONV_PLAN can force (best of 3
+    rounds of 4 back-to-back calls), and the planner's own pick.  Reports,
+    per source, the summed time of the planner's picks and of the best plan
+    per layer phase."""
+    st = torch.cuda.current_stream().cuda_stream
+    algo = mx.ALGO_IMPLICIT_GEMM
+    totals = defaultdict(lambda: [0.0, 0.0])
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        best = 1e9
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(200_000)
+            e0.record()
+            for _ in range(4):
+                fn()
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) / 4 * 1e3)
+        return best
+
+    try:
+        for xs, co, k, s, pad, src in plan_sweep_layers():
+            d = mx.conv_desc(xs, (co, xs[1], k, k), (s, s), (pad, pad))
+            x = torch.randn(xs, device="cuda")
+            w = torch.randn(co, xs[1], k, k, device="cuda") * 0.05
+            y = torch.empty(xs[0], co, d.oh, d.ow, device="cuda")
+            dy, dx = torch.randn_like(y), torch.empty_like(x)
+            dw, db = torch.empty_like(w), torch.empty(co, device="cuda")
+            phases = [(mx.MX_CONV_FORWARD, "fwd", lambda: mx.conv2d_forward(d, x, w, None, y, algo, st)),
+                      (mx.MX_CONV_DINPUT, "dx", lambda: mx.conv2d_backward_input(d, dy, w, dx, algo, st)),
+                      (mx.MX_CONV_DWEIGHT, "dw", lambda: mx.conv2d_backward_weight(d, x, dy, dw, db, algo, st))]
+            for phase, name, fn in phases:
+                if (name == "dx" and xs[1] == 3) or mx.conv2d_select(d, phase) != algo:
+                    continue
+                os.environ.pop("MX_CONV_PLAN", None)
+                plan = mx.conv2d_plan(d, phase, algo)
+                auto = f"{plan['tile']},{plan['splits']}"
+                times = {auto: timed(fn)}
+                for tile in range(6):
+                    for splits in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128):
+                        os.environ["MX_CONV_PLAN"] = f"{tile},{splits}"
+                        try:
+                            p = mx.conv2d_plan(d, phase, algo)
+                        except mx.MXError:
+                            continue
+                        key = f"{p['tile']},{p['splits']}"
+                        if p["tile"] == tile and key not in times:
+                            times[key] = timed(fn)
+                os.environ.pop("MX_CONV_PLAN", None)
+                best = min(times, key=times.get)
+                totals[src][0] += times[auto]
+                totals[src][1] += times[best]
+                print(json.dumps({"source": src, "x": xs, "cout": co, "k": k, "stride": s, "pad": pad, "phase": name,
+                                  "planner": auto, "planner_us": round(times[auto], 2), "best": best,
+                                  "best_us": round(times[best], 2)}), flush=True)
+    finally:
+        os.environ.pop("MX_CONV_PLAN", None)
+    return {"planner_above_best_pct": {src: round(100 * (t[0] / t[1] - 1), 2) for src, t in totals.items()},
+            "planner_us": {src: round(t[0], 1) for src, t in totals.items()},
+            "best_us": {src: round(t[1], 1) for src, t in totals.items()}}
+
+
 def back_to_back_us(torch, fn, reps, warmup):
     """Average microseconds per call of `reps` calls issued back to back on the
     current stream between one pair of HIP events.  A spin kernel queued
@@ -1102,6 +1188,8 @@ def main(argv=None):
                     help="sweep the 4-read / 3-write probe's memory schedule at C5's size (one JSON object)")
     ap.add_argument("--rule-sweep", choices=["grid", "random"],
                     help="time both algorithms on 3x3 stride-1 layers in every phase against AUTO's Winograd rule")
+    ap.add_argument("--plan-sweep", action="store_true",
+                    help="time every (tile, K split) plan of the convolution planner against its own picks")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-winograd", action="store_true", help="route C3's 3x3 stride-1 layers (all three phases) to implicit GEMM")
@@ -1132,6 +1220,9 @@ def main(argv=None):
     L = Launcher(mx, stream)
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 
+    if args.plan_sweep:
+        print(json.dumps(run_plan_sweep(torch, mx)), flush=True)
+        return 0
     if args.rule_sweep:
         print(json.dumps(run_rule_sweep(torch, mx, args.rule_sweep)), flush=True)
         return 0

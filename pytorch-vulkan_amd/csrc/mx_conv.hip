@@ -609,9 +609,9 @@ const char* tile_name(int tile, int phase) {
 // finalize moves (splits + 1) outputs' bytes at an effective 3.1 TB/s.  The
 // two constants were fitted on MI355X to every (tile, split) plan of 83
 // layer phases (C3's implicit-GEMM layers and the small C1 / C4 layers, each
-// plan forced and timed): the planner's picks sum to 0.1% above the best
-// plan per layer on C3 and 1.6% on the small layers, against 0.5% and 8.9%
-// with the earlier 0.56 and 8 TB/s.
+// plan forced and timed): the planner's picks sum to 0.1-0.4% above the
+// best plan per layer on C3 and 1.5-1.6% on the small layers, against 0.5%
+// and 8.9% with the earlier 0.56 and 8 TB/s.
 double plan_cost(const TileInfo& ti, int64_t M, int64_t Ncols, int64_t G, int64_t splits, int64_t kps,
                  int64_t out_elems) {
   const double cu = cu_count();
