@@ -51,30 +51,32 @@ MX_TILE_KERNEL(C) void conv_dw_kernel(ConvArgs p) {
 
   const int64_t dw_elems = int64_t(p.G) * p.Cout_g * p.Ncols;
   float* dst = (p.splits == 1 ? p.out : p.ws + split * dw_elems) + int64_t(g) * p.Cout_g * p.Ncols;
-  // Column n of the GEMM is weight column n, or with channel-blocked columns
-  // (channel block cb, tap t, channel in block c) weight column (16cb + c)*KK + t.
-  int ccol[C::FN];
-  bool cok[C::FN];
+  // This group's dW (or partial; weights are below 2^31 bytes) as a buffer
+  // resource: stores outside the valid rows / columns go to kOffNone and are
+  // dropped, so they run straight through without branches.  Column n of the
+  // GEMM is weight column n, or with channel-blocked columns (channel block
+  // cb, tap t, channel in block c) weight column (16cb + c)*KK + t.
+  const i32x4 ro = buffer_rsrc(dst, int64_t(p.Cout_g) * p.Ncols * 4);
+  uint32_t ccol[C::FN];
   const int kblk = p.KK * kChanBlock;
 #pragma unroll
   for (int j = 0; j < C::FN; ++j) {
     const int n = col0 + acc_col<C>(j);
-    cok[j] = n < p.Ncols;
+    int c = n;
     if (p.cols_blocked) {
       const int cb = n / kblk, rem = n - cb * kblk;
       const int t = rem / kChanBlock;
-      ccol[j] = cb * kblk + (rem - t * kChanBlock) * p.KK + t;
-    } else {
-      ccol[j] = n;
+      c = cb * kblk + (rem - t * kChanBlock) * p.KK + t;
     }
+    ccol[j] = n < p.Ncols ? uint32_t(c) * 4u : kOffNone;
   }
   for_each_acc_row<C>([&](int r, int i, int v) {
     const int co = row0 + r;
-    if (co >= p.M) return;
-    float* d = dst + int64_t(co) * p.Ncols;
+    const bool rok = co < p.M;
+    const uint32_t roff = uint32_t(co * p.Ncols) * 4u;
 #pragma unroll
     for (int j = 0; j < C::FN; ++j)
-      if (cok[j]) d[ccol[j]] = acc.v[i][j][v];
+      bstore(acc.v[i][j][v], ro, (rok && ccol[j] != kOffNone) ? roff + ccol[j] : kOffNone, 0);
   });
   if (p.db != nullptr && tn == 0) {
     float* dbd = (p.splits == 1 ? p.db : p.ws_db + int64_t(split) * p.Cout) + g * p.Cout_g;

@@ -112,26 +112,31 @@ __device__ __forceinline__ void dx_tile(const ConvArgs& p, int g, int lin, int s
     });
     return;
   }
-  // Output offset of each fragment column (img * Cin * HW + phase position), once.
-  int cbase[C::FN];
-  bool cok[C::FN];
+  // The output (one launch's dx, or one split's partial, below 2^31 bytes)
+  // as a buffer resource: stores outside the tile's valid rows / columns go
+  // to kOffNone and are dropped, so the stores run straight through without
+  // a branch or a 64-bit address per element.  Byte offset of each fragment
+  // column (img * Cin * HW + phase position), once.
+  const i32x4 ro = buffer_rsrc(out, p.out_elems * 4);
+  uint32_t cbase[C::FN];
 #pragma unroll
   for (int j = 0; j < C::FN; ++j) {
     const int pos = col0 + acc_col<C>(j);
-    cok[j] = pos < p.Ncols;
-    const int pp = cok[j] ? pos : 0;
+    const bool cok = pos < p.Ncols;
+    const int pp = cok ? pos : 0;
     const int img = pp / p.HpWp;
     const int q = pp - img * p.HpWp;
     const int i = q / p.Wp;
-    cbase[j] = img * p.Cin * p.HW + (p.pa + p.sh * i) * p.W + p.pb + p.sw * (q - i * p.Wp);
+    cbase[j] = cok ? uint32_t(img * p.Cin * p.HW + (p.pa + p.sh * i) * p.W + p.pb + p.sw * (q - i * p.Wp)) * 4u
+                   : kOffNone;
   }
   for_each_acc_row<C>([&](int r, int i, int v) {
     const int ci = row0 + r;
-    if (ci >= p.M) return;
-    float* dst = out + int64_t(g * p.Cin_g + ci) * p.HW;
+    const bool rok = ci < p.M;
+    const uint32_t roff = uint32_t((g * p.Cin_g + ci) * p.HW) * 4u;
 #pragma unroll
     for (int j = 0; j < C::FN; ++j)
-      if (cok[j]) dst[cbase[j]] = acc.v[i][j][v];
+      bstore(acc.v[i][j][v], ro, (rok && cbase[j] != kOffNone) ? roff + cbase[j] : kOffNone, 0);
   });
 }
 
