@@ -626,6 +626,65 @@ def plan_sweep_layers():
     return [(*key, src) for key, src in layers.items()]
 
 
+def run_blas_compare(torch, mx):
+    """Each distinct 1x1 stride-1 layer of C3 (batch 64) run two ways on the
+    same operands, best of 3 rounds of 20 back-to-back calls: the forward and
+    the input gradient through this library's implicit GEMM, and the same
+    products as torch.matmul batched over the images (hipBLASLt on this
+    image): y[n] = W x[n] and dx[n] = W^T dy[n].  Reports per-layer times,
+    TFLOP/s and the largest difference between the two results."""
+    st = torch.cuda.current_stream().cuda_stream
+
+    def timed(fn, n=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        best = 1e9
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) / n * 1e3)
+        return best
+
+    rows, seen = [], set()
+    sums = defaultdict(float)
+    for name, xs, cout, k, stride, pad in resnet50_convs(64):
+        if k != 1 or stride != 1 or (xs, cout) in seen:
+            continue
+        seen.add((xs, cout))
+        n, cin, h, w = xs
+        g = torch.Generator(device="cuda").manual_seed(len(rows))
+        x = torch.randn(xs, device="cuda", generator=g)
+        wt = torch.randn(cout, cin, device="cuda", generator=g) / math.sqrt(cin)
+        dy = torch.randn(n, cout, h, w, device="cuda", generator=g)
+        d = mx.conv_desc(xs, (cout, cin, 1, 1), (1, 1), (0, 0))
+        w4 = wt.view(cout, cin, 1, 1)
+        y, y_ref = torch.empty_like(dy), torch.empty_like(dy)
+        dx, dx_ref = torch.empty_like(x), torch.empty_like(x)
+        wT = wt.t().contiguous()
+        t = {"fwd_ours_us": timed(lambda: mx.conv2d_forward(d, x, w4, None, y, mx.ALGO_IMPLICIT_GEMM, st)),
+             "fwd_blas_us": timed(lambda: torch.matmul(wt, x.view(n, cin, h * w), out=y_ref.view(n, cout, h * w))),
+             "dx_ours_us": timed(lambda: mx.conv2d_backward_input(d, dy, w4, dx, mx.ALGO_IMPLICIT_GEMM, st)),
+             "dx_blas_us": timed(lambda: torch.matmul(wT, dy.view(n, cout, h * w), out=dx_ref.view(n, cin, h * w)))}
+        flops = 2.0 * n * h * w * cin * cout
+        row = {"layer": name, "shape": f"{cin}->{cout} {h}x{w}", "gflop": round(flops / 1e9, 3)}
+        for key, us in t.items():
+            row[key] = round(us, 1)
+            row[key.replace("_us", "_tflops")] = round(flops / us / 1e6, 1)
+            sums[key] += us
+        row["fwd_max_diff"] = float((y - y_ref).abs().max())
+        row["dx_max_diff"] = float((dx - dx_ref).abs().max())
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+        del x, dy, y, y_ref, dx, dx_ref
+    return {"metric": "1x1 conv: implicit GEMM vs torch.matmul (hipBLASLt)", "layers": rows,
+            "sums_us": {k: round(v, 1) for k, v in sums.items()}}
+
+
 def run_plan_sweep(torch, mx):
     """The convolution planner against every (tile, K split) plan: each
     implicit-GEMM phase of the sweep's layers (phases AUTO sends to Winograd
@@ -1188,6 +1247,8 @@ def main(argv=None):
                     help="sweep the 4-read / 3-write probe's memory schedule at C5's size (one JSON object)")
     ap.add_argument("--rule-sweep", choices=["grid", "random"],
                     help="time both algorithms on 3x3 stride-1 layers in every phase against AUTO's Winograd rule")
+    ap.add_argument("--blas-compare", action="store_true",
+                    help="time C3's 1x1 stride-1 forwards and input gradients against torch.matmul (hipBLASLt)")
     ap.add_argument("--plan-sweep", action="store_true",
                     help="time every (tile, K split) plan of the convolution planner against its own picks")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1220,6 +1281,9 @@ def main(argv=None):
     L = Launcher(mx, stream)
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 
+    if args.blas_compare:
+        print(json.dumps(run_blas_compare(torch, mx)), flush=True)
+        return 0
     if args.plan_sweep:
         print(json.dumps(run_plan_sweep(torch, mx)), flush=True)
         return 0
