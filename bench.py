@@ -685,6 +685,70 @@ def run_blas_compare(torch, mx):
             "sums_us": {k: round(v, 1) for k, v in sums.items()}}
 
 
+def run_miopen_compare(torch, mx, find):
+    """The C3 step (53 layers, forward + dInput + dWeight, batch 64) through
+    PyTorch-ROCm's own convolutions, which call MIOpen, beside the same step
+    through this library, in one process on the same data.  MIOpen runs in
+    its immediate mode (torch's default) or, with `find`, with
+    torch.backends.cudnn.benchmark = True (MIOpen's find: every layer's
+    solvers searched on its first call; several minutes, one progress line
+    per layer on stderr).  Best of 3 rounds of 5 steps each way."""
+    torch.backends.cudnn.benchmark = bool(find)
+    L = Launcher(mx, torch.cuda.current_stream().cuda_stream)
+    calls, total, _ = build_c3(torch, mx, L, 64)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    layers = []
+    for name, xs, cout, k, stride, pad in resnet50_convs(64):
+        oh = (xs[2] + 2 * pad - k) // stride + 1
+        x = torch.randn(xs, device="cuda", generator=g)
+        w = torch.randn((cout, xs[1], k, k), device="cuda", generator=g) * math.sqrt(2.0 / (cout * k * k))
+        dy = torch.randn((xs[0], cout, oh, oh), device="cuda", generator=g)
+        layers.append((name, x, w, dy, stride, pad))
+    conv_bwd = torch.ops.aten.convolution_backward
+
+    def layer_torch(name, x, w, dy, s, p):
+        torch.nn.functional.conv2d(x, w, None, s, p)
+        conv_bwd(dy, x, w, None, (s, s), (p, p), (1, 1), False, (0, 0), 1, (name != "stem", True, False))
+
+    t0 = time.time()
+    for lay in layers:
+        layer_torch(*lay)
+        torch.cuda.synchronize()
+        print(f"[miopen] {lay[0]} ready at {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
+    setup_s = time.time() - t0
+
+    def best_ms(step):
+        best = 1e9
+        for _ in range(3):
+            for _ in range(2):
+                step()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                step()
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) / 5)
+        return best
+
+    def ours():
+        for c in calls:
+            c[3]()
+
+    def theirs():
+        for lay in layers:
+            layer_torch(*lay)
+
+    ms_ours, ms_miopen = best_ms(ours), best_ms(theirs)
+    return {"metric": "C3 step: this library vs PyTorch-ROCm convolutions (MIOpen)",
+            "miopen_mode": "find (cudnn.benchmark = True)" if find else "immediate (torch default)",
+            "miopen_setup_s": round(setup_s, 1), "gflop_per_step": round(total / 1e9, 2),
+            "ours_ms": round(ms_ours, 3), "ours_tflops": round(total / ms_ours / 1e9, 1),
+            "miopen_ms": round(ms_miopen, 3), "miopen_tflops": round(total / ms_miopen / 1e9, 1),
+            "speedup": round(ms_miopen / ms_ours, 3)}
+
+
 def run_plan_sweep(torch, mx):
     """The convolution planner against every (tile, K split) plan: each
     implicit-GEMM phase of the sweep's layers (phases AUTO sends to Winograd
@@ -1247,6 +1311,8 @@ def main(argv=None):
                     help="sweep the 4-read / 3-write probe's memory schedule at C5's size (one JSON object)")
     ap.add_argument("--rule-sweep", choices=["grid", "random"],
                     help="time both algorithms on 3x3 stride-1 layers in every phase against AUTO's Winograd rule")
+    ap.add_argument("--miopen-compare", choices=["immediate", "find"],
+                    help="time the C3 step against PyTorch-ROCm's MIOpen convolutions")
     ap.add_argument("--blas-compare", action="store_true",
                     help="time C3's 1x1 stride-1 forwards and input gradients against torch.matmul (hipBLASLt)")
     ap.add_argument("--plan-sweep", action="store_true",
@@ -1281,6 +1347,9 @@ def main(argv=None):
     L = Launcher(mx, stream)
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 
+    if args.miopen_compare:
+        print(json.dumps(run_miopen_compare(torch, mx, args.miopen_compare == "find")), flush=True)
+        return 0
     if args.blas_compare:
         print(json.dumps(run_blas_compare(torch, mx)), flush=True)
         return 0
