@@ -685,17 +685,14 @@ def run_blas_compare(torch, mx):
             "sums_us": {k: round(v, 1) for k, v in sums.items()}}
 
 
-def run_miopen_compare(torch, mx, find):
+def miopen_c3_step(torch, find, progress=True):
     """The C3 step (53 layers, forward + dInput + dWeight, batch 64) through
-    PyTorch-ROCm's own convolutions, which call MIOpen, beside the same step
-    through this library, in one process on the same data.  MIOpen runs in
-    its immediate mode (torch's default) or, with `find`, with
-    torch.backends.cudnn.benchmark = True (MIOpen's find: every layer's
-    solvers searched on its first call; several minutes, one progress line
-    per layer on stderr).  Best of 3 rounds of 5 steps each way."""
+    PyTorch-ROCm's own convolutions, which call MIOpen: immediate mode
+    (torch's default heuristics) or, with `find`, cudnn.benchmark = True
+    (every layer's solvers searched on its first call; several minutes, one
+    progress line per layer on stderr).  Returns (best ms per step over 3
+    rounds of 5 steps, setup seconds, the step function)."""
     torch.backends.cudnn.benchmark = bool(find)
-    L = Launcher(mx, torch.cuda.current_stream().cuda_stream)
-    calls, total, _ = build_c3(torch, mx, L, 64)
     g = torch.Generator(device="cuda").manual_seed(0)
     layers = []
     for name, xs, cout, k, stride, pad in resnet50_convs(64):
@@ -714,33 +711,48 @@ def run_miopen_compare(torch, mx, find):
     for lay in layers:
         layer_torch(*lay)
         torch.cuda.synchronize()
-        print(f"[miopen] {lay[0]} ready at {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
+        if progress:
+            print(f"[miopen] {lay[0]} ready at {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
     setup_s = time.time() - t0
 
-    def best_ms(step):
-        best = 1e9
-        for _ in range(3):
-            for _ in range(2):
-                step()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(5):
-                step()
-            e1.record()
-            e1.synchronize()
-            best = min(best, e0.elapsed_time(e1) / 5)
-        return best
+    def step():
+        for lay in layers:
+            layer_torch(*lay)
+
+    ms = best_step_ms(torch, step)
+    torch.backends.cudnn.benchmark = False
+    return ms, setup_s
+
+
+def best_step_ms(torch, step, rounds=3, steps=5):
+    best = 1e9
+    for _ in range(rounds):
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) / steps)
+    return best
+
+
+def run_miopen_compare(torch, mx, find):
+    """The C3 step through PyTorch-ROCm's MIOpen convolutions (miopen_c3_step)
+    beside the same step through this library, in one process on the same
+    data, best of 3 rounds of 5 steps each way."""
+    L = Launcher(mx, torch.cuda.current_stream().cuda_stream)
+    calls, total, _ = build_c3(torch, mx, L, 64)
 
     def ours():
         for c in calls:
             c[3]()
 
-    def theirs():
-        for lay in layers:
-            layer_torch(*lay)
-
-    ms_ours, ms_miopen = best_ms(ours), best_ms(theirs)
+    ms_miopen, setup_s = miopen_c3_step(torch, find)
+    ms_ours = best_step_ms(torch, ours)
     return {"metric": "C3 step: this library vs PyTorch-ROCm convolutions (MIOpen)",
             "miopen_mode": "find (cudnn.benchmark = True)" if find else "immediate (torch default)",
             "miopen_setup_s": round(setup_s, 1), "gflop_per_step": round(total / 1e9, 2),
@@ -1482,6 +1494,22 @@ def main(argv=None):
             comps["c4"].get("conv_gemm_executed_tflop_s"), "); roofline", comps["c4"].get("roofline"))
         comps["streams"] = run_streams(torch)
         log("streams", comps["streams"])
+        if args.workload == "c3" and not args.no_winograd:
+            # The headline step through PyTorch-ROCm's own convolutions (MIOpen,
+            # torch's default immediate mode) on this box: a vendor-library
+            # baseline, not the product path.
+            try:
+                ms_m, setup_s = miopen_c3_step(torch, False, progress=False)
+                comps["miopen"] = {
+                    "workload": "C3 step through torch.nn.functional.conv2d + aten.convolution_backward on the "
+                                "CUDA device (MIOpen, immediate mode: torch's default)",
+                    "ms_per_step": round(ms_m, 4), "value": round(flops_step / ms_m / 1e9, 3), "unit": "TFLOP/s",
+                    "setup_s": round(setup_s, 1), "headline_ms_per_step": round(ms_step, 4),
+                    "miopen_over_headline_time": round(ms_m / ms_step, 3)}
+            except Exception as e:  # a baseline only: never fail the bench on it
+                comps["miopen"] = {"error": f"{type(e).__name__}: {e}"}
+            log("miopen", comps["miopen"])
+            torch.cuda.empty_cache()
         result["components"] = comps
 
     # ---------------- CPU baselines (bounded samples, same seeded inputs)
