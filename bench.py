@@ -724,6 +724,55 @@ def miopen_c3_step(torch, find, progress=True):
     return ms, setup_s
 
 
+def torch_rocm_c2_c5(torch):
+    """C2's step and C5's AdamW step through PyTorch-ROCm's own kernels on the
+    CUDA device, on tensors of the same shapes and distributions: addmm / mm
+    (hipBLASLt) and sum for C2; torch._fused_adamw_ (the kernel behind
+    torch.optim.AdamW(fused=True)) for C5, after the same 10 warm-up steps.
+    Vendor / framework baselines beside the components, not the product
+    path."""
+    import numpy as np
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    M, K, N = 8192, 4096, 4096
+    X = torch.randn(M, K, device="cuda", generator=g)
+    W = (torch.rand(N, K, device="cuda", generator=g) * 2 - 1) / 64
+    b = (torch.rand(N, device="cuda", generator=g) * 2 - 1) / 64
+    dY = torch.randn(M, N, device="cuda", generator=g)
+    Y, dX, dW = torch.empty(M, N, device="cuda"), torch.empty_like(X), torch.empty_like(W)
+
+    def c2():
+        torch.addmm(b, X, W.t(), out=Y)
+        torch.mm(dY, W, out=dX)
+        torch.mm(dY.t(), X, out=dW)
+        dY.sum(0)
+
+    ms = best_step_ms(torch, c2)
+    out["c2"] = {"ms_per_step": round(ms, 4), "value": round(3 * 2.0 * M * N * K / ms / 1e9, 3), "unit": "TFLOP/s",
+                 "kernels": "torch.addmm / torch.mm (hipBLASLt) + sum"}
+    del X, W, b, dY, Y, dX, dW
+    rng = np.random.default_rng(0)
+    sizes = np.exp(rng.uniform(math.log(64), math.log(4194304), 250)).astype(np.int64)
+    P = [torch.randn(int(n), device="cuda", generator=g) * 0.02 for n in sizes]
+    G = [torch.randn(int(n), device="cuda", generator=g) * 1e-3 for n in sizes]
+    Mo = [torch.zeros(int(n), device="cuda") for n in sizes]
+    V = [torch.zeros(int(n), device="cuda") for n in sizes]
+    steps = [torch.zeros((), device="cuda") for _ in sizes]
+
+    def c5():
+        torch._foreach_add_(steps, 1)
+        torch._fused_adamw_(P, G, Mo, V, [], steps, lr=1e-3, beta1=0.9, beta2=0.999, weight_decay=0.01, eps=1e-8,
+                            amsgrad=False, maximize=False)
+
+    for _ in range(10):
+        c5()
+    ms = best_step_ms(torch, c5, steps=10)
+    numel = int(sizes.sum())
+    out["c5"] = {"ms_per_step": round(ms, 4), "value": round(28.0 * numel / ms / 1e6, 1), "unit": "GB/s",
+                 "kernels": "torch._fused_adamw_ (+ one _foreach_add_ for the step counters)"}
+    return out
+
+
 def best_step_ms(torch, step, rounds=3, steps=5):
     best = 1e9
     for _ in range(rounds):
@@ -1510,6 +1559,14 @@ def main(argv=None):
                 comps["miopen"] = {"error": f"{type(e).__name__}: {e}"}
             log("miopen", comps["miopen"])
             torch.cuda.empty_cache()
+        try:
+            for key, v in torch_rocm_c2_c5(torch).items():
+                v["this_library_over_torch_rocm"] = round(comps[key]["value"] / v["value"], 3)
+                comps[key]["torch_rocm"] = v
+                log(key, "torch-rocm", v)
+        except Exception as e:  # a baseline only: never fail the bench on it
+            log("torch-rocm baselines failed:", f"{type(e).__name__}: {e}")
+        torch.cuda.empty_cache()
         result["components"] = comps
 
     # ---------------- CPU baselines (bounded samples, same seeded inputs)
