@@ -724,6 +724,48 @@ def miopen_c3_step(torch, find, progress=True):
     return ms, setup_s
 
 
+def run_mfma_probe(torch):
+    """The engine clock under sustained FP32 matrix load: register-only MFMA
+    chains (libmxprobe.so's mxp_mfma_chain) on every CU, three workgroups per
+    CU, about 5 ms per launch, launched one after another from idle (after 2 s
+    without GPU work).  Per launch: TFLOP/s from HIP events and the median
+    engine clock over workgroups (cycle counter against the 100 MHz real-time
+    counter).  Alternates the two FP32 MFMA shapes on random operands, then
+    one launch of each on zeros."""
+    import ctypes as C
+    import numpy as np
+    lib = C.CDLL(os.path.join(REPO, "libmxprobe.so"))
+    lib.mxp_mfma_chain.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    st = torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks, iters = 3 * cus, 2000
+    out = torch.empty(blocks * 256, device="cuda")
+    clk = torch.zeros(2 * blocks, dtype=torch.int64, device="cuda")
+    rand = torch.randn(1 << 20, device="cuda")
+    zero = torch.zeros(1 << 20, device="cuda")
+    torch.cuda.synchronize()
+    time.sleep(2.0)
+    rows = []
+    plan = [(shape, "randn") for _ in range(6) for shape in (0, 1)] + [(0, "zeros"), (1, "zeros")]
+    for i, (shape, data) in enumerate(plan):
+        inp = rand if data == "randn" else zero
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        assert lib.mxp_mfma_chain(shape, C.c_void_p(inp.data_ptr()), C.c_void_p(out.data_ptr()), blocks, iters,
+                                  C.c_void_p(clk.data_ptr()), C.c_void_p(st)) == 0
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1)
+        c = clk.cpu().numpy().reshape(-1, 2).astype(np.float64)
+        ghz = float(np.median(c[:, 0] / (c[:, 1] / 100e6) / 1e9))
+        tf = blocks * 4 * iters * 131072.0 / ms / 1e9
+        rows.append({"launch": i, "mfma": "32x32x2" if shape == 0 else "16x16x4", "operands": data,
+                     "ms": round(ms, 3), "tflops": round(tf, 1), "frac_of_157.3": round(tf / PEAK_FP32_TFLOPS, 3),
+                     "clock_ghz": round(ghz, 3)})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+    return {"metric": "FP32 MFMA chains from idle: TFLOP/s and engine clock per launch", "launches": rows}
+
+
 def torch_rocm_c2_c5(torch):
     """C2's step and C5's AdamW step through PyTorch-ROCm's own kernels on the
     CUDA device, on tensors of the same shapes and distributions: addmm / mm
@@ -1372,6 +1414,8 @@ def main(argv=None):
                     help="sweep the 4-read / 3-write probe's memory schedule at C5's size (one JSON object)")
     ap.add_argument("--rule-sweep", choices=["grid", "random"],
                     help="time both algorithms on 3x3 stride-1 layers in every phase against AUTO's Winograd rule")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="FP32 MFMA chains from idle: TFLOP/s and engine clock per launch")
     ap.add_argument("--miopen-compare", choices=["immediate", "find"],
                     help="time the C3 step against PyTorch-ROCm's MIOpen convolutions")
     ap.add_argument("--blas-compare", action="store_true",
@@ -1408,6 +1452,9 @@ def main(argv=None):
     L = Launcher(mx, stream)
     log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
 
+    if args.mfma_probe:
+        print(json.dumps(run_mfma_probe(torch)), flush=True)
+        return 0
     if args.miopen_compare:
         print(json.dumps(run_miopen_compare(torch, mx, args.miopen_compare == "find")), flush=True)
         return 0

@@ -1,4 +1,4 @@
-// HBM stream probes for bench.py: the access patterns of the multi-tensor
+// Measurement probes for bench.py.  HBM streams: the access patterns of the multi-tensor
 // AdamW kernel (mx_adamw.hip) with trivial arithmetic, so the benchmark can
 // report AdamW against what the same pattern reaches on the same GPU in the
 // same run.  Measurement infrastructure only: not part of the drop-in C ABI
@@ -14,6 +14,15 @@
 //                       (two divisions and a square root, fixed
 //                       hyperparameters), next chunk's loads issued before
 //                       this chunk's stores                           (4 reads, 3 writes)
+//
+//   int mxp_mfma_chain(int shape, const float* in, float* out, int blocks, int iters,
+//                      unsigned long long* clk, void* stream)
+//
+//   Register-only chains of FP32 MFMAs (shape 0: v_mfma_f32_32x32x2f32 on
+//   four accumulators, shape 1: v_mfma_f32_16x16x4f32 on sixteen), operands
+//   read once from `in` (real data or zeros), iters x 131072 FLOPs per wave.
+//   Each workgroup records its cycle-counter and 100 MHz real-time-counter
+//   spans in clk[2b], clk[2b + 1], which give the engine clock it ran at.
 //
 // n must be a multiple of 4096 (one chunk); buffers 16-byte aligned.  Chunks
 // of 4096 elements are dealt round-robin to per_cu * CUs workgroups, a thread
@@ -239,6 +248,64 @@ extern "C" int mxp_mix_sweep(int vec, int prefetch, int contig, float* const* bu
     case 8: launch_sweep_v<8>(prefetch, contig, bufs, n, grid, s); break;
     default: return int(hipErrorInvalidValue);
   }
+  return int(hipGetLastError());
+}
+
+namespace {
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int SHAPE>
+__global__ __launch_bounds__(256) void mfma_chain_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                          int iters, unsigned long long* __restrict__ clk) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  float a[8], b[8];
+  for (int i = 0; i < 8; ++i) {
+    a[i] = in[(t * 16 + i) & 1048575];
+    b[i] = in[(t * 16 + 8 + i) & 1048575];
+  }
+  const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.f;
+  if constexpr (SHAPE == 0) {
+    f32x16 acc[4];
+    for (int j = 0; j < 4; ++j) acc[j] = f32x16{0.f};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q], b[(q + j) & 7], acc[j], 0, 0, 0);
+    }
+    for (int j = 0; j < 4; ++j)
+      for (int v = 0; v < 16; ++v) s += acc[j][v];
+  } else {
+    f32x4 acc[16];
+    for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[(q + j) & 7], b[(q * 3 + j) & 7], acc[j], 0, 0, 0);
+    }
+    for (int j = 0; j < 16; ++j)
+      for (int v = 0; v < 4; ++v) s += acc[j][v];
+  }
+  const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  out[t] = s;
+  if (threadIdx.x == 0) {
+    clk[2 * blockIdx.x] = c1 - c0;
+    clk[2 * blockIdx.x + 1] = r1 - r0;
+  }
+}
+}  // namespace
+
+extern "C" int mxp_mfma_chain(int shape, const float* in, float* out, int blocks, int iters,
+                              unsigned long long* clk, void* stream) {
+  if (blocks <= 0 || iters <= 0 || shape < 0 || shape > 1) return int(hipErrorInvalidValue);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (shape == 0)
+    hipLaunchKernelGGL(mfma_chain_kernel<0>, dim3(blocks), dim3(256), 0, s, in, out, iters, clk);
+  else
+    hipLaunchKernelGGL(mfma_chain_kernel<1>, dim3(blocks), dim3(256), 0, s, in, out, iters, clk);
   return int(hipGetLastError());
 }
 
